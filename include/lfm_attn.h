@@ -1,0 +1,170 @@
+/*
+ * lfm_attn.h -- C-ABI of the MI355X (gfx950) attention path for the LFM2 /
+ * LFM2.5 / LFM3 forward stacks.
+ *
+ * The reference engine (avisheksharmacoder/laii) has no FFI for attention:
+ * each forward stack fills a task-context struct and calls
+ * lfm2_parallel_for(pool, n_items, chunk, worker, &ctx).  Every lfm_hip_*
+ * entry point below replaces one of those dispatches (cited per function) and
+ * takes the same fields, minus the thread pool and the optional Q8_K output
+ * (which stays with the caller, in front of the wo projection).
+ *
+ * Conventions
+ *   - Pointers passed to lfm_hip_* are DEVICE pointers (hipMalloc'd, or from
+ *     lfm_attn_dev_alloc).  Layouts are the reference's: KV caches are
+ *     token-major uint16_t (IEEE binary16) [slot][n_head_kv][head_dim], Q and
+ *     outputs are float [row][n_head_q][head_dim].
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *     and is asynchronous; lfm_attn_stream_sync() waits for it.
+ *   - Every function returns LFM_ATTN_OK (0) or a negative status.  Invalid
+ *     shapes and positions are rejected on the host before any launch; no
+ *     partial work is enqueued for a rejected call.
+ *   - Entry points that split the key range across workgroups use a
+ *     library-owned device workspace (grown on demand, one per device);
+ *     calls that overlap on one device from several host threads race on it.
+ */
+#ifndef LFM_ATTN_H
+#define LFM_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ---------------------------------------------------------------- */
+#define LFM_ATTN_OK            0
+#define LFM_ATTN_E_INVALID    -1 /* null pointer, bad shape or geometry            */
+#define LFM_ATTN_E_RANGE      -2 /* position outside the cache / window            */
+#define LFM_ATTN_E_UNSUPPORTED -3 /* shape this build has no kernel for            */
+#define LFM_ATTN_E_DEVICE     -4 /* HIP runtime error (see lfm_attn_last_error)    */
+#define LFM_ATTN_E_NOMEM      -5 /* device allocation failed                       */
+
+typedef void *lfm_attn_stream_t; /* hipStream_t */
+
+const char *lfm_attn_status_string(int status);
+/* Text of the last HIP error seen by this thread ("" if none). */
+const char *lfm_attn_last_error(void);
+const char *lfm_attn_version(void);
+
+/* ---- device plumbing (so C11 callers need no HIP headers) ------------------ */
+int lfm_attn_device_count(int *count);
+int lfm_attn_set_device(int device);
+int lfm_attn_dev_alloc(void **ptr, size_t bytes);
+int lfm_attn_dev_free(void *ptr);
+int lfm_attn_copy_h2d(void *dst_dev, const void *src_host, size_t bytes, lfm_attn_stream_t stream);
+int lfm_attn_copy_d2h(void *dst_host, const void *src_dev, size_t bytes, lfm_attn_stream_t stream);
+int lfm_attn_copy_d2d(void *dst_dev, const void *src_dev, size_t bytes, lfm_attn_stream_t stream);
+int lfm_attn_memset(void *dst_dev, int value, size_t bytes, lfm_attn_stream_t stream);
+int lfm_attn_stream_sync(lfm_attn_stream_t stream);
+
+/* ---- index math (host copy of what the kernels compute) -------------------- */
+/* Row plan of tools/lfm3_engine.c:862-873:
+ * out5 = {t_start, count, seg1_slot, seg1_len, seg2_len}. */
+int lfm_attn_seg_plan(uint32_t abs_pos, uint32_t window_len, uint32_t cap, uint32_t out5[5]);
+/* Slot holding absolute position p: p % cap with a window, p without. */
+uint32_t lfm_attn_slot_of(uint32_t p, uint32_t window_len, uint32_t cap);
+
+/* ---- RoPE tables (host, double-precision angles; bit-identical) ------------- */
+/* Replaces lfm2_rope_lut_init, tools/lfm2_kernels_fast.c:370-388.
+ * cos_lut/sin_lut: HOST float[max_seq][head_dim/2]. */
+int lfm_attn_rope_lut_lfm2(float *cos_lut, float *sin_lut, uint32_t max_seq, uint32_t head_dim,
+                           float freq_base);
+/* Replaces lfm3_rope_lut_init, tools/lfm3_engine.c:403-450 (partial RoPE:
+ * identity pairs for i >= rope_dim/2 and for rope_freqs[i] >= 1e10 or <= 0). */
+int lfm_attn_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq, uint32_t head_dim,
+                           uint32_t rope_dim, float freq_base, const float *rope_freqs,
+                           uint32_t n_rope_freqs);
+
+/* ---- prologue: per-head QK-RMSNorm + NeoX RoPE (+ RNE fp16 KV store) -------- */
+/* Replaces lfm2_qk_norm_rope_simd (tools/lfm2_kernels_fast.c:403-497, :511-547)
+ * and lfm3_qk_norm_rope_simd (tools/lfm3_engine.c:463-525, :599-666).
+ * vec: [n_heads][head_dim] float.  norm_w: [head_dim] or NULL (no norm).
+ * cos_lut/sin_lut: DEVICE [>= pos+1][head_dim/2].  With dst_f16 != NULL the
+ * rotated heads are stored there as RNE fp16 and vec is not modified;
+ * otherwise vec is rotated in place.  head_dim even, <= 256. */
+int lfm_hip_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
+                         const float *norm_w, float eps, const float *cos_lut,
+                         const float *sin_lut, uint32_t pos, lfm_attn_stream_t stream);
+
+/* Replaces lfm2_store_fp32_to_fp16_simd (tools/lfm2_kernels_fast.c:500-507,
+ * :549-555) and lfm3_store_f32_to_f16 (tools/lfm3_engine.c:133-153): RNE. */
+int lfm_hip_store_fp32_to_fp16(uint16_t *dst_f16, const float *src, uint32_t n,
+                               lfm_attn_stream_t stream);
+
+/* Batched prologue for n_seq sequences x n_rows consecutive tokens (row r of
+ * sequence s is position pos_0[s] + r): Q rotated in place, K rotated and
+ * stored as RNE fp16 at slot lfm_attn_slot_of(pos, window_len, cap), V stored
+ * as RNE fp16 at the same slot.  This is the per-token prologue of
+ * lfm2_forward_gqa_batch (tools/lfm2_prefill_batch.c:1029-1072) and
+ * lfm3_forward_batch_core (tools/lfm3_engine.c:2006-2016) over many sequences.
+ * q: [n_seq][n_rows][n_head_q][hd]; k, v: [n_seq][n_rows][n_head_kv][hd];
+ * k_seq/v_seq: DEVICE arrays of n_seq DEVICE cache pointers; pos_0: DEVICE
+ * uint32_t[n_seq]. */
+int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *const *k_seq,
+                         uint16_t *const *v_seq, const uint32_t *pos_0, uint32_t n_seq,
+                         uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                         const float *q_norm_w, const float *k_norm_w, float eps,
+                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
+                         uint32_t cap, lfm_attn_stream_t stream);
+
+/* ---- attention ------------------------------------------------------------ */
+/* A1 -- replaces OnlineGQATaskCtx + lfm2_parallel_for(pool, ceil(n_head_q/4), 1,
+ * lfm2_online_gqa_f16_worker_simd, &ctx), tools/lfm2_kernels_fast.c:685-697,
+ * 700-872, 1052-1066.  head_dim 64; kv_h = h / kv_mul; keys [0, pos].
+ * q, xb_out: [n_head_q][64] float; caches [>= pos+1][kv_dim] fp16. */
+int lfm_hip_online_gqa_f16(const float *q, const uint16_t *k_cache_f16,
+                           const uint16_t *v_cache_f16, float *xb_out, uint32_t n_head_q,
+                           uint32_t kv_mul, uint32_t kv_dim, uint32_t pos, float scale,
+                           lfm_attn_stream_t stream);
+
+/* A2 -- replaces GQAAttnTaskCtx + lfm2_parallel_for(pool, n_head_q, 1,
+ * lfm2_gqa_heads_worker_task, &ctx), tools/lfm2_threadpool.c:745-931, as called
+ * at tools/lfm2_prefill_batch.c:1074-1091 and tools/lfm2_forward.c:1018-1035.
+ * With both f16 caches non-NULL: FP16 online branch (only the first 64 output
+ * dims are written when head_dim > 64, as the reference does).  Otherwise the
+ * FP32 caches k_cache/v_cache ([max_seq_len][kv_dim] float) are used.
+ * head_dim % 8 == 0, head_dim <= 256. */
+int lfm_hip_gqa_heads(const float *q, const float *k_cache, const float *v_cache,
+                      const uint16_t *k_cache_f16, const uint16_t *v_cache_f16, float *xb,
+                      uint32_t n_head_q, uint32_t kv_mul, uint32_t head_dim, uint32_t kv_dim,
+                      uint32_t max_seq_len, uint32_t pos, float scale, lfm_attn_stream_t stream);
+
+/* A3 -- replaces lfm3_online_gqa_f16_dispatch, tools/lfm3_engine.c:1155-1204
+ * (workers :851-946, :1057-1153).  Row b is position pos_0 + b and attends
+ * the plan of lfm_attn_seg_plan(pos_0 + b, window_len, swa_cap); output is
+ * o * (gate_sig[b][h] / l) (gate 1 when gate_sig is NULL).
+ * q_batch, xb_out: [B][n_head_q][head_dim]; gate_sig: [B][n_head_q] or NULL. */
+int lfm_hip_lfm3_online_gqa_f16_dispatch(const float *q_batch, const float *gate_sig,
+                                         const uint16_t *k_cache_f16,
+                                         const uint16_t *v_cache_f16, float *xb_out, uint32_t B,
+                                         uint32_t pos_0, uint32_t window_len, uint32_t swa_cap,
+                                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                                         lfm_attn_stream_t stream);
+
+/* Multi-sequence form of A1/A2/A3 (decode batches and the B<=8 speculative
+ * verify of tools/lfm2_speculative_pld.c:388-461 over many sequences): n_seq
+ * independent caches, n_rows consecutive query rows per sequence; row r of
+ * sequence s is position pos_0[s] + r and attends
+ * lfm_attn_seg_plan(pos_0[s] + r, window_len, cap) of its own cache.
+ * q, out: [n_seq][n_rows][n_head_q][head_dim] float.
+ * gate: [n_seq][n_rows][n_head_q] float or NULL; sigmoid is applied in the
+ *   epilogue when gate_is_logit != 0 (tools/lfm3_engine.c:1588-1597), the
+ *   values are used as-is otherwise.
+ * k_seq, v_seq: DEVICE arrays of n_seq DEVICE cache pointers; pos_0: DEVICE
+ *   uint32_t[n_seq].
+ * max_keys_hint: upper bound of keys any row attends (sizes the key split;
+ *   0 = unknown).  Correctness does not depend on it.
+ * scale: multiplies q.k (1/sqrtf(head_dim) in every reference caller). */
+int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
+                           const uint16_t *const *k_seq, const uint16_t *const *v_seq,
+                           const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
+                           uint32_t max_keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                           uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                           lfm_attn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LFM_ATTN_H */

@@ -1,0 +1,25 @@
+"""laii_amd -- MI355X (gfx950) attention path of the LFM2/LFM2.5/LFM3 engine.
+
+The product is the native library laii_amd/liblfm_attn.so (C-ABI in
+include/lfm_attn.h: HIP kernels + C11 host code).  This package is its Python
+host mirror: ctypes bindings named after the reference's dispatch calls.
+"""
+from ._lib import LIB_PATH, LfmAttnError, load  # noqa: F401
+from .attention import (  # noqa: F401
+    DeviceArray,
+    device_count,
+    gqa_f16_varlen,
+    gqa_heads,
+    lfm3_online_gqa_f16_dispatch,
+    online_gqa_f16,
+    pointer_table,
+    qk_norm_rope,
+    qkv_prologue,
+    require_gpu,
+    rope_lut_lfm2,
+    rope_lut_lfm3,
+    seg_plan,
+    slot_of,
+    store_fp32_to_fp16,
+    sync,
+)

@@ -1,0 +1,83 @@
+"""ctypes binding of laii_amd/liblfm_attn.so (the C-ABI of include/lfm_attn.h).
+
+Loading fails loudly: there is no CPU fallback anywhere in the package.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "liblfm_attn.so")
+
+_u32 = C.c_uint32
+_f32 = C.c_float
+_int = C.c_int
+_vp = C.c_void_p
+_sz = C.c_size_t
+
+# name -> (restype, argtypes); every function declared in include/lfm_attn.h
+SIGNATURES = {
+    "lfm_attn_status_string": (C.c_char_p, [_int]),
+    "lfm_attn_last_error": (C.c_char_p, []),
+    "lfm_attn_version": (C.c_char_p, []),
+    "lfm_attn_device_count": (_int, [C.POINTER(_int)]),
+    "lfm_attn_set_device": (_int, [_int]),
+    "lfm_attn_dev_alloc": (_int, [C.POINTER(_vp), _sz]),
+    "lfm_attn_dev_free": (_int, [_vp]),
+    "lfm_attn_copy_h2d": (_int, [_vp, _vp, _sz, _vp]),
+    "lfm_attn_copy_d2h": (_int, [_vp, _vp, _sz, _vp]),
+    "lfm_attn_copy_d2d": (_int, [_vp, _vp, _sz, _vp]),
+    "lfm_attn_memset": (_int, [_vp, _int, _sz, _vp]),
+    "lfm_attn_stream_sync": (_int, [_vp]),
+    "lfm_attn_seg_plan": (_int, [_u32, _u32, _u32, C.POINTER(_u32)]),
+    "lfm_attn_slot_of": (_u32, [_u32, _u32, _u32]),
+    "lfm_attn_rope_lut_lfm2": (_int, [_vp, _vp, _u32, _u32, _f32]),
+    "lfm_attn_rope_lut_lfm3": (_int, [_vp, _vp, _u32, _u32, _u32, _f32, _vp, _u32]),
+    "lfm_hip_qk_norm_rope": (_int, [_vp, _vp, _u32, _u32, _vp, _f32, _vp, _vp, _u32, _vp]),
+    "lfm_hip_store_fp32_to_fp16": (_int, [_vp, _vp, _u32, _vp]),
+    "lfm_hip_qkv_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
+                                    _vp, _vp, _f32, _vp, _vp, _u32, _u32, _vp]),
+    "lfm_hip_online_gqa_f16": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32, _vp]),
+    "lfm_hip_gqa_heads": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                                 _f32, _vp]),
+    "lfm_hip_lfm3_online_gqa_f16_dispatch": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                                    _u32, _u32, _u32, _u32, _vp]),
+    "lfm_hip_gqa_f16_varlen": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                      _u32, _u32, _u32, _u32, _f32, _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LfmAttnError(RuntimeError):
+    def __init__(self, status: int, where: str, detail: str = ""):
+        self.status = status
+        super().__init__(f"{where}: status {status} ({detail})")
+
+
+def load() -> C.CDLL:
+    """Load the native library (built by laii_amd.build / __graft_entry__.build)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+        lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def check(status: int, where: str) -> None:
+    if status != 0:
+        lib = load()
+        raise LfmAttnError(status, where, lib.lfm_attn_status_string(status).decode() + " " +
+                           lib.lfm_attn_last_error().decode())

@@ -1,0 +1,193 @@
+"""Python mirror of the reference's attention dispatch interface, running on
+the MI355X kernels through the C-ABI.
+
+Function names and argument meaning follow the reference task contexts:
+  online_gqa_f16                 OnlineGQATaskCtx        tools/lfm2_kernels_fast.c:685-697
+  gqa_heads                      GQAAttnTaskCtx          tools/lfm2_threadpool.c:746-762
+  lfm3_online_gqa_f16_dispatch   lfm3_online_gqa_f16_dispatch tools/lfm3_engine.c:1155-1168
+  qk_norm_rope                   lfm2/lfm3_qk_norm_rope_* tools/lfm2_kernels_fast.c:403-547,
+                                                          tools/lfm3_engine.c:463-666
+  rope_lut_lfm2 / rope_lut_lfm3  lfm2_rope_lut_init / lfm3_rope_lut_init
+Tensors are DeviceArray objects (device memory) or raw device addresses (int).
+Every call raises LfmAttnError on a non-zero status; nothing falls back to
+the CPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence, Union
+
+import numpy as np
+
+from ._lib import check, load
+
+Ptr = Union["DeviceArray", int, None]
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(load().lfm_attn_device_count(C.byref(n)), "lfm_attn_device_count")
+    return int(n.value)
+
+
+def require_gpu() -> None:
+    if device_count() < 1:
+        raise RuntimeError("no HIP device visible: the attention path runs only on the GPU")
+
+
+class DeviceArray:
+    """A device allocation with numpy upload/download (no torch involved)."""
+
+    def __init__(self, shape, dtype):
+        self.shape = tuple(int(x) for x in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p(0)
+        check(load().lfm_attn_dev_alloc(C.byref(p), self.nbytes), "lfm_attn_dev_alloc")
+        self.ptr = int(p.value or 0)
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray, stream=None) -> "DeviceArray":
+        arr = np.ascontiguousarray(arr)
+        d = cls(arr.shape, arr.dtype)
+        d.upload(arr, stream)
+        return d
+
+    @classmethod
+    def zeros(cls, shape, dtype) -> "DeviceArray":
+        d = cls(shape, dtype)
+        check(load().lfm_attn_memset(d.ptr, 0, d.nbytes, None), "lfm_attn_memset")
+        return d
+
+    def upload(self, arr: np.ndarray, stream=None) -> None:
+        arr = np.ascontiguousarray(arr, dtype=self.dtype)
+        assert arr.nbytes == self.nbytes, (arr.nbytes, self.nbytes)
+        check(load().lfm_attn_copy_h2d(self.ptr, arr.ctypes.data, self.nbytes, stream),
+              "lfm_attn_copy_h2d")
+        if stream is None:
+            check(load().lfm_attn_stream_sync(None), "lfm_attn_stream_sync")
+
+    def numpy(self, stream=None) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(load().lfm_attn_copy_d2h(out.ctypes.data, self.ptr, self.nbytes, stream),
+              "lfm_attn_copy_d2h")
+        return out
+
+    def free(self) -> None:
+        if getattr(self, "ptr", 0):
+            load().lfm_attn_dev_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def __int__(self) -> int:
+        return self.ptr
+
+
+def _p(x: Ptr) -> Optional[int]:
+    if x is None:
+        return None
+    return int(x)
+
+
+def sync(stream=None) -> None:
+    check(load().lfm_attn_stream_sync(stream), "lfm_attn_stream_sync")
+
+
+def seg_plan(abs_pos: int, window_len: int, cap: int):
+    out = (C.c_uint32 * 5)()
+    check(load().lfm_attn_seg_plan(abs_pos, window_len, cap, out), "lfm_attn_seg_plan")
+    return tuple(int(x) for x in out)
+
+
+def slot_of(p: int, window_len: int, cap: int) -> int:
+    return int(load().lfm_attn_slot_of(p, window_len, cap))
+
+
+def rope_lut_lfm2(max_seq: int, head_dim: int, freq_base: float):
+    c = np.empty((max_seq, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    check(load().lfm_attn_rope_lut_lfm2(c.ctypes.data, s.ctypes.data, max_seq, head_dim, freq_base),
+          "lfm_attn_rope_lut_lfm2")
+    return c, s
+
+
+def rope_lut_lfm3(max_seq: int, head_dim: int, rope_dim: int, freq_base: float,
+                  rope_freqs: Optional[np.ndarray] = None):
+    c = np.empty((max_seq, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    rf = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+    check(load().lfm_attn_rope_lut_lfm3(c.ctypes.data, s.ctypes.data, max_seq, head_dim, rope_dim,
+                                        freq_base, None if rf is None else rf.ctypes.data,
+                                        0 if rf is None else rf.size), "lfm_attn_rope_lut_lfm3")
+    return c, s
+
+
+def qk_norm_rope(vec: Ptr, dst_f16: Ptr, n_heads: int, head_dim: int, norm_w: Ptr, eps: float,
+                 cos_lut: Ptr, sin_lut: Ptr, pos: int, stream=None) -> None:
+    check(load().lfm_hip_qk_norm_rope(_p(vec), _p(dst_f16), n_heads, head_dim, _p(norm_w), eps,
+                                      _p(cos_lut), _p(sin_lut), pos, stream), "lfm_hip_qk_norm_rope")
+
+
+def store_fp32_to_fp16(dst_f16: Ptr, src: Ptr, n: int, stream=None) -> None:
+    check(load().lfm_hip_store_fp32_to_fp16(_p(dst_f16), _p(src), n, stream),
+          "lfm_hip_store_fp32_to_fp16")
+
+
+def qkv_prologue(q: Ptr, k: Ptr, v: Ptr, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr, n_seq: int,
+                 n_rows: int, n_head_q: int, n_head_kv: int, head_dim: int, q_norm_w: Ptr,
+                 k_norm_w: Ptr, eps: float, cos_lut: Ptr, sin_lut: Ptr, window_len: int = 0,
+                 cap: int = 0, stream=None) -> None:
+    check(load().lfm_hip_qkv_prologue(_p(q), _p(k), _p(v), _p(k_seq), _p(v_seq), _p(pos_0), n_seq,
+                                      n_rows, n_head_q, n_head_kv, head_dim, _p(q_norm_w),
+                                      _p(k_norm_w), eps, _p(cos_lut), _p(sin_lut), window_len, cap,
+                                      stream), "lfm_hip_qkv_prologue")
+
+
+def online_gqa_f16(q: Ptr, k_cache_f16: Ptr, v_cache_f16: Ptr, xb_out: Ptr, n_head_q: int,
+                   kv_mul: int, kv_dim: int, pos: int, scale: float = 0.125, stream=None) -> None:
+    check(load().lfm_hip_online_gqa_f16(_p(q), _p(k_cache_f16), _p(v_cache_f16), _p(xb_out),
+                                        n_head_q, kv_mul, kv_dim, pos, scale, stream),
+          "lfm_hip_online_gqa_f16")
+
+
+def gqa_heads(q: Ptr, k_cache: Ptr, v_cache: Ptr, k_cache_f16: Ptr, v_cache_f16: Ptr, xb: Ptr,
+              n_head_q: int, kv_mul: int, head_dim: int, kv_dim: int, max_seq_len: int, pos: int,
+              scale: Optional[float] = None, stream=None) -> None:
+    if scale is None:
+        scale = float(1.0 / np.sqrt(np.float32(head_dim)))
+    check(load().lfm_hip_gqa_heads(_p(q), _p(k_cache), _p(v_cache), _p(k_cache_f16),
+                                   _p(v_cache_f16), _p(xb), n_head_q, kv_mul, head_dim, kv_dim,
+                                   max_seq_len, pos, scale, stream), "lfm_hip_gqa_heads")
+
+
+def lfm3_online_gqa_f16_dispatch(q_batch: Ptr, gate_sig: Ptr, k_cache_f16: Ptr, v_cache_f16: Ptr,
+                                 xb_out: Ptr, B: int, pos_0: int, window_len: int, swa_cap: int,
+                                 n_head_q: int, n_head_kv: int, head_dim: int,
+                                 stream=None) -> None:
+    check(load().lfm_hip_lfm3_online_gqa_f16_dispatch(_p(q_batch), _p(gate_sig), _p(k_cache_f16),
+                                                      _p(v_cache_f16), _p(xb_out), B, pos_0,
+                                                      window_len, swa_cap, n_head_q, n_head_kv,
+                                                      head_dim, stream),
+          "lfm_hip_lfm3_online_gqa_f16_dispatch")
+
+
+def gqa_f16_varlen(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr,
+                   out: Ptr, n_seq: int, n_rows: int, max_keys_hint: int, n_head_q: int,
+                   n_head_kv: int, head_dim: int, window_len: int = 0, cap: int = 0,
+                   scale: Optional[float] = None, stream=None) -> None:
+    if scale is None:
+        scale = float(1.0 / np.sqrt(np.float32(head_dim)))
+    check(load().lfm_hip_gqa_f16_varlen(_p(q), _p(gate), int(bool(gate_is_logit)), _p(k_seq),
+                                        _p(v_seq), _p(pos_0), _p(out), n_seq, n_rows,
+                                        max_keys_hint, n_head_q, n_head_kv, head_dim, window_len,
+                                        cap, scale, stream), "lfm_hip_gqa_f16_varlen")
+
+
+def pointer_table(arrays: Sequence[Union["DeviceArray", int]]) -> DeviceArray:
+    """Device array of device pointers (the k_seq / v_seq arguments)."""
+    return DeviceArray.from_numpy(np.array([int(a) for a in arrays], dtype=np.uint64))

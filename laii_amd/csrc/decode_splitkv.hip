@@ -1,0 +1,452 @@
+/*
+ * decode_splitkv.hip -- split-KV online-softmax GQA attention over fp16 KV
+ * caches on gfx950 MFMA (decode, B<=8 speculative verify, LFM3 SWA ring and
+ * full layers).
+ *
+ * Reference semantics: tools/lfm2_kernels_fast.c:700-810 (A1),
+ * tools/lfm2_threadpool.c:764-828 (A2 fp16 branch), tools/lfm3_engine.c:851-946
+ * (A3: ring segments, gate epilogue o * gate / l).  The softmax is the same
+ * mathematical function; keys are visited in 32-key sub-tiles instead of one
+ * at a time, and partial results of key splits are merged by log-sum-exp.
+ *
+ * Work decomposition: one wave64 workgroup per (key split, KV head, sequence).
+ * The wave owns every query column that reads its KV head: column
+ * n = row * kv_mul + j (row of the speculative batch, q head kvh*kv_mul + j),
+ * so each K/V byte of the split is read from HBM exactly once.
+ *
+ * Per 32-key sub-tile:
+ *   S^T[key][col] = K . Q^T      v_mfma_f32_16x16x32_f16, A = K rows loaded
+ *                                straight from HBM (16 B per lane), B = Q^T.
+ *                                Q is held as fp16 hi + lo (q*scale*log2e =
+ *                                hi + lo), both accumulated into one S^T, so
+ *                                scores keep ~fp32 accuracy.
+ *   online softmax (exp2 domain) on the S^T accumulator: column max over the
+ *                                8 scores a lane holds + 2 cross-row shuffles.
+ *   O^T[d][col] += V^T . P^T     the S^T accumulator layout IS the B-operand
+ *                                layout of the next MFMA (keys 4g..4g+3 and
+ *                                16+4g..19+4g of column l%16), so P needs no
+ *                                shuffle; P is split hi + lo like Q.  V^T comes
+ *                                from LDS: V rows are loaded 16 B per lane,
+ *                                four keys per lane are packed per dim and
+ *                                written as 8-byte [d][key] runs.
+ * Loads of sub-tile i+1 are issued before sub-tile i is consumed.
+ */
+#include <hip/hip_runtime.h>
+
+#include "attn_index.h"
+#include "kernels.h"
+#include "lfm_attn.h"
+
+namespace lfm {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e     = 1.4426950408889634f;
+constexpr float kNegBig    = -1e30f; /* running-max sentinel (finite)          */
+constexpr int kVtStride    = 36;     /* halfs per d-row of the LDS V^T tile    */
+
+struct SplitParams {
+    const float *q;
+    const float *gate;
+    const uint16_t *k_base;
+    const uint16_t *v_base;
+    const uint16_t *const *k_seq;
+    const uint16_t *const *v_seq;
+    uint64_t seq_stride;
+    const uint32_t *pos0_dev;
+    float *out;
+    float *part_o;   /* [seq][kvh][split][col][HD] unnormalised O            */
+    float2 *part_ml; /* [seq][kvh][split][col] (running max, sum) in log2 units */
+    uint32_t pos0_host, n_rows, n_head_q, n_head_kv, kv_mul, ncols;
+    uint32_t window, cap, n_splits, out_dims;
+    int gate_is_logit;
+    float qscale; /* scale * log2(e) */
+};
+
+__device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
+
+__device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float gate_value(const float *gate, size_t idx, int is_logit) {
+    if (!gate) return 1.0f;
+    const float g = gate[idx];
+    return is_logit ? 1.0f / (1.0f + expf(-g)) : g;
+}
+
+template <int HD, int NT>
+__global__ __launch_bounds__(64) void k_splitkv(const SplitParams P) {
+    constexpr int NS  = HD / 32; /* MFMA k-steps of Q.K^T (32 dims each)          */
+    constexpr int NM  = HD / 16; /* 16-dim tiles of O^T                            */
+    constexpr int NVL = HD / 16; /* 16-byte V pieces per lane per 32-key sub-tile  */
+    constexpr int CH  = HD / 8;  /* 16-byte chunks per V row                       */
+    constexpr int QPP = 64 / CH; /* 4-key quads covered by one pass of 64 lanes    */
+    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * kVtStride];
+
+    const int lane = threadIdx.x;
+    const int l16  = lane & 15;
+    const int g    = lane >> 4;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+
+    const uint32_t pos0  = P.pos0_dev ? P.pos0_dev[s] : P.pos0_host;
+    const uint32_t last  = pos0 + P.n_rows - 1u;
+    const uint32_t lo    = lfm_plan_row(pos0, P.window, P.cap).t_start;
+    const uint32_t total = last - lo + 1u;
+    uint32_t chunk       = (total + P.n_splits - 1u) / P.n_splits;
+    chunk                = (chunk + 31u) & ~31u;
+    const uint32_t kb    = lo + split * chunk;
+    const uint32_t ke    = min(kb + chunk, last + 1u); /* exclusive; empty if kb > last */
+    const size_t part    = ((size_t)(s * P.n_head_kv + kvh) * P.n_splits + split) * P.ncols;
+
+    if (kb > last) {
+        /* empty split (short sequence): mark every column as contributing nothing */
+        for (uint32_t n = lane; n < P.ncols; n += 64) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
+        return;
+    }
+
+    const uint16_t *kc = P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride;
+    const uint16_t *vc = P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride;
+    const size_t row   = (size_t)P.n_head_kv * HD; /* elements per cache slot */
+    kc += (size_t)kvh * HD;
+    vc += (size_t)kvh * HD;
+
+    /* ---- per-column row bounds and Q fragments ------------------------------ */
+    uint32_t col_lo[NT], col_hi[NT];
+    half8_t qh[NT][NS], ql[NT][NS];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t n = (uint32_t)(l16 + 16 * nt);
+        col_lo[nt] = 0xFFFFFFFFu; /* padding column: every key masked */
+        col_hi[nt] = 0u;
+        if (n < P.ncols) {
+            const uint32_t r   = n / P.kv_mul;
+            const uint32_t h   = kvh * P.kv_mul + (n - r * P.kv_mul);
+            const uint32_t abs = pos0 + r;
+            col_lo[nt]         = lfm_plan_row(abs, P.window, P.cap).t_start;
+            col_hi[nt]         = abs;
+            const float *qp    = P.q + (((size_t)s * P.n_rows + r) * P.n_head_q + h) * HD + 8 * g;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                const float4 a = *reinterpret_cast<const float4 *>(qp + 32 * st);
+                const float4 b = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
+                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float xs      = x[j] * P.qscale;
+                    const _Float16 hi   = (_Float16)xs;
+                    qh[nt][st][j]       = hi;
+                    ql[nt][st][j]       = (_Float16)(xs - (float)hi);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                qh[nt][st] = (half8_t)(_Float16)0.0f;
+                ql[nt][st] = (half8_t)(_Float16)0.0f;
+            }
+        }
+    }
+    /* keys every real column may see without a per-key test */
+    const uint32_t free_lo = lfm_plan_row(last, P.window, P.cap).t_start;
+    const uint32_t free_hi = min(pos0, ke - 1u);
+
+    /* ---- sub-tile loader ------------------------------------------------------ */
+    auto load_tile = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
+        const uint32_t base = P.window ? (p0 % P.cap) : p0;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            uint32_t off = (uint32_t)(16 * kt + l16);
+            if (p0 + off >= ke) off = ke - 1u - p0; /* clamp: masked later */
+            uint32_t slot = base + off;
+            if (P.window) { while (slot >= P.cap) slot -= P.cap; }
+            const uint16_t *kp = kc + (size_t)slot * row + 8 * g;
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+                kd[kt][st] = *reinterpret_cast<const u32x4_t *>(kp + 32 * st);
+        }
+#pragma unroll
+        for (int ps = 0; ps < HD / 64; ++ps) {
+            const int quad = ps * QPP + lane / CH;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t off = (uint32_t)(4 * quad + i);
+                if (p0 + off >= ke) off = ke - 1u - p0;
+                uint32_t slot = base + off;
+                if (P.window) { while (slot >= P.cap) slot -= P.cap; }
+                vd[ps * 4 + i] = *reinterpret_cast<const u32x4_t *>(vc + (size_t)slot * row + 8 * (lane % CH));
+            }
+        }
+    };
+
+    float4_t oacc[NM][NT];
+    float mrun[NT], lrun[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        mrun[nt] = kNegBig;
+        lrun[nt] = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
+    }
+
+    /* one 32-key sub-tile: V^T to LDS, S^T, online softmax, O^T update */
+    auto process = [&](uint32_t p0, const u32x4_t (&kcur)[2][NS], const u32x4_t (&vcur)[NVL]) {
+        __syncthreads(); /* previous sub-tile's V^T reads are done */
+#pragma unroll
+        for (int ps = 0; ps < HD / 64; ++ps) {
+            const int quad = ps * QPP + lane / CH;
+            const int c    = lane % CH;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t a0 = vcur[ps * 4 + 0][w], a1 = vcur[ps * 4 + 1][w];
+                const uint32_t a2 = vcur[ps * 4 + 2][w], a3 = vcur[ps * 4 + 3][w];
+                u32x2_t even, odd; /* dims 8c+2w and 8c+2w+1 of keys 4quad..4quad+3 */
+                even[0] = (a0 & 0xFFFFu) | (a1 << 16);
+                even[1] = (a2 & 0xFFFFu) | (a3 << 16);
+                odd[0]  = (a0 >> 16) | (a1 & 0xFFFF0000u);
+                odd[1]  = (a2 >> 16) | (a3 & 0xFFFF0000u);
+                *reinterpret_cast<u32x2_t *>(&vt[(8 * c + 2 * w) * kVtStride + 4 * quad])     = even;
+                *reinterpret_cast<u32x2_t *>(&vt[(8 * c + 2 * w + 1) * kVtStride + 4 * quad]) = odd;
+            }
+        }
+
+        /* S^T = K . Q^T (log2 units) */
+        float4_t sacc[2][NT];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float4_t acc = (float4_t)0.0f;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    acc = mfma(as_half8(kcur[kt][st]), qh[nt][st], acc);
+                    acc = mfma(as_half8(kcur[kt][st]), ql[nt][st], acc);
+                }
+                sacc[kt][nt] = acc;
+            }
+
+        /* masks: only sub-tiles touching a row bound or the split end */
+        const bool need_mask = (p0 < free_lo) || (p0 + 31u > free_hi);
+        if (need_mask) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t key = p0 + (uint32_t)(16 * kt + 4 * g + i);
+                        const bool ok = key < ke && key >= col_lo[nt] && key <= col_hi[nt];
+                        if (!ok) sacc[kt][nt][i] = -INFINITY;
+                    }
+        }
+
+        /* online softmax; P^T fragments (hi, lo) */
+        half8_t ph[NT], pl[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            float mx = fmaxf(fmaxf(fmaxf(sacc[0][nt][0], sacc[0][nt][1]), fmaxf(sacc[0][nt][2], sacc[0][nt][3])),
+                             fmaxf(fmaxf(sacc[1][nt][0], sacc[1][nt][1]), fmaxf(sacc[1][nt][2], sacc[1][nt][3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float mnew  = fmaxf(mrun[nt], mx);
+            const float alpha = __builtin_amdgcn_exp2f(mrun[nt] - mnew);
+            mrun[nt]          = mnew;
+            float psum        = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float p      = __builtin_amdgcn_exp2f(sacc[kt][nt][i] - mnew);
+                    psum              += p;
+                    const _Float16 hi  = (_Float16)p;
+                    ph[nt][4 * kt + i] = hi;
+                    pl[nt][4 * kt + i] = (_Float16)(p - (float)hi);
+                }
+            lrun[nt] = lrun[nt] * alpha + psum;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
+        }
+
+        __syncthreads(); /* V^T of this sub-tile is in LDS */
+        /* O^T += V^T . P^T */
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) {
+            const uint16_t *src = &vt[(16 * mt + l16) * kVtStride + 4 * g];
+            const u32x2_t x0    = *reinterpret_cast<const u32x2_t *>(src);
+            const u32x2_t x1    = *reinterpret_cast<const u32x2_t *>(src + 16);
+            u32x4_t a;
+            a[0] = x0[0]; a[1] = x0[1]; a[2] = x1[0]; a[3] = x1[1];
+            const half8_t av = as_half8(a);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                oacc[mt][nt] = mfma(av, ph[nt], oacc[mt][nt]);
+                oacc[mt][nt] = mfma(av, pl[nt], oacc[mt][nt]);
+            }
+        }
+    };
+
+    /* two register buffers; the loads of sub-tile i+1 are in flight while
+     * sub-tile i is consumed */
+    const uint32_t nsub = (ke - kb + 31u) / 32u;
+    u32x4_t kA[2][NS], vA[NVL], kB[2][NS], vB[NVL];
+    load_tile(kb, kA, vA);
+    for (uint32_t it = 0; it < nsub; it += 2u) {
+        const uint32_t p0 = kb + 32u * it;
+        if (it + 1u < nsub) load_tile(p0 + 32u, kB, vB);
+        process(p0, kA, vA);
+        if (it + 1u >= nsub) break;
+        if (it + 2u < nsub) load_tile(p0 + 64u, kA, vA);
+        process(p0 + 32u, kB, vB);
+    }
+
+    /* ---- epilogue ---------------------------------------------------------- */
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        float lt = lrun[nt] + __shfl_xor(lrun[nt], 16);
+        lt += __shfl_xor(lt, 32);
+        const uint32_t n = (uint32_t)(l16 + 16 * nt);
+        if (n >= P.ncols) continue;
+        const uint32_t r = n / P.kv_mul;
+        const uint32_t h = kvh * P.kv_mul + (n - r * P.kv_mul);
+        if (P.n_splits == 1u) {
+            const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+            const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+            const float inv   = (lt > 0.0f) ? gv / lt : 0.0f;
+            float *op         = P.out + orow * HD;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const uint32_t d = (uint32_t)(16 * mt + 4 * g);
+                if (d < P.out_dims) {
+                    float4 v = make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv,
+                                           oacc[mt][nt][2] * inv, oacc[mt][nt][3] * inv);
+                    *reinterpret_cast<float4 *>(op + d) = v;
+                }
+            }
+        } else {
+            float *po = P.part_o + (part + n) * HD;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const uint32_t d = (uint32_t)(16 * mt + 4 * g);
+                *reinterpret_cast<float4 *>(po + d) =
+                    make_float4(oacc[mt][nt][0], oacc[mt][nt][1], oacc[mt][nt][2], oacc[mt][nt][3]);
+            }
+            if (g == 0) P.part_ml[part + n] = make_float2(mrun[nt], lt);
+        }
+    }
+}
+
+/* Log-sum-exp merge of the key splits of one (sequence, KV head, column);
+ * applies 1/l and the gate.  One thread per output dim. */
+template <int HD>
+__global__ __launch_bounds__(HD) void k_merge(const SplitParams P) {
+    const uint32_t n = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    const uint32_t d = threadIdx.x;
+    const size_t base = (size_t)(s * P.n_head_kv + kvh) * P.n_splits * P.ncols + n;
+    float M = kNegBig;
+    for (uint32_t sp = 0; sp < P.n_splits; ++sp) {
+        const float2 ml = P.part_ml[base + (size_t)sp * P.ncols];
+        if (ml.y > 0.0f) M = fmaxf(M, ml.x);
+    }
+    float L = 0.0f, O = 0.0f;
+    for (uint32_t sp = 0; sp < P.n_splits; ++sp) {
+        const size_t idx = base + (size_t)sp * P.ncols;
+        const float2 ml  = P.part_ml[idx];
+        if (ml.y > 0.0f) {
+            const float w = __builtin_amdgcn_exp2f(ml.x - M);
+            L += ml.y * w;
+            O += P.part_o[idx * HD + d] * w;
+        }
+    }
+    const uint32_t r  = n / P.kv_mul;
+    const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
+    const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+    const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+    if (d < P.out_dims) P.out[orow * HD + d] = O * ((L > 0.0f) ? gv / L : 0.0f);
+}
+
+template <int HD, int NT>
+hipError_t launch_hd_nt(const SplitParams &p, uint32_t n_seq, hipStream_t stream) {
+    dim3 grid(p.n_splits, p.n_head_kv, n_seq);
+    hipLaunchKernelGGL((k_splitkv<HD, NT>), grid, dim3(64), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_splits == 1u) return e;
+    hipLaunchKernelGGL((k_merge<HD>), dim3(p.ncols, p.n_head_kv, n_seq), dim3(HD), 0, stream, p);
+    return hipGetLastError();
+}
+
+uint32_t choose_splits(const AttnBatch &b, uint32_t max_keys_hint) {
+    const char *env = getenv("LFM_ATTN_SPLITS");
+    if (env && atoi(env) > 0) return (uint32_t)atoi(env);
+    uint32_t keys = max_keys_hint;
+    if (keys == 0u) keys = b.window ? b.window + b.n_rows - 1u : 4096u;
+    const uint64_t base   = (uint64_t)b.n_seq * b.n_head_kv;
+    const uint64_t target = 2048; /* workgroups: ~8 resident waves per CU x 256 CUs */
+    uint64_t splits       = (target + base - 1) / base;
+    const uint64_t by_len = (keys + 127u) / 128u; /* keep >= 4 sub-tiles per split */
+    if (splits > by_len) splits = by_len;
+    if (splits < 1) splits = 1;
+    if (splits > 256) splits = 256;
+    return (uint32_t)splits;
+}
+
+} // namespace
+
+bool splitkv_supports(const AttnBatch &b) {
+    if (b.head_dim != 64u && b.head_dim != 128u) return false;
+    const uint32_t kv_mul = b.n_head_q / b.n_head_kv;
+    const uint32_t ncols  = b.n_rows * kv_mul;
+    if (b.head_dim == 64u) return ncols <= 64u;
+    return ncols <= 32u;
+}
+
+int launch_splitkv(const AttnBatch &b, uint32_t max_keys_hint, hipStream_t stream) {
+    if (!splitkv_supports(b)) return LFM_ATTN_E_UNSUPPORTED;
+    SplitParams p{};
+    p.q             = b.q;
+    p.gate          = b.gate;
+    p.gate_is_logit = b.gate_is_logit;
+    p.k_base        = static_cast<const uint16_t *>(b.k_base);
+    p.v_base        = static_cast<const uint16_t *>(b.v_base);
+    p.k_seq         = reinterpret_cast<const uint16_t *const *>(b.k_seq);
+    p.v_seq         = reinterpret_cast<const uint16_t *const *>(b.v_seq);
+    p.seq_stride    = b.seq_stride;
+    p.pos0_dev      = b.pos0_dev;
+    p.pos0_host     = b.pos0_host;
+    p.out           = b.out;
+    p.n_rows        = b.n_rows;
+    p.n_head_q      = b.n_head_q;
+    p.n_head_kv     = b.n_head_kv;
+    p.kv_mul        = b.n_head_q / b.n_head_kv;
+    p.ncols         = b.n_rows * p.kv_mul;
+    p.window        = b.window;
+    p.cap           = b.cap;
+    p.out_dims      = b.out_dims;
+    p.qscale        = b.scale * kLog2e;
+    p.n_splits      = choose_splits(b, max_keys_hint);
+    if (p.n_splits > 1u) {
+        const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
+        const size_t bytes  = n_part * b.head_dim * sizeof(float) + n_part * sizeof(float2) + 256;
+        int st              = LFM_ATTN_OK;
+        char *ws            = static_cast<char *>(workspace(bytes, stream, &st));
+        if (!ws) return st;
+        p.part_o  = reinterpret_cast<float *>(ws);
+        p.part_ml = reinterpret_cast<float2 *>(ws + ((n_part * b.head_dim * sizeof(float) + 255) & ~(size_t)255));
+    }
+    const uint32_t nt = (p.ncols + 15u) / 16u;
+    hipError_t e      = hipSuccess;
+    if (b.head_dim == 64u) {
+        if (nt == 1u) e = launch_hd_nt<64, 1>(p, b.n_seq, stream);
+        else if (nt == 2u) e = launch_hd_nt<64, 2>(p, b.n_seq, stream);
+        else e = launch_hd_nt<64, 4>(p, b.n_seq, stream);
+    } else {
+        if (nt == 1u) e = launch_hd_nt<128, 1>(p, b.n_seq, stream);
+        else e = launch_hd_nt<128, 2>(p, b.n_seq, stream);
+    }
+    return hip_status(e);
+}
+
+} // namespace lfm

@@ -1,0 +1,66 @@
+/*
+ * kernels.h -- internal interface between the extern "C" shim (shim.hip) and
+ * the kernel translation units.  Not part of the public ABI.
+ */
+#ifndef LFM_ATTN_KERNELS_H
+#define LFM_ATTN_KERNELS_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace lfm {
+
+/* One batch of attention rows over fp16 (or fp32) KV caches.
+ * Sequence s uses cache k_seq[s] (device array) when k_seq != nullptr, else
+ * k_base + s * seq_stride elements.  Its first row is position pos0_dev[s]
+ * (device array) when pos0_dev != nullptr, else pos0_host. */
+struct AttnBatch {
+    const float *q            = nullptr; /* [n_seq][n_rows][n_head_q][head_dim]     */
+    const float *gate         = nullptr; /* [n_seq][n_rows][n_head_q] or null       */
+    int gate_is_logit         = 0;
+    const void *k_base        = nullptr;
+    const void *v_base        = nullptr;
+    const void *const *k_seq  = nullptr;
+    const void *const *v_seq  = nullptr;
+    uint64_t seq_stride       = 0;       /* elements between sequences (k_base form) */
+    const uint32_t *pos0_dev  = nullptr;
+    uint32_t pos0_host        = 0;
+    float *out                = nullptr; /* [n_seq][n_rows][n_head_q][head_dim]     */
+    uint32_t out_dims         = 0;       /* dims written per head (<= head_dim)     */
+    uint32_t n_seq = 1, n_rows = 1, n_head_q = 0, n_head_kv = 0, head_dim = 0;
+    uint32_t window = 0, cap = 0;
+    float scale = 0.0f;
+};
+
+/* Device workspace owned by the shim (grown on demand). */
+void *workspace(size_t bytes, hipStream_t stream, int *status);
+
+/* Split-KV MFMA kernel for fp16 caches, head_dim 64 or 128, up to 64 query
+ * columns (n_rows * kv_mul) per KV head.  Returns LFM_ATTN_E_UNSUPPORTED for
+ * other shapes (the caller then uses the generic kernel). */
+int launch_splitkv(const AttnBatch &b, uint32_t max_keys_hint, hipStream_t stream);
+bool splitkv_supports(const AttnBatch &b);
+
+/* Generic one-wave-per-head kernel (any head_dim % 8 == 0, <= 256), fp16 or
+ * fp32 caches; follows the reference's per-key recurrence. */
+int launch_generic(const AttnBatch &b, bool kv_f32, hipStream_t stream);
+
+/* Prologue kernels. */
+int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
+                        const float *norm_w, float eps, const float *cos_lut,
+                        const float *sin_lut, uint32_t pos, hipStream_t stream);
+int launch_store_f16(uint16_t *dst, const float *src, uint32_t n, hipStream_t stream);
+int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *const *k_seq,
+                        uint16_t *const *v_seq, const uint32_t *pos_0, uint32_t n_seq,
+                        uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                        const float *q_norm_w, const float *k_norm_w, float eps,
+                        const float *cos_lut, const float *sin_lut, uint32_t window_len,
+                        uint32_t cap, hipStream_t stream);
+
+/* Record a HIP error for lfm_attn_last_error and map it to a status. */
+int hip_status(hipError_t e);
+
+} // namespace lfm
+
+#endif

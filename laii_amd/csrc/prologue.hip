@@ -1,0 +1,160 @@
+/*
+ * prologue.hip -- per-head QK-RMSNorm + NeoX RoPE and the RNE fp16 KV stores
+ * that precede every attention call in the reference forward stacks.
+ *
+ *   lfm2_qk_norm_rope_avx2 / _scalar   tools/lfm2_kernels_fast.c:403-497, 511-547
+ *   lfm3_qk_norm_rope_128_avx2 / _scalar tools/lfm3_engine.c:463-525, 599-642
+ *   lfm2_store_fp32_to_fp16_*          tools/lfm2_kernels_fast.c:500-507, 549-555
+ *   batched per-token prologue         tools/lfm2_prefill_batch.c:1029-1072,
+ *                                      tools/lfm3_engine.c:2006-2016
+ *
+ * Per head: irms = 1/sqrtf(sum(x^2)/head_dim + eps); x <- (x*irms)*w (skipped
+ * when w is NULL); pairs (i, i+head_dim/2) rotate by the LUT row of the
+ * position: lo' = lo*c - hi*s, hi' = hi*c + lo*s (fused multiply-add, as the
+ * AVX2 kernels do).  fp16 stores round to nearest even.  One wave64 per head;
+ * lane j owns the pairs j and j+64.
+ */
+#include <hip/hip_runtime.h>
+
+#include "attn_index.h"
+#include "kernels.h"
+#include "lfm_attn.h"
+
+namespace lfm {
+namespace {
+
+__device__ __forceinline__ uint16_t f16_rne(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x); /* v_cvt_f16_f32, round-to-nearest-even */
+}
+
+__device__ __forceinline__ float wave_sum_uniform(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+
+/* Normalise + rotate one head held as pairs; writes fp32 (vec_out) or fp16. */
+__device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, uint16_t *dst_f16,
+                                               uint32_t hd, const float *norm_w, float eps,
+                                               const float *cos_row, const float *sin_row) {
+    const uint32_t half = hd / 2u;
+    const uint32_t lane = threadIdx.x;
+    float x0[2], x1[2];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t i = lane + 64u * j;
+        x0[j] = i < half ? in[i] : 0.0f;
+        x1[j] = i < half ? in[i + half] : 0.0f;
+        ss += x0[j] * x0[j] + x1[j] * x1[j];
+    }
+    if (norm_w) {
+        const float irms = 1.0f / sqrtf(wave_sum_uniform(ss) / (float)hd + eps);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t i = lane + 64u * j;
+            if (i < half) {
+                x0[j] = (x0[j] * irms) * norm_w[i];
+                x1[j] = (x1[j] * irms) * norm_w[i + half];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t i = lane + 64u * j;
+        if (i >= half) continue;
+        const float c = cos_row[i], s = sin_row[i];
+        const float r0 = __builtin_fmaf(x0[j], c, -(x1[j] * s));
+        const float r1 = __builtin_fmaf(x1[j], c, x0[j] * s);
+        if (dst_f16) {
+            dst_f16[i]        = f16_rne(r0);
+            dst_f16[i + half] = f16_rne(r1);
+        } else {
+            vec_out[i]        = r0;
+            vec_out[i + half] = r1;
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void k_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t hd,
+                                                     const float *norm_w, float eps,
+                                                     const float *cos_row, const float *sin_row) {
+    const size_t off = (size_t)blockIdx.x * hd;
+    norm_rope_head(vec + off, vec + off, dst_f16 ? dst_f16 + off : nullptr, hd, norm_w, eps,
+                   cos_row, sin_row);
+}
+
+__global__ __launch_bounds__(256) void k_store_f16(uint16_t *dst, const float *src, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) dst[i] = f16_rne(src[i]);
+}
+
+struct PrologueParams {
+    float *q;
+    const float *k;
+    const float *v;
+    uint16_t *const *k_seq;
+    uint16_t *const *v_seq;
+    const uint32_t *pos_0;
+    const float *q_norm_w;
+    const float *k_norm_w;
+    const float *cos_lut;
+    const float *sin_lut;
+    uint32_t n_rows, n_head_q, n_head_kv, head_dim, window, cap;
+    float eps;
+};
+
+/* blockIdx.x < n_head_q: query head, rotated in place.  Otherwise KV head
+ * j = blockIdx.x - n_head_q: K rotated into the fp16 cache slot, V stored. */
+__global__ __launch_bounds__(64) void k_qkv_prologue(const PrologueParams P) {
+    const uint32_t b = blockIdx.x, r = blockIdx.y, s = blockIdx.z;
+    const uint32_t hd   = P.head_dim;
+    const uint32_t pos  = P.pos_0[s] + r;
+    const uint32_t half = hd / 2u;
+    const float *cos_row = P.cos_lut + (size_t)pos * half;
+    const float *sin_row = P.sin_lut + (size_t)pos * half;
+    if (b < P.n_head_q) {
+        float *qh = P.q + (((size_t)s * P.n_rows + r) * P.n_head_q + b) * hd;
+        norm_rope_head(qh, qh, nullptr, hd, P.q_norm_w, P.eps, cos_row, sin_row);
+        return;
+    }
+    const uint32_t j    = b - P.n_head_q;
+    const uint32_t slot = lfm_slot_of(pos, P.window, P.cap);
+    const size_t kv_dim = (size_t)P.n_head_kv * hd;
+    const size_t src    = (((size_t)s * P.n_rows + r) * P.n_head_kv + j) * hd;
+    uint16_t *kd = P.k_seq[s] + (size_t)slot * kv_dim + (size_t)j * hd;
+    uint16_t *vd = P.v_seq[s] + (size_t)slot * kv_dim + (size_t)j * hd;
+    norm_rope_head(P.k + src, nullptr, kd, hd, P.k_norm_w, P.eps, cos_row, sin_row);
+    for (uint32_t i = threadIdx.x; i < hd; i += 64u) vd[i] = f16_rne(P.v[src + i]);
+}
+
+} // namespace
+
+int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
+                        const float *norm_w, float eps, const float *cos_lut,
+                        const float *sin_lut, uint32_t pos, hipStream_t stream) {
+    const size_t row = (size_t)pos * (head_dim / 2u);
+    hipLaunchKernelGGL(k_qk_norm_rope, dim3(n_heads), dim3(64), 0, stream, vec, dst_f16, head_dim,
+                       norm_w, eps, cos_lut + row, sin_lut + row);
+    return hip_status(hipGetLastError());
+}
+
+int launch_store_f16(uint16_t *dst, const float *src, uint32_t n, hipStream_t stream) {
+    hipLaunchKernelGGL(k_store_f16, dim3((n + 255u) / 256u), dim3(256), 0, stream, dst, src, n);
+    return hip_status(hipGetLastError());
+}
+
+int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *const *k_seq,
+                        uint16_t *const *v_seq, const uint32_t *pos_0, uint32_t n_seq,
+                        uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                        const float *q_norm_w, const float *k_norm_w, float eps,
+                        const float *cos_lut, const float *sin_lut, uint32_t window_len,
+                        uint32_t cap, hipStream_t stream) {
+    PrologueParams P{q, k, v, k_seq, v_seq, pos_0, q_norm_w, k_norm_w, cos_lut, sin_lut,
+                     n_rows, n_head_q, n_head_kv, head_dim, window_len, cap, eps};
+    hipLaunchKernelGGL(k_qkv_prologue, dim3(n_head_q + n_head_kv, n_rows, n_seq), dim3(64), 0,
+                       stream, P);
+    return hip_status(hipGetLastError());
+}
+
+} // namespace lfm

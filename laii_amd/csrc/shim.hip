@@ -1,0 +1,309 @@
+/*
+ * shim.hip -- the extern "C" entry points of include/lfm_attn.h: argument
+ * validation on the host, workspace management, and dispatch to the kernel
+ * translation units.  No entry point enqueues work for a rejected call.
+ */
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <stdio.h>
+#include <string.h>
+#include <vector>
+
+#include "attn_index.h"
+#include "kernels.h"
+#include "lfm_attn.h"
+
+namespace lfm {
+
+static thread_local char g_last_error[256] = "";
+
+int hip_status(hipError_t e) {
+    if (e == hipSuccess) return LFM_ATTN_OK;
+    snprintf(g_last_error, sizeof g_last_error, "%s: %s", hipGetErrorName(e), hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? LFM_ATTN_E_NOMEM : LFM_ATTN_E_DEVICE;
+}
+
+namespace {
+struct Workspace {
+    void *ptr    = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::vector<Workspace> g_ws;
+} // namespace
+
+void *workspace(size_t bytes, hipStream_t stream, int *status) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { *status = hip_status(e); return nullptr; }
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    if ((size_t)dev >= g_ws.size()) g_ws.resize((size_t)dev + 1);
+    Workspace &w = g_ws[(size_t)dev];
+    if (w.bytes >= bytes) return w.ptr;
+    if (w.ptr) {
+        /* work already enqueued may still read the old buffer */
+        e = hipStreamSynchronize(stream);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) { *status = hip_status(e); return nullptr; }
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+        w.bytes = 0;
+    }
+    size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes + bytes / 4;
+    e = hipMalloc(&w.ptr, want);
+    if (e != hipSuccess) { w.ptr = nullptr; *status = hip_status(e); return nullptr; }
+    w.bytes = want;
+    return w.ptr;
+}
+
+} // namespace lfm
+
+using lfm::AttnBatch;
+
+static inline hipStream_t to_stream(lfm_attn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0u; }
+
+static int dispatch_f16(const AttnBatch &b, uint32_t max_keys, hipStream_t stream) {
+    const bool fast = lfm::splitkv_supports(b) && aligned16(b.q) && aligned16(b.out) &&
+                      (b.k_seq || (aligned16(b.k_base) && aligned16(b.v_base)));
+    if (fast) return lfm::launch_splitkv(b, max_keys, stream);
+    return lfm::launch_generic(b, false, stream);
+}
+
+extern "C" {
+
+const char *lfm_attn_status_string(int status) {
+    switch (status) {
+    case LFM_ATTN_OK: return "ok";
+    case LFM_ATTN_E_INVALID: return "invalid argument";
+    case LFM_ATTN_E_RANGE: return "position out of range";
+    case LFM_ATTN_E_UNSUPPORTED: return "unsupported shape";
+    case LFM_ATTN_E_DEVICE: return "device error";
+    case LFM_ATTN_E_NOMEM: return "out of device memory";
+    default: return "unknown status";
+    }
+}
+
+const char *lfm_attn_last_error(void) { return lfm::g_last_error; }
+
+const char *lfm_attn_version(void) { return "lfm_attn 0.1 gfx950"; }
+
+int lfm_attn_device_count(int *count) {
+    if (!count) return LFM_ATTN_E_INVALID;
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e == hipErrorNoDevice) { *count = 0; return LFM_ATTN_OK; }
+    return lfm::hip_status(e);
+}
+
+int lfm_attn_set_device(int device) { return lfm::hip_status(hipSetDevice(device)); }
+
+int lfm_attn_dev_alloc(void **ptr, size_t bytes) {
+    if (!ptr) return LFM_ATTN_E_INVALID;
+    *ptr = nullptr;
+    if (bytes == 0) return LFM_ATTN_OK;
+    return lfm::hip_status(hipMalloc(ptr, bytes));
+}
+
+int lfm_attn_dev_free(void *ptr) { return ptr ? lfm::hip_status(hipFree(ptr)) : LFM_ATTN_OK; }
+
+int lfm_attn_copy_h2d(void *dst, const void *src, size_t bytes, lfm_attn_stream_t stream) {
+    if ((!dst || !src) && bytes) return LFM_ATTN_E_INVALID;
+    if (!bytes) return LFM_ATTN_OK;
+    return lfm::hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, to_stream(stream)));
+}
+
+int lfm_attn_copy_d2h(void *dst, const void *src, size_t bytes, lfm_attn_stream_t stream) {
+    if ((!dst || !src) && bytes) return LFM_ATTN_E_INVALID;
+    if (!bytes) return LFM_ATTN_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, to_stream(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(to_stream(stream));
+    return lfm::hip_status(e);
+}
+
+int lfm_attn_copy_d2d(void *dst, const void *src, size_t bytes, lfm_attn_stream_t stream) {
+    if ((!dst || !src) && bytes) return LFM_ATTN_E_INVALID;
+    if (!bytes) return LFM_ATTN_OK;
+    return lfm::hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, to_stream(stream)));
+}
+
+int lfm_attn_memset(void *dst, int value, size_t bytes, lfm_attn_stream_t stream) {
+    if (!dst && bytes) return LFM_ATTN_E_INVALID;
+    if (!bytes) return LFM_ATTN_OK;
+    return lfm::hip_status(hipMemsetAsync(dst, value, bytes, to_stream(stream)));
+}
+
+int lfm_attn_stream_sync(lfm_attn_stream_t stream) {
+    return lfm::hip_status(hipStreamSynchronize(to_stream(stream)));
+}
+
+int lfm_attn_seg_plan(uint32_t abs_pos, uint32_t window_len, uint32_t cap, uint32_t out5[5]) {
+    if (!out5) return LFM_ATTN_E_INVALID;
+    if (window_len > 0u && (cap == 0u || window_len > cap)) return LFM_ATTN_E_INVALID;
+    const lfm_seg_plan_t p = lfm_plan_row(abs_pos, window_len, cap);
+    out5[0] = p.t_start;
+    out5[1] = p.count;
+    out5[2] = p.seg1_slot;
+    out5[3] = p.seg1_len;
+    out5[4] = p.seg2_len;
+    return LFM_ATTN_OK;
+}
+
+uint32_t lfm_attn_slot_of(uint32_t p, uint32_t window_len, uint32_t cap) {
+    if (window_len > 0u && cap == 0u) return 0u;
+    return lfm_slot_of(p, window_len, cap);
+}
+
+/* ---- prologue ----------------------------------------------------------------- */
+int lfm_hip_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
+                         const float *norm_w, float eps, const float *cos_lut,
+                         const float *sin_lut, uint32_t pos, lfm_attn_stream_t stream) {
+    if (!vec || !cos_lut || !sin_lut || n_heads == 0u) return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || (head_dim & 1u) || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    return lfm::launch_qk_norm_rope(vec, dst_f16, n_heads, head_dim, norm_w, eps, cos_lut, sin_lut,
+                                    pos, to_stream(stream));
+}
+
+int lfm_hip_store_fp32_to_fp16(uint16_t *dst_f16, const float *src, uint32_t n,
+                               lfm_attn_stream_t stream) {
+    if (!dst_f16 || !src) return n ? LFM_ATTN_E_INVALID : LFM_ATTN_OK;
+    if (n == 0u) return LFM_ATTN_OK;
+    return lfm::launch_store_f16(dst_f16, src, n, to_stream(stream));
+}
+
+int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *const *k_seq,
+                         uint16_t *const *v_seq, const uint32_t *pos_0, uint32_t n_seq,
+                         uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                         const float *q_norm_w, const float *k_norm_w, float eps,
+                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
+                         uint32_t cap, lfm_attn_stream_t stream) {
+    if (!q || !k || !v || !k_seq || !v_seq || !pos_0 || !cos_lut || !sin_lut) return LFM_ATTN_E_INVALID;
+    if (n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u) return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || (head_dim & 1u) || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (window_len > 0u && (cap == 0u || window_len > cap)) return LFM_ATTN_E_INVALID;
+    return lfm::launch_qkv_prologue(q, k, v, k_seq, v_seq, pos_0, n_seq, n_rows, n_head_q, n_head_kv,
+                                    head_dim, q_norm_w, k_norm_w, eps, cos_lut, sin_lut, window_len,
+                                    cap, to_stream(stream));
+}
+
+/* ---- attention -------------------------------------------------------------- */
+int lfm_hip_online_gqa_f16(const float *q, const uint16_t *k_cache_f16,
+                           const uint16_t *v_cache_f16, float *xb_out, uint32_t n_head_q,
+                           uint32_t kv_mul, uint32_t kv_dim, uint32_t pos, float scale,
+                           lfm_attn_stream_t stream) {
+    if (!q || !k_cache_f16 || !v_cache_f16 || !xb_out) return LFM_ATTN_E_INVALID;
+    if (n_head_q == 0u || kv_mul == 0u || n_head_q % kv_mul != 0u) return LFM_ATTN_E_INVALID;
+    if (kv_dim != (n_head_q / kv_mul) * 64u) return LFM_ATTN_E_INVALID;
+    if (pos >= 0x7FFFFFFFu) return LFM_ATTN_E_RANGE;
+    AttnBatch b;
+    b.q = q;
+    b.k_base = k_cache_f16;
+    b.v_base = v_cache_f16;
+    b.pos0_host = pos;
+    b.out = xb_out;
+    b.out_dims = 64u;
+    b.n_head_q = n_head_q;
+    b.n_head_kv = n_head_q / kv_mul;
+    b.head_dim = 64u;
+    b.scale = scale;
+    return dispatch_f16(b, pos + 1u, to_stream(stream));
+}
+
+int lfm_hip_gqa_heads(const float *q, const float *k_cache, const float *v_cache,
+                      const uint16_t *k_cache_f16, const uint16_t *v_cache_f16, float *xb,
+                      uint32_t n_head_q, uint32_t kv_mul, uint32_t head_dim, uint32_t kv_dim,
+                      uint32_t max_seq_len, uint32_t pos, float scale, lfm_attn_stream_t stream) {
+    const bool f16 = k_cache_f16 && v_cache_f16;
+    if (!q || !xb || (!f16 && (!k_cache || !v_cache))) return LFM_ATTN_E_INVALID;
+    if (n_head_q == 0u || kv_mul == 0u || n_head_q % kv_mul != 0u) return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || head_dim % 8u != 0u || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (kv_dim != (n_head_q / kv_mul) * head_dim) return LFM_ATTN_E_INVALID;
+    if (pos >= max_seq_len || pos >= 0x7FFFFFFFu) return LFM_ATTN_E_RANGE;
+    AttnBatch b;
+    b.q = q;
+    b.pos0_host = pos;
+    b.out = xb;
+    b.n_head_q = n_head_q;
+    b.n_head_kv = n_head_q / kv_mul;
+    b.head_dim = head_dim;
+    b.scale = scale;
+    if (f16) {
+        /* tools/lfm2_threadpool.c:783: the fp16 branch writes n_vec*8 dims */
+        b.out_dims = head_dim <= 64u ? head_dim : 64u;
+        b.k_base = k_cache_f16;
+        b.v_base = v_cache_f16;
+        return dispatch_f16(b, pos + 1u, to_stream(stream));
+    }
+    b.out_dims = head_dim;
+    b.k_base = k_cache;
+    b.v_base = v_cache;
+    return lfm::launch_generic(b, true, to_stream(stream));
+}
+
+int lfm_hip_lfm3_online_gqa_f16_dispatch(const float *q_batch, const float *gate_sig,
+                                         const uint16_t *k_cache_f16,
+                                         const uint16_t *v_cache_f16, float *xb_out, uint32_t B,
+                                         uint32_t pos_0, uint32_t window_len, uint32_t swa_cap,
+                                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                                         lfm_attn_stream_t stream) {
+    if (!q_batch || !k_cache_f16 || !v_cache_f16 || !xb_out) return LFM_ATTN_E_INVALID;
+    if (B == 0u || n_head_q == 0u || n_head_kv == 0u || n_head_q % n_head_kv != 0u)
+        return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || head_dim % 8u != 0u || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (window_len > 0u && (swa_cap == 0u || window_len > swa_cap)) return LFM_ATTN_E_INVALID;
+    if (lfm_check_rows(pos_0, B, window_len, swa_cap) != 0 || pos_0 >= 0x7FFFFFFFu)
+        return LFM_ATTN_E_RANGE;
+    AttnBatch b;
+    b.q = q_batch;
+    b.gate = gate_sig;
+    b.k_base = k_cache_f16;
+    b.v_base = v_cache_f16;
+    b.pos0_host = pos_0;
+    b.out = xb_out;
+    b.out_dims = head_dim;
+    b.n_rows = B;
+    b.n_head_q = n_head_q;
+    b.n_head_kv = n_head_kv;
+    b.head_dim = head_dim;
+    b.window = window_len;
+    b.cap = swa_cap;
+    b.scale = 1.0f / sqrtf((float)head_dim);
+    const uint32_t max_keys = window_len ? window_len : pos_0 + B;
+    return dispatch_f16(b, max_keys, to_stream(stream));
+}
+
+int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
+                           const uint16_t *const *k_seq, const uint16_t *const *v_seq,
+                           const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
+                           uint32_t max_keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                           uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                           lfm_attn_stream_t stream) {
+    if (!q || !k_seq || !v_seq || !pos_0 || !out) return LFM_ATTN_E_INVALID;
+    if (n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u ||
+        n_head_q % n_head_kv != 0u)
+        return LFM_ATTN_E_INVALID;
+    if (n_seq > 65535u || n_head_kv > 65535u) return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || head_dim % 8u != 0u || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (window_len > 0u && (cap == 0u || window_len > cap)) return LFM_ATTN_E_INVALID;
+    AttnBatch b;
+    b.q = q;
+    b.gate = gate;
+    b.gate_is_logit = gate_is_logit;
+    b.k_seq = reinterpret_cast<const void *const *>(k_seq);
+    b.v_seq = reinterpret_cast<const void *const *>(v_seq);
+    b.pos0_dev = pos_0;
+    b.out = out;
+    b.out_dims = head_dim;
+    b.n_seq = n_seq;
+    b.n_rows = n_rows;
+    b.n_head_q = n_head_q;
+    b.n_head_kv = n_head_kv;
+    b.head_dim = head_dim;
+    b.window = window_len;
+    b.cap = cap;
+    b.scale = scale;
+    return dispatch_f16(b, max_keys_hint, to_stream(stream));
+}
+
+} /* extern "C" */

@@ -1,0 +1,274 @@
+"""ctypes bindings for the oracle (liboracle.so) and the reference build
+(_ref/libref_attn.so).  TEST INFRASTRUCTURE ONLY -- the checker, never the
+thing measured or shipped.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libref_attn.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_u32 = C.c_uint32
+_f32 = C.c_float
+
+
+def build(ref: bool = True) -> None:
+    """Compile the oracle (and the reference library where its sources exist)."""
+    subprocess.run(["make", "-s", "-C", HERE, "oracle"] + (["ref"] if ref else []), check=True)
+
+
+def _opt(arr, ptr_type):
+    return None if arr is None else arr.ctypes.data_as(ptr_type)
+
+
+class Oracle:
+    """Scalar C11 restatement of the reference attention path."""
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            build(ref=False)
+        L = self.lib = C.CDLL(path)
+        L.orc_f16_to_f32.restype = _f32
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16.argtypes = [_f32]
+        L.orc_f32_to_f16_n.argtypes = [_f32p, _u16p, C.c_size_t]
+        L.orc_f16_to_f32_n.argtypes = [_u16p, _f32p, C.c_size_t]
+        L.orc_rope_lut_lfm2.argtypes = [_f32p, _f32p, _u32, _u32, _f32]
+        L.orc_rope_lut_lfm3.argtypes = [_f32p, _f32p, _u32, _u32, _u32, _f32, C.c_void_p, _u32]
+        L.orc_qk_norm_rope.argtypes = [_f32p, C.c_void_p, _u32, _u32, C.c_void_p, _f32, _f32p, _f32p]
+        L.orc_online_gqa_f16.argtypes = [_f32p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32, _f32]
+        L.orc_gqa_heads.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
+                                    _u32, _u32, _u32, _u32, _u32, _f32]
+        L.orc_lfm3_plan.argtypes = [_u32, _u32, _u32, _u32p]
+        L.orc_lfm3_slots.restype = _u32
+        L.orc_lfm3_slots.argtypes = [_u32, _u32, _u32, _u32p]
+        L.orc_lfm3_online_gqa_f16.argtypes = [_f32p, C.c_void_p, _u16p, _u16p, _f32p, _u32, _u32,
+                                              _u32, _u32, _u32, _u32, _u32]
+        L.orc_gen1_gqa_attend.argtypes = [_f32p, _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p,
+                                          _f32p, _f32p, _u32, _u32, _u32, _u32, _f32, _f32]
+        L.orc_causal_rows_f16.argtypes = [_f32p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32, _u32]
+        L.orc_decode_batch_mt.argtypes = [_f32p, C.c_void_p, C.c_void_p, _u32p, _f32p, _u32, _u32,
+                                          _u32, _u32, _u32]
+
+    # -- fp16 -----------------------------------------------------------------
+    def f32_to_f16(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, dtype=np.uint16)
+        self.lib.orc_f32_to_f16_n(x.reshape(-1), out.reshape(-1), x.size)
+        return out
+
+    def f16_to_f32(self, h: np.ndarray) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.shape, dtype=np.float32)
+        self.lib.orc_f16_to_f32_n(h.reshape(-1), out.reshape(-1), h.size)
+        return out
+
+    # -- RoPE / prologue ---------------------------------------------------------
+    def rope_lut_lfm2(self, max_seq, head_dim, base):
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        self.lib.orc_rope_lut_lfm2(c, s, max_seq, head_dim, base)
+        return c, s
+
+    def rope_lut_lfm3(self, max_seq, head_dim, rope_dim, base, rope_freqs=None):
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        rf = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+        self.lib.orc_rope_lut_lfm3(c, s, max_seq, head_dim, rope_dim, base,
+                                   _opt(rf, C.c_void_p), 0 if rf is None else rf.size)
+        return c, s
+
+    def qk_norm_rope(self, vec, n_heads, head_dim, norm_w, eps, cos_row, sin_row, store_f16=False):
+        """Returns the rotated fp32 heads, or the RNE fp16 store when store_f16."""
+        v = np.ascontiguousarray(vec, np.float32).copy().reshape(-1)
+        nw = None if norm_w is None else np.ascontiguousarray(norm_w, np.float32)
+        dst = np.zeros(n_heads * head_dim, np.uint16) if store_f16 else None
+        self.lib.orc_qk_norm_rope(v, _opt(dst, C.c_void_p), n_heads, head_dim,
+                                  _opt(nw, C.c_void_p), eps,
+                                  np.ascontiguousarray(cos_row, np.float32),
+                                  np.ascontiguousarray(sin_row, np.float32))
+        return dst if store_f16 else v
+
+    # -- attention ---------------------------------------------------------------
+    def online_gqa_f16(self, q, k16, v16, n_head_q, kv_mul, kv_dim, pos, scale=0.125):
+        out = np.zeros(n_head_q * 64, np.float32)
+        self.lib.orc_online_gqa_f16(np.ascontiguousarray(q, np.float32).reshape(-1),
+                                    k16.reshape(-1), v16.reshape(-1), out, n_head_q, kv_mul,
+                                    kv_dim, pos, scale)
+        return out
+
+    def gqa_heads(self, q, n_head_q, kv_mul, head_dim, kv_dim, pos, k32=None, v32=None,
+                  k16=None, v16=None, out=None):
+        o = np.zeros(n_head_q * head_dim, np.float32) if out is None else out.copy()
+        arrs = [None if a is None else np.ascontiguousarray(a).reshape(-1)
+                for a in (k32, v32, k16, v16)]
+        self.lib.orc_gqa_heads(np.ascontiguousarray(q, np.float32).reshape(-1),
+                               *[_opt(a, C.c_void_p) for a in arrs], o, n_head_q, kv_mul,
+                               head_dim, kv_dim, pos, 1.0 / np.sqrt(np.float32(head_dim)))
+        return o
+
+    def lfm3_plan(self, abs_pos, window, cap):
+        out = np.zeros(5, np.uint32)
+        self.lib.orc_lfm3_plan(abs_pos, window, cap, out)
+        return tuple(int(x) for x in out)
+
+    def lfm3_slots(self, abs_pos, window, cap):
+        buf = np.zeros(abs_pos + 1, np.uint32)
+        n = self.lib.orc_lfm3_slots(abs_pos, window, cap, buf)
+        return buf[:n]
+
+    def lfm3_online_gqa_f16(self, q, gate, k16, v16, B, pos_0, window, cap, n_head_q, n_head_kv,
+                            head_dim):
+        out = np.zeros(B * n_head_q * head_dim, np.float32)
+        g = None if gate is None else np.ascontiguousarray(gate, np.float32).reshape(-1)
+        self.lib.orc_lfm3_online_gqa_f16(np.ascontiguousarray(q, np.float32).reshape(-1),
+                                         _opt(g, C.c_void_p), k16.reshape(-1), v16.reshape(-1),
+                                         out, B, pos_0, window, cap, n_head_q, n_head_kv,
+                                         head_dim)
+        return out
+
+    def gen1_gqa_attend(self, q, k, v, q_norm, k_norm, k_cache, v_cache, pos, nq, nkv, hd, eps,
+                        theta):
+        out = np.zeros(nq * hd, np.float32)
+        q = np.ascontiguousarray(q, np.float32).copy()
+        k = np.ascontiguousarray(k, np.float32).copy()
+        qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+        kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+        self.lib.orc_gen1_gqa_attend(out, q, k, np.ascontiguousarray(v, np.float32),
+                                     _opt(qn, C.c_void_p), _opt(kn, C.c_void_p),
+                                     k_cache.reshape(-1), v_cache.reshape(-1), pos, nq, nkv, hd,
+                                     eps, theta)
+        return out
+
+    def causal_rows_f16(self, q_rows, k16, v16, n_rows, pos_0, n_head_q, n_head_kv, head_dim):
+        out = np.zeros(n_rows * n_head_q * head_dim, np.float32)
+        self.lib.orc_causal_rows_f16(np.ascontiguousarray(q_rows, np.float32).reshape(-1),
+                                     k16.reshape(-1), v16.reshape(-1), out, n_rows, pos_0,
+                                     n_head_q, n_head_kv, head_dim)
+        return out
+
+    def decode_batch_mt(self, q, k_list, v_list, pos, n_head_q, n_head_kv, head_dim, n_threads):
+        n_seq = len(k_list)
+        kp = (C.c_void_p * n_seq)(*[k.ctypes.data for k in k_list])
+        vp = (C.c_void_p * n_seq)(*[v.ctypes.data for v in v_list])
+        out = np.zeros(n_seq * n_head_q * head_dim, np.float32)
+        self.lib.orc_decode_batch_mt(np.ascontiguousarray(q, np.float32).reshape(-1), kp, vp,
+                                     np.ascontiguousarray(pos, np.uint32), out, n_seq, n_head_q,
+                                     n_head_kv, head_dim, n_threads)
+        return out
+
+
+class Reference:
+    """The reference's own kernels, compiled from /root/reference (ref_shim.c)."""
+
+    @staticmethod
+    def available(path: str = REF_SO) -> bool:
+        return os.path.exists(path)
+
+    def __init__(self, path: str = REF_SO):
+        L = self.lib = C.CDLL(path)
+        L.ref_has_avx2.restype = C.c_int
+        L.ref_rope_lut_lfm2.argtypes = [_f32p, _f32p, _u32, _u32, _f32]
+        L.ref_rope_lut_lfm3.argtypes = [_f32p, _f32p, _u32, _u32, _u32, _f32, C.c_void_p, _u32]
+        L.ref_qk_norm_rope_lfm2.argtypes = [_f32p, C.c_void_p, _u32, C.c_void_p, _f32, _f32p,
+                                            _f32p, _u32, _u32, C.c_int]
+        L.ref_qk_norm_rope_lfm3.argtypes = [_f32p, C.c_void_p, _u32, _u32, C.c_void_p, _f32, _f32p,
+                                            _f32p, _u32, _u32, C.c_int]
+        L.ref_store_fp32_to_fp16.argtypes = [_u16p, _f32p, _u32]
+        L.ref_fp16_to_fp32.restype = _f32
+        L.ref_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.ref_online_gqa_f16.argtypes = [_f32p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32, _u32]
+        L.ref_gqa_heads.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
+                                    _u32, _u32, _u32, _u32, _u32, _u32, _u32]
+        L.ref_lfm3_dispatch.argtypes = [_f32p, C.c_void_p, _u16p, _u16p, _f32p, _u32, _u32, _u32,
+                                        _u32, _u32, _u32, _u32, _u32]
+        L.ref_time_decode_batch.restype = C.c_double
+        L.ref_time_decode_batch.argtypes = [_f32p, C.c_void_p, C.c_void_p, _u32p, _f32p, _u32,
+                                            _u32, _u32, _u32, _u32, C.POINTER(_u32)]
+        self.has_avx2 = bool(L.ref_has_avx2())
+
+    def rope_lut_lfm2(self, max_seq, head_dim, base):
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        assert self.lib.ref_rope_lut_lfm2(c, s, max_seq, head_dim, base) == 0
+        return c, s
+
+    def rope_lut_lfm3(self, max_seq, head_dim, rope_dim, base, rope_freqs=None):
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        rf = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+        assert self.lib.ref_rope_lut_lfm3(c, s, max_seq, head_dim, rope_dim, base,
+                                          _opt(rf, C.c_void_p),
+                                          0 if rf is None else rf.size) == 0
+        return c, s
+
+    def qk_norm_rope(self, vec, n_heads, head_dim, norm_w, eps, cos_lut, sin_lut, pos,
+                     store_f16=False, scalar=False):
+        v = np.ascontiguousarray(vec, np.float32).copy().reshape(-1)
+        nw = None if norm_w is None else np.ascontiguousarray(norm_w, np.float32)
+        dst = np.zeros(n_heads * head_dim, np.uint16) if store_f16 else None
+        c = np.ascontiguousarray(cos_lut, np.float32)
+        s = np.ascontiguousarray(sin_lut, np.float32)
+        if head_dim == 64 and c.shape[1] == 32 and not getattr(self, "_force_lfm3", False):
+            rc = self.lib.ref_qk_norm_rope_lfm2(v, _opt(dst, C.c_void_p), n_heads,
+                                                _opt(nw, C.c_void_p), eps, c, s, c.shape[0], pos,
+                                                int(scalar))
+        else:
+            rc = self.lib.ref_qk_norm_rope_lfm3(v, _opt(dst, C.c_void_p), n_heads, head_dim,
+                                                _opt(nw, C.c_void_p), eps, c, s, c.shape[0], pos,
+                                                int(scalar))
+        assert rc == 0
+        return dst if store_f16 else v
+
+    def store_f16(self, x):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        out = np.empty(x.size, np.uint16)
+        self.lib.ref_store_fp32_to_fp16(out, x, x.size)
+        return out
+
+    def online_gqa_f16(self, q, k16, v16, n_head_q, kv_mul, kv_dim, pos, n_threads=2):
+        out = np.zeros(n_head_q * 64, np.float32)
+        self.lib.ref_online_gqa_f16(np.ascontiguousarray(q, np.float32).reshape(-1),
+                                    k16.reshape(-1), v16.reshape(-1), out, n_head_q, kv_mul,
+                                    kv_dim, pos, n_threads)
+        return out
+
+    def gqa_heads(self, q, n_head_q, kv_mul, head_dim, kv_dim, max_seq, pos, k32=None, v32=None,
+                  k16=None, v16=None, n_threads=2):
+        out = np.zeros(n_head_q * head_dim, np.float32)
+        arrs = [None if a is None else np.ascontiguousarray(a).reshape(-1)
+                for a in (k32, v32, k16, v16)]
+        self.lib.ref_gqa_heads(np.ascontiguousarray(q, np.float32).reshape(-1),
+                               *[_opt(a, C.c_void_p) for a in arrs], out, n_head_q, kv_mul,
+                               head_dim, kv_dim, max_seq, pos, n_threads)
+        return out
+
+    def lfm3_dispatch(self, q, gate, k16, v16, B, pos_0, window, cap, n_head_q, n_head_kv,
+                      head_dim, n_threads=2):
+        out = np.zeros(B * n_head_q * head_dim, np.float32)
+        g = None if gate is None else np.ascontiguousarray(gate, np.float32).reshape(-1)
+        self.lib.ref_lfm3_dispatch(np.ascontiguousarray(q, np.float32).reshape(-1),
+                                   _opt(g, C.c_void_p), k16.reshape(-1), v16.reshape(-1), out, B,
+                                   pos_0, window, cap, n_head_q, n_head_kv, head_dim, n_threads)
+        return out
+
+    def time_decode_batch(self, q, k_list, v_list, pos, n_head_q, n_head_kv, n_threads, reps):
+        n_seq = len(k_list)
+        kp = (C.c_void_p * n_seq)(*[k.ctypes.data for k in k_list])
+        vp = (C.c_void_p * n_seq)(*[v.ctypes.data for v in v_list])
+        out = np.zeros(n_seq * n_head_q * 64, np.float32)
+        used = _u32(0)
+        dt = self.lib.ref_time_decode_batch(np.ascontiguousarray(q, np.float32).reshape(-1), kp,
+                                            vp, np.ascontiguousarray(pos, np.uint32), out, n_seq,
+                                            n_head_q, n_head_kv, n_threads, reps, C.byref(used))
+        return dt, int(used.value), out

@@ -1,0 +1,491 @@
+/*
+ * oracle/cpu_attn.c -- TEST INFRASTRUCTURE ONLY (parity checker + "port" CPU
+ * baseline).  Scalar C11 restatement of the reference attention path; see
+ * cpu_attn.h.  Never linked into the product library.
+ *
+ * Pinning (what checks each function independently of this file):
+ *   orc_f32_to_f16 / orc_f16_to_f32 : numpy float16 (IEEE RNE) over all 65536
+ *                                     halves and random / tie / edge floats.
+ *   orc_rope_lut_*                   : reference LUT builders compiled from
+ *                                     source (oracle/_ref), closed form cos/sin,
+ *                                     partial-RoPE identity pairs.
+ *   orc_qk_norm_rope                 : reference AVX2/scalar kernels (oracle/_ref),
+ *                                     numpy float64 closed form, norm invariant.
+ *   orc_online_gqa_f16, orc_gqa_heads, orc_lfm3_online_gqa_f16,
+ *   orc_causal_rows_f16             : numpy float64 softmax(QK^T)V brute force,
+ *                                     reference workers (oracle/_ref), golden
+ *                                     vectors under tests/golden/.
+ *   orc_lfm3_plan / orc_lfm3_slots   : brute-force window enumeration.
+ *   orc_gen1_gqa_attend              : tests/fixtures_attention.bin (PyTorch).
+ */
+#define _GNU_SOURCE
+#include "cpu_attn.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* A8: include/lfm2_simd_avx2.h:163-188 (IEEE half -> single).              */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp  = (h >> 10) & 0x1Fu;
+    uint32_t mant = h & 0x03FFu;
+    uint32_t bits;
+    if (exp == 0u) {
+        if (mant == 0u) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { mant <<= 1; ++e; } while ((mant & 0x0400u) == 0u);
+            mant &= 0x03FFu;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+        }
+    } else if (exp == 31u) {
+        bits = sign | 0x7F800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + (127u - 15u)) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+/* A8: the F16C store used by every KV write in the reference
+ * (_mm256_cvtps_ph(..., _MM_FROUND_TO_NEAREST_INT), tools/lfm2_kernels_fast.c:477-484,
+ * 505; tools/lfm3_engine.c:518-519): IEEE round-to-nearest-even, overflow to
+ * infinity, NaN stays NaN (quieted). */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax   = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) {
+        if (ax > 0x7F800000u) return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x03FFu));
+        return (uint16_t)(sign | 0x7C00u);
+    }
+    if (ax >= 0x38800000u) { /* |f| >= 2^-14: normal half or overflow */
+        uint32_t h   = ((ax >> 23) - 112u) << 10 | ((ax >> 13) & 0x03FFu);
+        uint32_t rem = ax & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h += 1u;
+        if (h >= 0x7C00u) h = 0x7C00u;
+        return (uint16_t)(sign | h);
+    }
+    if (ax < 0x33000000u) return (uint16_t)sign; /* < 2^-25: rounds to zero */
+    /* subnormal half: value / 2^-24 = m * 2^(E-126) with E <= 112 */
+    const uint32_t E     = ax >> 23;
+    const uint32_t m     = (ax & 0x7FFFFFu) | 0x800000u;
+    const uint32_t shift = 126u - E;
+    uint32_t q           = m >> shift;
+    const uint32_t rem   = m & ((1u << shift) - 1u);
+    const uint32_t half  = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (q & 1u))) q += 1u;
+    return (uint16_t)(sign | q);
+}
+
+void orc_f32_to_f16_n(const float *src, uint16_t *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f32_to_f16(src[i]);
+}
+
+void orc_f16_to_f32_n(const uint16_t *src, float *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f16_to_f32(src[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* A4: tools/lfm2_kernels_fast.c:370-388 -- double-precision angle, float
+ * entries, layout [pos][head_dim/2]. */
+void orc_rope_lut_lfm2(float *cos_lut, float *sin_lut, uint32_t max_seq,
+                       uint32_t head_dim, float freq_base) {
+    const uint32_t half = head_dim / 2u;
+    for (uint32_t i = 0; i < half; ++i) {
+        const double freq = pow((double)freq_base, -((double)(2u * i) / (double)head_dim));
+        for (uint32_t p = 0; p < max_seq; ++p) {
+            const double angle = (double)p * freq;
+            cos_lut[(size_t)p * half + i] = (float)cos(angle);
+            sin_lut[(size_t)p * half + i] = (float)sin(angle);
+        }
+    }
+}
+
+/* A5: tools/lfm3_engine.c:403-450 -- partial RoPE: pairs i >= rope_dim/2, and
+ * pairs whose rope_freqs factor is >= 1e10 or <= 0, get the identity
+ * rotation (cos 1, sin 0); other frequencies are divided by the factor. */
+void orc_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq,
+                       uint32_t head_dim, uint32_t rope_dim, float freq_base,
+                       const float *rope_freqs, uint32_t n_rope_freqs) {
+    const uint32_t half     = head_dim / 2u;
+    const uint32_t rot_half = (rope_dim > 0u && rope_dim <= head_dim) ? (rope_dim / 2u) : half;
+    for (uint32_t i = 0; i < half; ++i) {
+        double freq = 0.0;
+        if (i < rot_half) {
+            freq = pow((double)freq_base, -((double)(2u * i) / (double)head_dim));
+            if (rope_freqs != NULL && i < n_rope_freqs) {
+                const double sf = (double)rope_freqs[i];
+                if (sf >= 1e10 || sf <= 0.0) freq = 0.0;
+                else freq /= sf;
+            }
+        }
+        for (uint32_t p = 0; p < max_seq; ++p) {
+            if (freq == 0.0) {
+                cos_lut[(size_t)p * half + i] = 1.0f;
+                sin_lut[(size_t)p * half + i] = 0.0f;
+            } else {
+                const double angle = (double)p * freq;
+                cos_lut[(size_t)p * half + i] = (float)cos(angle);
+                sin_lut[(size_t)p * half + i] = (float)sin(angle);
+            }
+        }
+    }
+}
+
+/* A4/A5: tools/lfm2_kernels_fast.c:511-547 (scalar LFM2, double sum of
+ * squares) generalised to any even head_dim as in tools/lfm3_engine.c:599-642:
+ * x <- (x * irms) * w with irms = 1/sqrtf(mean(x^2) + eps); NeoX rotation of
+ * pairs (i, i + head_dim/2); with dst_f16 the rotated head is stored as RNE
+ * fp16 and vec is left untouched, otherwise vec is overwritten. */
+void orc_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads,
+                      uint32_t head_dim, const float *norm_w, float eps,
+                      const float *cos_row, const float *sin_row) {
+    const uint32_t half = head_dim / 2u;
+    float tmp[512];
+    for (uint32_t h = 0; h < n_heads; ++h) {
+        const float *hp = vec + (size_t)h * head_dim;
+        for (uint32_t i = 0; i < head_dim; ++i) tmp[i] = hp[i];
+        if (norm_w != NULL) {
+            double ss = 0.0;
+            for (uint32_t i = 0; i < head_dim; ++i) ss += (double)tmp[i] * (double)tmp[i];
+            const float irms = 1.0f / sqrtf((float)(ss / (double)head_dim) + eps);
+            for (uint32_t i = 0; i < head_dim; ++i) tmp[i] = (tmp[i] * irms) * norm_w[i];
+        }
+        for (uint32_t i = 0; i < half; ++i) {
+            const float x0 = tmp[i], x1 = tmp[i + half];
+            const float c = cos_row[i], s = sin_row[i];
+            const float r0 = x0 * c - x1 * s;
+            const float r1 = x1 * c + x0 * s;
+            if (dst_f16 != NULL) {
+                dst_f16[(size_t)h * head_dim + i]        = orc_f32_to_f16(r0);
+                dst_f16[(size_t)h * head_dim + i + half] = orc_f32_to_f16(r1);
+            } else {
+                vec[(size_t)h * head_dim + i]        = r0;
+                vec[(size_t)h * head_dim + i + half] = r1;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* One query head streamed over a contiguous run of cache rows with the
+ * reference's single-pass recurrence (tools/lfm2_kernels_fast.c:845-866,
+ * tools/lfm3_engine.c:1068-1089): a larger score rescales the running sums by
+ * alpha = expf(m - s) (0 on the first key, m <= -1e29), a smaller one adds
+ * beta = expf(s - m).  Updates vo[0..head_dim), *m, *l in place. */
+static void orc_head_segment(const float *q_h, const uint16_t *k_ptr, const uint16_t *v_ptr,
+                             size_t stride, uint32_t seg_len, uint32_t head_dim, float scale,
+                             float *vo, float *m_p, float *l_p) {
+    float m = *m_p, l = *l_p;
+    for (uint32_t t = 0; t < seg_len; ++t) {
+        float dot = 0.0f;
+        for (uint32_t i = 0; i < head_dim; ++i) dot += q_h[i] * orc_f16_to_f32(k_ptr[i]);
+        const float score = dot * scale;
+        if (score > m) {
+            const float alpha = (m <= -1e29f) ? 0.0f : expf(m - score);
+            l = l * alpha + 1.0f;
+            m = score;
+            for (uint32_t i = 0; i < head_dim; ++i) vo[i] = vo[i] * alpha + orc_f16_to_f32(v_ptr[i]);
+        } else {
+            const float beta = expf(score - m);
+            l += beta;
+            for (uint32_t i = 0; i < head_dim; ++i) vo[i] += beta * orc_f16_to_f32(v_ptr[i]);
+        }
+        k_ptr += stride;
+        v_ptr += stride;
+    }
+    *m_p = m;
+    *l_p = l;
+}
+
+/* A1: tools/lfm2_kernels_fast.c:814-872 (scalar worker; the AVX2 worker
+ * :700-810 is the same recurrence).  head_dim is 64; kv_h = h / kv_mul; the
+ * output is vo * (1/l).  All ceil(n_head_q/4) work items are run in order. */
+void orc_online_gqa_f16(const float *q, const uint16_t *k_cache_f16,
+                        const uint16_t *v_cache_f16, float *xb_out,
+                        uint32_t n_head_q, uint32_t kv_mul, uint32_t kv_dim,
+                        uint32_t pos, float scale) {
+    for (uint32_t h = 0; h < n_head_q; ++h) {
+        const uint32_t kv_h = h / kv_mul;
+        float vo[64] = {0.0f};
+        float m = -1e30f, l = 0.0f;
+        orc_head_segment(q + (size_t)h * 64u, k_cache_f16 + (size_t)kv_h * 64u,
+                         v_cache_f16 + (size_t)kv_h * 64u, kv_dim, pos + 1u, 64u, scale,
+                         vo, &m, &l);
+        const float inv_l = 1.0f / l;
+        for (uint32_t i = 0; i < 64u; ++i) xb_out[(size_t)h * 64u + i] = vo[i] * inv_l;
+    }
+}
+
+/* A2: tools/lfm2_threadpool.c:764-931.  FP16 branch (:778-828): the shifted
+ * recurrence (expf(-1e30 - s) == 0 on the first key), output vo * (l>0 ? 1/l : 0)
+ * over n_vec*8 dims with n_vec = (head_dim <= 64) ? head_dim/8 : 8, i.e. only
+ * the first 64 dims when head_dim > 64 (reference quirk, reproduced).
+ * FP32 branch (:887-928, taken when the f16 caches are NULL): two-pass
+ * softmax -- scores, max, expf, normalise by 1/sum, weighted V sum in t order. */
+void orc_gqa_heads(const float *q, const float *k_cache, const float *v_cache,
+                   const uint16_t *k_cache_f16, const uint16_t *v_cache_f16,
+                   float *xb, uint32_t n_head_q, uint32_t kv_mul,
+                   uint32_t head_dim, uint32_t kv_dim, uint32_t pos, float scale) {
+    for (uint32_t h = 0; h < n_head_q; ++h) {
+        const float *q_head = q + (size_t)h * head_dim;
+        const uint32_t kv_h = h / kv_mul;
+        float *out_head     = xb + (size_t)h * head_dim;
+        if (k_cache_f16 != NULL && v_cache_f16 != NULL) {
+            const uint32_t n_out = (head_dim <= 64u) ? head_dim : 64u;
+            float vo[512] = {0.0f};
+            float m = -1e30f, l = 0.0f;
+            for (uint32_t t = 0; t <= pos; ++t) {
+                const uint16_t *kt = k_cache_f16 + (size_t)t * kv_dim + (size_t)kv_h * head_dim;
+                const uint16_t *vt = v_cache_f16 + (size_t)t * kv_dim + (size_t)kv_h * head_dim;
+                float dot = 0.0f;
+                for (uint32_t i = 0; i < head_dim; ++i) dot += q_head[i] * orc_f16_to_f32(kt[i]);
+                const float s = dot * scale;
+                if (s > m) {
+                    const float sp = expf(m - s);
+                    m = s;
+                    l = l * sp + 1.0f;
+                    for (uint32_t i = 0; i < n_out; ++i) vo[i] = vo[i] * sp + orc_f16_to_f32(vt[i]);
+                } else {
+                    const float w = expf(s - m);
+                    l += w;
+                    for (uint32_t i = 0; i < n_out; ++i) vo[i] += orc_f16_to_f32(vt[i]) * w;
+                }
+            }
+            const float inv_l = (l > 0.0f) ? (1.0f / l) : 0.0f;
+            for (uint32_t i = 0; i < n_out; ++i) out_head[i] = vo[i] * inv_l;
+            continue;
+        }
+        float *scores = (float *)malloc(((size_t)pos + 1u) * sizeof(float));
+        float max_score = -1e30f;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            const float *k_t = k_cache + (size_t)t * kv_dim + (size_t)kv_h * head_dim;
+            float dot = 0.0f;
+            for (uint32_t i = 0; i < head_dim; ++i) dot += q_head[i] * k_t[i];
+            scores[t] = dot * scale;
+            if (scores[t] > max_score) max_score = scores[t];
+        }
+        float sum_exp = 0.0f;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            scores[t] = expf(scores[t] - max_score);
+            sum_exp += scores[t];
+        }
+        const float inv_sum = 1.0f / sum_exp;
+        for (uint32_t t = 0; t <= pos; ++t) scores[t] *= inv_sum;
+        for (uint32_t i = 0; i < head_dim; ++i) out_head[i] = 0.0f;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            const float *v_t = v_cache + (size_t)t * kv_dim + (size_t)kv_h * head_dim;
+            for (uint32_t i = 0; i < head_dim; ++i) out_head[i] += scores[t] * v_t[i];
+        }
+        free(scores);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* A3 row plan, literally tools/lfm3_engine.c:1073-1080 (== :862-873). */
+void orc_lfm3_plan(uint32_t abs_pos, uint32_t window_len, uint32_t swa_cap, uint32_t out5[5]) {
+    const uint32_t t_start = (window_len > 0u && abs_pos + 1u > window_len)
+                           ? (abs_pos + 1u - window_len) : 0u;
+    const uint32_t count     = abs_pos - t_start + 1u;
+    const uint32_t seg1_slot = (window_len > 0u) ? (t_start % swa_cap) : t_start;
+    const uint32_t seg1_len  = (window_len > 0u && seg1_slot + count > swa_cap)
+                             ? (swa_cap - seg1_slot) : count;
+    out5[0] = t_start;
+    out5[1] = count;
+    out5[2] = seg1_slot;
+    out5[3] = seg1_len;
+    out5[4] = count - seg1_len;
+}
+
+/* Slots in the order the reference workers visit them: seg1 from seg1_slot,
+ * then seg2 from slot 0 (tools/lfm3_engine.c:1103-1114).  Returns count. */
+uint32_t orc_lfm3_slots(uint32_t abs_pos, uint32_t window_len, uint32_t swa_cap,
+                        uint32_t *slots_out) {
+    uint32_t p[5];
+    orc_lfm3_plan(abs_pos, window_len, swa_cap, p);
+    uint32_t n = 0;
+    for (uint32_t t = 0; t < p[3]; ++t) slots_out[n++] = p[2] + t;
+    for (uint32_t t = 0; t < p[4]; ++t) slots_out[n++] = t;
+    return n;
+}
+
+/* A3: tools/lfm3_engine.c:1116-1153 (scalar worker) + :1155-1204 (dispatch:
+ * kv_mul = n_head_q / n_head_kv, scale = 1/sqrtf(head_dim)).  Row b is query
+ * position pos_0 + b; output = vo * (l > 0 ? gate/l : 0) with gate = 1 when
+ * gate_sig is NULL. */
+void orc_lfm3_online_gqa_f16(const float *q_batch, const float *gate_sig,
+                             const uint16_t *k_cache_f16, const uint16_t *v_cache_f16,
+                             float *xb_out, uint32_t B, uint32_t pos_0,
+                             uint32_t window_len, uint32_t swa_cap,
+                             uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim) {
+    const uint32_t kv_mul = (n_head_kv > 0u) ? (n_head_q / n_head_kv) : 1u;
+    const size_t stride   = (size_t)n_head_kv * head_dim;
+    const float scale     = 1.0f / sqrtf((float)head_dim);
+    for (uint32_t b = 0; b < B; ++b) {
+        uint32_t p[5];
+        orc_lfm3_plan(pos_0 + b, window_len, swa_cap, p);
+        const float *q_tok = q_batch + (size_t)b * n_head_q * head_dim;
+        float *o_tok       = xb_out + (size_t)b * n_head_q * head_dim;
+        const float *g_tok = gate_sig ? gate_sig + (size_t)b * n_head_q : NULL;
+        for (uint32_t h = 0; h < n_head_q; ++h) {
+            const size_t kv_off = (size_t)(h / kv_mul) * head_dim;
+            float vo[512] = {0.0f};
+            float m = -1e30f, l = 0.0f;
+            orc_head_segment(q_tok + (size_t)h * head_dim,
+                             k_cache_f16 + (size_t)p[2] * stride + kv_off,
+                             v_cache_f16 + (size_t)p[2] * stride + kv_off,
+                             stride, p[3], head_dim, scale, vo, &m, &l);
+            if (p[4] > 0u) {
+                orc_head_segment(q_tok + (size_t)h * head_dim, k_cache_f16 + kv_off,
+                                 v_cache_f16 + kv_off, stride, p[4], head_dim, scale,
+                                 vo, &m, &l);
+            }
+            const float gv    = g_tok ? g_tok[h] : 1.0f;
+            const float inv_l = (l > 0.0f) ? (gv / l) : 0.0f;
+            for (uint32_t i = 0; i < head_dim; ++i) o_tok[(size_t)h * head_dim + i] = vo[i] * inv_l;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* A6: src/lfm_forward.c:181-244 after the projections.  RMSNorm per
+ * src/lfm_simd.c:125-170 (float sum of squares, x * r * w), RoPE per
+ * src/lfm_forward.c:97-111 (float powf/cosf/sinf per call), FP32 append at
+ * pos (:198-202), two-pass softmax attention (:204-244). */
+void orc_gen1_gqa_attend(float *attn_out, float *q, float *k, const float *v,
+                         const float *q_norm, const float *k_norm,
+                         float *k_cache, float *v_cache, uint32_t pos,
+                         uint32_t n_heads_q, uint32_t n_heads_kv, uint32_t head_dim,
+                         float eps, float theta) {
+    const uint32_t half  = head_dim / 2u;
+    const uint32_t group = n_heads_q / n_heads_kv;
+    for (uint32_t pass = 0; pass < 2u; ++pass) {
+        float *vec          = pass == 0u ? q : k;
+        const float *w      = pass == 0u ? q_norm : k_norm;
+        const uint32_t nh   = pass == 0u ? n_heads_q : n_heads_kv;
+        for (uint32_t h = 0; h < nh; ++h) {
+            float *x = vec + (size_t)h * head_dim;
+            float ss = 0.0f;
+            for (uint32_t i = 0; i < head_dim; ++i) ss += x[i] * x[i];
+            const float r = 1.0f / sqrtf((ss / (float)head_dim) + eps);
+            for (uint32_t i = 0; i < head_dim; ++i) x[i] = w ? x[i] * r * w[i] : x[i] * r;
+            for (uint32_t i = 0; i < half; ++i) {
+                const float freq = 1.0f / powf(theta, (float)(2u * i) / (float)head_dim);
+                const float phi  = (float)pos * freq;
+                const float c = cosf(phi), s = sinf(phi);
+                const float x0 = x[i], x1 = x[i + half];
+                x[i]        = x0 * c - x1 * s;
+                x[i + half] = x1 * c + x0 * s;
+            }
+        }
+    }
+    const size_t kv_dim = (size_t)n_heads_kv * head_dim;
+    memcpy(k_cache + (size_t)pos * kv_dim, k, kv_dim * sizeof(float));
+    memcpy(v_cache + (size_t)pos * kv_dim, v, kv_dim * sizeof(float));
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float *scores = (float *)malloc(((size_t)pos + 1u) * sizeof(float));
+    for (uint32_t hq = 0; hq < n_heads_q; ++hq) {
+        const uint32_t hkv = hq / group;
+        const float *qh = q + (size_t)hq * head_dim;
+        float *out_h = attn_out + (size_t)hq * head_dim;
+        memset(out_h, 0, head_dim * sizeof(float));
+        float max_score = -1e30f;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            const float *kt = k_cache + (size_t)t * kv_dim + (size_t)hkv * head_dim;
+            float dot = 0.0f;
+            for (uint32_t i = 0; i < head_dim; ++i) dot += qh[i] * kt[i];
+            scores[t] = dot * scale;
+            if (scores[t] > max_score) max_score = scores[t];
+        }
+        float sum_exp = 0.0f;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            scores[t] = expf(scores[t] - max_score);
+            sum_exp += scores[t];
+        }
+        const float inv_sum = 1.0f / sum_exp;
+        for (uint32_t t = 0; t <= pos; ++t) scores[t] *= inv_sum;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            const float *vt = v_cache + (size_t)t * kv_dim + (size_t)hkv * head_dim;
+            for (uint32_t d = 0; d < head_dim; ++d) out_h[d] += scores[t] * vt[d];
+        }
+    }
+    free(scores);
+}
+
+/* A7: tools/lfm2_prefill_batch.c:1029-1092 -- row r is position pos_0 + r and
+ * attends [0, pos_0 + r] through the per-head task (FP16 branch), one row at
+ * a time; the cache must already hold rows 0 .. pos_0 + n_rows - 1. */
+void orc_causal_rows_f16(const float *q_rows, const uint16_t *k_cache_f16,
+                         const uint16_t *v_cache_f16, float *out_rows,
+                         uint32_t n_rows, uint32_t pos_0, uint32_t n_head_q,
+                         uint32_t n_head_kv, uint32_t head_dim) {
+    const uint32_t kv_dim = n_head_kv * head_dim;
+    const float scale     = 1.0f / sqrtf((float)head_dim);
+    for (uint32_t r = 0; r < n_rows; ++r) {
+        orc_gqa_heads(q_rows + (size_t)r * n_head_q * head_dim, NULL, NULL, k_cache_f16,
+                      v_cache_f16, out_rows + (size_t)r * n_head_q * head_dim, n_head_q,
+                      n_head_q / n_head_kv, head_dim, kv_dim, pos_0 + r, scale);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Threaded batched decode: the reference's work item (4 query heads,
+ * tools/lfm2_kernels_fast.c:706-710) claimed dynamically like
+ * lfm2_threadpool_claim_chunk (tools/lfm2_threadpool.c:506-520), but over all
+ * (sequence, head group) pairs of the batch. */
+typedef struct {
+    const float *q;
+    const uint16_t *const *k_seq;
+    const uint16_t *const *v_seq;
+    const uint32_t *pos;
+    float *out;
+    uint32_t n_seq, n_head_q, n_head_kv, head_dim, n_groups;
+    atomic_uint next;
+} orc_batch_job;
+
+static void *orc_batch_worker(void *arg) {
+    orc_batch_job *j = (orc_batch_job *)arg;
+    const uint32_t kv_mul = j->n_head_q / j->n_head_kv;
+    const size_t stride   = (size_t)j->n_head_kv * j->head_dim;
+    const float scale     = 1.0f / sqrtf((float)j->head_dim);
+    float vo[512];
+    for (;;) {
+        const uint32_t item = atomic_fetch_add_explicit(&j->next, 1u, memory_order_relaxed);
+        if (item >= j->n_seq * j->n_groups) break;
+        const uint32_t s = item / j->n_groups, g = item % j->n_groups;
+        const uint32_t h_end = (g * 4u + 4u < j->n_head_q) ? g * 4u + 4u : j->n_head_q;
+        for (uint32_t h = g * 4u; h < h_end; ++h) {
+            const size_t kv_off = (size_t)(h / kv_mul) * j->head_dim;
+            const size_t qo     = ((size_t)s * j->n_head_q + h) * j->head_dim;
+            float m = -1e30f, l = 0.0f;
+            memset(vo, 0, j->head_dim * sizeof(float));
+            orc_head_segment(j->q + qo, j->k_seq[s] + kv_off, j->v_seq[s] + kv_off, stride,
+                             j->pos[s] + 1u, j->head_dim, scale, vo, &m, &l);
+            const float inv_l = 1.0f / l;
+            for (uint32_t i = 0; i < j->head_dim; ++i) j->out[qo + i] = vo[i] * inv_l;
+        }
+    }
+    return NULL;
+}
+
+void orc_decode_batch_mt(const float *q, const uint16_t *const *k_seq,
+                         const uint16_t *const *v_seq, const uint32_t *pos,
+                         float *out, uint32_t n_seq, uint32_t n_head_q,
+                         uint32_t n_head_kv, uint32_t head_dim, uint32_t n_threads) {
+    orc_batch_job job = {q, k_seq, v_seq, pos, out, n_seq, n_head_q, n_head_kv, head_dim,
+                         (n_head_q + 3u) / 4u, 0u};
+    if (n_threads < 1u) n_threads = 1u;
+    if (n_threads > 256u) n_threads = 256u;
+    pthread_t th[256];
+    for (uint32_t t = 1; t < n_threads; ++t) pthread_create(&th[t], NULL, orc_batch_worker, &job);
+    orc_batch_worker(&job);
+    for (uint32_t t = 1; t < n_threads; ++t) pthread_join(th[t], NULL);
+}

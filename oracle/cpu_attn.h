@@ -1,0 +1,89 @@
+/*
+ * oracle/cpu_attn.h -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A scalar C11 restatement of the reference CPU attention path
+ * (avisheksharmacoder/laii), used as the parity checker for the HIP kernels
+ * and as the "port" CPU baseline.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it; the product library never does.
+ *
+ * Each function names the reference code it follows (file:line).  Where the
+ * reference has several ISA variants of one algorithm (AVX2 / NEON / scalar)
+ * the oracle follows the scalar variant's arithmetic; the variants differ only
+ * in fp32 summation order.
+ */
+#ifndef LFM_ORACLE_CPU_ATTN_H
+#define LFM_ORACLE_CPU_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- A8: IEEE binary16 <-> binary32 ------------------------------------ */
+float    orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f); /* round-to-nearest-even, F16C semantics */
+void     orc_f32_to_f16_n(const float *src, uint16_t *dst, size_t n);
+void     orc_f16_to_f32_n(const uint16_t *src, float *dst, size_t n);
+
+/* ---- A4/A5: RoPE tables ------------------------------------------------- */
+void orc_rope_lut_lfm2(float *cos_lut, float *sin_lut, uint32_t max_seq,
+                       uint32_t head_dim, float freq_base);
+void orc_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq,
+                       uint32_t head_dim, uint32_t rope_dim, float freq_base,
+                       const float *rope_freqs, uint32_t n_rope_freqs);
+
+/* ---- A4/A5: per-head RMSNorm + NeoX RoPE (+ RNE fp16 store) ------------- */
+void orc_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads,
+                      uint32_t head_dim, const float *norm_w, float eps,
+                      const float *cos_row, const float *sin_row);
+
+/* ---- A1: LFM2 d=64 single-pass online softmax GQA ---------------------- */
+void orc_online_gqa_f16(const float *q, const uint16_t *k_cache_f16,
+                        const uint16_t *v_cache_f16, float *xb_out,
+                        uint32_t n_head_q, uint32_t kv_mul, uint32_t kv_dim,
+                        uint32_t pos, float scale);
+
+/* ---- A2: per-head GQA task (FP16 online branch / FP32 two-pass) -------- */
+void orc_gqa_heads(const float *q, const float *k_cache, const float *v_cache,
+                   const uint16_t *k_cache_f16, const uint16_t *v_cache_f16,
+                   float *xb, uint32_t n_head_q, uint32_t kv_mul,
+                   uint32_t head_dim, uint32_t kv_dim, uint32_t pos, float scale);
+
+/* ---- A3: LFM3 row plan + online GQA with SWA ring and output gate ------- */
+void     orc_lfm3_plan(uint32_t abs_pos, uint32_t window_len, uint32_t swa_cap,
+                       uint32_t out5[5]);
+uint32_t orc_lfm3_slots(uint32_t abs_pos, uint32_t window_len, uint32_t swa_cap,
+                        uint32_t *slots_out);
+void orc_lfm3_online_gqa_f16(const float *q_batch, const float *gate_sig,
+                             const uint16_t *k_cache_f16, const uint16_t *v_cache_f16,
+                             float *xb_out, uint32_t B, uint32_t pos_0,
+                             uint32_t window_len, uint32_t swa_cap,
+                             uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim);
+
+/* ---- A6: Gen-1 FP32 step (norm, per-call RoPE, FP32 append, two-pass) --- */
+void orc_gen1_gqa_attend(float *attn_out, float *q, float *k, const float *v,
+                         const float *q_norm, const float *k_norm,
+                         float *k_cache, float *v_cache, uint32_t pos,
+                         uint32_t n_heads_q, uint32_t n_heads_kv, uint32_t head_dim,
+                         float eps, float theta);
+
+/* ---- A7: causal batch (prefill / speculative verify) over FP16 KV ------- */
+void orc_causal_rows_f16(const float *q_rows, const uint16_t *k_cache_f16,
+                         const uint16_t *v_cache_f16, float *out_rows,
+                         uint32_t n_rows, uint32_t pos_0, uint32_t n_head_q,
+                         uint32_t n_head_kv, uint32_t head_dim);
+
+/* ---- Multi-threaded drivers (CPU baseline "port") ---------------------- */
+/* Batched decode over n_seq independent caches; work items are
+ * (sequence, 4-head group) pairs spread over n_threads pthreads. */
+void orc_decode_batch_mt(const float *q, const uint16_t *const *k_seq,
+                         const uint16_t *const *v_seq, const uint32_t *pos,
+                         float *out, uint32_t n_seq, uint32_t n_head_q,
+                         uint32_t n_head_kv, uint32_t head_dim, uint32_t n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LFM_ORACLE_CPU_ATTN_H */

@@ -1,0 +1,237 @@
+/*
+ * oracle/ref_shim.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Exposes the reference's own CPU attention kernels (compiled from the
+ * sources where they lie under /root/reference; nothing is copied) as plain C
+ * functions, so tests can pin the oracle restatement against the real thing
+ * and bench.py can time the reference as the CPU baseline.  Built by
+ * oracle/Makefile into oracle/_ref/libref_attn.so, only where /root/reference
+ * exists; the resulting library travels with the tree.
+ *
+ * The reference pool pins the calling thread and sets FTZ/DAZ on it
+ * (tools/lfm2_threadpool.c:384-414); every entry point here restores the
+ * caller's affinity mask and MXCSR before returning.
+ */
+#define _GNU_SOURCE 1
+#define LFM2_LOADER_NO_MAIN 1
+#define LFM2_THREADPOOL_NO_MAIN 1
+#define LFM2_FORWARD_NO_MAIN 1
+#define LFM2_DECODE_1X4_NO_MAIN 1
+#define LFM2_KERNELS_FAST_NO_MAIN 1
+#define LFM2_PREFILL_BATCH_NO_MAIN 1
+#define LFM2_SPECULATIVE_PLD_NO_MAIN 1
+#define LFM3_ENGINE_NO_MAIN 1
+#include "tools/lfm3_engine.c"
+
+#include <sched.h>
+#include <time.h>
+#include <xmmintrin.h>
+
+typedef struct {
+    cpu_set_t aff;
+    unsigned  csr;
+} shim_state;
+
+static void shim_save(shim_state *s) {
+    CPU_ZERO(&s->aff);
+    sched_getaffinity(0, sizeof s->aff, &s->aff);
+    s->csr = _mm_getcsr();
+}
+
+static void shim_restore(const shim_state *s) {
+    sched_setaffinity(0, sizeof s->aff, &s->aff);
+    _mm_setcsr(s->csr);
+}
+
+static GGUFTensor shim_f32_tensor(const float *data, uint64_t n) {
+    GGUFTensor t;
+    memset(&t, 0, sizeof t);
+    t.n_dims = 1;
+    t.ne[0]  = n;
+    t.ne[1] = t.ne[2] = t.ne[3] = 1;
+    t.type   = GGML_TYPE_F32;
+    t.bytes  = (size_t)n * sizeof(float);
+    t.data   = data;
+    return t;
+}
+
+int ref_has_avx2(void) { return LFM2_HAS_AVX2 ? 1 : 0; }
+
+/* lfm2_rope_lut_init, tools/lfm2_kernels_fast.c:370-388 */
+int ref_rope_lut_lfm2(float *cos_out, float *sin_out, uint32_t max_seq, uint32_t head_dim,
+                      float freq_base) {
+    LFM2RoPELUT lut;
+    if (!lfm2_rope_lut_init(&lut, max_seq, head_dim, freq_base)) return -1;
+    memcpy(cos_out, lut.cos_lut, (size_t)max_seq * (head_dim / 2) * sizeof(float));
+    memcpy(sin_out, lut.sin_lut, (size_t)max_seq * (head_dim / 2) * sizeof(float));
+    lfm2_rope_lut_free(&lut);
+    return 0;
+}
+
+/* lfm3_rope_lut_init, tools/lfm3_engine.c:403-450 */
+int ref_rope_lut_lfm3(float *cos_out, float *sin_out, uint32_t max_seq, uint32_t head_dim,
+                      uint32_t rope_dim, float freq_base, const float *rope_freqs,
+                      uint32_t n_rope_freqs) {
+    LFM2RoPELUT lut;
+    GGUFTensor rf = shim_f32_tensor(rope_freqs, n_rope_freqs);
+    if (!lfm3_rope_lut_init(&lut, max_seq, head_dim, rope_dim, freq_base,
+                            rope_freqs ? &rf : NULL)) return -1;
+    memcpy(cos_out, lut.cos_lut, (size_t)max_seq * (head_dim / 2) * sizeof(float));
+    memcpy(sin_out, lut.sin_lut, (size_t)max_seq * (head_dim / 2) * sizeof(float));
+    lfm2_rope_lut_free(&lut);
+    return 0;
+}
+
+/* Wrap a caller LUT in 64-byte aligned storage (the AVX2 kernels use
+ * aligned loads of the cos/sin rows). */
+static int shim_lut(LFM2RoPELUT *lut, const float *cos_lut, const float *sin_lut,
+                    uint32_t max_seq, uint32_t half) {
+    const size_t bytes = (size_t)max_seq * half * sizeof(float);
+    lut->max_seq_len = max_seq;
+    lut->half_dim    = half;
+    lut->cos_lut     = (float *)lfm2_aligned_alloc_64(bytes);
+    lut->sin_lut     = (float *)lfm2_aligned_alloc_64(bytes);
+    if (!lut->cos_lut || !lut->sin_lut) return -1;
+    memcpy(lut->cos_lut, cos_lut, bytes);
+    memcpy(lut->sin_lut, sin_lut, bytes);
+    return 0;
+}
+
+/* lfm2_qk_norm_rope_avx2 (tools/lfm2_kernels_fast.c:403-497) or the scalar
+ * kernel (:511-547); head_dim is 64. */
+int ref_qk_norm_rope_lfm2(float *vec, uint16_t *dst_f16, uint32_t n_heads, const float *norm_w,
+                          float eps, const float *cos_lut, const float *sin_lut,
+                          uint32_t max_seq, uint32_t pos, int force_scalar) {
+    LFM2RoPELUT lut;
+    if (shim_lut(&lut, cos_lut, sin_lut, max_seq, 32u) != 0) return -1;
+    GGUFTensor nw = shim_f32_tensor(norm_w, 64u);
+#if LFM2_HAS_AVX2
+    if (!force_scalar)
+        lfm2_qk_norm_rope_avx2(vec, dst_f16, n_heads, 64u, norm_w ? &nw : NULL, eps, &lut, pos);
+    else
+#endif
+        lfm2_qk_norm_rope_scalar(vec, dst_f16, n_heads, 64u, norm_w ? &nw : NULL, eps, &lut, pos);
+    lfm2_rope_lut_free(&lut);
+    return 0;
+}
+
+/* lfm3_qk_norm_rope_simd (tools/lfm3_engine.c:644-666) / scalar (:599-642). */
+int ref_qk_norm_rope_lfm3(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
+                          const float *norm_w, float eps, const float *cos_lut,
+                          const float *sin_lut, uint32_t max_seq, uint32_t pos, int force_scalar) {
+    LFM2RoPELUT lut;
+    if (shim_lut(&lut, cos_lut, sin_lut, max_seq, head_dim / 2u) != 0) return -1;
+    GGUFTensor nw = shim_f32_tensor(norm_w, head_dim);
+    if (force_scalar)
+        lfm3_qk_norm_rope_scalar(vec, dst_f16, n_heads, head_dim, norm_w ? &nw : NULL, eps, &lut, pos);
+    else
+        lfm3_qk_norm_rope_simd(vec, dst_f16, n_heads, head_dim, norm_w ? &nw : NULL, eps, &lut, pos);
+    lfm2_rope_lut_free(&lut);
+    return 0;
+}
+
+/* lfm2_store_fp32_to_fp16_simd (tools/lfm2_kernels_fast.c:500-507) */
+void ref_store_fp32_to_fp16(uint16_t *dst, const float *src, uint32_t n) {
+    uint32_t i = 0;
+#if LFM2_HAS_AVX2
+    for (; i + 8u <= n; i += 8u) lfm2_store_fp32_to_fp16_avx2(dst + i, src + i, 8u);
+#endif
+    for (; i < n; ++i) dst[i] = fp32_to_fp16(src[i]);
+}
+
+float ref_fp16_to_fp32(uint16_t h) { return lfm2_fp16_to_fp32(h); }
+
+/* OnlineGQATaskCtx + lfm2_parallel_for (tools/lfm2_kernels_fast.c:1052-1066). */
+void ref_online_gqa_f16(const float *q, const uint16_t *k16, const uint16_t *v16, float *out,
+                        uint32_t n_head_q, uint32_t kv_mul, uint32_t kv_dim, uint32_t pos,
+                        uint32_t n_threads) {
+    shim_state st;
+    shim_save(&st);
+    LFM2ThreadPool pool;
+    lfm2_threadpool_init(&pool, n_threads);
+    OnlineGQATaskCtx ctx = {
+        .pool = &pool, .q = q, .k_cache_f16 = k16, .v_cache_f16 = v16, .xb_out = out,
+        .xb_q8_out = NULL, .n_head_q = n_head_q, .kv_mul = kv_mul, .kv_dim = kv_dim,
+        .pos = pos, .scale = 1.0f / sqrtf(64.0f)};
+    lfm2_parallel_for(&pool, (n_head_q + 3u) / 4u, 1, lfm2_online_gqa_f16_worker_simd, &ctx);
+    lfm2_threadpool_free(&pool);
+    shim_restore(&st);
+}
+
+/* GQAAttnTaskCtx + lfm2_gqa_heads_worker_task (tools/lfm2_prefill_batch.c:1074-1091);
+ * f16 caches NULL selects the FP32 two-pass branch. */
+void ref_gqa_heads(const float *q, const float *k32, const float *v32, const uint16_t *k16,
+                   const uint16_t *v16, float *out, uint32_t n_head_q, uint32_t kv_mul,
+                   uint32_t head_dim, uint32_t kv_dim, uint32_t max_seq, uint32_t pos,
+                   uint32_t n_threads) {
+    shim_state st;
+    shim_save(&st);
+    LFM2ThreadPool pool;
+    lfm2_threadpool_init(&pool, n_threads);
+    float *att = (float *)calloc((size_t)n_head_q * max_seq, sizeof(float));
+    GQAAttnTaskCtx ctx = {
+        .pool = &pool, .q = q, .k_cache = k32, .v_cache = v32, .k_cache_f16 = k16,
+        .v_cache_f16 = v16, .att = att, .xb = out, .n_head_q = n_head_q, .kv_mul = kv_mul,
+        .head_dim = head_dim, .kv_dim = kv_dim, .max_seq_len = max_seq, .pos = pos,
+        .scale = 1.0f / sqrtf((float)head_dim)};
+    lfm2_parallel_for(&pool, n_head_q, 1, lfm2_gqa_heads_worker_task, &ctx);
+    free(att);
+    lfm2_threadpool_free(&pool);
+    shim_restore(&st);
+}
+
+/* lfm3_online_gqa_f16_dispatch (tools/lfm3_engine.c:1155-1204). */
+void ref_lfm3_dispatch(const float *q, const float *gate, const uint16_t *k16, const uint16_t *v16,
+                       float *out, uint32_t B, uint32_t pos_0, uint32_t window_len,
+                       uint32_t swa_cap, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                       uint32_t n_threads) {
+    shim_state st;
+    shim_save(&st);
+    LFM2ThreadPool pool;
+    lfm2_threadpool_init(&pool, n_threads);
+    lfm3_online_gqa_f16_dispatch(&pool, q, gate, k16, v16, out, NULL, B, pos_0, window_len,
+                                 swa_cap, n_head_q, n_head_kv, head_dim);
+    lfm2_threadpool_free(&pool);
+    shim_restore(&st);
+}
+
+static double shim_now(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+/* CPU baseline, reference-faithful: one pool, each sequence dispatched as
+ * the engine dispatches one decode step (ceil(n_head_q/4) items,
+ * tools/lfm2_kernels_fast.c:1065-1066), sequences one after another.
+ * head_dim is 64.  Runs `reps` passes and returns the seconds of the fastest;
+ * *threads_out receives the pool's actual worker count. */
+double ref_time_decode_batch(const float *q, const uint16_t *const *k_seq,
+                             const uint16_t *const *v_seq, const uint32_t *pos, float *out,
+                             uint32_t n_seq, uint32_t n_head_q, uint32_t n_head_kv,
+                             uint32_t n_threads, uint32_t reps, uint32_t *threads_out) {
+    shim_state st;
+    shim_save(&st);
+    LFM2ThreadPool pool;
+    lfm2_threadpool_init(&pool, n_threads);
+    if (threads_out) *threads_out = pool.n_threads;
+    const uint32_t kv_dim = n_head_kv * 64u;
+    double best = 1e30;
+    for (uint32_t r = 0; r < reps; ++r) {
+        const double t0 = shim_now();
+        for (uint32_t s = 0; s < n_seq; ++s) {
+            OnlineGQATaskCtx ctx = {
+                .pool = &pool, .q = q + (size_t)s * n_head_q * 64u, .k_cache_f16 = k_seq[s],
+                .v_cache_f16 = v_seq[s], .xb_out = out + (size_t)s * n_head_q * 64u,
+                .xb_q8_out = NULL, .n_head_q = n_head_q, .kv_mul = n_head_q / n_head_kv,
+                .kv_dim = kv_dim, .pos = pos[s], .scale = 1.0f / sqrtf(64.0f)};
+            lfm2_parallel_for(&pool, (n_head_q + 3u) / 4u, 1, lfm2_online_gqa_f16_worker_simd,
+                              &ctx);
+        }
+        const double dt = shim_now() - t0;
+        if (dt < best) best = dt;
+    }
+    lfm2_threadpool_free(&pool);
+    shim_restore(&st);
+    return best;
+}
