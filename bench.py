@@ -1,0 +1,284 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path (one GPU).
+
+Headline (value): batched decode attention, LFM2-1.2B GQA shape -- 64
+independent sequences, 32 query / 8 KV heads, head_dim 64, fp16 KV, every
+context 8192 (north-star size).  One step = one attention
+call over the whole batch (split-KV kernel + merge), inputs resident in HBM.
+value = algorithmic bytes / step time (KV read once + Q read + O written).
+
+Also reported: config 2 with ctx ~ U[512, 8192], config 3 (B=8 speculative
+verify), config 5 (LFM3 SWA ring and full layer), each as GB/s, and the
+reference's CPU attention timed on this host (cpu_baseline).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, datasheet
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, datasheet
+
+
+class Hip:
+    """Minimal HIP runtime access for events (plumbing only)."""
+
+    def __init__(self):
+        rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+        self.lib = C.CDLL(os.path.join(rocm, "lib", "libamdhip64.so"))
+        for n in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize",
+                  "hipEventElapsedTime", "hipDeviceSynchronize", "hipEventDestroy"):
+            getattr(self.lib, n).restype = C.c_int
+        self.lib.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.lib.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [C.c_void_p]
+
+    def event(self):
+        ev = C.c_void_p()
+        assert self.lib.hipEventCreate(C.byref(ev)) == 0
+        return ev
+
+    def record(self, ev, stream=None):
+        assert self.lib.hipEventRecord(ev, stream) == 0
+
+    def elapsed_ms(self, a, b) -> float:
+        assert self.lib.hipEventSynchronize(b) == 0
+        ms = C.c_float()
+        assert self.lib.hipEventElapsedTime(C.byref(ms), a, b) == 0
+        return float(ms.value)
+
+    def sync(self):
+        assert self.lib.hipDeviceSynchronize() == 0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+class DecodeWorkload:
+    """n_seq sequences, n_rows query rows each (row r at position pos0[s] + r),
+    `copies` independent replicas of all device inputs (rotated per step so
+    the working set exceeds the 256 MB last-level cache)."""
+
+    def __init__(self, la, rng, name, n_seq, n_rows, nq, nkv, hd, ctx, window=0, cap=0,
+                 gate=False, copies=1, keep_host=0):
+        self.la, self.name = la, name
+        self.n_seq, self.n_rows, self.nq, self.nkv, self.hd = n_seq, n_rows, nq, nkv, hd
+        self.window, self.cap = window, cap
+        ctx = np.asarray(ctx, np.int64)
+        self.pos0 = (ctx if n_rows > 1 else ctx - 1).astype(np.uint32)  # first row position
+        last = self.pos0.astype(np.int64) + n_rows - 1
+        self.slots = [int(cap) if window else int(l) + 1 for l in last]
+        if window:
+            t0 = np.maximum(0, last + 1 - window)
+            self.keys = (last - t0 + 1).astype(np.int64)
+        else:
+            self.keys = last + 1
+        self.max_keys = int(self.keys.max())
+        self.host_k, self.host_v = [], []
+        self.sets = []
+        for c in range(copies):
+            kd, vd = [], []
+            for s in range(n_seq):
+                k = f16(rng.standard_normal((self.slots[s], nkv, hd), dtype=np.float32) * np.float32(0.5))
+                v = f16(rng.standard_normal((self.slots[s], nkv, hd), dtype=np.float32) * np.float32(0.5))
+                if c == 0 and s < keep_host:
+                    self.host_k.append(k)
+                    self.host_v.append(v)
+                kd.append(la.DeviceArray.from_numpy(k))
+                vd.append(la.DeviceArray.from_numpy(v))
+            q = rng.standard_normal((n_seq, n_rows, nq, hd), dtype=np.float32)
+            g = rng.standard_normal((n_seq, n_rows, nq)).astype(np.float32) if gate else None
+            if c == 0:
+                self.host_q, self.host_g = q, g
+            self.sets.append(dict(kd=kd, vd=vd, kt=la.pointer_table(kd), vt=la.pointer_table(vd),
+                                  q=la.DeviceArray.from_numpy(q),
+                                  g=None if g is None else la.DeviceArray.from_numpy(g),
+                                  out=la.DeviceArray.zeros((n_seq, n_rows, nq, hd), np.float32),
+                                  pos=la.DeviceArray.from_numpy(self.pos0)))
+        # algorithmic bytes of one step: each attended K and V byte once, Q read, O written
+        self.kv_bytes = int(self.keys.sum()) * nkv * hd * 2 * 2
+        self.qo_bytes = n_seq * n_rows * nq * hd * 4 * 2
+        self.bytes = self.kv_bytes + self.qo_bytes
+        self.flops = int(self.keys.sum()) * n_rows * nq * hd * 4  # upper bound for verify rows
+        self._i = 0
+
+    def step(self):
+        st = self.sets[self._i % len(self.sets)]
+        self._i += 1
+        self.la.gqa_f16_varlen(st["q"], st["g"], True, st["kt"], st["vt"], st["pos"], st["out"],
+                               self.n_seq, self.n_rows, self.max_keys, self.nq, self.nkv, self.hd,
+                               self.window, self.cap)
+
+    def output(self, copy=0):
+        return self.sets[copy]["out"].numpy()
+
+
+def time_steps(hip, wl, steps, warmup):
+    for _ in range(warmup):
+        wl.step()
+    hip.sync()
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0)
+    for _ in range(steps):
+        wl.step()
+    hip.record(e1)
+    hip.sync()
+    return hip.elapsed_ms(e0, e1) / steps
+
+
+def time_main_kernel(hip, la, wl, steps):
+    """Average duration of the split-KV kernel alone (HIP events recorded by
+    the library immediately around that launch, on its stream)."""
+    lib = la.load()
+    evs = [(hip.event(), hip.event()) for _ in range(steps)]
+    for a, b in evs:
+        lib.lfm_attn_profile_events(a, b)
+        wl.step()
+    lib.lfm_attn_profile_events(None, None)
+    hip.sync()
+    return float(np.mean([hip.elapsed_ms(a, b) for a, b in evs]))
+
+
+def cpu_baseline(wl, n_threads, max_seconds=8.0):
+    """The reference's AVX2 decode worker (oracle/_ref) on a sample of the
+    headline batch, dispatched per sequence as the engine does; falls back to
+    the C restatement when the reference build is absent."""
+    from oracle.bindings import Oracle, Reference
+
+    n = len(wl.host_k)
+    q = wl.host_q[:n, 0].reshape(n, -1)
+    pos = wl.pos0[:n]
+    sample_bytes = int(wl.keys[:n].sum()) * wl.nkv * wl.hd * 4 + n * wl.nq * wl.hd * 8
+    if Reference.available():
+        ref = Reference()
+        dt, used, out = ref.time_decode_batch(q, wl.host_k, wl.host_v, pos, wl.nq, wl.nkv, n_threads,
+                                              1)
+        reps = max(1, min(20, int(max_seconds / max(dt, 1e-3))))
+        dt, used, out = ref.time_decode_batch(q, wl.host_k, wl.host_v, pos, wl.nq, wl.nkv,
+                                              n_threads, reps)
+        kind = "reference"
+    else:
+        orc = Oracle()
+        t0 = time.perf_counter()
+        out = orc.decode_batch_mt(q, wl.host_k, wl.host_v, pos, wl.nq, wl.nkv, wl.hd, n_threads)
+        dt, used, kind = time.perf_counter() - t0, n_threads, "port"
+    return dict(value=round(sample_bytes / dt / 1e9, 3), unit="GB/s", cores=int(used), kind=kind,
+                sample=f"{n} of {wl.n_seq} sequences x ctx {int(wl.keys[0])}, 32q/8kv d64, "
+                       f"best of repeated passes, {dt * 1e3:.1f} ms per pass"), out.reshape(n, wl.nq, wl.hd)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU's share only; --gpus {args.gpus} is not supported "
+              "(the sharding plan is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import laii_amd as la
+
+    la.require_gpu()
+    hip = Hip()
+    rng = np.random.default_rng(20261201)
+    t_setup = time.perf_counter()
+
+    head = DecodeWorkload(la, rng, "decode_b64_ctx8192", 64, 1, 32, 8, 64, [8192] * 64,
+                          keep_host=8)
+    log(f"headline inputs ready ({time.perf_counter() - t_setup:.1f} s)")
+    ms = time_steps(hip, head, args.steps, args.warmup)
+    k_ms = time_main_kernel(hip, la, head, args.steps)
+    log(f"headline: {ms * 1e3:.1f} us/step, kernel {k_ms * 1e3:.1f} us")
+    value = head.bytes / (ms * 1e-3) / 1e9
+    achieved = head.bytes / (k_ms * 1e-3) / 1e9
+    gpu_out = head.output()
+
+    secondary = {}
+    if not args.quick:
+        cases = [
+            ("cfg2_varlen_b64_ctxU512_8192", dict(n_seq=64, n_rows=1, nq=32, nkv=8, hd=64,
+                                                  ctx=rng.integers(512, 8193, size=64))),
+            ("cfg3_verify_b16_rows8_ctx4096", dict(n_seq=16, n_rows=8, nq=32, nkv=8, hd=64,
+                                                   ctx=[4096] * 16, copies=4)),
+            ("cfg5_lfm3_swa_b32_cap256_pos1000", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
+                                                      ctx=[1001] * 32, window=256, cap=256,
+                                                      gate=True, copies=36)),
+            ("cfg5_lfm3_full_b32_ctx32768", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
+                                                 ctx=[32768] * 32, gate=True)),
+            ("cfg1_decode_b1_16q8kv_ctx1024", dict(n_seq=1, n_rows=1, nq=16, nkv=8, hd=64,
+                                                   ctx=[1024], copies=1)),
+        ]
+        for name, kw in cases:
+            wl = DecodeWorkload(la, rng, name, **kw)
+            sms = time_steps(hip, wl, args.steps, args.warmup)
+            kms = time_main_kernel(hip, la, wl, args.steps)
+            log(f"{name}: {sms * 1e3:.1f} us/step")
+            secondary[name] = dict(GBps=round(wl.bytes / (sms * 1e-3) / 1e9, 1),
+                                   kernel_GBps=round(wl.bytes / (kms * 1e-3) / 1e9, 1),
+                                   us_per_step=round(sms * 1e3, 2), bytes=wl.bytes,
+                                   pct_hbm_peak=round(100 * wl.bytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
+            del wl
+
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        n_thr = max(1, min(16, os.cpu_count() or 1) - 1)  # reference policy: N_phys - 1
+        log(f"cpu baseline with {n_thr} threads")
+        cpu, cpu_out = cpu_baseline(head, n_thr)
+        g = gpu_out[:cpu_out.shape[0], 0]
+        parity = dict(max_abs=float(np.abs(g - cpu_out).max()),
+                      rel_l2=float(np.linalg.norm(g - cpu_out) / np.linalg.norm(cpu_out)),
+                      vs=cpu["kind"], sequences=int(cpu_out.shape[0]))
+
+    line = {
+        "metric": "decode attn KV GB/s (% HBM peak) + prefill attn TFLOP/s, LFM2-1.2B GQA shape",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 KV / f32 softmax+accumulate",
+        "data": "synthetic, seeded N(0,1) Q and 0.5*N(0,1) fp16 K/V",
+        "config": {"workload": "decode_b64_ctx8192", "n_seq": 64, "n_head_q": 32, "n_head_kv": 8,
+                   "head_dim": 64, "ctx": 8192, "kv_bytes": head.kv_bytes,
+                   "algorithmic_bytes": head.bytes},
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_splitkv<64,1>", "kernel_us": round(k_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+        "parity_vs_cpu": parity,
+        "secondary": secondary,
+        "setup_s": round(time.perf_counter() - t_setup, 1),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

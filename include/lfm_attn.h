@@ -59,6 +59,12 @@ int lfm_attn_copy_d2d(void *dst_dev, const void *src_dev, size_t bytes, lfm_attn
 int lfm_attn_memset(void *dst_dev, int value, size_t bytes, lfm_attn_stream_t stream);
 int lfm_attn_stream_sync(lfm_attn_stream_t stream);
 
+/* Observability: while set (per host thread), every attention call records
+ * `before` / `after` (hipEvent_t handles) on its stream immediately around its
+ * main attention kernel, excluding the split merge; hipEventElapsedTime of the
+ * pair is that kernel's duration.  NULL, NULL switches it off. */
+int lfm_attn_profile_events(void *before, void *after);
+
 /* ---- index math (host copy of what the kernels compute) -------------------- */
 /* Row plan of tools/lfm3_engine.c:862-873:
  * out5 = {t_start, count, seg1_slot, seg1_len, seg2_len}. */

@@ -31,6 +31,7 @@ SIGNATURES = {
     "lfm_attn_copy_d2d": (_int, [_vp, _vp, _sz, _vp]),
     "lfm_attn_memset": (_int, [_vp, _int, _sz, _vp]),
     "lfm_attn_stream_sync": (_int, [_vp]),
+    "lfm_attn_profile_events": (_int, [_vp, _vp]),
     "lfm_attn_seg_plan": (_int, [_u32, _u32, _u32, C.POINTER(_u32)]),
     "lfm_attn_slot_of": (_u32, [_u32, _u32, _u32]),
     "lfm_attn_rope_lut_lfm2": (_int, [_vp, _vp, _u32, _u32, _f32]),

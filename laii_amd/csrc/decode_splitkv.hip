@@ -62,7 +62,7 @@ struct SplitParams {
     float *part_o;   /* [seq][kvh][split][col][HD] unnormalised O            */
     float2 *part_ml; /* [seq][kvh][split][col] (running max, sum) in log2 units */
     uint32_t pos0_host, n_rows, n_head_q, n_head_kv, kv_mul, ncols;
-    uint32_t window, cap, n_splits, out_dims;
+    uint32_t window, cap, n_splits, chunk, out_dims;
     int gate_is_logit;
     float qscale; /* scale * log2(e) */
 };
@@ -97,8 +97,10 @@ __global__ __launch_bounds__(64) void k_splitkv(const SplitParams P) {
     const uint32_t last  = pos0 + P.n_rows - 1u;
     const uint32_t lo    = lfm_plan_row(pos0, P.window, P.cap).t_start;
     const uint32_t total = last - lo + 1u;
-    uint32_t chunk       = (total + P.n_splits - 1u) / P.n_splits;
-    chunk                = (chunk + 31u) & ~31u;
+    /* fixed-length chunks keep the work per workgroup uniform across a ragged
+     * batch; a sequence longer than n_splits chunks gets longer chunks */
+    uint32_t chunk = P.chunk;
+    if ((uint64_t)chunk * P.n_splits < total) chunk = (((total + P.n_splits - 1u) / P.n_splits) + 31u) & ~31u;
     const uint32_t kb    = lo + split * chunk;
     const uint32_t ke    = min(kb + chunk, last + 1u); /* exclusive; empty if kb > last */
     const size_t part    = ((size_t)(s * P.n_head_kv + kvh) * P.n_splits + split) * P.ncols;
@@ -371,26 +373,33 @@ __global__ __launch_bounds__(HD) void k_merge(const SplitParams P) {
 template <int HD, int NT>
 hipError_t launch_hd_nt(const SplitParams &p, uint32_t n_seq, hipStream_t stream) {
     dim3 grid(p.n_splits, p.n_head_kv, n_seq);
+    hipEvent_t ev0, ev1;
+    profile_events(&ev0, &ev1);
+    if (ev0) (void)hipEventRecord(ev0, stream);
     hipLaunchKernelGGL((k_splitkv<HD, NT>), grid, dim3(64), 0, stream, p);
     hipError_t e = hipGetLastError();
+    if (ev1) (void)hipEventRecord(ev1, stream);
     if (e != hipSuccess || p.n_splits == 1u) return e;
     hipLaunchKernelGGL((k_merge<HD>), dim3(p.ncols, p.n_head_kv, n_seq), dim3(HD), 0, stream, p);
     return hipGetLastError();
 }
 
-uint32_t choose_splits(const AttnBatch &b, uint32_t max_keys_hint) {
-    const char *env = getenv("LFM_ATTN_SPLITS");
-    if (env && atoi(env) > 0) return (uint32_t)atoi(env);
+/* Key chunk per workgroup (multiple of 32) and the number of chunks the grid
+ * covers.  Aim for enough one-wave workgroups to keep ~12 waves per CU busy. */
+void choose_split(const AttnBatch &b, uint32_t max_keys_hint, uint32_t *n_splits, uint32_t *chunk) {
     uint32_t keys = max_keys_hint;
     if (keys == 0u) keys = b.window ? b.window + b.n_rows - 1u : 4096u;
-    const uint64_t base   = (uint64_t)b.n_seq * b.n_head_kv;
-    const uint64_t target = 2048; /* workgroups: ~8 resident waves per CU x 256 CUs */
-    uint64_t splits       = (target + base - 1) / base;
-    const uint64_t by_len = (keys + 127u) / 128u; /* keep >= 4 sub-tiles per split */
-    if (splits > by_len) splits = by_len;
-    if (splits < 1) splits = 1;
-    if (splits > 256) splits = 256;
-    return (uint32_t)splits;
+    const uint64_t pairs  = (uint64_t)b.n_seq * b.n_head_kv;
+    const uint64_t target = 4096; /* workgroups */
+    uint64_t c = ((uint64_t)keys * pairs + target - 1) / target;
+    if (c < 128) c = 128; /* >= 4 sub-tiles per workgroup */
+    const char *env = getenv("LFM_ATTN_CHUNK");
+    if (env && atoi(env) > 0) c = (uint64_t)atoi(env);
+    c = (c + 31) & ~(uint64_t)31;
+    uint64_t n = (keys + c - 1) / c;
+    if (n > 1024) { n = 1024; c = (((keys + n - 1) / n) + 31) & ~(uint64_t)31; }
+    *n_splits = (uint32_t)(n ? n : 1);
+    *chunk    = (uint32_t)c;
 }
 
 } // namespace
@@ -426,7 +435,7 @@ int launch_splitkv(const AttnBatch &b, uint32_t max_keys_hint, hipStream_t strea
     p.cap           = b.cap;
     p.out_dims      = b.out_dims;
     p.qscale        = b.scale * kLog2e;
-    p.n_splits      = choose_splits(b, max_keys_hint);
+    choose_split(b, max_keys_hint, &p.n_splits, &p.chunk);
     if (p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
         const size_t bytes  = n_part * b.head_dim * sizeof(float) + n_part * sizeof(float2) + 256;

@@ -58,6 +58,9 @@ int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *cons
                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
                         uint32_t cap, hipStream_t stream);
 
+/* Events recorded around the main attention kernel (null when off). */
+void profile_events(hipEvent_t *before, hipEvent_t *after);
+
 /* Record a HIP error for lfm_attn_last_error and map it to a status. */
 int hip_status(hipError_t e);
 

@@ -17,6 +17,13 @@
 namespace lfm {
 
 static thread_local char g_last_error[256] = "";
+static thread_local hipEvent_t g_prof_before = nullptr;
+static thread_local hipEvent_t g_prof_after  = nullptr;
+
+void profile_events(hipEvent_t *before, hipEvent_t *after) {
+    *before = g_prof_before;
+    *after  = g_prof_after;
+}
 
 int hip_status(hipError_t e) {
     if (e == hipSuccess) return LFM_ATTN_OK;
@@ -88,6 +95,13 @@ const char *lfm_attn_status_string(int status) {
 const char *lfm_attn_last_error(void) { return lfm::g_last_error; }
 
 const char *lfm_attn_version(void) { return "lfm_attn 0.1 gfx950"; }
+
+int lfm_attn_profile_events(void *before, void *after) {
+    if ((before == nullptr) != (after == nullptr)) return LFM_ATTN_E_INVALID;
+    lfm::g_prof_before = reinterpret_cast<hipEvent_t>(before);
+    lfm::g_prof_after  = reinterpret_cast<hipEvent_t>(after);
+    return LFM_ATTN_OK;
+}
 
 int lfm_attn_device_count(int *count) {
     if (!count) return LFM_ATTN_E_INVALID;

@@ -1,0 +1,106 @@
+"""CPU checks of the C-ABI library: it loads, exports every function the
+public header declares, builds bit-identical RoPE tables, and rejects bad
+arguments with the documented status before touching a device."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import laii_amd as la
+from laii_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lfm_attn.h")
+
+E_INVALID, E_RANGE = -1, -2
+FAKE = 4096  # never dereferenced: validation rejects the call first
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lfm_(?:attn|hip)_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    names = header_functions()
+    assert len(names) >= 20
+    lib = la.load()
+    syms = subprocess.run(["nm", "-D", "--defined-only", la.LIB_PATH], capture_output=True,
+                          text=True, check=True).stdout
+    for n in names:
+        assert re.search(rf"\bT {n}$", syms, flags=re.M), f"{n} not exported"
+        assert hasattr(lib, n)
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_no_cpu_fallback_symbols():
+    """The product library must not carry a CPU attention path."""
+    syms = subprocess.run(["nm", "-D", la.LIB_PATH], capture_output=True, text=True).stdout
+    assert "orc_" not in syms and "ref_" not in syms.replace("_ref", "")
+
+
+def test_device_count_without_gpu():
+    n = la.device_count()
+    assert n >= 0
+
+
+def test_status_strings():
+    lib = la.load()
+    for st in (0, -1, -2, -3, -4, -5):
+        assert lib.lfm_attn_status_string(st)
+
+
+def test_rope_lut_lfm2_bit_exact(orc):
+    for hd, base in ((64, 1e6), (64, 1e4), (128, 1e6), (16, 1e6)):
+        c, s = la.rope_lut_lfm2(1500, hd, base)
+        oc, os_ = orc.rope_lut_lfm2(1500, hd, base)
+        assert np.array_equal(c, oc) and np.array_equal(s, os_)
+
+
+def test_rope_lut_lfm3_bit_exact(orc, ref):
+    rf = np.array([1.0] * 32 + [1e30] * 32, np.float32)
+    for args in ((128, 128, 1e6, rf), (128, 128, 1e4, None), (128, 64, 1e6, None),
+                 (64, 64, 1e6, np.array([2.0, 0.0, -1.0, 1e10] * 8, np.float32))):
+        c, s = la.rope_lut_lfm3(700, *args)
+        rc, rs = ref.rope_lut_lfm3(700, *args)
+        oc, os_ = orc.rope_lut_lfm3(700, *args)
+        assert np.array_equal(c, rc) and np.array_equal(s, rs)
+        assert np.array_equal(c, oc) and np.array_equal(s, os_)
+
+
+def test_rejections_before_launch():
+    lib = la.load()
+    # A1: null pointer, kv_dim inconsistent with n_head_q / kv_mul, kv_mul not dividing
+    assert lib.lfm_hip_online_gqa_f16(None, FAKE, FAKE, FAKE, 16, 2, 512, 5, 0.125, None) == E_INVALID
+    assert lib.lfm_hip_online_gqa_f16(FAKE, FAKE, FAKE, FAKE, 16, 2, 256, 5, 0.125, None) == E_INVALID
+    assert lib.lfm_hip_online_gqa_f16(FAKE, FAKE, FAKE, FAKE, 16, 3, 384, 5, 0.125, None) == E_INVALID
+    # A2: pos outside the cache, head_dim not a multiple of 8
+    assert lib.lfm_hip_gqa_heads(FAKE, None, None, FAKE, FAKE, FAKE, 8, 2, 64, 256, 100, 100, 0.125,
+                                 None) == E_RANGE
+    assert lib.lfm_hip_gqa_heads(FAKE, None, None, FAKE, FAKE, FAKE, 8, 2, 12, 48, 100, 5, 0.125,
+                                 None) == E_INVALID
+    assert lib.lfm_hip_gqa_heads(FAKE, None, None, None, FAKE, FAKE, 8, 2, 64, 256, 100, 5, 0.125,
+                                 None) == E_INVALID
+    # A3: window larger than its ring, linear rows beyond the cache, B == 0
+    assert lib.lfm_hip_lfm3_online_gqa_f16_dispatch(FAKE, None, FAKE, FAKE, FAKE, 1, 10, 300, 264,
+                                                    16, 4, 128, None) == E_INVALID
+    assert lib.lfm_hip_lfm3_online_gqa_f16_dispatch(FAKE, None, FAKE, FAKE, FAKE, 4, 4094, 0, 4096,
+                                                    16, 4, 128, None) == E_RANGE
+    assert lib.lfm_hip_lfm3_online_gqa_f16_dispatch(FAKE, None, FAKE, FAKE, FAKE, 0, 0, 0, 4096,
+                                                    16, 4, 128, None) == E_INVALID
+    # varlen: heads not grouped evenly, odd head_dim
+    assert lib.lfm_hip_gqa_f16_varlen(FAKE, None, 0, FAKE, FAKE, FAKE, FAKE, 4, 1, 0, 30, 8, 64, 0,
+                                      0, 0.125, None) == E_INVALID
+    assert lib.lfm_hip_gqa_f16_varlen(FAKE, None, 0, FAKE, FAKE, FAKE, FAKE, 4, 1, 0, 32, 8, 60, 0,
+                                      0, 0.125, None) == E_INVALID
+    # prologue
+    assert lib.lfm_hip_qk_norm_rope(FAKE, None, 4, 63, None, 1e-5, FAKE, FAKE, 0, None) == E_INVALID
+    assert lib.lfm_hip_qkv_prologue(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 16, 4, 128, None, None,
+                                    1e-5, FAKE, FAKE, 300, 264, None) == E_INVALID
+    out5 = (C.c_uint32 * 5)()
+    assert lib.lfm_attn_seg_plan(5, 300, 264, out5) == E_INVALID

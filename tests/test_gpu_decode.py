@@ -221,20 +221,18 @@ def test_varlen_lfm3_swa_cfg5(gpu, orc, cap):
 
 
 def test_split_count_invariance(gpu, orc):
-    """Size-independent property: the key split count must not change results
-    beyond fp32 rounding."""
+    """Size-independent property: the key chunk per workgroup (and so the
+    number of splits merged) must not change results beyond fp32 rounding."""
     la = gpu
-    rng = np.random.default_rng(5)
     outs = []
-    for splits in ("1", "3", "17"):
-        os.environ["LFM_ATTN_SPLITS"] = splits
+    for chunk in ("1000000", "96", "32"):
+        os.environ["LFM_ATTN_CHUNK"] = chunk
         try:
             got, want = _varlen_case(la, orc, np.random.default_rng(5), 3, 2, 32, 8, 64,
                                      [3000, 100, 2047])
         finally:
-            os.environ.pop("LFM_ATTN_SPLITS", None)
-        parity(got, want, what=f"splits={splits}")
+            os.environ.pop("LFM_ATTN_CHUNK", None)
+        parity(got, want, what=f"chunk={chunk}")
         outs.append(got)
     assert np.abs(outs[0] - outs[1]).max() < 1e-5
     assert np.abs(outs[0] - outs[2]).max() < 1e-5
-    del rng

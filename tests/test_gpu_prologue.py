@@ -2,7 +2,7 @@
 import numpy as np
 import pytest
 
-from helpers import f16, f16_to_f32, parity
+from helpers import f16, parity
 
 pytestmark = pytest.mark.gpu
 
@@ -97,4 +97,3 @@ def test_qkv_prologue_batched(gpu, orc):
             d = np.abs(ks[slot].reshape(-1).astype(np.int32) - wk.astype(np.int32))
             assert d.max() <= 1
             assert np.array_equal(vs[slot].reshape(-1), f16(v[s, r]).reshape(-1))
-    del f16_to_f32
