@@ -91,7 +91,7 @@ class DecodeWorkload:
             self.keys = (last - t0 + 1).astype(np.int64)
         else:
             self.keys = last + 1
-        self.max_keys = int(self.keys.max())
+        self.keys_hint = int(round(float(self.keys.mean())))  # the engine knows its positions
         self.host_k, self.host_v = [], []
         self.sets = []
         for c in range(copies):
@@ -124,11 +124,32 @@ class DecodeWorkload:
         st = self.sets[self._i % len(self.sets)]
         self._i += 1
         self.la.gqa_f16_varlen(st["q"], st["g"], True, st["kt"], st["vt"], st["pos"], st["out"],
-                               self.n_seq, self.n_rows, self.max_keys, self.nq, self.nkv, self.hd,
+                               self.n_seq, self.n_rows, self.keys_hint, self.nq, self.nkv, self.hd,
                                self.window, self.cap)
 
     def output(self, copy=0):
         return self.sets[copy]["out"].numpy()
+
+
+class PrefillWorkload:
+    """causal prefill, B sequences of N tokens, fp16 Q/K/V
+    (0.5*N(0,1), RoPE assumed applied), fp32 softmax/accumulate, fp32 out."""
+
+    def __init__(self, la, rng, n_seq=4, n_tok=4096, nq=32, nkv=8, hd=64):
+        self.la, self.n_seq, self.n_tok, self.nq, self.nkv, self.hd = la, n_seq, n_tok, nq, nkv, hd
+        self.q = la.DeviceArray.from_numpy(
+            f16(rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32) * np.float32(0.5)))
+        self.k = la.DeviceArray.from_numpy(
+            f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * np.float32(0.5)))
+        self.v = la.DeviceArray.from_numpy(
+            f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * np.float32(0.5)))
+        self.out = la.DeviceArray.zeros((n_seq, n_tok, nq, hd), np.float32)
+        # causal algorithmic FLOPs: 2 GEMMs x 2 flop x d per (row, key <= row) per head
+        self.flops = 4 * hd * nq * n_seq * n_tok * (n_tok + 1) // 2
+
+    def step(self):
+        self.la.prefill_f16(self.q, self.k, self.v, self.out, self.n_seq, self.n_tok, 0,
+                            self.n_tok * self.nkv * self.hd, self.nq, self.nkv, self.hd)
 
 
 def time_steps(hip, wl, steps, warmup):
@@ -241,6 +262,15 @@ def main():
                                    pct_hbm_peak=round(100 * wl.bytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
             del wl
 
+    pf = PrefillWorkload(la, rng)
+    pms = time_steps(hip, pf, max(5, args.steps // 5), 3)
+    pkms = time_main_kernel(hip, la, pf, max(5, args.steps // 5))
+    prefill = dict(workload="cfg4_prefill_b4_n4096_32q8kv_d64", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
+                   kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4),
+                   flops=pf.flops, pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1))
+    log(f"prefill: {pms:.3f} ms/step, {prefill['TFLOPs']} TFLOP/s")
+    del pf
+
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -272,6 +302,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_splitkv<64,1>", "kernel_us": round(k_ms * 1e3, 2)},
+        "prefill": prefill,
         "cpu_baseline": cpu,
         "parity_vs_cpu": parity,
         "secondary": secondary,

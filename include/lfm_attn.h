@@ -160,15 +160,30 @@ int lfm_hip_lfm3_online_gqa_f16_dispatch(const float *q_batch, const float *gate
  *   values are used as-is otherwise.
  * k_seq, v_seq: DEVICE arrays of n_seq DEVICE cache pointers; pos_0: DEVICE
  *   uint32_t[n_seq].
- * max_keys_hint: upper bound of keys any row attends (sizes the key split;
- *   0 = unknown).  Correctness does not depend on it.
+ * keys_hint: typical (mean) number of keys a row attends; it only sizes the
+ *   key split (0 = unknown).  Correctness does not depend on it.
  * scale: multiplies q.k (1/sqrtf(head_dim) in every reference caller). */
 int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
                            const uint16_t *const *k_seq, const uint16_t *const *v_seq,
                            const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
-                           uint32_t max_keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                           uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
                            uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
                            lfm_attn_stream_t stream);
+
+/* Causal prefill on MFMA -- the prompt path of lfm2_prefill_prompt /
+ * lfm2_forward_batch (tools/lfm2_prefill_batch.c:1129-1199), whose attention
+ * runs lfm2_gqa_heads_worker_task once per row (:1029-1092).  Row i of
+ * sequence s is position pos_0 + i and attends keys [0, pos_0 + i] of that
+ * sequence's cache, which must already hold rows 0 .. pos_0 + n_tok - 1.
+ * q:   [n_seq][n_tok][n_head_q][head_dim] fp16 (RoPE applied).
+ * k,v: sequence s at k + s * kv_seq_stride elements, [slot][n_head_kv][head_dim].
+ * out: [n_seq][n_tok][n_head_q][head_dim] float.
+ * head_dim 64 (MFMA kernel); other head dims return LFM_ATTN_E_UNSUPPORTED.
+ * Softmax and accumulation are fp32; P enters the P.V product as fp16. */
+int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+                        uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
+                        uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
+                        lfm_attn_stream_t stream);
 
 #ifdef __cplusplus
 }

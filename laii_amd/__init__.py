@@ -13,6 +13,7 @@ from .attention import (  # noqa: F401
     lfm3_online_gqa_f16_dispatch,
     online_gqa_f16,
     pointer_table,
+    prefill_f16,
     qk_norm_rope,
     qkv_prologue,
     require_gpu,

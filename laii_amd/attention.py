@@ -177,15 +177,27 @@ def lfm3_online_gqa_f16_dispatch(q_batch: Ptr, gate_sig: Ptr, k_cache_f16: Ptr, 
 
 
 def gqa_f16_varlen(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr,
-                   out: Ptr, n_seq: int, n_rows: int, max_keys_hint: int, n_head_q: int,
+                   out: Ptr, n_seq: int, n_rows: int, keys_hint: int, n_head_q: int,
                    n_head_kv: int, head_dim: int, window_len: int = 0, cap: int = 0,
                    scale: Optional[float] = None, stream=None) -> None:
     if scale is None:
         scale = float(1.0 / np.sqrt(np.float32(head_dim)))
     check(load().lfm_hip_gqa_f16_varlen(_p(q), _p(gate), int(bool(gate_is_logit)), _p(k_seq),
                                         _p(v_seq), _p(pos_0), _p(out), n_seq, n_rows,
-                                        max_keys_hint, n_head_q, n_head_kv, head_dim, window_len,
+                                        keys_hint, n_head_q, n_head_kv, head_dim, window_len,
                                         cap, scale, stream), "lfm_hip_gqa_f16_varlen")
+
+
+def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0: int,
+                kv_seq_stride: int, n_head_q: int, n_head_kv: int, head_dim: int,
+                scale: Optional[float] = None, stream=None) -> None:
+    """Causal prefill: row i of each sequence (position pos_0 + i) attends
+    keys [0, pos_0 + i] (tools/lfm2_prefill_batch.c:1029-1092)."""
+    if scale is None:
+        scale = float(1.0 / np.sqrt(np.float32(head_dim)))
+    check(load().lfm_hip_prefill_f16(_p(q), _p(k), _p(v), _p(out), n_seq, n_tok, pos_0,
+                                     kv_seq_stride, n_head_q, n_head_kv, head_dim, scale, stream),
+          "lfm_hip_prefill_f16")
 
 
 def pointer_table(arrays: Sequence[Union["DeviceArray", int]]) -> DeviceArray:

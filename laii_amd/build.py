@@ -22,7 +22,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["shim.hip", "decode_splitkv.hip", "generic.hip", "prologue.hip"]
+HIP_SOURCES = ["shim.hip", "decode_splitkv.hip", "generic.hip", "prologue.hip", "prefill_fa.hip"]
 C_SOURCES = ["lfm_attn_host.c"]
 
 HIP_FLAGS = [

@@ -73,25 +73,40 @@ __device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+/* LDS ordering between the lanes of one wave: each wave owns its V^T tile,
+ * so no workgroup barrier is needed; wait for this wave's LDS traffic and
+ * keep the compiler from moving LDS accesses across this point. */
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f); /* lgkmcnt(0) */
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float gate_value(const float *gate, size_t idx, int is_logit) {
     if (!gate) return 1.0f;
     const float g = gate[idx];
     return is_logit ? 1.0f / (1.0f + expf(-g)) : g;
 }
 
-template <int HD, int NT>
-__global__ __launch_bounds__(64) void k_splitkv(const SplitParams P) {
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
     constexpr int NS  = HD / 32; /* MFMA k-steps of Q.K^T (32 dims each)          */
     constexpr int NM  = HD / 16; /* 16-dim tiles of O^T                            */
     constexpr int NVL = HD / 16; /* 16-byte V pieces per lane per 32-key sub-tile  */
     constexpr int CH  = HD / 8;  /* 16-byte chunks per V row                       */
     constexpr int QPP = 64 / CH; /* 4-key quads covered by one pass of 64 lanes    */
-    __shared__ __attribute__((aligned(16))) uint16_t vt[HD * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
 
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int l16  = lane & 15;
     const int g    = lane >> 4;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+    /* the W waves of a workgroup take W adjacent KV heads over the same key
+     * chunk, so each workgroup streams contiguous runs of the cache rows */
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y * W + (uint32_t)wave, s = blockIdx.z;
+    if (kvh >= P.n_head_kv) return; /* waves only synchronise with themselves */
+    uint16_t *vt = vt_all[wave];
 
     const uint32_t pos0  = P.pos0_dev ? P.pos0_dev[s] : P.pos0_host;
     const uint32_t last  = pos0 + P.n_rows - 1u;
@@ -197,7 +212,7 @@ __global__ __launch_bounds__(64) void k_splitkv(const SplitParams P) {
 
     /* one 32-key sub-tile: V^T to LDS, S^T, online softmax, O^T update */
     auto process = [&](uint32_t p0, const u32x4_t (&kcur)[2][NS], const u32x4_t (&vcur)[NVL]) {
-        __syncthreads(); /* previous sub-tile's V^T reads are done */
+        wave_lds_sync(); /* previous sub-tile's V^T reads are done */
 #pragma unroll
         for (int ps = 0; ps < HD / 64; ++ps) {
             const int quad = ps * QPP + lane / CH;
@@ -273,7 +288,7 @@ __global__ __launch_bounds__(64) void k_splitkv(const SplitParams P) {
             for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
         }
 
-        __syncthreads(); /* V^T of this sub-tile is in LDS */
+        wave_lds_sync(); /* V^T of this sub-tile is in LDS */
         /* O^T += V^T . P^T */
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) {
@@ -341,58 +356,123 @@ __global__ __launch_bounds__(64) void k_splitkv(const SplitParams P) {
     }
 }
 
-/* Log-sum-exp merge of the key splits of one (sequence, KV head, column);
- * applies 1/l and the gate.  One thread per output dim. */
+/* Log-sum-exp merge of the key splits; applies 1/l and the gate.
+ * SG adjacent lanes share one (pair, column, 4 output dims): each reduces the
+ * splits sg, sg+SG, ... with a running max, then the SG partial results are
+ * combined through lane shuffles and lane sg == 0 writes the output. */
 template <int HD>
-__global__ __launch_bounds__(HD) void k_merge(const SplitParams P) {
-    const uint32_t n = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
-    const uint32_t d = threadIdx.x;
-    const size_t base = (size_t)(s * P.n_head_kv + kvh) * P.n_splits * P.ncols + n;
-    float M = kNegBig;
-    for (uint32_t sp = 0; sp < P.n_splits; ++sp) {
-        const float2 ml = P.part_ml[base + (size_t)sp * P.ncols];
-        if (ml.y > 0.0f) M = fmaxf(M, ml.x);
-    }
-    float L = 0.0f, O = 0.0f;
-    for (uint32_t sp = 0; sp < P.n_splits; ++sp) {
-        const size_t idx = base + (size_t)sp * P.ncols;
-        const float2 ml  = P.part_ml[idx];
-        if (ml.y > 0.0f) {
-            const float w = __builtin_amdgcn_exp2f(ml.x - M);
-            L += ml.y * w;
-            O += P.part_o[idx * HD + d] * w;
+__global__ __launch_bounds__(256) void k_merge(const SplitParams P, uint32_t n_items, uint32_t SG) {
+    constexpr uint32_t D4 = HD / 4;
+    const uint32_t t    = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t sg   = t % SG;
+    const uint32_t item = t / SG;
+    const bool live     = item < n_items;
+    const uint32_t d4   = item % D4;
+    const uint32_t rest = item / D4;
+    const uint32_t n    = rest % P.ncols;
+    const uint32_t pair = live ? rest / P.ncols : 0u; /* s * n_head_kv + kvh */
+    const size_t base   = (size_t)pair * P.n_splits * P.ncols + n;
+    float M = kNegBig, L = 0.0f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
+#pragma unroll 4
+        for (uint32_t sp = sg; sp < P.n_splits; sp += SG) {
+            const size_t idx = base + (size_t)sp * P.ncols;
+            const float2 ml  = P.part_ml[idx];
+            const float4 o   = *reinterpret_cast<const float4 *>(P.part_o + idx * HD + 4 * d4);
+            if (ml.y > 0.0f) {
+                const float Mn = fmaxf(M, ml.x);
+                const float a  = __builtin_amdgcn_exp2f(M - Mn);
+                const float b  = __builtin_amdgcn_exp2f(ml.x - Mn);
+                L   = L * a + ml.y * b;
+                O.x = O.x * a + o.x * b;
+                O.y = O.y * a + o.y * b;
+                O.z = O.z * a + o.z * b;
+                O.w = O.w * a + o.w * b;
+                M   = Mn;
+            }
         }
     }
+    for (uint32_t off = 1; off < SG; off <<= 1) {
+        const float M2 = __shfl_xor(M, (int)off), L2 = __shfl_xor(L, (int)off);
+        const float x2 = __shfl_xor(O.x, (int)off), y2 = __shfl_xor(O.y, (int)off);
+        const float z2 = __shfl_xor(O.z, (int)off), w2 = __shfl_xor(O.w, (int)off);
+        const float Mn = fmaxf(M, M2);
+        const float a  = __builtin_amdgcn_exp2f(M - Mn), b = __builtin_amdgcn_exp2f(M2 - Mn);
+        L   = L * a + L2 * b;
+        O.x = O.x * a + x2 * b;
+        O.y = O.y * a + y2 * b;
+        O.z = O.z * a + z2 * b;
+        O.w = O.w * a + w2 * b;
+        M   = Mn;
+    }
+    if (!live || sg != 0u) return;
+    const uint32_t s  = pair / P.n_head_kv, kvh = pair % P.n_head_kv;
     const uint32_t r  = n / P.kv_mul;
     const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
     const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
     const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
-    if (d < P.out_dims) P.out[orow * HD + d] = O * ((L > 0.0f) ? gv / L : 0.0f);
+    const float inv   = (L > 0.0f) ? gv / L : 0.0f;
+    const uint32_t d  = 4 * d4;
+    if (d < P.out_dims)
+        *reinterpret_cast<float4 *>(P.out + orow * HD + d) = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+}
+
+template <int HD, int NT, int W>
+hipError_t launch_hd_nt_w(const SplitParams &p, uint32_t n_seq, hipStream_t stream) {
+    dim3 grid(p.n_splits, (p.n_head_kv + W - 1) / W, n_seq);
+    hipEvent_t ev0, ev1;
+    profile_events(&ev0, &ev1);
+    if (ev0) (void)hipEventRecord(ev0, stream);
+    hipLaunchKernelGGL((k_splitkv<HD, NT, W>), grid, dim3(64 * W), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (ev1) (void)hipEventRecord(ev1, stream);
+    if (e != hipSuccess || p.n_splits == 1u) return e;
+    const uint32_t n_items = n_seq * p.n_head_kv * p.ncols * (HD / 4);
+    uint32_t sg = 1;
+    while (sg < 16u && sg * 4u < p.n_splits) sg <<= 1; /* ~4 splits per lane */
+    const uint64_t threads = (uint64_t)n_items * sg;
+    hipLaunchKernelGGL((k_merge<HD>), dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, stream, p,
+                       n_items, sg);
+    return hipGetLastError();
+}
+
+/* Waves per workgroup: W adjacent KV heads over one key chunk.  Measured on
+ * MI355X: all KV heads of a row together (W = n_head_kv, up to 8) for
+ * head_dim 64; W = 2 for head_dim 128, whose waves are register-heavy.
+ * LFM_ATTN_WAVES overrides (tuning). */
+uint32_t choose_waves(uint32_t n_head_kv, uint32_t head_dim) {
+    uint32_t w = head_dim == 64u ? 8u : 2u;
+    const char *env = getenv("LFM_ATTN_WAVES");
+    if (env && atoi(env) > 0) w = (uint32_t)atoi(env);
+    while (w > 1u && w > n_head_kv) w >>= 1;
+    return w >= 8u ? 8u : (w >= 4u ? 4u : (w >= 2u ? 2u : 1u));
 }
 
 template <int HD, int NT>
 hipError_t launch_hd_nt(const SplitParams &p, uint32_t n_seq, hipStream_t stream) {
-    dim3 grid(p.n_splits, p.n_head_kv, n_seq);
-    hipEvent_t ev0, ev1;
-    profile_events(&ev0, &ev1);
-    if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv<HD, NT>), grid, dim3(64), 0, stream, p);
-    hipError_t e = hipGetLastError();
-    if (ev1) (void)hipEventRecord(ev1, stream);
-    if (e != hipSuccess || p.n_splits == 1u) return e;
-    hipLaunchKernelGGL((k_merge<HD>), dim3(p.ncols, p.n_head_kv, n_seq), dim3(HD), 0, stream, p);
-    return hipGetLastError();
+    const uint32_t w = choose_waves(p.n_head_kv, HD);
+    if (w == 8u) return launch_hd_nt_w<HD, NT, 8>(p, n_seq, stream);
+    if (w == 4u) return launch_hd_nt_w<HD, NT, 4>(p, n_seq, stream);
+    if (w == 2u) return launch_hd_nt_w<HD, NT, 2>(p, n_seq, stream);
+    return launch_hd_nt_w<HD, NT, 1>(p, n_seq, stream);
 }
 
-/* Key chunk per workgroup (multiple of 32) and the number of chunks the grid
- * covers.  Aim for enough one-wave workgroups to keep ~12 waves per CU busy. */
-void choose_split(const AttnBatch &b, uint32_t max_keys_hint, uint32_t *n_splits, uint32_t *chunk) {
-    uint32_t keys = max_keys_hint;
+/* Key chunk per wave (multiple of 32) and the number of chunks the grid
+ * covers.  Each wave keeps one 32-key sub-tile in flight, so throughput
+ * follows the number of waves; about 4096 waves over the batch measured best
+ * on MI355X (two residency rounds).  Chunks stay >= 16 x the query columns so
+ * the split partials remain a small fraction of the KV bytes.
+ * keys_hint is the typical number of keys per row; LFM_ATTN_CHUNK overrides. */
+void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, uint32_t *chunk) {
+    uint32_t keys = keys_hint;
     if (keys == 0u) keys = b.window ? b.window + b.n_rows - 1u : 4096u;
     const uint64_t pairs  = (uint64_t)b.n_seq * b.n_head_kv;
-    const uint64_t target = 4096; /* workgroups */
+    const uint64_t ncols  = (uint64_t)b.n_rows * (b.n_head_q / b.n_head_kv);
+    const uint64_t target = 4096; /* waves */
     uint64_t c = ((uint64_t)keys * pairs + target - 1) / target;
-    if (c < 128) c = 128; /* >= 4 sub-tiles per workgroup */
+    if (c < 64) c = 64;
+    if (c < 16 * ncols) c = 16 * ncols;
     const char *env = getenv("LFM_ATTN_CHUNK");
     if (env && atoi(env) > 0) c = (uint64_t)atoi(env);
     c = (c + 31) & ~(uint64_t)31;
@@ -412,7 +492,7 @@ bool splitkv_supports(const AttnBatch &b) {
     return ncols <= 32u;
 }
 
-int launch_splitkv(const AttnBatch &b, uint32_t max_keys_hint, hipStream_t stream) {
+int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
     if (!splitkv_supports(b)) return LFM_ATTN_E_UNSUPPORTED;
     SplitParams p{};
     p.q             = b.q;
@@ -435,7 +515,7 @@ int launch_splitkv(const AttnBatch &b, uint32_t max_keys_hint, hipStream_t strea
     p.cap           = b.cap;
     p.out_dims      = b.out_dims;
     p.qscale        = b.scale * kLog2e;
-    choose_split(b, max_keys_hint, &p.n_splits, &p.chunk);
+    choose_split(b, keys_hint, &p.n_splits, &p.chunk);
     if (p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
         const size_t bytes  = n_part * b.head_dim * sizeof(float) + n_part * sizeof(float2) + 256;

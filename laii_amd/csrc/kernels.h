@@ -39,12 +39,19 @@ void *workspace(size_t bytes, hipStream_t stream, int *status);
 /* Split-KV MFMA kernel for fp16 caches, head_dim 64 or 128, up to 64 query
  * columns (n_rows * kv_mul) per KV head.  Returns LFM_ATTN_E_UNSUPPORTED for
  * other shapes (the caller then uses the generic kernel). */
-int launch_splitkv(const AttnBatch &b, uint32_t max_keys_hint, hipStream_t stream);
+int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream);
 bool splitkv_supports(const AttnBatch &b);
 
 /* Generic one-wave-per-head kernel (any head_dim % 8 == 0, <= 256), fp16 or
  * fp32 caches; follows the reference's per-key recurrence. */
 int launch_generic(const AttnBatch &b, bool kv_f32, hipStream_t stream);
+
+/* Causal MFMA prefill (fp16 Q/K/V, fp32 out). */
+bool prefill_supports(uint32_t head_dim, uint32_t kv_mul);
+int launch_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+                   uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
+                   uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
+                   hipStream_t stream);
 
 /* Prologue kernels. */
 int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,

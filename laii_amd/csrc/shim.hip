@@ -71,10 +71,10 @@ using lfm::AttnBatch;
 static inline hipStream_t to_stream(lfm_attn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0u; }
 
-static int dispatch_f16(const AttnBatch &b, uint32_t max_keys, hipStream_t stream) {
+static int dispatch_f16(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
     const bool fast = lfm::splitkv_supports(b) && aligned16(b.q) && aligned16(b.out) &&
                       (b.k_seq || (aligned16(b.k_base) && aligned16(b.v_base)));
-    if (fast) return lfm::launch_splitkv(b, max_keys, stream);
+    if (fast) return lfm::launch_splitkv(b, keys_hint, stream);
     return lfm::launch_generic(b, false, stream);
 }
 
@@ -290,7 +290,7 @@ int lfm_hip_lfm3_online_gqa_f16_dispatch(const float *q_batch, const float *gate
 int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
                            const uint16_t *const *k_seq, const uint16_t *const *v_seq,
                            const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
-                           uint32_t max_keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                           uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
                            uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
                            lfm_attn_stream_t stream) {
     if (!q || !k_seq || !v_seq || !pos_0 || !out) return LFM_ATTN_E_INVALID;
@@ -317,7 +317,26 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
     b.window = window_len;
     b.cap = cap;
     b.scale = scale;
-    return dispatch_f16(b, max_keys_hint, to_stream(stream));
+    return dispatch_f16(b, keys_hint, to_stream(stream));
+}
+
+int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+                        uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
+                        uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
+                        lfm_attn_stream_t stream) {
+    if (!q || !k || !v || !out) return LFM_ATTN_E_INVALID;
+    if (n_seq == 0u || n_tok == 0u || n_head_q == 0u || n_head_kv == 0u ||
+        n_head_q % n_head_kv != 0u)
+        return LFM_ATTN_E_INVALID;
+    if (n_seq > 65535u || n_head_kv > 65535u) return LFM_ATTN_E_INVALID;
+    if ((uint64_t)pos_0 + n_tok > 0x7FFFFFFFull) return LFM_ATTN_E_RANGE;
+    if (n_seq > 1u && kv_seq_stride < ((uint64_t)pos_0 + n_tok) * n_head_kv * head_dim)
+        return LFM_ATTN_E_INVALID; /* sequences would overlap */
+    if (!lfm::prefill_supports(head_dim, n_head_q / n_head_kv)) return LFM_ATTN_E_UNSUPPORTED;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (kv_seq_stride % 8u))
+        return LFM_ATTN_E_INVALID;
+    return lfm::launch_prefill(q, k, v, out, n_seq, n_tok, pos_0, kv_seq_stride, n_head_q,
+                               n_head_kv, head_dim, scale, to_stream(stream));
 }
 
 } /* extern "C" */
