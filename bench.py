@@ -28,6 +28,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, datasheet
+# HBM bytes per launch of the headline kernel from two rocprofv3 PMC passes
+# (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, factors from a 2 GiB read/copy
+# kernel); profiles/k_splitkv_decode_b64_ctx8192_pmc.md
+HEADLINE_TRAFFIC_BYTES = 1082510000
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, datasheet
 
 
@@ -91,7 +95,7 @@ class DecodeWorkload:
             self.keys = (last - t0 + 1).astype(np.int64)
         else:
             self.keys = last + 1
-        self.keys_hint = int(round(float(self.keys.mean())))  # the engine knows its positions
+        self.keys_hint = int(self.keys.max())  # upper bound of keys per row (sizes the grid)
         self.host_k, self.host_v = [], []
         self.sets = []
         for c in range(copies):
@@ -300,7 +304,8 @@ def main():
                    "algorithmic_bytes": head.bytes},
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": HEADLINE_TRAFFIC_BYTES,
                      "kernel": "k_splitkv<64,1>", "kernel_us": round(k_ms * 1e3, 2)},
         "prefill": prefill,
         "cpu_baseline": cpu,

@@ -160,8 +160,9 @@ int lfm_hip_lfm3_online_gqa_f16_dispatch(const float *q_batch, const float *gate
  *   values are used as-is otherwise.
  * k_seq, v_seq: DEVICE arrays of n_seq DEVICE cache pointers; pos_0: DEVICE
  *   uint32_t[n_seq].
- * keys_hint: typical (mean) number of keys a row attends; it only sizes the
- *   key split (0 = unknown).  Correctness does not depend on it.
+ * keys_hint: upper bound of the keys a row attends (the engine knows its
+ *   positions); it sizes the key split (0 = unknown).  Rows attending more
+ *   keys are still handled correctly, with longer chunks.
  * scale: multiplies q.k (1/sqrtf(head_dim) in every reference caller). */
 int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
                            const uint16_t *const *k_seq, const uint16_t *const *v_seq,
@@ -184,6 +185,68 @@ int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                         uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                         lfm_attn_stream_t stream);
+
+/* ---- engine context: device-resident KV + host-pointer calls (C11) -------- */
+/* The forward stacks own their KV caches in host memory
+ * (tools/lfm2_forward.c:612-622, tools/lfm3_engine.c:1740-1769).  A GPU
+ * drop-in keeps them in HBM instead: the context owns one fp16 K and V cache
+ * per attention layer (same token-major layout), the RoPE tables and the
+ * QK-norm weights, and each call moves only Q/K/V/gate in and the attention
+ * output out.  Calls are synchronous (the output is in host memory on
+ * return), like the pool dispatch they replace; a context is not thread-safe. */
+typedef struct lfm_attn_ctx lfm_attn_ctx;
+
+typedef struct {
+    uint32_t n_layers;        /* attention layers held by the context              */
+    uint32_t n_head_q;
+    uint32_t n_head_kv;
+    uint32_t head_dim;
+    uint32_t max_seq;         /* positions (LUT rows, linear cache slots)          */
+    uint32_t sliding_window;  /* SWA window (LFM3), 0 when no layer uses one       */
+    uint32_t swa_cap;         /* ring slots of SWA layers (engine: window + 8)     */
+    const uint8_t *layer_is_swa; /* [n_layers] or NULL (no SWA layer)             */
+    float eps;                /* QK RMSNorm epsilon                                */
+    float rope_base;          /* full / LFM2 layers                                */
+    float rope_base_swa;      /* SWA layers (LFM3: 1e4)                            */
+    uint32_t rope_dim;        /* LFM3 partial RoPE (0 = head_dim)                  */
+    const float *rope_freqs;  /* LFM3 rope_freqs factors or NULL                   */
+    uint32_t n_rope_freqs;
+    int lfm3;                 /* 1: LFM3 tables (lfm3_rope_lut_init), 0: LFM2      */
+} lfm_attn_geom;
+
+int lfm_attn_ctx_create(lfm_attn_ctx **out, const lfm_attn_geom *geom);
+void lfm_attn_ctx_destroy(lfm_attn_ctx *ctx);
+/* Per-layer QK-RMSNorm weights ([head_dim] host floats, NULL = no norm). */
+int lfm_attn_ctx_set_norms(lfm_attn_ctx *ctx, uint32_t layer, const float *q_norm_w,
+                           const float *k_norm_w);
+
+/* One attention step of `layer` for B consecutive positions pos_0 .. pos_0+B-1
+ * (B = 1 decode; B <= 8 prompt chunk or speculative verify):
+ *   QK-RMSNorm + RoPE of q and k, RNE fp16 store of k and v at each position's
+ *   slot, then attention of row b over its window, times sigmoid(gate) when
+ *   gate_logits is non-NULL.
+ * Replaces steps 3-4 of lfm2_forward_gqa_fast (tools/lfm2_kernels_fast.c:1046-1066),
+ * the per-token loop of lfm2_forward_gqa_batch (tools/lfm2_prefill_batch.c:1029-1092)
+ * and the attention block of lfm3_forward_token_internal / lfm3_forward_batch_core
+ * (tools/lfm3_engine.c:1885-1896, 2006-2022).
+ * q: [B][n_head_q][head_dim], k, v: [B][n_head_kv][head_dim], gate_logits:
+ * [B][n_head_q] or NULL, out: [B][n_head_q][head_dim] -- all HOST floats.
+ * Returns LFM_ATTN_E_RANGE when pos_0 + B > max_seq. */
+int lfm_attn_ctx_forward(lfm_attn_ctx *ctx, uint32_t layer, uint32_t pos_0, uint32_t B,
+                         const float *q, const float *k, const float *v,
+                         const float *gate_logits, float *out);
+
+/* Copy `n_slots` cache rows of a layer starting at `slot` between the device
+ * cache and host memory (fp16 bits, [slot][n_head_kv][head_dim]) -- the data
+ * a checkpoint or .lfmcache file stores (tools/lfm2_moe_checkpoint.c:472-560,
+ * tools/lfm2_sys_cache.c:504-799).  Round trips are bit-exact. */
+int lfm_attn_ctx_kv_export(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uint32_t n_slots,
+                           uint16_t *k_host, uint16_t *v_host);
+int lfm_attn_ctx_kv_import(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uint32_t n_slots,
+                           const uint16_t *k_host, const uint16_t *v_host);
+/* Device address of a layer's caches (for callers that drive lfm_hip_* directly). */
+int lfm_attn_ctx_kv_device(lfm_attn_ctx *ctx, uint32_t layer, uint16_t **k_dev, uint16_t **v_dev,
+                           uint32_t *n_slots);
 
 #ifdef __cplusplus
 }

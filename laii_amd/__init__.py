@@ -7,6 +7,7 @@ host mirror: ctypes bindings named after the reference's dispatch calls.
 from ._lib import LIB_PATH, LfmAttnError, load  # noqa: F401
 from .attention import (  # noqa: F401
     DeviceArray,
+    EngineContext,
     device_count,
     gqa_f16_varlen,
     gqa_heads,

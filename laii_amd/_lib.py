@@ -51,6 +51,27 @@ SIGNATURES = {
                                       _u32, _u32, _u32, _u32, _f32, _vp]),
 }
 
+
+
+class Geom(C.Structure):
+    """lfm_attn_geom of include/lfm_attn.h."""
+    _fields_ = [("n_layers", _u32), ("n_head_q", _u32), ("n_head_kv", _u32), ("head_dim", _u32),
+                ("max_seq", _u32), ("sliding_window", _u32), ("swa_cap", _u32),
+                ("layer_is_swa", C.POINTER(C.c_uint8)), ("eps", _f32), ("rope_base", _f32),
+                ("rope_base_swa", _f32), ("rope_dim", _u32), ("rope_freqs", C.POINTER(_f32)),
+                ("n_rope_freqs", _u32), ("lfm3", _int)]
+
+
+SIGNATURES.update({
+    "lfm_attn_ctx_create": (_int, [C.POINTER(_vp), C.POINTER(Geom)]),
+    "lfm_attn_ctx_destroy": (None, [_vp]),
+    "lfm_attn_ctx_set_norms": (_int, [_vp, _u32, _vp, _vp]),
+    "lfm_attn_ctx_forward": (_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _vp]),
+    "lfm_attn_ctx_kv_export": (_int, [_vp, _u32, _u32, _u32, _vp, _vp]),
+    "lfm_attn_ctx_kv_import": (_int, [_vp, _u32, _u32, _u32, _vp, _vp]),
+    "lfm_attn_ctx_kv_device": (_int, [_vp, _u32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_u32)]),
+})
+
 _lock = threading.Lock()
 _lib = None
 

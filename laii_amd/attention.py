@@ -19,7 +19,7 @@ from typing import Optional, Sequence, Union
 
 import numpy as np
 
-from ._lib import check, load
+from ._lib import Geom, check, load
 
 Ptr = Union["DeviceArray", int, None]
 
@@ -203,3 +203,77 @@ def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0:
 def pointer_table(arrays: Sequence[Union["DeviceArray", int]]) -> DeviceArray:
     """Device array of device pointers (the k_seq / v_seq arguments)."""
     return DeviceArray.from_numpy(np.array([int(a) for a in arrays], dtype=np.uint64))
+
+
+class EngineContext:
+    """Device-resident KV + RoPE tables for the attention layers of one model
+    (lfm_attn_ctx of include/lfm_attn.h).  forward() is the per-layer
+    attention step of the forward stacks with host arrays in and out."""
+
+    def __init__(self, n_layers, n_head_q, n_head_kv, head_dim, max_seq, eps=1e-5,
+                 rope_base=1e6, lfm3=False, sliding_window=0, swa_cap=0, layer_is_swa=None,
+                 rope_base_swa=1e4, rope_dim=0, rope_freqs=None):
+        self._keep = []
+        g = Geom()
+        g.n_layers, g.n_head_q, g.n_head_kv, g.head_dim = n_layers, n_head_q, n_head_kv, head_dim
+        g.max_seq, g.sliding_window, g.swa_cap = max_seq, sliding_window, swa_cap
+        if layer_is_swa is not None:
+            arr = (C.c_uint8 * n_layers)(*[1 if x else 0 for x in layer_is_swa])
+            self._keep.append(arr)
+            g.layer_is_swa = C.cast(arr, C.POINTER(C.c_uint8))
+        g.eps, g.rope_base, g.rope_base_swa, g.rope_dim = eps, rope_base, rope_base_swa, rope_dim
+        if rope_freqs is not None:
+            rf = np.ascontiguousarray(rope_freqs, np.float32)
+            self._keep.append(rf)
+            g.rope_freqs = rf.ctypes.data_as(C.POINTER(C.c_float))
+            g.n_rope_freqs = rf.size
+        g.lfm3 = 1 if lfm3 else 0
+        self.n_head_q, self.n_head_kv, self.head_dim = n_head_q, n_head_kv, head_dim
+        h = C.c_void_p()
+        check(load().lfm_attn_ctx_create(C.byref(h), C.byref(g)), "lfm_attn_ctx_create")
+        self.h = h.value
+
+    def set_norms(self, layer, q_norm_w, k_norm_w):
+        qn = None if q_norm_w is None else np.ascontiguousarray(q_norm_w, np.float32)
+        kn = None if k_norm_w is None else np.ascontiguousarray(k_norm_w, np.float32)
+        check(load().lfm_attn_ctx_set_norms(self.h, layer, None if qn is None else qn.ctypes.data,
+                                            None if kn is None else kn.ctypes.data),
+              "lfm_attn_ctx_set_norms")
+
+    def forward(self, layer, pos_0, q, k, v, gate_logits=None):
+        q = np.ascontiguousarray(q, np.float32)
+        B = q.size // (self.n_head_q * self.head_dim)
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        g = None if gate_logits is None else np.ascontiguousarray(gate_logits, np.float32)
+        out = np.empty(B * self.n_head_q * self.head_dim, np.float32)
+        check(load().lfm_attn_ctx_forward(self.h, layer, pos_0, B, q.ctypes.data, k.ctypes.data,
+                                          v.ctypes.data, None if g is None else g.ctypes.data,
+                                          out.ctypes.data), "lfm_attn_ctx_forward")
+        return out
+
+    def kv_export(self, layer, slot, n_slots):
+        row = self.n_head_kv * self.head_dim
+        kh = np.empty((n_slots, row), np.uint16)
+        vh = np.empty((n_slots, row), np.uint16)
+        check(load().lfm_attn_ctx_kv_export(self.h, layer, slot, n_slots, kh.ctypes.data,
+                                            vh.ctypes.data), "lfm_attn_ctx_kv_export")
+        return kh, vh
+
+    def kv_import(self, layer, slot, k_host, v_host):
+        kh = np.ascontiguousarray(k_host, np.uint16)
+        vh = np.ascontiguousarray(v_host, np.uint16)
+        n = kh.size // (self.n_head_kv * self.head_dim)
+        check(load().lfm_attn_ctx_kv_import(self.h, layer, slot, n, kh.ctypes.data,
+                                            vh.ctypes.data), "lfm_attn_ctx_kv_import")
+
+    def close(self):
+        if getattr(self, "h", None):
+            load().lfm_attn_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -23,7 +23,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["shim.hip", "decode_splitkv.hip", "generic.hip", "prologue.hip", "prefill_fa.hip"]
-C_SOURCES = ["lfm_attn_host.c"]
+C_SOURCES = ["lfm_attn_host.c", "lfm_attn_ctx.c"]
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall",
@@ -31,7 +31,8 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{CSRC}", f"-I{INCLUDE}",
 ]
-C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", f"-I{CSRC}", f"-I{INCLUDE}"]
+C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+           f"-I{ROCM}/include", f"-I{CSRC}", f"-I{INCLUDE}"]
 
 
 def _run(cmd, verbose):

@@ -463,7 +463,7 @@ hipError_t launch_hd_nt(const SplitParams &p, uint32_t n_seq, hipStream_t stream
  * follows the number of waves; about 4096 waves over the batch measured best
  * on MI355X (two residency rounds).  Chunks stay >= 16 x the query columns so
  * the split partials remain a small fraction of the KV bytes.
- * keys_hint is the typical number of keys per row; LFM_ATTN_CHUNK overrides. */
+ * keys_hint bounds the keys per row; LFM_ATTN_CHUNK overrides. */
 void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, uint32_t *chunk) {
     uint32_t keys = keys_hint;
     if (keys == 0u) keys = b.window ? b.window + b.n_rows - 1u : 4096u;

@@ -1,0 +1,281 @@
+/*
+ * lfm_attn_ctx.c -- C11 engine context: device-resident KV caches, RoPE
+ * tables and QK-norm weights per attention layer, and the host-pointer
+ * attention step the forward stacks call (include/lfm_attn.h).
+ *
+ * Each step stages q | k | v | gate | position in one pinned host buffer,
+ * moves it with a single host-to-device copy, runs the batched prologue
+ * (QK-RMSNorm + RoPE, RNE fp16 K/V store at the position's slot) and the
+ * attention kernel, and returns the output with a single device-to-host copy,
+ * all on the context's stream.
+ */
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "lfm_attn.h"
+
+#define LFM_CTX_MAX_ROWS 8u /* LFM2_MAX_BATCH, tools/lfm2_prefill_batch.c:88 */
+
+struct lfm_attn_ctx {
+    lfm_attn_geom g;
+    uint8_t *is_swa;      /* [n_layers] */
+    uint32_t *slots;      /* [n_layers] cache rows */
+    uint16_t **k_cache;   /* [n_layers] device */
+    uint16_t **v_cache;
+    float **q_norm;       /* [n_layers] device or NULL */
+    float **k_norm;
+    uint16_t **tables;    /* device: [n_layers][2] {k_cache, v_cache} pointer pairs */
+    float *cos_full, *sin_full, *cos_swa, *sin_swa; /* device LUTs [max_seq][hd/2] */
+    unsigned char *stage_host;  /* pinned: q | k | v | gate | pos | out */
+    unsigned char *stage_dev;
+    size_t off_k, off_v, off_g, off_pos, off_out, stage_in_bytes, out_bytes;
+    hipStream_t stream;
+};
+
+static int st_of(hipError_t e) {
+    if (e == hipSuccess) return LFM_ATTN_OK;
+    return e == hipErrorOutOfMemory ? LFM_ATTN_E_NOMEM : LFM_ATTN_E_DEVICE;
+}
+
+static size_t align256(size_t x) { return (x + 255u) & ~(size_t)255u; }
+
+void lfm_attn_ctx_destroy(lfm_attn_ctx *c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (uint32_t l = 0; c->k_cache && l < c->g.n_layers; ++l) {
+        (void)hipFree(c->k_cache[l]);
+        (void)hipFree(c->v_cache[l]);
+        if (c->q_norm) (void)hipFree(c->q_norm[l]);
+        if (c->k_norm) (void)hipFree(c->k_norm[l]);
+    }
+    (void)hipFree(c->tables);
+    (void)hipFree(c->cos_full);
+    (void)hipFree(c->sin_full);
+    (void)hipFree(c->cos_swa);
+    (void)hipFree(c->sin_swa);
+    (void)hipFree(c->stage_dev);
+    if (c->stage_host) (void)hipHostFree(c->stage_host);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    free(c->is_swa);
+    free(c->slots);
+    free(c->k_cache);
+    free(c->v_cache);
+    free(c->q_norm);
+    free(c->k_norm);
+    free(c);
+}
+
+/* Build a RoPE table on the host (bit-identical to the reference builders)
+ * and upload it. */
+static int upload_lut(lfm_attn_ctx *c, int swa, float **cos_d, float **sin_d) {
+    const lfm_attn_geom *g = &c->g;
+    const size_t n = (size_t)g->max_seq * (g->head_dim / 2u);
+    float *hc = (float *)malloc(n * sizeof(float));
+    float *hs = (float *)malloc(n * sizeof(float));
+    int st = (hc && hs) ? LFM_ATTN_OK : LFM_ATTN_E_NOMEM;
+    if (st == LFM_ATTN_OK) {
+        if (!g->lfm3)
+            st = lfm_attn_rope_lut_lfm2(hc, hs, g->max_seq, g->head_dim, g->rope_base);
+        else if (swa) /* tools/lfm3_engine.c:1720-1723: full rotation, no rope_freqs */
+            st = lfm_attn_rope_lut_lfm3(hc, hs, g->max_seq, g->head_dim, g->head_dim,
+                                        g->rope_base_swa, NULL, 0);
+        else
+            st = lfm_attn_rope_lut_lfm3(hc, hs, g->max_seq, g->head_dim, g->rope_dim,
+                                        g->rope_base, g->rope_freqs, g->n_rope_freqs);
+    }
+    if (st == LFM_ATTN_OK) st = st_of(hipMalloc((void **)cos_d, n * sizeof(float)));
+    if (st == LFM_ATTN_OK) st = st_of(hipMalloc((void **)sin_d, n * sizeof(float)));
+    if (st == LFM_ATTN_OK) st = st_of(hipMemcpy(*cos_d, hc, n * sizeof(float), hipMemcpyHostToDevice));
+    if (st == LFM_ATTN_OK) st = st_of(hipMemcpy(*sin_d, hs, n * sizeof(float), hipMemcpyHostToDevice));
+    free(hc);
+    free(hs);
+    return st;
+}
+
+int lfm_attn_ctx_create(lfm_attn_ctx **out, const lfm_attn_geom *geom) {
+    if (!out || !geom) return LFM_ATTN_E_INVALID;
+    *out = NULL;
+    const lfm_attn_geom *g = geom;
+    if (g->n_layers == 0u || g->n_head_q == 0u || g->n_head_kv == 0u ||
+        g->n_head_q % g->n_head_kv != 0u || g->head_dim == 0u || g->head_dim % 8u != 0u ||
+        g->head_dim > 256u || g->max_seq == 0u || g->max_seq >= 0x7FFFFFFFu)
+        return LFM_ATTN_E_INVALID;
+    int any_swa = 0;
+    for (uint32_t l = 0; g->layer_is_swa && l < g->n_layers; ++l) any_swa |= g->layer_is_swa[l] != 0;
+    if (any_swa && (g->sliding_window == 0u || g->swa_cap < g->sliding_window)) return LFM_ATTN_E_INVALID;
+
+    lfm_attn_ctx *c = (lfm_attn_ctx *)calloc(1, sizeof *c);
+    if (!c) return LFM_ATTN_E_NOMEM;
+    c->g = *g;
+    c->g.layer_is_swa = NULL;
+    c->g.rope_freqs = NULL; /* only used while building the table below */
+    const uint32_t L = g->n_layers;
+    c->is_swa  = (uint8_t *)calloc(L, 1);
+    c->slots   = (uint32_t *)calloc(L, sizeof(uint32_t));
+    c->k_cache = (uint16_t **)calloc(L, sizeof(uint16_t *));
+    c->v_cache = (uint16_t **)calloc(L, sizeof(uint16_t *));
+    c->q_norm  = (float **)calloc(L, sizeof(float *));
+    c->k_norm  = (float **)calloc(L, sizeof(float *));
+    int st = (c->is_swa && c->slots && c->k_cache && c->v_cache && c->q_norm && c->k_norm)
+                 ? LFM_ATTN_OK : LFM_ATTN_E_NOMEM;
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamCreate(&c->stream));
+    const size_t kv_dim = (size_t)g->n_head_kv * g->head_dim;
+    uint16_t **host_tables = (uint16_t **)calloc(2u * L, sizeof(uint16_t *));
+    if (!host_tables && st == LFM_ATTN_OK) st = LFM_ATTN_E_NOMEM;
+    for (uint32_t l = 0; st == LFM_ATTN_OK && l < L; ++l) {
+        c->is_swa[l] = (g->layer_is_swa && g->layer_is_swa[l]) ? 1u : 0u;
+        c->slots[l]  = c->is_swa[l] ? g->swa_cap : g->max_seq;
+        const size_t bytes = (size_t)c->slots[l] * kv_dim * sizeof(uint16_t);
+        st = st_of(hipMalloc((void **)&c->k_cache[l], bytes));
+        if (st == LFM_ATTN_OK) st = st_of(hipMalloc((void **)&c->v_cache[l], bytes));
+        if (st == LFM_ATTN_OK) st = st_of(hipMemset(c->k_cache[l], 0, bytes));
+        if (st == LFM_ATTN_OK) st = st_of(hipMemset(c->v_cache[l], 0, bytes));
+        host_tables[2u * l]      = c->k_cache[l];
+        host_tables[2u * l + 1u] = c->v_cache[l];
+    }
+    if (st == LFM_ATTN_OK) st = st_of(hipMalloc((void **)&c->tables, 2u * L * sizeof(uint16_t *)));
+    if (st == LFM_ATTN_OK)
+        st = st_of(hipMemcpy(c->tables, host_tables, 2u * L * sizeof(uint16_t *), hipMemcpyHostToDevice));
+    free(host_tables);
+    if (st == LFM_ATTN_OK) {
+        lfm_attn_geom full = *g; /* rope_freqs still points at the caller's factors here */
+        lfm_attn_geom saved = c->g;
+        c->g = full;
+        st = upload_lut(c, 0, &c->cos_full, &c->sin_full);
+        if (st == LFM_ATTN_OK && any_swa) st = upload_lut(c, 1, &c->cos_swa, &c->sin_swa);
+        c->g = saved;
+    }
+    /* staging: q | k | v | gate | pos, then out */
+    const size_t R = LFM_CTX_MAX_ROWS;
+    c->off_k          = align256(R * g->n_head_q * g->head_dim * sizeof(float));
+    c->off_v          = c->off_k + align256(R * kv_dim * sizeof(float));
+    c->off_g          = c->off_v + align256(R * kv_dim * sizeof(float));
+    c->off_pos        = c->off_g + align256(R * g->n_head_q * sizeof(float));
+    c->stage_in_bytes = c->off_pos + align256(sizeof(uint32_t));
+    c->off_out        = c->stage_in_bytes;
+    c->out_bytes      = R * g->n_head_q * g->head_dim * sizeof(float);
+    if (st == LFM_ATTN_OK)
+        st = st_of(hipHostMalloc((void **)&c->stage_host, c->off_out + c->out_bytes, hipHostMallocDefault));
+    if (st == LFM_ATTN_OK) st = st_of(hipMalloc((void **)&c->stage_dev, c->off_out + c->out_bytes));
+    if (st != LFM_ATTN_OK) {
+        lfm_attn_ctx_destroy(c);
+        return st;
+    }
+    *out = c;
+    return LFM_ATTN_OK;
+}
+
+int lfm_attn_ctx_set_norms(lfm_attn_ctx *c, uint32_t layer, const float *q_norm_w,
+                           const float *k_norm_w) {
+    if (!c || layer >= c->g.n_layers) return LFM_ATTN_E_INVALID;
+    const size_t bytes = (size_t)c->g.head_dim * sizeof(float);
+    const float *src[2] = {q_norm_w, k_norm_w};
+    float **dst[2]      = {&c->q_norm[layer], &c->k_norm[layer]};
+    for (int i = 0; i < 2; ++i) {
+        if (!src[i]) {
+            (void)hipFree(*dst[i]);
+            *dst[i] = NULL;
+            continue;
+        }
+        if (!*dst[i]) {
+            int st = st_of(hipMalloc((void **)dst[i], bytes));
+            if (st != LFM_ATTN_OK) return st;
+        }
+        int st = st_of(hipMemcpy(*dst[i], src[i], bytes, hipMemcpyHostToDevice));
+        if (st != LFM_ATTN_OK) return st;
+    }
+    return LFM_ATTN_OK;
+}
+
+int lfm_attn_ctx_forward(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32_t B,
+                         const float *q, const float *k, const float *v,
+                         const float *gate_logits, float *out) {
+    if (!c || !q || !k || !v || !out || layer >= c->g.n_layers) return LFM_ATTN_E_INVALID;
+    if (B == 0u || B > LFM_CTX_MAX_ROWS) return LFM_ATTN_E_INVALID;
+    const lfm_attn_geom *g = &c->g;
+    if ((uint64_t)pos_0 + B > g->max_seq) return LFM_ATTN_E_RANGE;
+    const int swa = c->is_swa[layer];
+    const uint32_t window = swa ? g->sliding_window : 0u;
+    const uint32_t cap    = c->slots[layer];
+    /* every row's window must survive the later rows' ring writes */
+    if (swa && (uint64_t)window + B - 1u > cap) return LFM_ATTN_E_INVALID;
+
+    const size_t qn = (size_t)B * g->n_head_q * g->head_dim;
+    const size_t kn = (size_t)B * g->n_head_kv * g->head_dim;
+    unsigned char *h = c->stage_host;
+    memcpy(h, q, qn * sizeof(float));
+    memcpy(h + c->off_k, k, kn * sizeof(float));
+    memcpy(h + c->off_v, v, kn * sizeof(float));
+    if (gate_logits) memcpy(h + c->off_g, gate_logits, (size_t)B * g->n_head_q * sizeof(float));
+    memcpy(h + c->off_pos, &pos_0, sizeof pos_0);
+    int st = st_of(hipMemcpyAsync(c->stage_dev, h, c->stage_in_bytes, hipMemcpyHostToDevice, c->stream));
+    if (st != LFM_ATTN_OK) return st;
+
+    unsigned char *d     = c->stage_dev;
+    float *qd            = (float *)d;
+    const uint32_t *posd = (const uint32_t *)(d + c->off_pos);
+    uint16_t *const *kt  = c->tables + 2u * layer;
+    uint16_t *const *vt  = c->tables + 2u * layer + 1u;
+    const float *cosd    = swa ? c->cos_swa : c->cos_full;
+    const float *sind    = swa ? c->sin_swa : c->sin_full;
+    st = lfm_hip_qkv_prologue(qd, (const float *)(d + c->off_k), (const float *)(d + c->off_v), kt, vt,
+                              posd, 1u, B, g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer],
+                              c->k_norm[layer], g->eps, cosd, sind, window, cap, c->stream);
+    if (st != LFM_ATTN_OK) return st;
+    const uint32_t keys = window ? window + B - 1u : pos_0 + B;
+    st = lfm_hip_gqa_f16_varlen(qd, gate_logits ? (const float *)(d + c->off_g) : NULL, 1,
+                                (const uint16_t *const *)kt, (const uint16_t *const *)vt, posd,
+                                (float *)(d + c->off_out), 1u, B, keys, g->n_head_q, g->n_head_kv,
+                                g->head_dim, window, cap, 1.0f / sqrtf((float)g->head_dim), c->stream);
+    if (st != LFM_ATTN_OK) return st;
+    st = st_of(hipMemcpyAsync(h + c->off_out, d + c->off_out, qn * sizeof(float),
+                              hipMemcpyDeviceToHost, c->stream));
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    if (st == LFM_ATTN_OK) memcpy(out, h + c->off_out, qn * sizeof(float));
+    return st;
+}
+
+static int kv_range(lfm_attn_ctx *c, uint32_t layer, uint32_t slot, uint32_t n_slots, size_t *off,
+                    size_t *bytes) {
+    if (!c || layer >= c->g.n_layers) return LFM_ATTN_E_INVALID;
+    if ((uint64_t)slot + n_slots > c->slots[layer]) return LFM_ATTN_E_RANGE;
+    const size_t row = (size_t)c->g.n_head_kv * c->g.head_dim;
+    *off   = (size_t)slot * row;
+    *bytes = (size_t)n_slots * row * sizeof(uint16_t);
+    return LFM_ATTN_OK;
+}
+
+int lfm_attn_ctx_kv_export(lfm_attn_ctx *c, uint32_t layer, uint32_t slot, uint32_t n_slots,
+                           uint16_t *k_host, uint16_t *v_host) {
+    size_t off = 0, bytes = 0;
+    int st = kv_range(c, layer, slot, n_slots, &off, &bytes);
+    if (st != LFM_ATTN_OK) return st;
+    if (k_host) st = st_of(hipMemcpyAsync(k_host, c->k_cache[layer] + off, bytes, hipMemcpyDeviceToHost, c->stream));
+    if (st == LFM_ATTN_OK && v_host)
+        st = st_of(hipMemcpyAsync(v_host, c->v_cache[layer] + off, bytes, hipMemcpyDeviceToHost, c->stream));
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    return st;
+}
+
+int lfm_attn_ctx_kv_import(lfm_attn_ctx *c, uint32_t layer, uint32_t slot, uint32_t n_slots,
+                           const uint16_t *k_host, const uint16_t *v_host) {
+    size_t off = 0, bytes = 0;
+    int st = kv_range(c, layer, slot, n_slots, &off, &bytes);
+    if (st != LFM_ATTN_OK) return st;
+    if (k_host) st = st_of(hipMemcpyAsync(c->k_cache[layer] + off, k_host, bytes, hipMemcpyHostToDevice, c->stream));
+    if (st == LFM_ATTN_OK && v_host)
+        st = st_of(hipMemcpyAsync(c->v_cache[layer] + off, v_host, bytes, hipMemcpyHostToDevice, c->stream));
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    return st;
+}
+
+int lfm_attn_ctx_kv_device(lfm_attn_ctx *c, uint32_t layer, uint16_t **k_dev, uint16_t **v_dev,
+                           uint32_t *n_slots) {
+    if (!c || layer >= c->g.n_layers) return LFM_ATTN_E_INVALID;
+    if (k_dev) *k_dev = c->k_cache[layer];
+    if (v_dev) *v_dev = c->v_cache[layer];
+    if (n_slots) *n_slots = c->slots[layer];
+    return LFM_ATTN_OK;
+}

@@ -104,3 +104,22 @@ def test_rejections_before_launch():
                                     1e-5, FAKE, FAKE, 300, 264, None) == E_INVALID
     out5 = (C.c_uint32 * 5)()
     assert lib.lfm_attn_seg_plan(5, 300, 264, out5) == E_INVALID
+
+
+def test_context_rejects_bad_geometry():
+    """Geometry is validated before any device call."""
+    import ctypes as C
+    from laii_amd._lib import Geom
+    lib = la.load()
+    g = Geom()
+    g.n_layers, g.n_head_q, g.n_head_kv, g.head_dim, g.max_seq = 1, 30, 8, 64, 128
+    h = C.c_void_p()
+    assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # 30 % 8 != 0
+    g.n_head_q, g.head_dim = 32, 60
+    assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # head_dim % 8
+    g.head_dim = 128
+    swa = (C.c_uint8 * 1)(1)
+    g.layer_is_swa = C.cast(swa, C.POINTER(C.c_uint8))
+    g.sliding_window, g.swa_cap = 256, 200
+    assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # window > ring
+    assert lib.lfm_attn_ctx_forward(None, 0, 0, 1, FAKE, FAKE, FAKE, None, FAKE) == E_INVALID
