@@ -31,6 +31,10 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{CSRC}", f"-I{INCLUDE}",
 ]
+# per-file additions: the prefill kernel takes maxima of MFMA results, which
+# are never NaN there; without the no-NaN assumption every fmaxf operand is
+# canonicalised first (one extra VALU op per score)
+HIP_FILE_FLAGS = {"prefill_fa.hip": ["-fno-honor-nans"]}
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
            f"-I{ROCM}/include", f"-I{CSRC}", f"-I{INCLUDE}"]
 
@@ -55,7 +59,8 @@ def build(verbose: bool = False) -> str:
     objs = []
     for src in HIP_SOURCES:
         obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        jobs.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([HIPCC, *HIP_FLAGS, *HIP_FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src),
+                     "-o", obj])
         objs.append(obj)
     for src in C_SOURCES:
         obj = os.path.join(BUILD, src.replace(".c", ".o"))

@@ -25,6 +25,8 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "kernels.h"
 #include "lfm_attn.h"
 
@@ -40,7 +42,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int KB       = 64;      /* keys per block                         */
 constexpr int KSTR     = 64 + 8;  /* halfs per K row in LDS (16 B pad)      */
-constexpr int VSTR     = KB + 4;  /* halfs per d row of V^T in LDS          */
+constexpr int VSTR     = KB + 8;  /* halfs per d row of V^T in LDS (16 B pad) */
 constexpr float kLazy  = 8.0f;    /* log2 headroom before the max is raised */
 
 struct PrefillParams {
@@ -117,35 +119,39 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     const uint32_t n_keys = hi_pos + 1u;
     const uint32_t nblk   = (n_keys + KB - 1) / KB;
 
-    /* ---- staging: waves 0-1 load K rows, waves 2-3 load V (4 keys / lane) */
+    /* ---- staging: waves 0-1 load K rows, waves 2-3 load V (4 keys / lane) --
+     * V^T is stored per d-row with the keys of each 32-key step permuted to
+     * [0-3,16-19, 4-7,20-23, 8-11,24-27, 12-15,28-31], so the P^T-matching
+     * A fragment of a lane (keys 4g..4g+3 and 16+4g..19+4g) is 16 contiguous
+     * bytes: one ds_read_b128. */
+    const int sc = tid & 7, srow = (tid & 127) >> 3;
+    const uint16_t *sbase = (tid < 128 ? kc + (size_t)srow * row : vc + (size_t)(4 * srow) * row) + 8 * sc;
+    const size_t sstep = (tid < 128 ? 16u : 1u) * row; /* between the 4 rows a lane loads */
     u32x4_t stage[4];
     auto load_block = [&](uint32_t kb) {
-        if (tid < 128) {
-            const int c = tid & 7, r0 = tid >> 3; /* 16 rows per pass */
+        const uint16_t *src = sbase + (size_t)kb * row;
+        if (kb + KB <= n_keys) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) stage[i] = *reinterpret_cast<const u32x4_t *>(src + i * sstep);
+        } else { /* last block: rows past the keys repeat the last key (masked) */
+            const uint32_t r0 = tid < 128 ? (uint32_t)srow : 4u * srow;
+            const uint32_t dr = tid < 128 ? 16u : 1u;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t key = kb + (uint32_t)(r0 + 16 * i);
+                uint32_t key = kb + r0 + dr * (uint32_t)i;
                 key = key < n_keys ? key : n_keys - 1u;
-                stage[i] = *reinterpret_cast<const u32x4_t *>(kc + (size_t)key * row + 8 * c);
-            }
-        } else {
-            const int t = tid - 128, c = t & 7, quad = t >> 3; /* 16 quads x 4 keys */
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t key = kb + (uint32_t)(4 * quad + i);
-                key = key < n_keys ? key : n_keys - 1u;
-                stage[i] = *reinterpret_cast<const u32x4_t *>(vc + (size_t)key * row + 8 * c);
+                stage[i] = *reinterpret_cast<const u32x4_t *>((tid < 128 ? kc : vc) + (size_t)key * row + 8 * sc);
             }
         }
     };
     auto store_block = [&](int buf) {
         if (tid < 128) {
-            const int c = tid & 7, r0 = tid >> 3;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u32x4_t *>(&ks[buf][(r0 + 16 * i) * KSTR + 8 * c]) = stage[i];
+                *reinterpret_cast<u32x4_t *>(&ks[buf][(srow + 16 * i) * KSTR + 8 * sc]) = stage[i];
         } else {
-            const int t = tid - 128, c = t & 7, quad = t >> 3;
+            const int quad = srow, j = quad >> 3, qq = quad & 7;
+            const int pos  = 32 * j + 8 * (qq & 3) + 4 * (qq >> 2);
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 const uint32_t a0 = stage[0][w], a1 = stage[1][w], a2 = stage[2][w], a3 = stage[3][w];
@@ -154,8 +160,8 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 even[1] = (a2 & 0xFFFFu) | (a3 << 16);
                 odd[0]  = (a0 >> 16) | (a1 & 0xFFFF0000u);
                 odd[1]  = (a2 >> 16) | (a3 & 0xFFFF0000u);
-                *reinterpret_cast<u32x2_t *>(&vts[buf][(8 * c + 2 * w) * VSTR + 4 * quad])     = even;
-                *reinterpret_cast<u32x2_t *>(&vts[buf][(8 * c + 2 * w + 1) * VSTR + 4 * quad]) = odd;
+                *reinterpret_cast<u32x2_t *>(&vts[buf][(8 * sc + 2 * w) * VSTR + pos])     = even;
+                *reinterpret_cast<u32x2_t *>(&vts[buf][(8 * sc + 2 * w + 1) * VSTR + pos]) = odd;
             }
         }
     };
@@ -171,16 +177,11 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     }
     const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    load_block(0);
-    store_block(0);
-    __syncthreads();
-
-    for (uint32_t b = 0; b < nblk; ++b) {
-        const int buf    = (int)(b & 1u);
+    /* one 64-key block; MASK only on blocks crossing the lowest query row */
+    auto block = [&](auto mask_tag, uint32_t b) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int buf     = (int)(b & 1u);
         const uint32_t kb = b * KB;
-        if (b + 1 < nblk) load_block(kb + KB);
-
-        /* S^T - m */
         float4_t sacc[MT][NT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -195,8 +196,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 sacc[mt][nt] = acc;
             }
         }
-        /* causal / length mask on blocks that reach past the lowest row */
-        if (kb + KB - 1u > lo_pos) {
+        if constexpr (MASK) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -204,22 +204,31 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const uint32_t key = kb + (uint32_t)(16 * mt + 4 * g + i);
-                        if (key > col_pos[nt] || !col_ok[nt]) sacc[mt][nt][i] = -INFINITY;
+                        if (key > col_pos[nt]) sacc[mt][nt][i] = -INFINITY;
                     }
         }
-        /* block max relative to m; first block sets m, later ones lazily */
+        /* block max relative to m: the first block sets m, later ones raise it
+         * only past 2^kLazy (rare), in a wave-uniform branch */
+        float mx[NT];
+        bool any_raise = false;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            float mx = -INFINITY;
+            float v = -INFINITY;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
-                mx = fmaxf(mx, fmaxf(fmaxf(sacc[mt][nt][0], sacc[mt][nt][1]),
-                                     fmaxf(sacc[mt][nt][2], sacc[mt][nt][3])));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const bool raise = (b == 0) ? (mx > -INFINITY) : (mx > kLazy);
-            if (__any(raise)) {
-                const float inc   = raise ? mx : 0.0f;
+                v = fmaxf(v, fmaxf(fmaxf(sacc[mt][nt][0], sacc[mt][nt][1]),
+                                   fmaxf(sacc[mt][nt][2], sacc[mt][nt][3])));
+            mx[nt] = v;
+            any_raise |= (b == 0u) ? true : (v > kLazy);
+        }
+        if (__builtin_amdgcn_ballot_w64(any_raise) != 0ull) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float v = mx[nt]; /* column max over the 4 lanes holding it */
+                v = fmaxf(v, __shfl_xor(v, 16));
+                v = fmaxf(v, __shfl_xor(v, 32));
+                const bool raise  = (b == 0u) ? (v > -INFINITY) : (v > kLazy);
+                const float inc   = raise ? v : 0.0f;
                 const float alpha = __builtin_amdgcn_exp2f(-inc);
                 m[nt] += inc;
                 l[nt] *= alpha;
@@ -229,13 +238,13 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
             }
         }
-        /* P^T fragments (fp16, RTZ) and l from the same fp16 values */
-        u32x4_t pf[2][NT];
+        /* per 32-key step: P^T fragments (fp16, RTZ), l from the same fp16
+         * values, then O^T += V^T . P^T */
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            float lsum = l[nt];
+        for (int j = 0; j < 2; ++j) {
+            u32x4_t pf[NT];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
+            for (int nt = 0; nt < NT; ++nt) {
                 const float4_t a = sacc[2 * j][nt], c = sacc[2 * j + 1][nt];
                 /* scalar temporaries: a bit_cast of an ext-vector element was
                  * miscompiled into four reads of element 0 */
@@ -243,33 +252,45 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 const half2_t h1 = exp2_pk(a[2], a[3]);
                 const half2_t h2 = exp2_pk(c[0], c[1]);
                 const half2_t h3 = exp2_pk(c[2], c[3]);
+                float lsum = l[nt];
                 lsum = __builtin_amdgcn_fdot2(h0, ones, lsum, false);
                 lsum = __builtin_amdgcn_fdot2(h1, ones, lsum, false);
                 lsum = __builtin_amdgcn_fdot2(h2, ones, lsum, false);
                 lsum = __builtin_amdgcn_fdot2(h3, ones, lsum, false);
+                l[nt] = lsum;
                 u32x4_t w;
                 w[0] = __builtin_bit_cast(uint32_t, h0);
                 w[1] = __builtin_bit_cast(uint32_t, h1);
                 w[2] = __builtin_bit_cast(uint32_t, h2);
                 w[3] = __builtin_bit_cast(uint32_t, h3);
-                pf[j][nt] = w;
+                pf[nt] = w;
             }
-            l[nt] = lsum;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const half8_t av = as_half8(*reinterpret_cast<const u32x4_t *>(
+                    &vts[buf][(16 * mt + l16) * VSTR + 32 * j + 8 * g]));
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
+            }
         }
-        /* O^T += V^T . P^T */
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint16_t *src = &vts[buf][(16 * mt + l16) * VSTR + 32 * j + 4 * g];
-                const u32x2_t x0 = *reinterpret_cast<const u32x2_t *>(src);
-                const u32x2_t x1 = *reinterpret_cast<const u32x2_t *>(src + 16);
-                u32x4_t a;
-                a[0] = x0[0]; a[1] = x0[1]; a[2] = x1[0]; a[3] = x1[1];
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(as_half8(a), as_half8(pf[j][nt]), oacc[mt][nt]);
-            }
-        if (b + 1 < nblk) store_block(buf ^ 1);
+    };
+
+    /* blocks [0, nfull) lie entirely at or below the lowest query row */
+    const uint32_t nfull = (lo_pos + 1u) / KB < nblk ? (lo_pos + 1u) / KB : nblk;
+    load_block(0);
+    store_block(0);
+    __syncthreads();
+    uint32_t b = 0;
+    for (; b < nfull; ++b) {
+        if (b + 1 < nblk) load_block((b + 1) * KB);
+        block(std::integral_constant<bool, false>{}, b);
+        if (b + 1 < nblk) store_block((int)((b + 1) & 1u));
+        __syncthreads();
+    }
+    for (; b < nblk; ++b) {
+        if (b + 1 < nblk) load_block((b + 1) * KB);
+        block(std::integral_constant<bool, true>{}, b);
+        if (b + 1 < nblk) store_block((int)((b + 1) & 1u));
         __syncthreads();
     }
 
