@@ -9,18 +9,25 @@
  *
  * Workgroup = 4 waves = TQ query positions x kv_mul query heads of one KV
  * head (256 query columns, TQ = 256 / kv_mul), so each K/V block staged in
- * LDS serves every query head that reads it.  Per 64-key block:
- *   S^T = K . Q^T - m    16x16x32 f16 MFMA; K fragments from LDS, Q^T from
- *                        registers; the running max enters as the
- *                        accumulator's initial value (no per-score subtract).
- *   p = exp2(S^T)        lazy max: the running max is raised only when a
- *                        block exceeds it by more than 2^8 (fp16 P stays
- *                        finite), which rescales O and l.
- *   l += p               v_dot2_f32_f16 over the fp16 P actually fed to the
- *                        MFMA, so numerator and denominator use the same P.
- *   O^T += V^T . P^T     V^T fragments from LDS (V is transposed while it is
- *                        staged), P^T straight from the S^T accumulator layout.
- * Causal masking only touches blocks that cross the diagonal; blocks above it
+ * LDS serves every query head that reads it.
+ *
+ * Staging: 64-key K and V blocks (row-major, 128-B rows) go through 16
+ * registers per thread into a ring of 3 LDS blocks: block b + 2 is fetched
+ * while block b is computed and stored at the next block boundary.  The 16-B
+ * chunks of row r are XOR-swizzled by 2*((r >> 2) & 3), which makes both the
+ * K fragment reads (ds_read_b128) and the transposing V reads
+ * (ds_read_b64_tr_b16) bank-conflict free.
+ *
+ * Compute runs in 32-key steps, software pipelined so that each step's
+ * basic block holds independent MFMA and VALU work:
+ *   S^T(k+1) = K . Q^T - m   16x16x32 f16 MFMA; the running max enters as
+ *                            the accumulator's initial value
+ *   p = exp2(S^T(k))         lazy max: raised only when a step exceeds it by
+ *                            more than 2^8 (fp16 P stays finite), which
+ *                            rescales O and l in a rare uniform branch
+ *   l += p                   v_dot2_f32_f16 over the fp16 P fed to the MFMA
+ *   O^T += V^T . P^T(k)      V^T fragments read transposed from row-major V
+ * Causal masking only touches steps that cross the diagonal; steps above it
  * are skipped.  Workgroups run heaviest-first (late query tiles first).
  */
 #include <hip/hip_runtime.h>
@@ -34,16 +41,20 @@ namespace lfm {
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
 
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr int KB       = 64;      /* keys per block                         */
-constexpr int KSTR     = 64 + 8;  /* halfs per K row in LDS (16 B pad)      */
-constexpr int VSTR     = KB + 8;  /* halfs per d row of V^T in LDS (16 B pad) */
-constexpr float kLazy  = 8.0f;    /* log2 headroom before the max is raised */
+constexpr float kLog2e  = 1.4426950408889634f;
+constexpr int KB        = 64;          /* keys per LDS block                       */
+constexpr int SB        = 32;          /* keys per compute step                    */
+constexpr int NBUF      = 3;           /* LDS ring of K/V blocks                   */
+constexpr int ROWB      = 128;         /* bytes per K/V row of one head (d = 64)   */
+constexpr int BLKB      = KB * ROWB;   /* bytes per K (or V) block                 */
+constexpr float kLazy   = 8.0f;        /* log2 headroom before the max is raised   */
 
 struct PrefillParams {
     const uint16_t *q;  /* [n_seq][n_tok][n_head_q][HD] fp16 */
@@ -67,20 +78,31 @@ __device__ __forceinline__ half2_t exp2_pk(float a, float b) {
                                                                   __builtin_amdgcn_exp2f(b)));
 }
 
+/* transposing LDS read: within each 16-lane group, lane l receives element
+ * l % 4 of the 8-byte chunks addressed by lanes l/4, l/4 + 4, l/4 + 8 and
+ * l/4 + 12 */
+__device__ __forceinline__ half4_t lds_read_tr(const uint8_t *p) {
+    return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4 *)p));
+}
+
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    return fmaxf(fmaxf(a, b), c);
+}
+
 template <int HD>
 __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     static_assert(HD == 64, "prefill kernel is specialised for head_dim 64");
-    constexpr int NT = 4; /* 16-column tiles per wave (64 columns)         */
-    constexpr int MT = 4; /* 16-key tiles per block                        */
+    constexpr int NT = 4; /* 16-column tiles per wave (64 columns) */
     constexpr int NM = HD / 16;
-    __shared__ __attribute__((aligned(16))) uint16_t ks[2][KB * KSTR];
-    __shared__ __attribute__((aligned(16))) uint16_t vts[2][HD * VSTR];
+    /* ring of NBUF blocks, each K (8 KB) then V (8 KB) */
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NBUF * 2 * BLKB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
     /* 1-D grid, heaviest query tiles first across all (sequence, KV head)
-     * pairs; consecutive workgroups take consecutive pairs, so the tiles of
-     * one pair all land on the same XCD (round-robin over 8) and share its L2 */
+     * pairs; consecutive workgroups take consecutive pairs, so with a pair
+     * count divisible by 8 the tiles of one pair land on one XCD (round-robin
+     * dispatch) and share its L2 */
     const uint32_t pairs = P.n_head_kv * P.n_seq;
     const uint32_t qt    = P.n_qtiles - 1u - blockIdx.x / pairs;
     const uint32_t pair  = blockIdx.x % pairs;
@@ -114,185 +136,207 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     }
     /* q*scale*log2(e) is rounded to fp16 once (relative error <= 2^-11 per
      * element), which keeps the score accumulator in log2 units */
-    const uint32_t lo_pos = P.pos_0 + t0;                                   /* smallest query position */
-    const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;         /* largest query position  */
+    const uint32_t lo_pos = P.pos_0 + t0;                               /* smallest query position */
+    const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;     /* largest query position  */
     const uint32_t n_keys = hi_pos + 1u;
     const uint32_t nblk   = (n_keys + KB - 1) / KB;
+    const uint32_t nsub   = (n_keys + SB - 1) / SB;
+    /* steps [0, nfull) lie entirely at or below the lowest query row */
+    const uint32_t nfull  = min((lo_pos + 1u) / SB, nsub);
 
-    /* ---- staging: waves 0-1 load K rows, waves 2-3 load V (4 keys / lane) --
-     * V^T is stored per d-row with the keys of each 32-key step permuted to
-     * [0-3,16-19, 4-7,20-23, 8-11,24-27, 12-15,28-31], so the P^T-matching
-     * A fragment of a lane (keys 4g..4g+3 and 16+4g..19+4g) is 16 contiguous
-     * bytes: one ds_read_b128. */
-    const int sc = tid & 7, srow = (tid & 127) >> 3;
-    const uint16_t *sbase = (tid < 128 ? kc + (size_t)srow * row : vc + (size_t)(4 * srow) * row) + 8 * sc;
-    const size_t sstep = (tid < 128 ? 16u : 1u) * row; /* between the 4 rows a lane loads */
+    /* ---- staging through registers: thread tid moves 16-B chunks tid and
+     * tid + 256 of each 8-KB K and V block; chunk p sits at byte 16*p of the
+     * block (row p/8, slot p%8) and holds the row's global chunk
+     * (p%8) ^ swz(row) */
+    uint32_t st_row[2], st_col[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t p = (uint32_t)tid + 256u * e, r = p >> 3;
+        st_row[e] = r;
+        st_col[e] = 8u * ((p & 7u) ^ (2u * ((r >> 2) & 3u))); /* halfs */
+    }
     u32x4_t stage[4];
-    auto load_block = [&](uint32_t kb) {
-        const uint16_t *src = sbase + (size_t)kb * row;
-        if (kb + KB <= n_keys) {
+    auto load_regs = [&](uint32_t blk) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) stage[i] = *reinterpret_cast<const u32x4_t *>(src + i * sstep);
-        } else { /* last block: rows past the keys repeat the last key (masked) */
-            const uint32_t r0 = tid < 128 ? (uint32_t)srow : 4u * srow;
-            const uint32_t dr = tid < 128 ? 16u : 1u;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t key = kb + r0 + dr * (uint32_t)i;
-                key = key < n_keys ? key : n_keys - 1u;
-                stage[i] = *reinterpret_cast<const u32x4_t *>((tid < 128 ? kc : vc) + (size_t)key * row + 8 * sc);
-            }
+        for (int e = 0; e < 2; ++e) {
+            uint32_t key = blk * KB + st_row[e];
+            key = key < n_keys ? key : n_keys - 1u; /* rows past the keys: masked */
+            const size_t off = (size_t)key * row + st_col[e];
+            stage[e]     = *reinterpret_cast<const u32x4_t *>(kc + off);
+            stage[2 + e] = *reinterpret_cast<const u32x4_t *>(vc + off);
         }
     };
-    auto store_block = [&](int buf) {
-        if (tid < 128) {
+    auto store_regs = [&](uint32_t blk) {
+        uint8_t *dst = ring + (blk % NBUF) * (2 * BLKB) + 16 * tid;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u32x4_t *>(&ks[buf][(srow + 16 * i) * KSTR + 8 * sc]) = stage[i];
-        } else {
-            const int quad = srow, j = quad >> 3, qq = quad & 7;
-            const int pos  = 32 * j + 8 * (qq & 3) + 4 * (qq >> 2);
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint32_t a0 = stage[0][w], a1 = stage[1][w], a2 = stage[2][w], a3 = stage[3][w];
-                u32x2_t even, odd;
-                even[0] = (a0 & 0xFFFFu) | (a1 << 16);
-                even[1] = (a2 & 0xFFFFu) | (a3 << 16);
-                odd[0]  = (a0 >> 16) | (a1 & 0xFFFF0000u);
-                odd[1]  = (a2 >> 16) | (a3 & 0xFFFF0000u);
-                *reinterpret_cast<u32x2_t *>(&vts[buf][(8 * sc + 2 * w) * VSTR + pos])     = even;
-                *reinterpret_cast<u32x2_t *>(&vts[buf][(8 * sc + 2 * w + 1) * VSTR + pos]) = odd;
-            }
+        for (int e = 0; e < 2; ++e) {
+            *reinterpret_cast<u32x4_t *>(dst + 4096 * e)        = stage[e];
+            *reinterpret_cast<u32x4_t *>(dst + BLKB + 4096 * e) = stage[2 + e];
         }
     };
+
+    /* fragment offsets in a block (bytes).  K: row 16*mt + l16, chunk 4*st + g.
+     * V (transposing read): lane l16 of group g addresses row 4g + l16/4 of
+     * a 16-key half, dims 16*mt + 4*(l16 % 4) */
+    const uint32_t kswz  = (uint32_t)(g ^ (2 * ((l16 >> 2) & 3)));
+    const uint32_t koff0 = (uint32_t)l16 * ROWB + 16u * kswz;
+    const uint32_t koff1 = (uint32_t)l16 * ROWB + 16u * (kswz ^ 4u);
+    uint32_t voff[NM];
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+        voff[mt] = BLKB + (uint32_t)(4 * g + (l16 >> 2)) * ROWB + 32u * (uint32_t)(mt ^ g) +
+                   16u * ((l16 >> 1) & 1) + 8u * (l16 & 1);
 
     float4_t oacc[NM][NT];
-    float m[NT], l[NT];
+    float4_t negm[NT]; /* -m splat: initial value of the score accumulator */
+    float l[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        m[nt] = 0.0f;
-        l[nt] = 0.0f;
+        negm[nt] = (float4_t)0.0f;
+        l[nt]    = 0.0f;
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
     }
     const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-    /* one 64-key block; MASK only on blocks crossing the lowest query row */
-    auto block = [&](auto mask_tag, uint32_t b) {
+    /* S^T of step k: two 16-key tiles x NT column tiles */
+    auto scores = [&](auto mask_tag, uint32_t k, float4_t (&sc)[2][NT]) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const int buf     = (int)(b & 1u);
-        const uint32_t kb = b * KB;
-        float4_t sacc[MT][NT];
+        const uint8_t *kb = ring + ((k >> 1) % NBUF) * (2 * BLKB) + (k & 1u) * (SB * ROWB);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint16_t *kr = &ks[buf][(16 * mt + l16) * KSTR + 8 * g];
-            const half8_t k0 = as_half8(*reinterpret_cast<const u32x4_t *>(kr));
-            const half8_t k1 = as_half8(*reinterpret_cast<const u32x4_t *>(kr + 32));
+        for (int mt = 0; mt < 2; ++mt) {
+            const half8_t k0 = as_half8(*reinterpret_cast<const u32x4_t *>(kb + mt * 16 * ROWB + koff0));
+            const half8_t k1 = as_half8(*reinterpret_cast<const u32x4_t *>(kb + mt * 16 * ROWB + koff1));
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                float4_t acc = (float4_t)(-m[nt]);
-                acc = mfma(k0, qf[nt][0], acc);
-                acc = mfma(k1, qf[nt][1], acc);
-                sacc[mt][nt] = acc;
-            }
+            for (int nt = 0; nt < NT; ++nt) sc[mt][nt] = mfma(k1, qf[nt][1], mfma(k0, qf[nt][0], negm[nt]));
         }
         if constexpr (MASK) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const uint32_t key = kb + (uint32_t)(16 * mt + 4 * g + i);
-                        if (key > col_pos[nt]) sacc[mt][nt][i] = -INFINITY;
+                        const uint32_t key = k * SB + (uint32_t)(16 * mt + 4 * g + i);
+                        if (key > col_pos[nt]) sc[mt][nt][i] = -INFINITY;
                     }
         }
-        /* block max relative to m: the first block sets m, later ones raise it
-         * only past 2^kLazy (rare), in a wave-uniform branch */
-        float mx[NT];
-        bool any_raise = false;
+    };
+
+    /* lazy max: raise m (and rescale O, l and the pending scores) when a
+     * column's step maximum exceeds it by more than 2^kLazy; the first step
+     * sets m to the exact column maximum.  step_max() is the per-lane part,
+     * rescale() the rare, wave-uniform branch. */
+    auto step_max = [&](auto first_tag, const float4_t (&sc)[2][NT], float (&mx)[NT]) {
+        constexpr bool FIRST = decltype(first_tag)::value;
+        bool any_raise = FIRST;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            float v = -INFINITY;
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                v = fmaxf(v, fmaxf(fmaxf(sacc[mt][nt][0], sacc[mt][nt][1]),
-                                   fmaxf(sacc[mt][nt][2], sacc[mt][nt][3])));
+            float v = max3(max3(sc[0][nt][0], sc[0][nt][1], sc[0][nt][2]), sc[0][nt][3], sc[1][nt][0]);
+            v = max3(max3(v, sc[1][nt][1], sc[1][nt][2]), sc[1][nt][3], -INFINITY);
             mx[nt] = v;
-            any_raise |= (b == 0u) ? true : (v > kLazy);
+            if constexpr (!FIRST) any_raise |= v > kLazy;
         }
+        return any_raise;
+    };
+    auto rescale = [&](auto first_tag, bool any_raise, float4_t (&sc)[2][NT], const float (&mx)[NT]) {
+        constexpr bool FIRST = decltype(first_tag)::value;
         if (__builtin_amdgcn_ballot_w64(any_raise) != 0ull) {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 float v = mx[nt]; /* column max over the 4 lanes holding it */
                 v = fmaxf(v, __shfl_xor(v, 16));
                 v = fmaxf(v, __shfl_xor(v, 32));
-                const bool raise  = (b == 0u) ? (v > -INFINITY) : (v > kLazy);
+                const bool raise  = FIRST ? (v > -INFINITY) : (v > kLazy);
                 const float inc   = raise ? v : 0.0f;
                 const float alpha = __builtin_amdgcn_exp2f(-inc);
-                m[nt] += inc;
+                negm[nt] -= inc;
                 l[nt] *= alpha;
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) sacc[mt][nt] -= inc;
+                sc[0][nt] -= inc;
+                sc[1][nt] -= inc;
 #pragma unroll
                 for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
             }
         }
-        /* per 32-key step: P^T fragments (fp16, RTZ), l from the same fp16
-         * values, then O^T += V^T . P^T */
+    };
+
+    /* P^T(k) = exp2(S^T(k)), l += P, O^T += V^T(k) . P^T(k) */
+    auto accumulate = [&](uint32_t k, const float4_t (&sc)[2][NT]) {
+        u32x4_t pf[NT];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            u32x4_t pf[NT];
+        for (int nt = 0; nt < NT; ++nt) {
+            const float4_t a = sc[0][nt], c = sc[1][nt];
+            /* scalar temporaries: a bit_cast of an ext-vector element was
+             * miscompiled into four reads of element 0 */
+            const half2_t h0 = exp2_pk(a[0], a[1]);
+            const half2_t h1 = exp2_pk(a[2], a[3]);
+            const half2_t h2 = exp2_pk(c[0], c[1]);
+            const half2_t h3 = exp2_pk(c[2], c[3]);
+            float lsum = l[nt];
+            lsum = __builtin_amdgcn_fdot2(h0, ones, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(h1, ones, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(h2, ones, lsum, false);
+            lsum = __builtin_amdgcn_fdot2(h3, ones, lsum, false);
+            l[nt] = lsum;
+            u32x4_t w;
+            w[0] = __builtin_bit_cast(uint32_t, h0);
+            w[1] = __builtin_bit_cast(uint32_t, h1);
+            w[2] = __builtin_bit_cast(uint32_t, h2);
+            w[3] = __builtin_bit_cast(uint32_t, h3);
+            pf[nt] = w;
+        }
+        const uint8_t *vb = ring + ((k >> 1) % NBUF) * (2 * BLKB) + (k & 1u) * (SB * ROWB);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const float4_t a = sacc[2 * j][nt], c = sacc[2 * j + 1][nt];
-                /* scalar temporaries: a bit_cast of an ext-vector element was
-                 * miscompiled into four reads of element 0 */
-                const half2_t h0 = exp2_pk(a[0], a[1]);
-                const half2_t h1 = exp2_pk(a[2], a[3]);
-                const half2_t h2 = exp2_pk(c[0], c[1]);
-                const half2_t h3 = exp2_pk(c[2], c[3]);
-                float lsum = l[nt];
-                lsum = __builtin_amdgcn_fdot2(h0, ones, lsum, false);
-                lsum = __builtin_amdgcn_fdot2(h1, ones, lsum, false);
-                lsum = __builtin_amdgcn_fdot2(h2, ones, lsum, false);
-                lsum = __builtin_amdgcn_fdot2(h3, ones, lsum, false);
-                l[nt] = lsum;
-                u32x4_t w;
-                w[0] = __builtin_bit_cast(uint32_t, h0);
-                w[1] = __builtin_bit_cast(uint32_t, h1);
-                w[2] = __builtin_bit_cast(uint32_t, h2);
-                w[3] = __builtin_bit_cast(uint32_t, h3);
-                pf[nt] = w;
-            }
+        for (int mt = 0; mt < NM; ++mt) {
+            const half4_t lo = lds_read_tr(vb + voff[mt]);
+            const half4_t hi = lds_read_tr(vb + 16 * ROWB + voff[mt]);
+            const half8_t av = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-            for (int mt = 0; mt < NM; ++mt) {
-                const half8_t av = as_half8(*reinterpret_cast<const u32x4_t *>(
-                    &vts[buf][(16 * mt + l16) * VSTR + 32 * j + 8 * g]));
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
-            }
+            for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
         }
     };
 
-    /* blocks [0, nfull) lie entirely at or below the lowest query row */
-    const uint32_t nfull = (lo_pos + 1u) / KB < nblk ? (lo_pos + 1u) / KB : nblk;
-    load_block(0);
-    store_block(0);
-    __syncthreads();
-    uint32_t b = 0;
-    for (; b < nfull; ++b) {
-        if (b + 1 < nblk) load_block((b + 1) * KB);
-        block(std::integral_constant<bool, false>{}, b);
-        if (b + 1 < nblk) store_block((int)((b + 1) & 1u));
+    /* entering LDS block b: block b (stored at the previous entry) becomes
+     * visible to every wave; the slot of block b + 1 is free (its previous
+     * block, b - 2, was last read before this barrier), so block b + 1 moves
+     * from the staging registers into it and block b + 2 is fetched */
+    auto enter_block = [&](uint32_t b) {
         __syncthreads();
+        if (b + 1u < nblk) store_regs(b + 1u);
+        if (b + 2u < nblk) load_regs(b + 2u);
+    };
+
+    /* ---- pipeline: step k overlaps S^T(k+1) with P(k) and PV(k) ------- */
+    load_regs(0u);
+    store_regs(0u);
+    if (nblk > 1u) load_regs(1u);
+    enter_block(0u);
+    float4_t scur[2][NT];
+    if (nfull > 0u) scores(std::false_type{}, 0u, scur);
+    else scores(std::true_type{}, 0u, scur);
+    {
+        float mx[NT];
+        const bool any_raise = step_max(std::true_type{}, scur, mx);
+        rescale(std::true_type{}, any_raise, scur, mx);
     }
-    for (; b < nblk; ++b) {
-        if (b + 1 < nblk) load_block((b + 1) * KB);
-        block(std::integral_constant<bool, true>{}, b);
-        if (b + 1 < nblk) store_block((int)((b + 1) & 1u));
-        __syncthreads();
-    }
+
+    auto step = [&](auto mask_tag, uint32_t k) {
+        float4_t snext[2][NT];
+        if (((k + 1u) & 1u) == 0u) enter_block((k + 1u) >> 1);
+        scores(mask_tag, k + 1u, snext);
+        accumulate(k, scur);
+        float mx[NT];
+        const bool any_raise = step_max(std::false_type{}, snext, mx);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) scur[mt][nt] = snext[mt][nt];
+        rescale(std::false_type{}, any_raise, scur, mx);
+    };
+    uint32_t k = 0;
+    for (; k + 1u < nfull; ++k) step(std::false_type{}, k);
+    for (; k + 1u < nsub; ++k) step(std::true_type{}, k);
+    accumulate(k, scur);
 
     /* ---- epilogue: O / l ------------------------------------------------- */
 #pragma unroll
