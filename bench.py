@@ -210,6 +210,18 @@ def cpu_baseline(wl, n_threads, max_seconds=8.0):
                        f"best of repeated passes, {dt * 1e3:.1f} ms per pass"), out.reshape(n, wl.nq, wl.hd)
 
 
+def run_prefill(hip, la, rng, steps):
+    pf = PrefillWorkload(la, rng)
+    n = max(5, steps // 5)
+    pms = time_steps(hip, pf, n, 3)
+    pkms = time_main_kernel(hip, la, pf, n)
+    prefill = dict(workload="cfg4_prefill_b4_n4096_32q8kv_d64", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
+                   kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4),
+                   flops=pf.flops, pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1))
+    log(f"prefill: {pms:.3f} ms/step, {prefill['TFLOPs']} TFLOP/s")
+    return prefill
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,6 +229,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config-4 prefill workload (for kernel profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share only; --gpus {args.gpus} is not supported "
@@ -229,6 +243,12 @@ def main():
     hip = Hip()
     rng = np.random.default_rng(20261201)
     t_setup = time.perf_counter()
+    if args.prefill_only:
+        prefill = run_prefill(hip, la, rng, args.steps)
+        print(json.dumps({"metric": "prefill attn TFLOP/s, config 4", "value": prefill["TFLOPs"],
+                          "unit": "TFLOP/s", "n_gpus": 1, "steps": max(5, args.steps // 5),
+                          "higher_is_better": True, "prefill": prefill}), flush=True)
+        return
 
     head = DecodeWorkload(la, rng, "decode_b64_ctx8192", 64, 1, 32, 8, 64, [8192] * 64,
                           keep_host=8)
@@ -266,14 +286,7 @@ def main():
                                    pct_hbm_peak=round(100 * wl.bytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
             del wl
 
-    pf = PrefillWorkload(la, rng)
-    pms = time_steps(hip, pf, max(5, args.steps // 5), 3)
-    pkms = time_main_kernel(hip, la, pf, max(5, args.steps // 5))
-    prefill = dict(workload="cfg4_prefill_b4_n4096_32q8kv_d64", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
-                   kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4),
-                   flops=pf.flops, pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1))
-    log(f"prefill: {pms:.3f} ms/step, {prefill['TFLOPs']} TFLOP/s")
-    del pf
+    prefill = run_prefill(hip, la, rng, args.steps)
 
     cpu = None
     parity = None
