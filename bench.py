@@ -156,6 +156,33 @@ class PrefillWorkload:
                             self.n_tok * self.nkv * self.hd, self.nq, self.nkv, self.hd)
 
 
+class KvShiftWorkload:
+    """Attention-sink eviction at the engine trigger (src/lfm2_api.c:871-891)
+    for the LFM2-1.2B attention layers: 6 layers x 8 KV heads x d64 caches of
+    max_seq 32768, position 32760, 64 sinks, n_discard = max_seq / 2.  Each
+    step moves the same rows (the caches are overwritten in place), so the
+    bytes per step are constant: every moved K and V byte is read and written."""
+
+    def __init__(self, la, rng, n_layers=6, nkv=8, hd=64, max_seq=32768, n_sink=64):
+        self.la = la
+        row = nkv * hd
+        self.k = [la.DeviceArray.from_numpy(f16(rng.standard_normal((max_seq, row), dtype=np.float32)))
+                  for _ in range(n_layers)]
+        self.v = [la.DeviceArray.from_numpy(f16(rng.standard_normal((max_seq, row), dtype=np.float32)))
+                  for _ in range(n_layers)]
+        c, s = la.rope_lut_lfm2(max_seq, hd, 1e6)
+        self.cos, self.sin = la.DeviceArray.from_numpy(c), la.DeviceArray.from_numpy(s)
+        self.args = (n_layers, nkv, hd, max_seq)
+        self.pos, self.n_sink, self.n_discard = max_seq - 8, n_sink, max_seq // 2
+        n_keep = self.pos - n_sink - self.n_discard
+        self.bytes = 4 * n_layers * n_keep * row * 2
+
+    def step(self):
+        n_layers, nkv, hd, max_seq = self.args
+        self.la.kv_cache_shift_sinks(self.k, self.v, [nkv] * n_layers, hd, self.cos, self.sin,
+                                     max_seq, self.pos, self.n_sink, self.n_discard)
+
+
 def time_steps(hip, wl, steps, warmup):
     for _ in range(warmup):
         wl.step()
@@ -287,6 +314,15 @@ def main():
             del wl
 
     prefill = run_prefill(hip, la, rng, args.steps)
+
+    if not args.quick:
+        ks = KvShiftWorkload(la, rng)
+        kms = time_steps(hip, ks, max(5, args.steps // 5), 2)
+        secondary["kv_shift_sinks_lfm2_1p2b_6layers_ctx32768"] = dict(
+            GBps=round(ks.bytes / (kms * 1e-3) / 1e9, 1), us_per_step=round(kms * 1e3, 2), bytes=ks.bytes,
+            pct_hbm_peak=round(100 * ks.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
+        log(f"kv shift: {kms * 1e3:.1f} us/step")
+        del ks
 
     cpu = None
     parity = None

@@ -186,6 +186,48 @@ int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                         lfm_attn_stream_t stream);
 
+/* ---- attention-sink eviction on device caches ------------------------------ */
+/* When the position nears max_seq the engine keeps the first n_sink rows,
+ * drops the next n_discard and moves the remaining n_keep = pos - n_sink -
+ * n_discard rows down to n_sink, counter-rotating every moved key by
+ * -n_discard positions with the RoPE table row of position n_discard
+ * (trigger: src/lfm2_api.c:871-891).  On return *inout_pos is the new
+ * position n_sink + n_keep.  Like the reference, nothing moves and
+ * *inout_pos stays when n_discard == 0 or *inout_pos <= n_sink + n_discard.
+ * Key pairs (i, i + head_dim/2) rotate as fma(lo, c, hi*s) and
+ * fma(hi, c, -(lo*s)) in fp32 with an RNE fp16 store, bit-identical to the
+ * reference's AVX2 kernels; values move unchanged.  Asynchronous on `stream`.
+ *
+ * LFM2 -- lfm2_kv_cache_shift_sinks (tools/lfm2_runtime_features.c:744-833,
+ * dispatcher :984-1001).  k_caches / v_caches: host arrays of n_layers device
+ * cache pointers ([max_seq][n_head_kv[l]][head_dim] fp16); a layer with a NULL
+ * cache or n_head_kv[l] == 0 (a ShortConv layer) is skipped.  cos_lut /
+ * sin_lut: the device LFM2 table ([lut_rows][head_dim/2], as built by
+ * lfm_attn_rope_lut_lfm2).  head_dim != 64 leaves everything unchanged, as
+ * the reference does.  Returns LFM_ATTN_E_RANGE when n_discard >= lut_rows. */
+int lfm_hip_kv_cache_shift_sinks(uint16_t *const *k_caches, uint16_t *const *v_caches,
+                                 uint32_t n_layers, const uint32_t *n_head_kv, uint32_t head_dim,
+                                 const float *cos_lut, const float *sin_lut, uint32_t lut_rows,
+                                 uint32_t *inout_pos, uint32_t n_sink, uint32_t n_discard,
+                                 lfm_attn_stream_t stream);
+/* LFM3 -- lfm3_kv_cache_shift_sinks (tools/lfm2_runtime_features.c:1055-1163).
+ * layer_kind[l]: 0 skipped (ShortConv), 1 full attention (linear cache,
+ * shifted like LFM2 with the full table), 2 sliding window (ring of swa_cap
+ * slots, 0 = window + 8; window = sliding_window, 0 = 256): the last
+ * min(new_pos, window) positions are re-slotted at their new positions, the
+ * kept ones counter-rotated with the SWA table.  The re-slotting goes through
+ * the library's device workspace.  Like the reference, nothing moves when
+ * n_discard is not below both table row counts or head_dim is odd. */
+int lfm_hip_lfm3_kv_cache_shift_sinks(uint16_t *const *k_caches, uint16_t *const *v_caches,
+                                      uint32_t n_layers, const uint32_t *n_head_kv,
+                                      const uint8_t *layer_kind, uint32_t head_dim,
+                                      const float *cos_full, const float *sin_full,
+                                      uint32_t full_rows, const float *cos_swa,
+                                      const float *sin_swa, uint32_t swa_rows,
+                                      uint32_t sliding_window, uint32_t swa_cap,
+                                      uint32_t *inout_pos, uint32_t n_sink, uint32_t n_discard,
+                                      lfm_attn_stream_t stream);
+
 /* ---- engine context: device-resident KV + host-pointer calls (C11) -------- */
 /* The forward stacks own their KV caches in host memory
  * (tools/lfm2_forward.c:612-622, tools/lfm3_engine.c:1740-1769).  A GPU
@@ -244,6 +286,12 @@ int lfm_attn_ctx_kv_export(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uin
                            uint16_t *k_host, uint16_t *v_host);
 int lfm_attn_ctx_kv_import(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uint32_t n_slots,
                            const uint16_t *k_host, const uint16_t *v_host);
+/* Attention-sink eviction over every layer of the context (LFM2: head_dim 64
+ * only, as the reference; LFM3: full and SWA layers), with the context's own
+ * tables; synchronous.  Same semantics as lfm_hip_kv_cache_shift_sinks /
+ * lfm_hip_lfm3_kv_cache_shift_sinks. */
+int lfm_attn_ctx_shift_sinks(lfm_attn_ctx *ctx, uint32_t *inout_pos, uint32_t n_sink,
+                             uint32_t n_discard);
 /* Device address of a layer's caches (for callers that drive lfm_hip_* directly). */
 int lfm_attn_ctx_kv_device(lfm_attn_ctx *ctx, uint32_t layer, uint16_t **k_dev, uint16_t **v_dev,
                            uint32_t *n_slots);

@@ -11,6 +11,8 @@ from .attention import (  # noqa: F401
     device_count,
     gqa_f16_varlen,
     gqa_heads,
+    kv_cache_shift_sinks,
+    lfm3_kv_cache_shift_sinks,
     lfm3_online_gqa_f16_dispatch,
     online_gqa_f16,
     pointer_table,

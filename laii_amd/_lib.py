@@ -49,6 +49,11 @@ SIGNATURES = {
                                    _u32, _f32, _vp]),
     "lfm_hip_gqa_f16_varlen": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _u32, _u32, _u32, _f32, _vp]),
+    "lfm_hip_kv_cache_shift_sinks": (_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32,
+                                            C.POINTER(_u32), _u32, _u32, _vp]),
+    "lfm_hip_lfm3_kv_cache_shift_sinks": (_int, [_vp, _vp, _u32, _vp, _vp, _u32, _vp, _vp, _u32,
+                                                 _vp, _vp, _u32, _u32, _u32, C.POINTER(_u32),
+                                                 _u32, _u32, _vp]),
 }
 
 
@@ -70,6 +75,7 @@ SIGNATURES.update({
     "lfm_attn_ctx_kv_export": (_int, [_vp, _u32, _u32, _u32, _vp, _vp]),
     "lfm_attn_ctx_kv_import": (_int, [_vp, _u32, _u32, _u32, _vp, _vp]),
     "lfm_attn_ctx_kv_device": (_int, [_vp, _u32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_u32)]),
+    "lfm_attn_ctx_shift_sinks": (_int, [_vp, C.POINTER(_u32), _u32, _u32]),
 })
 
 _lock = threading.Lock()

@@ -200,6 +200,44 @@ def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0:
           "lfm_hip_prefill_f16")
 
 
+def _host_ptrs(arrays) -> "C.Array":
+    return (C.c_void_p * len(arrays))(*[None if a is None else int(a) for a in arrays])
+
+
+def kv_cache_shift_sinks(k_caches, v_caches, n_head_kv, head_dim: int, cos_lut: Ptr, sin_lut: Ptr,
+                         lut_rows: int, pos: int, n_sink: int, n_discard: int, stream=None) -> int:
+    """lfm2_kv_cache_shift_sinks (tools/lfm2_runtime_features.c:744-833) on
+    device caches: returns the new position.  k_caches / v_caches: per-layer
+    device caches (None for a ShortConv layer); cos_lut / sin_lut: the device
+    LFM2 RoPE table."""
+    n = len(k_caches)
+    nkv = (C.c_uint32 * n)(*n_head_kv)
+    p = C.c_uint32(pos)
+    check(load().lfm_hip_kv_cache_shift_sinks(_host_ptrs(k_caches), _host_ptrs(v_caches), n, nkv,
+                                              head_dim, _p(cos_lut), _p(sin_lut), lut_rows,
+                                              C.byref(p), n_sink, n_discard, stream),
+          "lfm_hip_kv_cache_shift_sinks")
+    return p.value
+
+
+def lfm3_kv_cache_shift_sinks(k_caches, v_caches, n_head_kv, layer_kind, head_dim: int,
+                              cos_full: Ptr, sin_full: Ptr, full_rows: int, cos_swa: Ptr,
+                              sin_swa: Ptr, swa_rows: int, sliding_window: int, swa_cap: int,
+                              pos: int, n_sink: int, n_discard: int, stream=None) -> int:
+    """lfm3_kv_cache_shift_sinks (tools/lfm2_runtime_features.c:1055-1163) on
+    device caches; layer_kind 0 = skipped, 1 = full, 2 = SWA ring.  Returns
+    the new position."""
+    n = len(k_caches)
+    nkv = (C.c_uint32 * n)(*n_head_kv)
+    kinds = (C.c_uint8 * n)(*layer_kind)
+    p = C.c_uint32(pos)
+    check(load().lfm_hip_lfm3_kv_cache_shift_sinks(
+        _host_ptrs(k_caches), _host_ptrs(v_caches), n, nkv, kinds, head_dim, _p(cos_full),
+        _p(sin_full), full_rows, _p(cos_swa), _p(sin_swa), swa_rows, sliding_window, swa_cap,
+        C.byref(p), n_sink, n_discard, stream), "lfm_hip_lfm3_kv_cache_shift_sinks")
+    return p.value
+
+
 def pointer_table(arrays: Sequence[Union["DeviceArray", int]]) -> DeviceArray:
     """Device array of device pointers (the k_seq / v_seq arguments)."""
     return DeviceArray.from_numpy(np.array([int(a) for a in arrays], dtype=np.uint64))
@@ -266,6 +304,14 @@ class EngineContext:
         n = kh.size // (self.n_head_kv * self.head_dim)
         check(load().lfm_attn_ctx_kv_import(self.h, layer, slot, n, kh.ctypes.data,
                                             vh.ctypes.data), "lfm_attn_ctx_kv_import")
+
+    def shift_sinks(self, pos, n_sink, n_discard):
+        """Attention-sink eviction over every layer (src/lfm2_api.c:871-891);
+        returns the new position."""
+        p = C.c_uint32(pos)
+        check(load().lfm_attn_ctx_shift_sinks(self.h, C.byref(p), n_sink, n_discard),
+              "lfm_attn_ctx_shift_sinks")
+        return p.value
 
     def close(self):
         if getattr(self, "h", None):

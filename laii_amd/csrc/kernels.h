@@ -65,6 +65,18 @@ int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *cons
                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
                         uint32_t cap, hipStream_t stream);
 
+/* Attention-sink eviction (kv_shift.hip).  launch_kv_shift moves rows
+ * [n_sink + n_discard, n_sink + n_discard + n_keep) down to n_sink and
+ * counter-rotates the keys; launch_kv_swa_repack re-slots an SWA ring
+ * window through the staging rows stage_k / stage_v ([n_valid][kv_dim]). */
+int launch_kv_shift(uint16_t *k, uint16_t *v, uint32_t kv_dim, uint32_t head_dim, uint32_t n_sink,
+                    uint32_t n_keep, uint32_t n_discard, const float *cos_row, const float *sin_row,
+                    hipStream_t stream);
+int launch_kv_swa_repack(uint16_t *k, uint16_t *v, uint32_t kv_dim, uint32_t head_dim, uint32_t cap,
+                         uint32_t t_start, uint32_t n_valid, uint32_t n_sink, uint32_t n_discard,
+                         const float *cos_row, const float *sin_row, uint16_t *stage_k,
+                         uint16_t *stage_v, hipStream_t stream);
+
 /* Events recorded around the main attention kernel (null when off). */
 void profile_events(hipEvent_t *before, hipEvent_t *after);
 

@@ -279,3 +279,40 @@ int lfm_attn_ctx_kv_device(lfm_attn_ctx *c, uint32_t layer, uint16_t **k_dev, ui
     if (n_slots) *n_slots = c->slots[layer];
     return LFM_ATTN_OK;
 }
+
+/* Attention-sink eviction over the context's layers: src/lfm2_api.c:871-891
+ * calls lfm3_kv_cache_shift_sinks for LFM3 and lfm2_kv_cache_shift_sinks for
+ * LFM2 with head_dim 64; the device entry points carry both. */
+int lfm_attn_ctx_shift_sinks(lfm_attn_ctx *c, uint32_t *inout_pos, uint32_t n_sink, uint32_t n_discard) {
+    if (!c || !inout_pos) return LFM_ATTN_E_INVALID;
+    const lfm_attn_geom *g = &c->g;
+    const uint32_t L = g->n_layers;
+    uint32_t *nkv = (uint32_t *)malloc(L * sizeof(uint32_t));
+    uint8_t *kind = (uint8_t *)malloc(L);
+    if (!nkv || !kind) {
+        free(nkv);
+        free(kind);
+        return LFM_ATTN_E_NOMEM;
+    }
+    for (uint32_t l = 0; l < L; ++l) {
+        nkv[l]  = g->n_head_kv;
+        kind[l] = c->is_swa[l] ? 2u : 1u;
+    }
+    int st;
+    if (!g->lfm3) {
+        st = lfm_hip_kv_cache_shift_sinks(c->k_cache, c->v_cache, L, nkv, g->head_dim, c->cos_full,
+                                          c->sin_full, g->max_seq, inout_pos, n_sink, n_discard,
+                                          c->stream);
+    } else {
+        const float *cs = c->cos_swa ? c->cos_swa : c->cos_full;
+        const float *ss = c->sin_swa ? c->sin_swa : c->sin_full;
+        st = lfm_hip_lfm3_kv_cache_shift_sinks(c->k_cache, c->v_cache, L, nkv, kind, g->head_dim,
+                                               c->cos_full, c->sin_full, g->max_seq, cs, ss, g->max_seq,
+                                               g->sliding_window, g->swa_cap, inout_pos, n_sink,
+                                               n_discard, c->stream);
+    }
+    free(nkv);
+    free(kind);
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    return st;
+}

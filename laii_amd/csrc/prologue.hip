@@ -24,6 +24,11 @@ namespace lfm {
 namespace {
 
 __device__ __forceinline__ uint16_t f16_rne(float x) {
+    /* x is first rounded to fp32 (the reference stores an fp32 result with
+     * _mm256_cvtps_ph): the barrier keeps the compiler from fusing a
+     * producing fma with this conversion into v_fma_mixlo_f16, whose single
+     * rounding differs from fp32-then-fp16 on ties */
+    asm volatile("" : "+v"(x));
     return __builtin_bit_cast(uint16_t, (_Float16)x); /* v_cvt_f16_f32, round-to-nearest-even */
 }
 

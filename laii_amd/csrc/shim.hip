@@ -339,4 +339,93 @@ int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                                n_head_kv, head_dim, scale, to_stream(stream));
 }
 
+/* ---- attention-sink eviction ------------------------------------------- */
+
+static inline int shift_caches_ok(uint16_t *const *k_caches, uint16_t *const *v_caches,
+                                  const uint32_t *n_head_kv, uint32_t n_layers) {
+    if (!k_caches || !v_caches || !n_head_kv) return 0;
+    for (uint32_t l = 0; l < n_layers; ++l)
+        if ((k_caches[l] && !aligned16(k_caches[l])) || (v_caches[l] && !aligned16(v_caches[l])))
+            return 0;
+    return 1;
+}
+
+int lfm_hip_kv_cache_shift_sinks(uint16_t *const *k_caches, uint16_t *const *v_caches,
+                                 uint32_t n_layers, const uint32_t *n_head_kv, uint32_t head_dim,
+                                 const float *cos_lut, const float *sin_lut, uint32_t lut_rows,
+                                 uint32_t *inout_pos, uint32_t n_sink, uint32_t n_discard,
+                                 lfm_attn_stream_t stream) {
+    if (!inout_pos) return LFM_ATTN_E_INVALID;
+    const uint32_t cur = *inout_pos;
+    /* tools/lfm2_runtime_features.c:752-758: no-op cases keep the position */
+    if (n_discard == 0u || (uint64_t)cur <= (uint64_t)n_sink + n_discard) return LFM_ATTN_OK;
+    if (head_dim != 64u) return LFM_ATTN_OK;
+    if (!shift_caches_ok(k_caches, v_caches, n_head_kv, n_layers) || !cos_lut || !sin_lut)
+        return LFM_ATTN_E_INVALID;
+    if (n_discard >= lut_rows) return LFM_ATTN_E_RANGE;
+    const uint32_t n_keep = cur - n_sink - n_discard;
+    const hipStream_t st = to_stream(stream);
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (!k_caches[l] || !v_caches[l] || n_head_kv[l] == 0u) continue; /* ShortConv layer */
+        const int r = lfm::launch_kv_shift(k_caches[l], v_caches[l], n_head_kv[l] * 64u, 64u, n_sink,
+                                           n_keep, n_discard, cos_lut + (size_t)n_discard * 32u,
+                                           sin_lut + (size_t)n_discard * 32u, st);
+        if (r != LFM_ATTN_OK) return r;
+    }
+    *inout_pos = n_sink + n_keep;
+    return LFM_ATTN_OK;
+}
+
+int lfm_hip_lfm3_kv_cache_shift_sinks(uint16_t *const *k_caches, uint16_t *const *v_caches,
+                                      uint32_t n_layers, const uint32_t *n_head_kv,
+                                      const uint8_t *layer_kind, uint32_t head_dim,
+                                      const float *cos_full, const float *sin_full,
+                                      uint32_t full_rows, const float *cos_swa,
+                                      const float *sin_swa, uint32_t swa_rows,
+                                      uint32_t sliding_window, uint32_t swa_cap,
+                                      uint32_t *inout_pos, uint32_t n_sink, uint32_t n_discard,
+                                      lfm_attn_stream_t stream) {
+    if (!inout_pos || !cos_full || !sin_full || !cos_swa || !sin_swa) return LFM_ATTN_E_INVALID;
+    const uint32_t cur = *inout_pos;
+    /* tools/lfm2_runtime_features.c:1066-1073: no-op cases keep the position */
+    if (n_discard == 0u || (uint64_t)cur <= (uint64_t)n_sink + n_discard) return LFM_ATTN_OK;
+    if (n_discard >= full_rows || n_discard >= swa_rows) return LFM_ATTN_OK;
+    if (head_dim % 2u != 0u) return LFM_ATTN_OK;
+    if (head_dim % 16u != 0u || head_dim > 256u) return LFM_ATTN_E_UNSUPPORTED;
+    if (!layer_kind || !shift_caches_ok(k_caches, v_caches, n_head_kv, n_layers))
+        return LFM_ATTN_E_INVALID;
+    const uint32_t half    = head_dim / 2u;
+    const uint32_t n_keep  = cur - (n_sink + n_discard);
+    const uint32_t new_pos = n_sink + n_keep;
+    const uint32_t swa_win = sliding_window > 0u ? sliding_window : 256u;
+    const uint32_t cap     = swa_cap > 0u ? swa_cap : swa_win + 8u;
+    if (cap < swa_win) return LFM_ATTN_E_INVALID;
+    const hipStream_t st = to_stream(stream);
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (layer_kind[l] == 0u || !k_caches[l] || !v_caches[l] || n_head_kv[l] == 0u) continue;
+        const uint32_t kv_dim = n_head_kv[l] * head_dim;
+        int r;
+        if (layer_kind[l] == 2u) {
+            /* :1101-1135: re-slot the window [new_pos - window, new_pos) */
+            const uint32_t t0      = new_pos > swa_win ? new_pos - swa_win : 0u;
+            const uint32_t n_valid = new_pos - t0;
+            int ws_st = LFM_ATTN_OK;
+            uint16_t *stage = (uint16_t *)lfm::workspace((size_t)2u * n_valid * kv_dim * sizeof(uint16_t),
+                                                         st, &ws_st);
+            if (!stage) return ws_st;
+            r = lfm::launch_kv_swa_repack(k_caches[l], v_caches[l], kv_dim, head_dim, cap, t0, n_valid,
+                                          n_sink, n_discard, cos_swa + (size_t)n_discard * half,
+                                          sin_swa + (size_t)n_discard * half, stage,
+                                          stage + (size_t)n_valid * kv_dim, st);
+        } else {
+            r = lfm::launch_kv_shift(k_caches[l], v_caches[l], kv_dim, head_dim, n_sink, n_keep,
+                                     n_discard, cos_full + (size_t)n_discard * half,
+                                     sin_full + (size_t)n_discard * half, st);
+        }
+        if (r != LFM_ATTN_OK) return r;
+    }
+    *inout_pos = new_pos;
+    return LFM_ATTN_OK;
+}
+
 } /* extern "C" */

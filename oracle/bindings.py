@@ -30,6 +30,33 @@ def _opt(arr, ptr_type):
     return None if arr is None else arr.ctypes.data_as(ptr_type)
 
 
+def _cache_ptrs(caches):
+    """Host pointer array over per-layer uint16 caches (None = skipped layer)."""
+    for c in caches:
+        assert c is None or (c.dtype == np.uint16 and c.flags.c_contiguous)
+    return (C.c_void_p * len(caches))(*[None if c is None else c.ctypes.data for c in caches])
+
+
+def _shift_lfm2(fn, k_caches, v_caches, n_head_kv, head_dim, cos_lut, sin_lut, pos, n_sink,
+                n_discard, with_rows):
+    n = len(k_caches)
+    args = [_cache_ptrs(k_caches), _cache_ptrs(v_caches), n, (_u32 * n)(*n_head_kv), head_dim,
+            cos_lut.ctypes.data, sin_lut.ctypes.data]
+    if with_rows:
+        args.append(cos_lut.shape[0])
+    return fn(*args, pos, n_sink, n_discard)
+
+
+def _shift_lfm3(fn, k_caches, v_caches, n_head_kv, layer_kind, head_dim, lut_full, lut_swa,
+                sliding_window, swa_cap, pos, n_sink, n_discard):
+    n = len(k_caches)
+    (cf, sf), (cw, sw) = lut_full, lut_swa
+    return fn(_cache_ptrs(k_caches), _cache_ptrs(v_caches), n, (_u32 * n)(*n_head_kv),
+              (C.c_uint8 * n)(*layer_kind), head_dim, cf.ctypes.data, sf.ctypes.data, cf.shape[0],
+              cw.ctypes.data, sw.ctypes.data, cw.shape[0], sliding_window, swa_cap, pos, n_sink,
+              n_discard)
+
+
 class Oracle:
     """Scalar C11 restatement of the reference attention path."""
 
@@ -59,6 +86,25 @@ class Oracle:
         L.orc_causal_rows_f16.argtypes = [_f32p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32, _u32]
         L.orc_decode_batch_mt.argtypes = [_f32p, C.c_void_p, C.c_void_p, _u32p, _f32p, _u32, _u32,
                                           _u32, _u32, _u32]
+        L.orc_kv_shift_sinks_lfm2.restype = _u32
+        L.orc_kv_shift_sinks_lfm2.argtypes = [C.c_void_p, C.c_void_p, _u32, C.c_void_p, _u32,
+                                              C.c_void_p, C.c_void_p, _u32, _u32, _u32]
+        L.orc_kv_shift_sinks_lfm3.restype = _u32
+        L.orc_kv_shift_sinks_lfm3.argtypes = [C.c_void_p, C.c_void_p, _u32, C.c_void_p, C.c_void_p,
+                                              _u32, C.c_void_p, C.c_void_p, _u32, C.c_void_p,
+                                              C.c_void_p, _u32, _u32, _u32, _u32, _u32, _u32]
+
+    # -- attention-sink eviction (caches modified in place) --------------------
+    def kv_shift_sinks_lfm2(self, k_caches, v_caches, n_head_kv, head_dim, lut, pos, n_sink,
+                            n_discard):
+        return _shift_lfm2(self.lib.orc_kv_shift_sinks_lfm2, k_caches, v_caches, n_head_kv,
+                           head_dim, lut[0], lut[1], pos, n_sink, n_discard, False)
+
+    def kv_shift_sinks_lfm3(self, k_caches, v_caches, n_head_kv, layer_kind, head_dim, lut_full,
+                            lut_swa, sliding_window, swa_cap, pos, n_sink, n_discard):
+        return _shift_lfm3(self.lib.orc_kv_shift_sinks_lfm3, k_caches, v_caches, n_head_kv,
+                           layer_kind, head_dim, lut_full, lut_swa, sliding_window, swa_cap, pos,
+                           n_sink, n_discard)
 
     # -- fp16 -----------------------------------------------------------------
     def f32_to_f16(self, x: np.ndarray) -> np.ndarray:
@@ -195,7 +241,25 @@ class Reference:
         L.ref_time_decode_batch.restype = C.c_double
         L.ref_time_decode_batch.argtypes = [_f32p, C.c_void_p, C.c_void_p, _u32p, _f32p, _u32,
                                             _u32, _u32, _u32, _u32, C.POINTER(_u32)]
+        L.ref_kv_shift_sinks_lfm2.restype = _u32
+        L.ref_kv_shift_sinks_lfm2.argtypes = [C.c_void_p, C.c_void_p, _u32, C.c_void_p, _u32,
+                                              C.c_void_p, C.c_void_p, _u32, _u32, _u32, _u32]
+        L.ref_kv_shift_sinks_lfm3.restype = _u32
+        L.ref_kv_shift_sinks_lfm3.argtypes = [C.c_void_p, C.c_void_p, _u32, C.c_void_p, C.c_void_p,
+                                              _u32, C.c_void_p, C.c_void_p, _u32, C.c_void_p,
+                                              C.c_void_p, _u32, _u32, _u32, _u32, _u32, _u32]
         self.has_avx2 = bool(L.ref_has_avx2())
+
+    def kv_shift_sinks_lfm2(self, k_caches, v_caches, n_head_kv, head_dim, lut, pos, n_sink,
+                            n_discard):
+        return _shift_lfm2(self.lib.ref_kv_shift_sinks_lfm2, k_caches, v_caches, n_head_kv,
+                           head_dim, lut[0], lut[1], pos, n_sink, n_discard, True)
+
+    def kv_shift_sinks_lfm3(self, k_caches, v_caches, n_head_kv, layer_kind, head_dim, lut_full,
+                            lut_swa, sliding_window, swa_cap, pos, n_sink, n_discard):
+        return _shift_lfm3(self.lib.ref_kv_shift_sinks_lfm3, k_caches, v_caches, n_head_kv,
+                           layer_kind, head_dim, lut_full, lut_swa, sliding_window, swa_cap, pos,
+                           n_sink, n_discard)
 
     def rope_lut_lfm2(self, max_seq, head_dim, base):
         c = np.empty((max_seq, head_dim // 2), np.float32)

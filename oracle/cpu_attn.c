@@ -17,6 +17,11 @@
  *                                     vectors under tests/golden/.
  *   orc_lfm3_plan / orc_lfm3_slots   : brute-force window enumeration.
  *   orc_gen1_gqa_attend              : tests/fixtures_attention.bin (PyTorch).
+ *   orc_kv_shift_sinks_lfm2 / _lfm3  : reference AVX2 shift kernels
+ *                                     (oracle/_ref, bit-exact), rotation
+ *                                     composition R(-d)R(p) = R(p-d) against
+ *                                     keys roped at the new position, values
+ *                                     moved unchanged, no-op cases.
  */
 #define _GNU_SOURCE
 #include "cpu_attn.h"
@@ -474,6 +479,110 @@ static void *orc_batch_worker(void *arg) {
         }
     }
     return NULL;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Attention-sink eviction.  Counter-rotation of one key head by the table row
+ * (c, s) of position n_discard: lfm3_counter_rotate_key_head_avx2
+ * (tools/lfm2_runtime_features.c:1026-1051) and the inline AVX2 loop of
+ * lfm2_kv_cache_shift_sinks_avx2 (:784-828) -- fmadd(lo, c, hi*s) and
+ * fmsub(hi, c, lo*s), RNE store. */
+static void orc_counter_rotate(uint16_t *kh, uint32_t head_dim, const float *c, const float *s) {
+    const uint32_t half = head_dim / 2u;
+    for (uint32_t i = 0; i < half; ++i) {
+        const float lo = orc_f16_to_f32(kh[i]), hi = orc_f16_to_f32(kh[i + half]);
+        const float hs = hi * s[i], ls = lo * s[i];
+        kh[i]        = orc_f32_to_f16(fmaf(lo, c[i], hs));
+        kh[i + half] = orc_f32_to_f16(fmaf(hi, c[i], -ls));
+    }
+}
+
+/* Linear-cache shift of one layer: memmove of values and keys, then every
+ * moved key counter-rotated (tools/lfm2_runtime_features.c:769-829). */
+static void orc_shift_linear(uint16_t *kc, uint16_t *vc, size_t kv_dim, uint32_t head_dim,
+                             uint32_t n_heads, uint32_t n_sink, uint32_t n_keep,
+                             uint32_t n_discard, const float *c, const float *s) {
+    memmove(vc + (size_t)n_sink * kv_dim, vc + (size_t)(n_sink + n_discard) * kv_dim,
+            (size_t)n_keep * kv_dim * sizeof(uint16_t));
+    memmove(kc + (size_t)n_sink * kv_dim, kc + (size_t)(n_sink + n_discard) * kv_dim,
+            (size_t)n_keep * kv_dim * sizeof(uint16_t));
+    for (uint32_t t = n_sink; t < n_sink + n_keep; ++t)
+        for (uint32_t h = 0; h < n_heads; ++h)
+            orc_counter_rotate(kc + (size_t)t * kv_dim + (size_t)h * head_dim, head_dim, c, s);
+}
+
+/* lfm2_kv_cache_shift_sinks_avx2, tools/lfm2_runtime_features.c:744-833. */
+uint32_t orc_kv_shift_sinks_lfm2(uint16_t **k_caches, uint16_t **v_caches, uint32_t n_layers,
+                                 const uint32_t *n_head_kv, uint32_t head_dim,
+                                 const float *cos_lut, const float *sin_lut, uint32_t pos,
+                                 uint32_t n_sink, uint32_t n_discard) {
+    if (n_discard == 0u || pos <= n_sink + n_discard) return pos; /* :752 */
+    if (head_dim != 64u) return pos;                                /* :755-758 */
+    const uint32_t n_keep = pos - (n_sink + n_discard);
+    const float *c = cos_lut + (size_t)n_discard * 32u, *s = sin_lut + (size_t)n_discard * 32u;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (!k_caches[l] || !v_caches[l] || n_head_kv[l] == 0u) continue;
+        orc_shift_linear(k_caches[l], v_caches[l], (size_t)n_head_kv[l] * 64u, 64u, n_head_kv[l],
+                         n_sink, n_keep, n_discard, c, s);
+    }
+    return n_sink + n_keep;
+}
+
+/* lfm3_kv_cache_shift_sinks, tools/lfm2_runtime_features.c:1055-1163. */
+uint32_t orc_kv_shift_sinks_lfm3(uint16_t **k_caches, uint16_t **v_caches, uint32_t n_layers,
+                                 const uint32_t *n_head_kv, const uint8_t *layer_kind,
+                                 uint32_t head_dim, const float *cos_full, const float *sin_full,
+                                 uint32_t full_rows, const float *cos_swa, const float *sin_swa,
+                                 uint32_t swa_rows, uint32_t sliding_window, uint32_t swa_cap,
+                                 uint32_t pos, uint32_t n_sink, uint32_t n_discard) {
+    if (n_discard == 0u || pos <= n_sink + n_discard) return pos;   /* :1067 */
+    if (n_discard >= full_rows || n_discard >= swa_rows) return pos; /* :1068 */
+    if (head_dim % 2u != 0u) return pos;                            /* :1072 */
+    const uint32_t half    = head_dim / 2u;
+    const uint32_t n_keep  = pos - (n_sink + n_discard);
+    const uint32_t new_pos = n_sink + n_keep;
+    const uint32_t win     = sliding_window > 0u ? sliding_window : 256u;
+    const uint32_t cap     = swa_cap > 0u ? swa_cap : win + 8u;
+    const float *cf = cos_full + (size_t)n_discard * half, *sf = sin_full + (size_t)n_discard * half;
+    const float *cw = cos_swa + (size_t)n_discard * half, *sw = sin_swa + (size_t)n_discard * half;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (layer_kind[l] == 0u || !k_caches[l] || !v_caches[l] || n_head_kv[l] == 0u) continue;
+        uint16_t *kc = k_caches[l], *vc = v_caches[l];
+        const size_t kv_dim = (size_t)n_head_kv[l] * head_dim;
+        if (layer_kind[l] == 2u) {
+            /* :1101-1135: gather the new window through temporaries, then
+             * store each position at its new ring slot */
+            const uint32_t t0 = new_pos > win ? new_pos - win : 0u;
+            const uint32_t n_valid = new_pos - t0;
+            uint16_t *tk = (uint16_t *)malloc((size_t)n_valid * kv_dim * sizeof(uint16_t));
+            uint16_t *tv = (uint16_t *)malloc((size_t)n_valid * kv_dim * sizeof(uint16_t));
+            if (!tk || !tv) {
+                free(tk);
+                free(tv);
+                continue;
+            }
+            for (uint32_t i = 0; i < n_valid; ++i) {
+                const uint32_t t = t0 + i;
+                const int kept = t >= n_sink;
+                const uint32_t so = (kept ? t + n_discard : t) % cap;
+                memcpy(tk + (size_t)i * kv_dim, kc + (size_t)so * kv_dim, kv_dim * sizeof(uint16_t));
+                memcpy(tv + (size_t)i * kv_dim, vc + (size_t)so * kv_dim, kv_dim * sizeof(uint16_t));
+                if (kept)
+                    for (uint32_t h = 0; h < n_head_kv[l]; ++h)
+                        orc_counter_rotate(tk + (size_t)i * kv_dim + (size_t)h * head_dim, head_dim, cw, sw);
+            }
+            for (uint32_t i = 0; i < n_valid; ++i) {
+                const uint32_t sn = (t0 + i) % cap;
+                memcpy(kc + (size_t)sn * kv_dim, tk + (size_t)i * kv_dim, kv_dim * sizeof(uint16_t));
+                memcpy(vc + (size_t)sn * kv_dim, tv + (size_t)i * kv_dim, kv_dim * sizeof(uint16_t));
+            }
+            free(tk);
+            free(tv);
+        } else {
+            orc_shift_linear(kc, vc, kv_dim, head_dim, n_head_kv[l], n_sink, n_keep, n_discard, cf, sf);
+        }
+    }
+    return new_pos;
 }
 
 void orc_decode_batch_mt(const float *q, const uint16_t *const *k_seq,

@@ -75,6 +75,23 @@ void orc_causal_rows_f16(const float *q_rows, const uint16_t *k_cache_f16,
                          uint32_t n_rows, uint32_t pos_0, uint32_t n_head_q,
                          uint32_t n_head_kv, uint32_t head_dim);
 
+/* ---- Next row: attention-sink eviction with RoPE counter-rotation ------- */
+/* Host caches: k_caches[l] / v_caches[l] are [rows][n_head_kv[l] * head_dim]
+ * fp16 bits (NULL or n_head_kv[l] == 0 = skipped layer); the LUTs are the
+ * engine tables ([rows][head_dim / 2]).  Both return the new position.  The
+ * rotation follows the AVX2 kernels (the default x86 build): lo' =
+ * fma(lo, c, hi*s), hi' = fma(hi, c, -(lo*s)), RNE fp16. */
+uint32_t orc_kv_shift_sinks_lfm2(uint16_t **k_caches, uint16_t **v_caches, uint32_t n_layers,
+                                 const uint32_t *n_head_kv, uint32_t head_dim,
+                                 const float *cos_lut, const float *sin_lut, uint32_t pos,
+                                 uint32_t n_sink, uint32_t n_discard);
+uint32_t orc_kv_shift_sinks_lfm3(uint16_t **k_caches, uint16_t **v_caches, uint32_t n_layers,
+                                 const uint32_t *n_head_kv, const uint8_t *layer_kind,
+                                 uint32_t head_dim, const float *cos_full, const float *sin_full,
+                                 uint32_t full_rows, const float *cos_swa, const float *sin_swa,
+                                 uint32_t swa_rows, uint32_t sliding_window, uint32_t swa_cap,
+                                 uint32_t pos, uint32_t n_sink, uint32_t n_discard);
+
 /* ---- Multi-threaded drivers (CPU baseline "port") ---------------------- */
 /* Batched decode over n_seq independent caches; work items are
  * (sequence, 4-head group) pairs spread over n_threads pthreads. */

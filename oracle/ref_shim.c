@@ -21,7 +21,9 @@
 #define LFM2_PREFILL_BATCH_NO_MAIN 1
 #define LFM2_SPECULATIVE_PLD_NO_MAIN 1
 #define LFM3_ENGINE_NO_MAIN 1
+#define LFM2_RUNTIME_FEATURES_NO_MAIN 1
 #include "tools/lfm3_engine.c"
+#include "tools/lfm2_runtime_features.c"
 
 #include <sched.h>
 #include <time.h>
@@ -234,4 +236,67 @@ double ref_time_decode_batch(const float *q, const uint16_t *const *k_seq,
     lfm2_threadpool_free(&pool);
     shim_restore(&st);
     return best;
+}
+
+/* ---- attention-sink eviction ------------------------------------------ */
+/* A model description carrying only what the shift functions read:
+ * n_layers, head_dim (n_embd / n_head_q for LFM2), n_head_kv, sliding_window
+ * and each layer's block type. */
+static LFM2Model *shim_model(uint32_t n_layers, const uint32_t *n_head_kv,
+                             const uint8_t *layer_kind, uint32_t head_dim,
+                             uint32_t sliding_window) {
+    if (n_layers > LFM2_MAX_LAYERS) return NULL;
+    LFM2Model *m = (LFM2Model *)calloc(1, sizeof *m);
+    if (!m) return NULL;
+    m->cfg.n_layers       = n_layers;
+    m->cfg.n_head_q       = 1;
+    m->cfg.n_embd         = head_dim;
+    m->cfg.head_dim       = head_dim;
+    m->cfg.sliding_window = sliding_window;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        m->cfg.n_head_kv[l] = n_head_kv[l];
+        const uint8_t kind  = layer_kind ? layer_kind[l] : (n_head_kv[l] ? 1u : 0u);
+        m->layers[l].block_type = kind == 0u ? LFM2_BLOCK_SHORTCONV
+                                : kind == 2u ? LFM2_BLOCK_SWA_ATTN : LFM2_BLOCK_GQA_ATTN;
+    }
+    return m;
+}
+
+/* lfm2_kv_cache_shift_sinks_avx2, tools/lfm2_runtime_features.c:744-833 */
+uint32_t ref_kv_shift_sinks_lfm2(uint16_t **k_caches, uint16_t **v_caches, uint32_t n_layers,
+                                 const uint32_t *n_head_kv, uint32_t head_dim, float *cos_lut,
+                                 float *sin_lut, uint32_t lut_rows, uint32_t pos, uint32_t n_sink,
+                                 uint32_t n_discard) {
+    LFM2Model *m = shim_model(n_layers, n_head_kv, NULL, head_dim, 0);
+    if (!m) return 0xFFFFFFFFu;
+    uint16_t *kc[LFM2_MAX_LAYERS] = {0}, *vc[LFM2_MAX_LAYERS] = {0};
+    for (uint32_t l = 0; l < n_layers; ++l) { kc[l] = k_caches[l]; vc[l] = v_caches[l]; }
+    LFM2RoPELUT lut = {lut_rows, head_dim / 2u, cos_lut, sin_lut};
+    shim_state st;
+    shim_save(&st);
+    lfm2_kv_cache_shift_sinks_avx2(kc, vc, m, &lut, &pos, n_sink, n_discard);
+    shim_restore(&st);
+    free(m);
+    return pos;
+}
+
+/* lfm3_kv_cache_shift_sinks, tools/lfm2_runtime_features.c:1055-1163 */
+uint32_t ref_kv_shift_sinks_lfm3(uint16_t **k_caches, uint16_t **v_caches, uint32_t n_layers,
+                                 const uint32_t *n_head_kv, const uint8_t *layer_kind,
+                                 uint32_t head_dim, float *cos_full, float *sin_full,
+                                 uint32_t full_rows, float *cos_swa, float *sin_swa,
+                                 uint32_t swa_rows, uint32_t sliding_window, uint32_t swa_cap,
+                                 uint32_t pos, uint32_t n_sink, uint32_t n_discard) {
+    LFM2Model *m = shim_model(n_layers, n_head_kv, layer_kind, head_dim, sliding_window);
+    if (!m) return 0xFFFFFFFFu;
+    uint16_t *kc[LFM2_MAX_LAYERS] = {0}, *vc[LFM2_MAX_LAYERS] = {0};
+    for (uint32_t l = 0; l < n_layers; ++l) { kc[l] = k_caches[l]; vc[l] = v_caches[l]; }
+    LFM2RoPELUT lf = {full_rows, head_dim / 2u, cos_full, sin_full};
+    LFM2RoPELUT ls = {swa_rows, head_dim / 2u, cos_swa, sin_swa};
+    shim_state st;
+    shim_save(&st);
+    lfm3_kv_cache_shift_sinks(kc, vc, m, &lf, &ls, swa_cap, &pos, n_sink, n_discard);
+    shim_restore(&st);
+    free(m);
+    return pos;
 }

@@ -123,3 +123,40 @@ def test_context_rejects_bad_geometry():
     g.sliding_window, g.swa_cap = 256, 200
     assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # window > ring
     assert lib.lfm_attn_ctx_forward(None, 0, 0, 1, FAKE, FAKE, FAKE, None, FAKE) == E_INVALID
+
+
+def test_shift_sinks_validation_before_launch():
+    """Sink-shift entry points: no-op cases return OK with the position kept,
+    bad arguments are rejected, all before any device access."""
+    lib = la.load()
+    ptrs = (C.c_void_p * 2)(FAKE, FAKE)
+    nkv = (C.c_uint32 * 2)(8, 8)
+    kinds = (C.c_uint8 * 2)(1, 2)
+    p = C.c_uint32(10)
+    shift2 = lib.lfm_hip_kv_cache_shift_sinks
+    shift3 = lib.lfm_hip_lfm3_kv_cache_shift_sinks
+    assert shift2(ptrs, ptrs, 2, nkv, 64, FAKE, FAKE, 100, C.byref(p), 4, 8, None) == 0
+    assert p.value == 10                                     # pos <= n_sink + n_discard
+    p.value = 50
+    assert shift2(ptrs, ptrs, 2, nkv, 64, FAKE, FAKE, 100, C.byref(p), 4, 0, None) == 0
+    assert p.value == 50                                     # n_discard == 0
+    assert shift2(ptrs, ptrs, 2, nkv, 128, FAKE, FAKE, 100, C.byref(p), 4, 8, None) == 0
+    assert p.value == 50                                     # LFM2 shifts head_dim 64 only
+    assert shift2(ptrs, ptrs, 2, nkv, 64, FAKE, FAKE, 100, None, 4, 8, None) == E_INVALID
+    p.value = 300
+    assert shift2(ptrs, ptrs, 2, nkv, 64, FAKE, FAKE, 100, C.byref(p), 4, 150, None) == E_RANGE
+    assert shift2(None, ptrs, 2, nkv, 64, FAKE, FAKE, 400, C.byref(p), 4, 150, None) == E_INVALID
+    odd = (C.c_void_p * 2)(FAKE + 2, FAKE)                   # misaligned cache
+    assert shift2(odd, ptrs, 2, nkv, 64, FAKE, FAKE, 400, C.byref(p), 4, 150, None) == E_INVALID
+    assert p.value == 300
+    # LFM3: rows of either table too few -> no-op; head_dim 72 unsupported; window > ring
+    assert shift3(ptrs, ptrs, 2, nkv, kinds, 128, FAKE, FAKE, 100, FAKE, FAKE, 400, 16, 24,
+                  C.byref(p), 4, 150, None) == 0 and p.value == 300
+    assert shift3(ptrs, ptrs, 2, nkv, kinds, 72, FAKE, FAKE, 400, FAKE, FAKE, 400, 16, 24,
+                  C.byref(p), 4, 150, None) == -3
+    assert shift3(ptrs, ptrs, 2, nkv, kinds, 128, FAKE, FAKE, 400, FAKE, FAKE, 400, 32, 24,
+                  C.byref(p), 4, 150, None) == E_INVALID
+    assert shift3(ptrs, ptrs, 2, nkv, kinds, 128, None, FAKE, 400, FAKE, FAKE, 400, 16, 24,
+                  C.byref(p), 4, 150, None) == E_INVALID
+    assert p.value == 300
+    assert lib.lfm_attn_ctx_shift_sinks(None, C.byref(p), 4, 8) == E_INVALID
