@@ -20,10 +20,12 @@
  *
  * Compute runs in 32-key steps, software pipelined so that each step's
  * basic block holds independent MFMA and VALU work:
- *   S^T(k+1) = K . Q^T - m   16x16x32 f16 MFMA; the running max enters as
- *                            the accumulator's initial value
- *   p = exp2(S^T(k))         lazy max: raised only when a step exceeds it by
- *                            more than 2^8 (fp16 P stays finite), which
+ *   S^T(k+1) = K . Q^T - m   16x16x32 f16 MFMA on Q*scale (exact in fp16
+ *                            for d = 64); the running max enters as the
+ *                            accumulator's initial value
+ *   p = exp(S^T(k))          exp2(s * log2 e) in fp32.  Lazy max: raised
+ *                            only when a step exceeds it by more than
+ *                            8 ln 2 (P <= 2^8, fp16 P stays finite), which
  *                            rescales O and l in a rare uniform branch
  *   l += p                   v_dot2_f32_f16 over the fp16 P fed to the MFMA
  *   O^T += V^T . P^T(k)      V^T fragments read transposed from row-major V
@@ -54,7 +56,8 @@ constexpr int SB        = 32;          /* keys per compute step                 
 constexpr int NBUF      = 3;           /* LDS ring of K/V blocks                   */
 constexpr int ROWB      = 128;         /* bytes per K/V row of one head (d = 64)   */
 constexpr int BLKB      = KB * ROWB;   /* bytes per K (or V) block                 */
-constexpr float kLazy   = 8.0f;        /* log2 headroom before the max is raised   */
+constexpr float kLn2    = 0.6931471805599453f;
+constexpr float kLazy   = 8.0f * kLn2; /* headroom (natural log units, = 2^8 in P)  */
 
 struct PrefillParams {
     const uint16_t *q;  /* [n_seq][n_tok][n_head_q][HD] fp16 */
@@ -63,7 +66,7 @@ struct PrefillParams {
     float *out;         /* [n_seq][n_tok][n_head_q][HD] */
     uint64_t kv_seq_stride;
     uint32_t n_seq, n_tok, pos_0, n_head_q, n_head_kv, kv_mul, tq, n_qtiles;
-    float qscale;       /* scale * log2(e) */
+    float scale;        /* softmax scale, applied to Q before its fp16 rounding */
 };
 
 __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
@@ -72,10 +75,11 @@ __device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-/* exp2 of two scores packed to fp16 (round toward zero) */
-__device__ __forceinline__ half2_t exp2_pk(float a, float b) {
-    return __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(__builtin_amdgcn_exp2f(a),
-                                                                  __builtin_amdgcn_exp2f(b)));
+/* exp of two scores (natural log units, as exp2 of x * log2(e) in fp32),
+ * packed to fp16 with round toward zero */
+__device__ __forceinline__ half2_t exp_pk(float a, float b) {
+    return __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(__builtin_amdgcn_exp2f(a * kLog2e),
+                                                                  __builtin_amdgcn_exp2f(b * kLog2e)));
 }
 
 /* transposing LDS read: within each 16-lane group, lane l receives element
@@ -130,12 +134,13 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
             u32x4_t raw = col_ok[nt] ? *reinterpret_cast<const u32x4_t *>(qp + 32 * st) : (u32x4_t)0u;
             half8_t h   = as_half8(raw);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (_Float16)((float)h[e] * P.qscale);
+            for (int e = 0; e < 8; ++e) h[e] = (_Float16)((float)h[e] * P.scale);
             qf[nt][st] = h;
         }
     }
-    /* q*scale*log2(e) is rounded to fp16 once (relative error <= 2^-11 per
-     * element), which keeps the score accumulator in log2 units */
+    /* q*scale is exact in fp16 for the power-of-two scale of d = 64 (0.125):
+     * the score accumulator holds q.k in natural log units at fp32 accuracy,
+     * and log2(e) is applied in fp32 inside the exponential */
     const uint32_t lo_pos = P.pos_0 + t0;                               /* smallest query position */
     const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;     /* largest query position  */
     const uint32_t n_keys = hi_pos + 1u;
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 v = fmaxf(v, __shfl_xor(v, 32));
                 const bool raise  = FIRST ? (v > -INFINITY) : (v > kLazy);
                 const float inc   = raise ? v : 0.0f;
-                const float alpha = __builtin_amdgcn_exp2f(-inc);
+                const float alpha = __builtin_amdgcn_exp2f(-inc * kLog2e);
                 negm[nt] -= inc;
                 l[nt] *= alpha;
                 sc[0][nt] -= inc;
@@ -268,10 +273,10 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
             const float4_t a = sc[0][nt], c = sc[1][nt];
             /* scalar temporaries: a bit_cast of an ext-vector element was
              * miscompiled into four reads of element 0 */
-            const half2_t h0 = exp2_pk(a[0], a[1]);
-            const half2_t h1 = exp2_pk(a[2], a[3]);
-            const half2_t h2 = exp2_pk(c[0], c[1]);
-            const half2_t h3 = exp2_pk(c[2], c[3]);
+            const half2_t h0 = exp_pk(a[0], a[1]);
+            const half2_t h1 = exp_pk(a[2], a[3]);
+            const half2_t h2 = exp_pk(c[0], c[1]);
+            const half2_t h3 = exp_pk(c[2], c[3]);
             float lsum = l[nt];
             lsum = __builtin_amdgcn_fdot2(h0, ones, lsum, false);
             lsum = __builtin_amdgcn_fdot2(h1, ones, lsum, false);
@@ -380,7 +385,7 @@ int launch_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, floa
     P.kv_mul = n_head_q / n_head_kv;
     P.tq = 256u / P.kv_mul;
     P.n_qtiles = (n_tok + P.tq - 1u) / P.tq;
-    P.qscale = scale * kLog2e;
+    P.scale = scale;
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);

@@ -87,3 +87,39 @@ def test_prefill_rejects_unsupported(gpu):
     o = la.DeviceArray.zeros(1 << 16, np.float32)
     assert lib.lfm_hip_prefill_f16(a.ptr, a.ptr, a.ptr, o.ptr, 1, 8, 0, 0, 8, 2, 128, 0.088,
                                    None) == -3
+
+
+@pytest.mark.parametrize("pattern", ["rising", "spike", "falling"])
+def test_prefill_lazy_max_raises(gpu, orc, pattern):
+    """Score patterns that force the lazy running max to be raised after the
+    first step (and in masked diagonal steps): keys whose scores climb by tens
+    of log2 units along the sequence ("rising"), isolated huge scores
+    ("spike"), and a large first block followed by tiny ones ("falling").
+    Against the oracle's causal rows."""
+    la = gpu
+    rng = np.random.default_rng({"rising": 1, "spike": 2, "falling": 3}[pattern])
+    n_seq, n_tok, nq, nkv, hd = 1, 300, 16, 4, 64
+    q = rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32)
+    k = rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * 0.5
+    # a shared direction so that every query scores each key by its scale
+    u = rng.standard_normal(hd).astype(np.float32)
+    u /= np.linalg.norm(u)
+    q += 3.0 * u
+    t = np.arange(n_tok, dtype=np.float32)
+    if pattern == "rising":
+        amp = 0.25 * t          # scores grow ~ 0.125 * 3 * 0.25 t: +28 log2 units by the end
+    elif pattern == "spike":
+        amp = np.where(t % 97 == 40, 60.0, 0.0).astype(np.float32)
+    else:
+        amp = np.where(t < 64, 40.0, 0.0).astype(np.float32)
+    k += amp[None, :, None, None] * u
+    q16 = f16(q)
+    k16 = f16(k)
+    v16 = f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32))
+    out = la.DeviceArray.zeros((n_seq, n_tok, nq, hd), np.float32)
+    la.prefill_f16(dev(la, q16), dev(la, k16), dev(la, v16), out, n_seq, n_tok, 0,
+                   n_tok * nkv * hd, nq, nkv, hd)
+    got = out.numpy()
+    assert np.all(np.isfinite(got))
+    want = oracle_rows(orc, q16, k16, v16, 0, range(n_tok), 0, nq, nkv)
+    parity(got[0], want, what=f"prefill lazy max {pattern}")
