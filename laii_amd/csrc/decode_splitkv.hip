@@ -472,7 +472,10 @@ void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, ui
     const uint64_t target = 4096; /* waves */
     uint64_t c = ((uint64_t)keys * pairs + target - 1) / target;
     if (c < 64) c = 64;
-    if (c < 16 * ncols) c = 16 * ncols;
+    /* many columns (speculative verify) make each split's partial results
+     * large: keep a split at least 12 keys per column (measured on MI355X
+     * for 8 rows x 4 heads: 384-key chunks beat 256 and 512 by 16 %) */
+    if (c < 12 * ncols) c = 12 * ncols;
     const char *env = getenv("LFM_ATTN_CHUNK");
     if (env && atoi(env) > 0) c = (uint64_t)atoi(env);
     c = (c + 31) & ~(uint64_t)31;
