@@ -63,11 +63,24 @@ struct SplitParams {
     float2 *part_ml; /* [seq][kvh][split][col] (running max, sum) in log2 units */
     uint32_t pos0_host, n_rows, n_head_q, n_head_kv, kv_mul, ncols;
     uint32_t window, cap, n_splits, chunk, out_dims;
+    /* balanced plan (k_splitkv_bal): n_wg workgroups share the batch's 32-key
+     * tiles evenly; each takes at least min_tiles */
+    uint32_t n_seq, n_groups, n_wg, min_tiles, wpg; /* n_wg: workgroups launched; wpg: KV heads per group */
+    uint32_t n_res, target_waves; /* resident workgroups; waves per uniform batch */
+    uint32_t *tile_prefix; /* [n_seq + 2] tiles before each sequence, then G (device positions) */
     int gate_is_logit;
     float qscale; /* scale * log2(e) */
 };
 
 __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
+
+/* Cache rows are read through global-address-space pointers: the
+ * per-sequence pointers come from a table, so the compiler would otherwise
+ * emit flat loads, which also count on lgkmcnt and make every LDS wait in the
+ * loop wait for the next sub-tile's loads as well. */
+typedef const __attribute__((address_space(1))) uint16_t *gu16_ptr;
+typedef const __attribute__((address_space(1))) u32x4_t *gu32x4_ptr;
+__device__ __forceinline__ u32x4_t load16(gu16_ptr p) { return *reinterpret_cast<gu32x4_ptr>(p); }
 
 __device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -89,45 +102,37 @@ __device__ __forceinline__ float gate_value(const float *gate, size_t idx, int i
     return is_logit ? 1.0f / (1.0f + expf(-g)) : g;
 }
 
-template <int HD, int NT, int W>
-__global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
+/* Keys [lo, last] that the rows of sequence s attend (their union). */
+struct SeqKeys {
+    uint32_t pos0, lo, last;
+};
+__device__ __forceinline__ SeqKeys seq_keys(const SplitParams &P, uint32_t s) {
+    SeqKeys k;
+    k.pos0 = P.pos0_dev ? P.pos0_dev[s] : P.pos0_host;
+    k.last = k.pos0 + P.n_rows - 1u;
+    k.lo   = lfm_plan_row(k.pos0, P.window, P.cap).t_start;
+    return k;
+}
+
+/* One wave: the attention of KV head kvh of sequence s over keys [kb, ke).
+ * direct: the range is the sequence's whole key set, so the normalised,
+ * gated output is written; otherwise the unnormalised O^T and (max, sum)
+ * go to the partial slots part + column. */
+template <int HD, int NT>
+__device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, uint32_t s, uint32_t pos0, uint32_t kvh,
+                                            uint32_t kb, uint32_t ke, bool direct, size_t part) {
     constexpr int NS  = HD / 32; /* MFMA k-steps of Q.K^T (32 dims each)          */
     constexpr int NM  = HD / 16; /* 16-dim tiles of O^T                            */
     constexpr int NVL = HD / 16; /* 16-byte V pieces per lane per 32-key sub-tile  */
     constexpr int CH  = HD / 8;  /* 16-byte chunks per V row                       */
     constexpr int QPP = 64 / CH; /* 4-key quads covered by one pass of 64 lanes    */
-    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
-
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     const int l16  = lane & 15;
     const int g    = lane >> 4;
-    /* the W waves of a workgroup take W adjacent KV heads over the same key
-     * chunk, so each workgroup streams contiguous runs of the cache rows */
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y * W + (uint32_t)wave, s = blockIdx.z;
-    if (kvh >= P.n_head_kv) return; /* waves only synchronise with themselves */
-    uint16_t *vt = vt_all[wave];
+    const uint32_t last = pos0 + P.n_rows - 1u;
 
-    const uint32_t pos0  = P.pos0_dev ? P.pos0_dev[s] : P.pos0_host;
-    const uint32_t last  = pos0 + P.n_rows - 1u;
-    const uint32_t lo    = lfm_plan_row(pos0, P.window, P.cap).t_start;
-    const uint32_t total = last - lo + 1u;
-    /* fixed-length chunks keep the work per workgroup uniform across a ragged
-     * batch; a sequence longer than n_splits chunks gets longer chunks */
-    uint32_t chunk = P.chunk;
-    if ((uint64_t)chunk * P.n_splits < total) chunk = (((total + P.n_splits - 1u) / P.n_splits) + 31u) & ~31u;
-    const uint32_t kb    = lo + split * chunk;
-    const uint32_t ke    = min(kb + chunk, last + 1u); /* exclusive; empty if kb > last */
-    const size_t part    = ((size_t)(s * P.n_head_kv + kvh) * P.n_splits + split) * P.ncols;
-
-    if (kb > last) {
-        /* empty split (short sequence): mark every column as contributing nothing */
-        for (uint32_t n = lane; n < P.ncols; n += 64) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
-        return;
-    }
-
-    const uint16_t *kc = P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride;
-    const uint16_t *vc = P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride;
+    gu16_ptr kc = (gu16_ptr)(P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride);
+    gu16_ptr vc = (gu16_ptr)(P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride);
     const size_t row   = (size_t)P.n_head_kv * HD; /* elements per cache slot */
     kc += (size_t)kvh * HD;
     vc += (size_t)kvh * HD;
@@ -181,10 +186,10 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
             if (p0 + off >= ke) off = ke - 1u - p0; /* clamp: masked later */
             uint32_t slot = base + off;
             if (P.window) { while (slot >= P.cap) slot -= P.cap; }
-            const uint16_t *kp = kc + (size_t)slot * row + 8 * g;
+            gu16_ptr kp = kc + (size_t)slot * row + 8 * g;
 #pragma unroll
             for (int st = 0; st < NS; ++st)
-                kd[kt][st] = *reinterpret_cast<const u32x4_t *>(kp + 32 * st);
+                kd[kt][st] = load16(kp + 32 * st);
         }
 #pragma unroll
         for (int ps = 0; ps < HD / 64; ++ps) {
@@ -195,7 +200,7 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
                 if (p0 + off >= ke) off = ke - 1u - p0;
                 uint32_t slot = base + off;
                 if (P.window) { while (slot >= P.cap) slot -= P.cap; }
-                vd[ps * 4 + i] = *reinterpret_cast<const u32x4_t *>(vc + (size_t)slot * row + 8 * (lane % CH));
+                vd[ps * 4 + i] = load16(vc + (size_t)slot * row + 8 * (lane % CH));
             }
         }
     };
@@ -329,7 +334,7 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
         if (n >= P.ncols) continue;
         const uint32_t r = n / P.kv_mul;
         const uint32_t h = kvh * P.kv_mul + (n - r * P.kv_mul);
-        if (P.n_splits == 1u) {
+        if (direct) {
             const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
             const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
             const float inv   = (lt > 0.0f) ? gv / lt : 0.0f;
@@ -354,6 +359,321 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
             if (g == 0) P.part_ml[part + n] = make_float2(mrun[nt], lt);
         }
     }
+}
+
+/* Grid form: workgroup (split, head group, sequence); the W waves take W
+ * adjacent KV heads over the same key chunk, so each workgroup streams
+ * contiguous runs of the cache rows.  Fixed-length chunks; a sequence longer
+ * than n_splits chunks gets longer chunks; splits past a short sequence's end
+ * mark their partials empty. */
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
+    const int lane       = threadIdx.x & 63;
+    const uint32_t wave  = threadIdx.x >> 6;
+    const uint32_t split = blockIdx.x, kvh = blockIdx.y * W + wave, s = blockIdx.z;
+    if (kvh >= P.n_head_kv) return; /* waves only synchronise with themselves */
+    const SeqKeys k      = seq_keys(P, s);
+    const uint32_t total = k.last - k.lo + 1u;
+    uint32_t chunk       = P.chunk;
+    if ((uint64_t)chunk * P.n_splits < total) chunk = (((total + P.n_splits - 1u) / P.n_splits) + 31u) & ~31u;
+    const uint32_t kb = k.lo + split * chunk;
+    const uint32_t ke = min(kb + chunk, k.last + 1u); /* exclusive; empty if kb > last */
+    const size_t part = ((size_t)(s * P.n_head_kv + kvh) * P.n_splits + split) * P.ncols;
+    if (kb > k.last) {
+        for (uint32_t n = lane; n < P.ncols; n += 64) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
+        return;
+    }
+    run_segment<HD, NT>(P, vt_all[wave], s, k.pos0, kvh, kb, ke, P.n_splits == 1u, part);
+}
+
+/* ---- balanced plan -----------------------------------------------------------------
+ * The batch's keys are cut into 32-key tiles and laid out as one sequence:
+ * sequence major, then KV-head group, then tile (so the groups of a cache row
+ * are read at the same time).  Workgroup g of G takes tiles
+ * [g*N/G, (g+1)*N/G) of the N, split at (sequence, group) boundaries into
+ * segments: every workgroup gets the same number of tiles (+-1) whatever the
+ * sequence lengths, and consecutive workgroups -- which the dispatcher
+ * spreads round-robin over the XCDs -- take consecutive tiles.  (A fixed
+ * (split, sequence) grid puts every sequence's split k on the same XCD, so
+ * short sequences leave XCDs idle.)  G is the resident workgroup count, or
+ * fewer so that each takes >= min_tiles; when every sequence has the same
+ * length, G is a multiple of the (sequence, group) count so that segments
+ * never straddle two sequences.
+ * Segment (g, unit v = s * n_groups + group) writes partial slot g + v: the
+ * workgroups meeting unit v are owner(first tile) .. owner(last tile), a run
+ * that no other unit's slots overlap, so slots are unique and number
+ * < G + n_seq * n_groups.  A unit that one workgroup covers whole is written
+ * directly. */
+__device__ __forceinline__ uint32_t tiles_at(const SplitParams &P, uint32_t pos0) {
+    const uint32_t lo = lfm_plan_row(pos0, P.window, P.cap).t_start;
+    return (pos0 + P.n_rows - 1u - lo + 32u) >> 5;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
+struct TilePlan {
+    uint32_t T;        /* tiles of all sequences, one group                   */
+    uint32_t G;        /* workgroups taking part                              */
+    uint32_t lane_pos; /* position of sequence `lane` (sequences 0..63)       */
+    bool uniform;      /* every sequence has the same number of tiles         */
+};
+
+/* Workgroups for the batch's totals. */
+__device__ __forceinline__ uint32_t plan_wgs(const SplitParams &P, uint32_t T, bool uniform) {
+    const uint64_t N     = (uint64_t)T * P.n_groups;
+    const uint32_t units = P.n_seq * P.n_groups;
+    uint64_t G;
+    if (uniform) {
+        /* equal sequences: every (sequence, group) unit gets n equal
+         * workgroups, about target_waves waves over the batch (several
+         * residency rounds absorb slow workgroups) */
+        const uint32_t tiles = T / P.n_seq;
+        uint64_t ct = ((uint64_t)tiles * P.n_seq * P.n_head_kv + P.target_waves - 1u) / P.target_waves;
+        if (ct < P.min_tiles) ct = P.min_tiles;
+        G = (uint64_t)units * ((tiles + ct - 1u) / ct);
+    } else {
+        /* ragged: one residency round of equal shares */
+        G = N / P.min_tiles;
+        if (G > P.n_res) G = P.n_res;
+    }
+    if (G > P.n_wg) G = P.n_wg;
+    if (uniform && G >= units) G -= G % units;
+    return (uint32_t)(G ? G : 1u);
+}
+
+/* All lanes of the wave take part (wave-wide reductions). */
+__device__ __forceinline__ TilePlan tile_plan(const SplitParams &P, int lane) {
+    TilePlan p;
+    if (!P.pos0_dev) {
+        p.lane_pos = P.pos0_host;
+        p.T        = P.n_seq * tiles_at(P, P.pos0_host);
+        p.uniform  = true;
+    } else {
+        uint32_t sum = 0, odd = 0, t0 = 0;
+        for (uint32_t b = 0; b < P.n_seq; b += 64u) {
+            const uint32_t s   = b + (uint32_t)lane;
+            const uint32_t pos = s < P.n_seq ? P.pos0_dev[s] : 0u;
+            uint32_t x         = s < P.n_seq ? tiles_at(P, pos) : 0u;
+            if (b == 0u) {
+                p.lane_pos = pos;
+                t0         = __shfl(x, 0);
+            }
+            sum += wave_sum(x);
+            if (s >= P.n_seq) x = t0;
+            odd |= (uint32_t)(__ballot(x != t0) != 0);
+        }
+        p.T       = sum;
+        p.uniform = odd == 0u;
+    }
+    p.G = plan_wgs(P, p.T, p.uniform);
+    return p;
+}
+
+__device__ __forceinline__ uint32_t pos_of(const SplitParams &P, const TilePlan &p, uint32_t s) {
+    if (!P.pos0_dev) return P.pos0_host;
+    return s < 64u ? (uint32_t)__shfl(p.lane_pos, (int)s) : P.pos0_dev[s];
+}
+
+/* Ragged batches: the sequence holding tile t (0 <= t < N) and its first
+ * tile (prefix over sequences of n_groups * tiles). */
+__device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int lane, uint32_t *s_out,
+                                         uint64_t *first_out) {
+    uint64_t base = 0;
+    for (uint32_t b = 0;; b += 64u) {
+        const uint32_t s    = b + (uint32_t)lane;
+        const uint32_t x    = s < P.n_seq ? tiles_at(P, P.pos0_dev[s]) * P.n_groups : 0u;
+        const uint32_t incl = wave_incl_scan(x, lane);
+        const uint32_t tot  = __shfl(incl, 63);
+        if (t < base + tot || b + 64u >= P.n_seq) {
+            const uint64_t m = __ballot(base + incl > t);
+            const int l      = m ? (int)__builtin_ctzll(m) : 0;
+            *s_out           = b + (uint32_t)l;
+            *first_out       = base + __shfl(incl - x, l);
+            return;
+        }
+        base += tot;
+    }
+}
+
+__device__ __forceinline__ uint32_t tile_owner(uint64_t t, uint64_t n_tiles, uint32_t G) {
+    return (uint32_t)(((t + 1u) * G - 1u) / n_tiles);
+}
+
+template <int HD, int NT, int W>
+__global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
+    const int lane       = threadIdx.x & 63;
+    const uint32_t wave  = threadIdx.x >> 6;
+    const uint32_t wg    = blockIdx.x;
+    const uint32_t units = P.n_seq * P.n_groups;
+    const TilePlan pl    = tile_plan(P, lane);
+    if (wg == 0u && wave == 0u && P.pos0_dev) {
+        /* tiles before each sequence and the plan, for the merge */
+        uint32_t base = 0;
+        for (uint32_t b = 0; b < P.n_seq; b += 64u) {
+            const uint32_t s    = b + (uint32_t)lane;
+            const uint32_t x    = s < P.n_seq ? tiles_at(P, pos_of(P, pl, s)) : 0u;
+            const uint32_t incl = wave_incl_scan(x, lane);
+            if (s < P.n_seq) P.tile_prefix[s] = base + incl - x;
+            base += __shfl(incl, 63);
+        }
+        if (lane == 0) {
+            P.tile_prefix[P.n_seq]      = base;
+            P.tile_prefix[P.n_seq + 1u] = pl.G;
+        }
+    }
+    if (wg >= pl.G) return;
+    if (pl.uniform) {
+        /* unit = (sequence, group), n workgroups per unit, equal shares */
+        const uint32_t tiles = pl.T / P.n_seq;
+        const uint32_t n     = pl.G / units;
+        const uint32_t unit  = wg / n, sp = wg - unit * n;
+        const uint32_t s = unit / P.n_groups, grp = unit - s * P.n_groups;
+        const uint32_t kvh = grp * W + wave;
+        if (kvh >= P.n_head_kv) return;
+        const uint32_t a    = (uint32_t)((uint64_t)sp * tiles / n);
+        const uint32_t b    = (uint32_t)((uint64_t)(sp + 1u) * tiles / n);
+        const uint32_t pos0 = pos_of(P, pl, s);
+        const uint32_t lo   = lfm_plan_row(pos0, P.window, P.cap).t_start;
+        const uint32_t kb   = lo + 32u * a;
+        const uint32_t ke   = min(lo + 32u * b, pos0 + P.n_rows);
+        const size_t slot   = (size_t)wg + unit;
+        run_segment<HD, NT>(P, vt_all[wave], s, pos0, kvh, kb, ke, n == 1u, (slot * P.n_head_kv + kvh) * P.ncols);
+        return;
+    }
+    const uint64_t N  = (uint64_t)pl.T * P.n_groups;
+    uint64_t t        = (uint64_t)wg * N / pl.G;
+    const uint64_t t1 = (uint64_t)(wg + 1u) * N / pl.G;
+    uint32_t s;
+    uint64_t first;
+    find_seq(P, t, lane, &s, &first);
+    while (t < t1) {
+        const uint32_t pos0  = pos_of(P, pl, s);
+        const uint32_t lo    = lfm_plan_row(pos0, P.window, P.cap).t_start;
+        const uint32_t tiles = (pos0 + P.n_rows - 1u - lo + 32u) >> 5;
+        const uint32_t grp   = (uint32_t)((t - first) / tiles);
+        const uint64_t u0    = first + (uint64_t)grp * tiles; /* the unit's tile 0 */
+        const uint64_t e     = min(t1, u0 + tiles);
+        const uint32_t a = (uint32_t)(t - u0), b = (uint32_t)(e - u0);
+        const uint32_t kvh = grp * W + wave;
+        if (kvh < P.n_head_kv) {
+            const uint32_t kb = lo + 32u * a;
+            const uint32_t ke = min(lo + 32u * b, pos0 + P.n_rows);
+            const size_t slot = (size_t)wg + (size_t)s * P.n_groups + grp;
+            run_segment<HD, NT>(P, vt_all[wave], s, pos0, kvh, kb, ke, a == 0u && b == tiles,
+                                (slot * P.n_head_kv + kvh) * P.ncols);
+        }
+        t = e;
+        if (t == first + (uint64_t)tiles * P.n_groups) {
+            first = t;
+            ++s;
+        }
+    }
+}
+
+/* Merge for the balanced plan.  Four adjacent lanes share one (sequence, KV
+ * head, column, 4 output dims) item: lane q of the four combines slots
+ * q, q+4, ... of the workgroups that met the unit, then the four results are
+ * combined through lane shuffles. */
+template <int HD>
+__global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
+    constexpr uint32_t D4 = HD / 4;
+    constexpr uint32_t SG = 4;
+    const uint32_t t      = blockIdx.x * 256u + threadIdx.x;
+    const uint32_t q      = t % SG;
+    const uint32_t per    = P.ncols * D4; /* items per (sequence, KV head) */
+    const uint32_t item   = t / SG;
+    const uint32_t w      = item / per;   /* s * n_head_kv + kvh */
+    const bool live       = w < P.n_seq * P.n_head_kv;
+    const uint32_t wl     = live ? w : 0u;
+    const uint32_t s = wl / P.n_head_kv, kvh = wl - s * P.n_head_kv;
+    const uint32_t grp = kvh / P.wpg;
+    const uint32_t rem = item - w * per;
+    const uint32_t n = rem / D4, d4 = rem - n * D4;
+    uint32_t T, G, tiles, before;
+    if (!P.pos0_dev) {
+        tiles  = tiles_at(P, P.pos0_host);
+        T      = P.n_seq * tiles;
+        before = s * tiles;
+        G      = plan_wgs(P, T, true);
+    } else { /* the attention kernel's plan */
+        before = P.tile_prefix[s];
+        tiles  = P.tile_prefix[s + 1u] - before;
+        T      = P.tile_prefix[P.n_seq];
+        G      = P.tile_prefix[P.n_seq + 1u];
+    }
+    const uint64_t N  = (uint64_t)T * P.n_groups;
+    const uint64_t u0 = (uint64_t)before * P.n_groups + (uint64_t)grp * tiles;
+    const uint32_t g0 = tile_owner(u0, N, G), g1 = tile_owner(u0 + tiles - 1u, N, G);
+    const size_t v    = (size_t)s * P.n_groups + grp;
+    float M = kNegBig, L = 0.0f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live && g0 != g1) {
+        for (uint32_t g = g0 + q; g <= g1; g += 2u * SG) {
+            /* two slots' loads in flight before either is combined */
+            float2 ml[2];
+            float4 o[2];
+#pragma unroll
+            for (uint32_t j = 0; j < 2u; ++j) {
+                ml[j] = make_float2(kNegBig, 0.0f);
+                o[j]  = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (g + j * SG <= g1) {
+                    const size_t idx = (((size_t)(g + j * SG) + v) * P.n_head_kv + kvh) * P.ncols + n;
+                    ml[j]            = P.part_ml[idx];
+                    o[j]             = *reinterpret_cast<const float4 *>(P.part_o + idx * HD + 4 * d4);
+                }
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 2u; ++j) {
+                if (!(ml[j].y > 0.0f)) continue;
+                const float Mn = fmaxf(M, ml[j].x);
+                const float a  = __builtin_amdgcn_exp2f(M - Mn);
+                const float b  = __builtin_amdgcn_exp2f(ml[j].x - Mn);
+                L   = L * a + ml[j].y * b;
+                O.x = O.x * a + o[j].x * b;
+                O.y = O.y * a + o[j].y * b;
+                O.z = O.z * a + o[j].z * b;
+                O.w = O.w * a + o[j].w * b;
+                M   = Mn;
+            }
+        }
+    }
+    for (uint32_t off = 1; off < SG; off <<= 1) {
+        const float M2 = __shfl_xor(M, (int)off), L2 = __shfl_xor(L, (int)off);
+        const float x2 = __shfl_xor(O.x, (int)off), y2 = __shfl_xor(O.y, (int)off);
+        const float z2 = __shfl_xor(O.z, (int)off), w2 = __shfl_xor(O.w, (int)off);
+        const float Mn = fmaxf(M, M2);
+        const float a  = __builtin_amdgcn_exp2f(M - Mn), b = __builtin_amdgcn_exp2f(M2 - Mn);
+        L   = L * a + L2 * b;
+        O.x = O.x * a + x2 * b;
+        O.y = O.y * a + y2 * b;
+        O.z = O.z * a + z2 * b;
+        O.w = O.w * a + w2 * b;
+        M   = Mn;
+    }
+    if (!live || g0 == g1 || q != 0u) return; /* g0 == g1: written directly */
+    const uint32_t r  = n / P.kv_mul;
+    const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
+    const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+    const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+    const float inv   = (L > 0.0f) ? gv / L : 0.0f;
+    const uint32_t d  = 4 * d4;
+    if (d < P.out_dims)
+        *reinterpret_cast<float4 *>(P.out + orow * HD + d) = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
 }
 
 /* Log-sum-exp merge of the key splits; applies 1/l and the gate.
@@ -430,7 +750,9 @@ hipError_t launch_hd_nt_w(const SplitParams &p, uint32_t n_seq, hipStream_t stre
     if (e != hipSuccess || p.n_splits == 1u) return e;
     const uint32_t n_items = n_seq * p.n_head_kv * p.ncols * (HD / 4);
     uint32_t sg = 1;
-    while (sg < 16u && sg * 4u < p.n_splits) sg <<= 1; /* ~4 splits per lane */
+    /* 2-3 splits per lane: measured on MI355X, 8 splits merge 2.2 us faster
+     * with 4 lanes per output than with 2 (each lane's loads are serial) */
+    while (sg < 16u && sg * 3u < p.n_splits) sg <<= 1;
     const uint64_t threads = (uint64_t)n_items * sg;
     hipLaunchKernelGGL((k_merge<HD>), dim3((uint32_t)((threads + 255u) / 256u)), dim3(256), 0, stream, p,
                        n_items, sg);
@@ -449,13 +771,136 @@ uint32_t choose_waves(uint32_t n_head_kv, uint32_t head_dim) {
     return w >= 8u ? 8u : (w >= 4u ? 4u : (w >= 2u ? 2u : 1u));
 }
 
+/* Workgroups of k_splitkv_bal<HD, NT, W> resident on the whole device at
+ * once (queried once per instantiation). */
+template <int HD, int NT, int W>
+uint32_t resident_wgs() {
+    static uint32_t cached = 0;
+    if (cached) return cached;
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W>, 64 * W, 0) !=
+            hipSuccess)
+        return 256u;
+    cached = (uint32_t)((cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1));
+    return cached;
+}
+
+/* Balanced plan: launch sized for the plan the device will pick, partial
+ * slots and the tile prefix table in the workspace, then the merge. */
+template <int HD, int NT, int W>
+int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
+    static uint32_t cus = 0;
+    if (!cus) {
+        int dev = 0, n = 0;
+        cus = (hipGetDevice(&dev) == hipSuccess &&
+               hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+                  ? (uint32_t)n
+                  : 256u;
+    }
+    p.wpg          = W;
+    p.n_groups     = (p.n_head_kv + W - 1u) / W;
+    p.n_res        = resident_wgs<HD, NT, W>();
+    /* 16 waves per CU over a batch of equal sequences: two residency rounds of
+     * 8-wave workgroups at head_dim 64 (measured best on MI355X) */
+    p.target_waves = 16u * cus;
+    /* each workgroup's partials cost about one 32-key tile per 32 query
+     * columns: keep >= 12 tiles per workgroup per 32 columns (measured on
+     * MI355X for 8 rows x 4 heads), and >= 2 tiles */
+    p.min_tiles = (12u * p.ncols + 31u) / 32u;
+    if (p.min_tiles < 2u) p.min_tiles = 2u;
+    /* launch: enough workgroups for either plan.  With at most `tiles`
+     * tiles per sequence, a uniform batch needs units * n, n <=
+     * ceil(target_waves / (n_seq * n_head_kv)) and n <= ceil(tiles /
+     * min_tiles); a ragged one min(n_res, N / min_tiles).  keys_hint bounds the
+     * tiles; without it (or if it is wrong) the device plan is capped by the
+     * launch, which only makes the shares longer. */
+    const uint64_t units = (uint64_t)p.n_groups * p.n_seq;
+    uint64_t n_launch;
+    {
+        uint32_t keys = p.pos0_dev ? keys_hint : 0u;
+        if (!p.pos0_dev) {
+            const uint32_t lo = lfm_plan_row(p.pos0_host, p.window, p.cap).t_start;
+            keys              = p.pos0_host + p.n_rows - lo;
+        }
+        const uint64_t pairs  = (uint64_t)p.n_seq * p.n_head_kv;
+        uint64_t per_unit     = (p.target_waves + pairs - 1u) / pairs; /* uniform n bound */
+        uint64_t ragged       = p.n_res;
+        if (keys) {
+            const uint64_t most = (((uint64_t)keys + 31u) / 32u + p.min_tiles - 1u) / p.min_tiles;
+            if (per_unit > most) per_unit = most;
+            if (ragged > units * most) ragged = units * most;
+        }
+        n_launch = units * per_unit;
+        if (n_launch < ragged) n_launch = ragged;
+        if (n_launch < units) n_launch = units;
+    }
+    if (const char *env = getenv("LFM_ATTN_CHUNK")) {
+        /* about c keys per workgroup (tests, tuning): enough workgroups for
+         * the longest sequences keys_hint allows; longer ones get more keys */
+        const int c = atoi(env);
+        if (c > 0) {
+            p.min_tiles   = (uint32_t)(c + 31) / 32u;
+            p.n_res       = 0x7fffffffu;
+            p.target_waves = 0x7fffffffu;
+            uint32_t keys = p.pos0_dev ? keys_hint : p.pos0_host + p.n_rows;
+            if (keys == 0u) keys = p.window ? p.window + p.n_rows - 1u : 4096u;
+            n_launch = units * (((keys + 31u) / 32u + p.min_tiles - 1u) / p.min_tiles);
+        }
+    }
+    if (n_launch > 0x1000000u) n_launch = 0x1000000u;
+    p.n_wg = (uint32_t)n_launch;
+    const size_t n_part  = ((size_t)n_launch + (size_t)p.n_groups * p.n_seq) * p.n_head_kv * p.ncols;
+    const size_t o_bytes = (n_part * HD * sizeof(float) + 255) & ~(size_t)255;
+    const size_t m_bytes = (n_part * sizeof(float2) + 255) & ~(size_t)255;
+    int st   = LFM_ATTN_OK;
+    char *ws = static_cast<char *>(workspace(o_bytes + m_bytes + ((size_t)p.n_seq + 2u) * sizeof(uint32_t), stream, &st));
+    if (!ws) return st;
+    p.part_o      = reinterpret_cast<float *>(ws);
+    p.part_ml     = reinterpret_cast<float2 *>(ws + o_bytes);
+    p.tile_prefix = reinterpret_cast<uint32_t *>(ws + o_bytes + m_bytes);
+    hipEvent_t ev0, ev1;
+    profile_events(&ev0, &ev1);
+    if (ev0) (void)hipEventRecord(ev0, stream);
+    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W>), dim3((uint32_t)n_launch), dim3(64 * W), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (ev1) (void)hipEventRecord(ev1, stream);
+    if (e != hipSuccess) return hip_status(e);
+    const uint64_t mt = (uint64_t)p.n_seq * p.n_head_kv * p.ncols * (HD / 4) * 4u;
+    hipLaunchKernelGGL((k_merge_bal<HD>), dim3((uint32_t)((mt + 255u) / 256u)), dim3(256), 0, stream, p);
+    return hip_status(hipGetLastError());
+}
+
+/* Plan choice.  A batch whose sequences may differ in length (positions on
+ * the device, more than one sequence) takes the balanced plan: measured on
+ * MI355X, 64 sequences of 512..8192 keys run 23 % faster than on the
+ * fixed-chunk grid, which leaves XCDs idle.  A batch that cannot be ragged
+ * (one sequence, or one shared host position) takes the grid, which skips the
+ * plan's position scan and table (1-9 % faster on equal-length batches).
+ * LFM_ATTN_PLAN=grid|balanced overrides (tuning and tests). */
+bool use_grid_plan(const AttnBatch &b) {
+    const char *env = getenv("LFM_ATTN_PLAN");
+    if (env && env[0] == 'g') return true;
+    if (env && env[0] == 'b') return false;
+    return !b.pos0_dev || b.n_seq == 1u;
+}
+
 template <int HD, int NT>
-hipError_t launch_hd_nt(const SplitParams &p, uint32_t n_seq, hipStream_t stream) {
+int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream) {
     const uint32_t w = choose_waves(p.n_head_kv, HD);
-    if (w == 8u) return launch_hd_nt_w<HD, NT, 8>(p, n_seq, stream);
-    if (w == 4u) return launch_hd_nt_w<HD, NT, 4>(p, n_seq, stream);
-    if (w == 2u) return launch_hd_nt_w<HD, NT, 2>(p, n_seq, stream);
-    return launch_hd_nt_w<HD, NT, 1>(p, n_seq, stream);
+    if (!grid) {
+        if (w == 8u) return launch_bal<HD, NT, 8>(p, keys_hint, stream);
+        if (w == 4u) return launch_bal<HD, NT, 4>(p, keys_hint, stream);
+        if (w == 2u) return launch_bal<HD, NT, 2>(p, keys_hint, stream);
+        return launch_bal<HD, NT, 1>(p, keys_hint, stream);
+    }
+    hipError_t e;
+    if (w == 8u) e = launch_hd_nt_w<HD, NT, 8>(p, n_seq, stream);
+    else if (w == 4u) e = launch_hd_nt_w<HD, NT, 4>(p, n_seq, stream);
+    else if (w == 2u) e = launch_hd_nt_w<HD, NT, 2>(p, n_seq, stream);
+    else e = launch_hd_nt_w<HD, NT, 1>(p, n_seq, stream);
+    return hip_status(e);
 }
 
 /* Key chunk per wave (multiple of 32) and the number of chunks the grid
@@ -518,6 +963,18 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
     p.cap           = b.cap;
     p.out_dims      = b.out_dims;
     p.qscale        = b.scale * kLog2e;
+    p.n_seq         = b.n_seq;
+    const uint32_t nt = (p.ncols + 15u) / 16u;
+    const bool grid   = use_grid_plan(b);
+    if (!grid) {
+        if (b.head_dim == 64u) {
+            if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream);
+            if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream);
+            return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream);
+        }
+        if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream);
+        return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream);
+    }
     choose_split(b, keys_hint, &p.n_splits, &p.chunk);
     if (p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
@@ -528,17 +985,13 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
         p.part_o  = reinterpret_cast<float *>(ws);
         p.part_ml = reinterpret_cast<float2 *>(ws + ((n_part * b.head_dim * sizeof(float) + 255) & ~(size_t)255));
     }
-    const uint32_t nt = (p.ncols + 15u) / 16u;
-    hipError_t e      = hipSuccess;
     if (b.head_dim == 64u) {
-        if (nt == 1u) e = launch_hd_nt<64, 1>(p, b.n_seq, stream);
-        else if (nt == 2u) e = launch_hd_nt<64, 2>(p, b.n_seq, stream);
-        else e = launch_hd_nt<64, 4>(p, b.n_seq, stream);
-    } else {
-        if (nt == 1u) e = launch_hd_nt<128, 1>(p, b.n_seq, stream);
-        else e = launch_hd_nt<128, 2>(p, b.n_seq, stream);
+        if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream);
+        if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream);
+        return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream);
     }
-    return hip_status(e);
+    if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream);
+    return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream);
 }
 
 } // namespace lfm

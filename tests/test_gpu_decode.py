@@ -246,3 +246,31 @@ def test_repeated_calls_shared_workspace(gpu, orc):
                                               (7, 1, 300), (1, 3, 9000)]):
         got, want = _varlen_case(gpu, orc, rng, n_seq, n_rows, 32, 8, 64, [ctx] * n_seq)
         parity(got, want, what=f"repeat {i}")
+
+
+@pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq", [(64, 32, 8, 1, 130), (128, 16, 4, 1, 9),
+                                                    (64, 32, 8, 8, 5), (64, 16, 8, 1, 1)])
+def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
+    """The balanced split (every workgroup takes the same number of key
+    tiles, cut at sequence and head-group boundaries) and the fixed-chunk grid
+    (LFM_ATTN_PLAN=grid) both match the oracle on ragged batches; also with
+    96-key shares (many more segments than sequences)."""
+    la = gpu
+    rng = np.random.default_rng(n_seq * 31 + hd)
+    ctx = [int(c) for c in rng.integers(0, 3000, size=n_seq)]
+    if n_seq > 1:
+        ctx[0], ctx[-1] = 0, 2999  # one-key and longest sequences
+    outs = []
+    for env in ({"LFM_ATTN_PLAN": "balanced"}, {"LFM_ATTN_PLAN": "grid"},
+                {"LFM_ATTN_PLAN": "balanced", "LFM_ATTN_CHUNK": "96"}):
+        os.environ.update(env)
+        try:
+            got, want = _varlen_case(la, orc, np.random.default_rng(4), n_seq, n_rows, nq, nkv, hd,
+                                     ctx)
+        finally:
+            for k in env:
+                os.environ.pop(k, None)
+        parity(got, want, what=f"{env}")
+        outs.append(got)
+    for o in outs[1:]:
+        assert np.abs(outs[0] - o).max() < 1e-5
