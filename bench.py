@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, datasheet
 # HBM bytes per launch of the headline kernel from two rocprofv3 PMC passes
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, factors from a 2 GiB read/copy
 # kernel); profiles/k_splitkv_decode_b64_ctx8192_pmc.md
-HEADLINE_TRAFFIC_BYTES = 1082510000
+HEADLINE_TRAFFIC_BYTES = 1082515661
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, datasheet
 
 
@@ -355,7 +355,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "kernel": "k_splitkv<64,1>", "kernel_us": round(k_ms * 1e3, 2)},
+                     "kernel": "k_splitkv_bal<64,1,8>", "kernel_us": round(k_ms * 1e3, 2)},
         "prefill": prefill,
         "cpu_baseline": cpu,
         "parity_vs_cpu": parity,
