@@ -115,6 +115,33 @@ int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *con
                          const float *cos_lut, const float *sin_lut, uint32_t window_len,
                          uint32_t cap, lfm_attn_stream_t stream);
 
+/* ---- projections beside the attention path ------------------------------- */
+/* Blocks are the reference's packed GGUF layouts (tools/lfm2_cpuid_quants.c:76-127):
+ * block_q8_K 292 B (float d, int8 qs[256], int16 bsums[16]); block_q4_K 144 B
+ * (fp16 d, fp16 dmin, uint8 scales[12], uint8 qs[128]).  n_cols % 256 == 0
+ * (else LFM_ATTN_E_UNSUPPORTED). */
+
+/* Q8_K quantization of n_rows rows of n_cols floats into y_q8_K
+ * [n_rows][n_cols/256] blocks, bit-identical to the engine's AVX2 quantizer:
+ * replaces lfm2_quantize_batch_q8_K_avx2 (tools/lfm2_prefill_batch.c:93-105)
+ * and lfm2_quantize_row_q8_K_avx2 (tools/lfm2_cpuid_quants.c:585-635), and
+ * the Q8_K output side effect of A1 (tools/lfm2_kernels_fast.c:804-807):
+ * quantizing xb_out as one row of n_head_q * 64 floats gives the same blocks
+ * as the per-4-head slices.  x 4-byte aligned; y 4-byte aligned. */
+int lfm_hip_quantize_q8_K(const float *x, void *y_q8_K, uint32_t n_rows, uint32_t n_cols,
+                          lfm_attn_stream_t stream);
+
+/* out[t][r] = (row r of the Q4_K matrix w_q4_K [n_rows][n_cols/256]) .
+ * (token t of x_q8_K [n_tokens][n_cols/256]), bit-identical to
+ * lfm2_vec_dot_q4_K_q8_K_avx2 (include/lfm2_simd_avx2.h:364-412) per row.
+ * Replaces lfm2_matmul_1x4_prequant_mt (tools/lfm2_decode_1x4.c:795-813,
+ * n_tokens = 1, e.g. the `wo` projection of x_q8 from attention) and the Q4_K
+ * branch of lfm2_matmul_batch_avx2_mt (tools/lfm2_prefill_batch.c:479-510,
+ * 598-634) after its quantize step.  w 16-byte aligned; x_q8_K and out
+ * 4-byte aligned. */
+int lfm_hip_matmul_q4_K(float *out, const void *w_q4_K, uint32_t n_rows, uint32_t n_cols,
+                        const void *x_q8_K, uint32_t n_tokens, lfm_attn_stream_t stream);
+
 /* ---- attention ------------------------------------------------------------ */
 /* A1 -- replaces OnlineGQATaskCtx + lfm2_parallel_for(pool, ceil(n_head_q/4), 1,
  * lfm2_online_gqa_f16_worker_simd, &ctx), tools/lfm2_kernels_fast.c:685-697,

@@ -14,11 +14,13 @@ from .attention import (  # noqa: F401
     kv_cache_shift_sinks,
     lfm3_kv_cache_shift_sinks,
     lfm3_online_gqa_f16_dispatch,
+    matmul_q4_K,
     online_gqa_f16,
     pointer_table,
     prefill_f16,
     qk_norm_rope,
     qkv_prologue,
+    quantize_q8_K,
     require_gpu,
     rope_lut_lfm2,
     rope_lut_lfm3,

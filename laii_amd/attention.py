@@ -138,6 +138,26 @@ def store_fp32_to_fp16(dst_f16: Ptr, src: Ptr, n: int, stream=None) -> None:
           "lfm_hip_store_fp32_to_fp16")
 
 
+Q4K_BYTES, Q8K_BYTES = 144, 292  # packed block_q4_K / block_q8_K
+
+
+def quantize_q8_K(x: Ptr, y_q8_K: Ptr, n_rows: int, n_cols: int, stream=None) -> None:
+    """Q8_K blocks of n_rows rows of n_cols floats (n_cols % 256 == 0) into
+    y_q8_K, [n_rows][n_cols / 256] packed 292-byte blocks
+    (lfm2_quantize_batch_q8_K_avx2, tools/lfm2_prefill_batch.c:93-105)."""
+    check(load().lfm_hip_quantize_q8_K(_p(x), _p(y_q8_K), n_rows, n_cols, stream),
+          "lfm_hip_quantize_q8_K")
+
+
+def matmul_q4_K(out: Ptr, w_q4_K: Ptr, n_rows: int, n_cols: int, x_q8_K: Ptr, n_tokens: int,
+                stream=None) -> None:
+    """out[t][r] = Q4_K row r . Q8_K token t (lfm2_matmul_1x4_prequant_mt,
+    tools/lfm2_decode_1x4.c:795-813; lfm2_matmul_batch_avx2_mt,
+    tools/lfm2_prefill_batch.c:598-634)."""
+    check(load().lfm_hip_matmul_q4_K(_p(out), _p(w_q4_K), n_rows, n_cols, _p(x_q8_K), n_tokens,
+                                     stream), "lfm_hip_matmul_q4_K")
+
+
 def qkv_prologue(q: Ptr, k: Ptr, v: Ptr, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr, n_seq: int,
                  n_rows: int, n_head_q: int, n_head_kv: int, head_dim: int, q_norm_w: Ptr,
                  k_norm_w: Ptr, eps: float, cos_lut: Ptr, sin_lut: Ptr, window_len: int = 0,

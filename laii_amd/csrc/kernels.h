@@ -65,6 +65,12 @@ int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *cons
                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
                         uint32_t cap, hipStream_t stream);
 
+/* Projections beside the attention path (quant_matmul.hip).  y/x_q8:
+ * packed block_q8_K rows; w: packed block_q4_K rows; n_cols % 256 == 0. */
+int launch_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_cols, hipStream_t stream);
+int launch_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols, const void *x_q8,
+                       uint32_t n_tokens, hipStream_t stream);
+
 /* Attention-sink eviction (kv_shift.hip).  launch_kv_shift moves rows
  * [n_sink + n_discard, n_sink + n_discard + n_keep) down to n_sink and
  * counter-rotates the keys; launch_kv_swa_repack re-slots an SWA ring

@@ -201,6 +201,27 @@ int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *con
                                     cap, to_stream(stream));
 }
 
+/* ---- projections beside the path ------------------------------------------- */
+static inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1u)) == 0u; }
+
+int lfm_hip_quantize_q8_K(const float *x, void *y_q8_K, uint32_t n_rows, uint32_t n_cols,
+                          lfm_attn_stream_t stream) {
+    if (n_rows == 0u || n_cols == 0u) return LFM_ATTN_OK;
+    if (!x || !y_q8_K) return LFM_ATTN_E_INVALID;
+    if (n_cols % 256u) return LFM_ATTN_E_UNSUPPORTED;
+    if (!aligned(x, 4) || !aligned(y_q8_K, 4)) return LFM_ATTN_E_INVALID;
+    return lfm::launch_quantize_q8_K(x, y_q8_K, n_rows, n_cols, to_stream(stream));
+}
+
+int lfm_hip_matmul_q4_K(float *out, const void *w_q4_K, uint32_t n_rows, uint32_t n_cols,
+                        const void *x_q8_K, uint32_t n_tokens, lfm_attn_stream_t stream) {
+    if (n_rows == 0u || n_tokens == 0u) return LFM_ATTN_OK;
+    if (!out || !w_q4_K || !x_q8_K || n_cols == 0u) return LFM_ATTN_E_INVALID;
+    if (n_cols % 256u) return LFM_ATTN_E_UNSUPPORTED;
+    if (!aligned(w_q4_K, 16) || !aligned(x_q8_K, 4) || !aligned(out, 4)) return LFM_ATTN_E_INVALID;
+    return lfm::launch_matmul_q4_K(out, w_q4_K, n_rows, n_cols, x_q8_K, n_tokens, to_stream(stream));
+}
+
 /* ---- attention -------------------------------------------------------------- */
 int lfm_hip_online_gqa_f16(const float *q, const uint16_t *k_cache_f16,
                            const uint16_t *v_cache_f16, float *xb_out, uint32_t n_head_q,

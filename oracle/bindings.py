@@ -57,6 +57,14 @@ def _shift_lfm3(fn, k_caches, v_caches, n_head_kv, layer_kind, head_dim, lut_ful
               n_discard)
 
 
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+Q4K_BYTES, Q8K_BYTES = 144, 292
+
+
+def _q8k_out(n_rows, n_cols):
+    return np.zeros((n_rows, (n_cols // 256) * Q8K_BYTES), np.uint8)
+
+
 class Oracle:
     """Scalar C11 restatement of the reference attention path."""
 
@@ -64,6 +72,10 @@ class Oracle:
         if not os.path.exists(path):
             build(ref=False)
         L = self.lib = C.CDLL(path)
+        L.orc_quantize_q8_K.argtypes = [_f32p, _u8p, _u32, _u32]
+        L.orc_dot_q4_K_q8_K.restype = _f32
+        L.orc_dot_q4_K_q8_K.argtypes = [_u8p, _u8p, _u32]
+        L.orc_matmul_q4_K.argtypes = [_f32p, _u8p, _u32, _u32, _u8p, _u32]
         L.orc_f16_to_f32.restype = _f32
         L.orc_f16_to_f32.argtypes = [C.c_uint16]
         L.orc_f32_to_f16.restype = C.c_uint16
@@ -214,6 +226,40 @@ class Oracle:
         return out
 
 
+def _quantize_q8_K(self, x):
+    """x: float32 [n_rows, n_cols] -> uint8 [n_rows, n_cols/256 * 292] (packed blocks)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = _q8k_out(*x.shape)
+    self._quant(x, y, x.shape[0], x.shape[1])
+    return y
+
+
+def _orc_quant(self, x, y, n_rows, n_cols):
+    self.lib.orc_quantize_q8_K(x, y, n_rows, n_cols)
+
+
+Oracle._quant = _orc_quant
+Oracle.quantize_q8_K = _quantize_q8_K
+
+
+def _orc_dot(self, w_row, x_q8, n_cols):
+    return float(self.lib.orc_dot_q4_K_q8_K(np.ascontiguousarray(w_row, np.uint8),
+                                             np.ascontiguousarray(x_q8, np.uint8), n_cols))
+
+
+def _orc_matmul(self, w, x_q8, n_cols):
+    """w: uint8 [n_rows, nb*144]; x_q8: uint8 [B, nb*292] -> float32 [B, n_rows]."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x_q8 = np.ascontiguousarray(x_q8, np.uint8)
+    out = np.zeros((x_q8.shape[0], w.shape[0]), np.float32)
+    self.lib.orc_matmul_q4_K(out, w, w.shape[0], n_cols, x_q8, x_q8.shape[0])
+    return out
+
+
+Oracle.dot_q4_K = _orc_dot
+Oracle.matmul_q4_K = _orc_matmul
+
+
 class Reference:
     """The reference's own kernels, compiled from /root/reference (ref_shim.c)."""
 
@@ -248,6 +294,11 @@ class Reference:
         L.ref_kv_shift_sinks_lfm3.argtypes = [C.c_void_p, C.c_void_p, _u32, C.c_void_p, C.c_void_p,
                                               _u32, C.c_void_p, C.c_void_p, _u32, C.c_void_p,
                                               C.c_void_p, _u32, _u32, _u32, _u32, _u32, _u32]
+        L.ref_quantize_q8_K.argtypes = [_f32p, _u8p, _u32, _u32]
+        L.ref_dot_q4_K_avx2.restype = _f32
+        L.ref_dot_q4_K_avx2.argtypes = [_u8p, _u8p, _u32]
+        L.ref_matmul_q4_K_prequant.argtypes = [_f32p, _u8p, _u32, _u32, _u8p]
+        L.ref_matmul_q4_K_batch.argtypes = [_f32p, _u8p, _u32, _u32, _f32p, _u32]
         self.has_avx2 = bool(L.ref_has_avx2())
 
     def kv_shift_sinks_lfm2(self, k_caches, v_caches, n_head_kv, head_dim, lut, pos, n_sink,
@@ -336,3 +387,37 @@ class Reference:
                                             vp, np.ascontiguousarray(pos, np.uint32), out, n_seq,
                                             n_head_q, n_head_kv, n_threads, reps, C.byref(used))
         return dt, int(used.value), out
+
+
+def _ref_quant(self, x, y, n_rows, n_cols):
+    self.lib.ref_quantize_q8_K(x, y, n_rows, n_cols)
+
+
+def _ref_dot(self, w_row, x_q8, n_cols):
+    return float(self.lib.ref_dot_q4_K_avx2(np.ascontiguousarray(w_row, np.uint8),
+                                             np.ascontiguousarray(x_q8, np.uint8), n_cols))
+
+
+def _ref_matmul_prequant(self, w, x_q8, n_cols):
+    """The engine's decode projection (1x4 rows): x_q8 uint8 [1, nb*292] -> float32 [1, n_rows]."""
+    w = np.ascontiguousarray(w, np.uint8)
+    out = np.zeros((1, w.shape[0]), np.float32)
+    self.lib.ref_matmul_q4_K_prequant(out, w, w.shape[0], n_cols, np.ascontiguousarray(x_q8, np.uint8))
+    return out
+
+
+def _ref_matmul_batch(self, w, x):
+    """The engine's batched projection from fp32 tokens x [B <= 8, n_cols] -> [B, n_rows]."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    assert x.shape[0] <= 8
+    out = np.zeros((x.shape[0], w.shape[0]), np.float32)
+    self.lib.ref_matmul_q4_K_batch(out, w, w.shape[0], x.shape[1], x, x.shape[0])
+    return out
+
+
+Reference._quant = _ref_quant
+Reference.quantize_q8_K = _quantize_q8_K
+Reference.dot_q4_K = _ref_dot
+Reference.matmul_q4_K_prequant = _ref_matmul_prequant
+Reference.matmul_q4_K_batch = _ref_matmul_batch

@@ -598,3 +598,109 @@ void orc_decode_batch_mt(const float *q, const uint16_t *const *k_seq,
     orc_batch_worker(&job);
     for (uint32_t t = 1; t < n_threads; ++t) pthread_join(th[t], NULL);
 }
+
+/* ==== next-row projections: Q8_K activations, Q4_K x Q8_K matmul ======== */
+
+/* 6-bit scale and min of sub-block j of a Q4_K super-block
+ * (get_scale_min_k4, tools/lfm2_cpuid_quants.c:180-189). */
+static void q4k_scale_min(int j, const uint8_t *q, int *sc, int *m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m  = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4);
+        *m  = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* packs_epi32 then packs_epi16: signed saturation to int8 */
+static int8_t sat_i8(int32_t v) {
+    if (v > 127) return 127;
+    if (v < -128) return -128;
+    return (int8_t)v;
+}
+
+void orc_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    uint8_t *out = (uint8_t *)y;
+    for (uint32_t t = 0; t < n_rows; ++t) {
+        for (uint32_t b = 0; b < nb; ++b) {
+            const float *xb = x + (size_t)t * n_cols + (size_t)b * 256u;
+            uint8_t *blk    = out + ((size_t)t * nb + b) * ORC_Q8K_BYTES;
+            float max_abs = 0.0f;
+            for (int i = 0; i < 256; ++i) {
+                const float a = fabsf(xb[i]);
+                if (a > max_abs) max_abs = a;
+            }
+            if (max_abs == 0.0f) {
+                memset(blk, 0, ORC_Q8K_BYTES);
+                continue;
+            }
+            const float d      = max_abs / 127.0f;
+            const float iscale = 127.0f / max_abs;
+            memcpy(blk, &d, 4);
+            for (int j = 0; j < 16; ++j) {
+                int32_t bsum = 0;
+                for (int l = 0; l < 16; ++l) {
+                    const float p   = xb[j * 16 + l] * iscale;
+                    const int32_t q = (int32_t)lrintf(p); /* round half to even */
+                    blk[4 + j * 16 + l] = (uint8_t)sat_i8(q);
+                    bsum += q;
+                }
+                const int16_t bs = (int16_t)bsum;
+                memcpy(blk + 260 + 2 * j, &bs, 2);
+            }
+        }
+    }
+}
+
+float orc_dot_q4_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    const uint8_t *w  = (const uint8_t *)w_row;
+    const uint8_t *xq = (const uint8_t *)x_q8;
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *wb = w + (size_t)b * ORC_Q4K_BYTES;
+        const uint8_t *xb = xq + (size_t)b * ORC_Q8K_BYTES;
+        float d8;
+        memcpy(&d8, xb, 4);
+        if (d8 == 0.0f) continue;
+        uint16_t dh, mh;
+        memcpy(&dh, wb, 2);
+        memcpy(&mh, wb + 2, 2);
+        const float d    = orc_f16_to_f32(dh) * d8;
+        const float dmin = orc_f16_to_f32(mh) * d8;
+        const uint8_t *scales = wb + 4, *qs = wb + 16;
+        const int8_t *q8      = (const int8_t *)(xb + 4);
+        int16_t bs[16];
+        memcpy(bs, xb + 260, sizeof bs);
+        int32_t dot = 0, mins = 0;
+        for (int j = 0; j < 4; ++j) { /* sub-blocks 2j (low nibbles) and 2j+1 (high) */
+            int sc1, m1, sc2, m2;
+            q4k_scale_min(2 * j, scales, &sc1, &m1);
+            q4k_scale_min(2 * j + 1, scales, &sc2, &m2);
+            mins += m1 * ((int32_t)bs[4 * j] + bs[4 * j + 1]) + m2 * ((int32_t)bs[4 * j + 2] + bs[4 * j + 3]);
+            int32_t lo = 0, hi = 0;
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q = qs[32 * j + l];
+                lo += (int32_t)(q & 0x0F) * q8[64 * j + l];
+                hi += (int32_t)(q >> 4) * q8[64 * j + 32 + l];
+            }
+            dot += sc1 * lo + sc2 * hi;
+        }
+        const float a = d * (float)dot;
+        const float m = dmin * (float)mins;
+        sumf += a - m;
+    }
+    return sumf;
+}
+
+void orc_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols,
+                     const void *x_q8, uint32_t n_tokens) {
+    const uint32_t nb = n_cols / 256u;
+    for (uint32_t t = 0; t < n_tokens; ++t)
+        for (uint32_t r = 0; r < n_rows; ++r)
+            out[(size_t)t * n_rows + r] =
+                orc_dot_q4_K_q8_K((const uint8_t *)w + (size_t)r * nb * ORC_Q4K_BYTES,
+                                  (const uint8_t *)x_q8 + (size_t)t * nb * ORC_Q8K_BYTES, n_cols);
+}

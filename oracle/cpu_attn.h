@@ -100,6 +100,34 @@ void orc_decode_batch_mt(const float *q, const uint16_t *const *k_seq,
                          float *out, uint32_t n_seq, uint32_t n_head_q,
                          uint32_t n_head_kv, uint32_t head_dim, uint32_t n_threads);
 
+/* ---- next-row projections: Q8_K activations, Q4_K x Q8_K matmul -------
+ * Blocks are the reference's packed GGUF layouts:
+ *   block_q4_K (144 B): fp16 d, fp16 dmin, scales[12] (6-bit scale/min pairs
+ *                       of 8 sub-blocks), qs[128] (256 4-bit weights)
+ *   block_q8_K (292 B): float d, int8 qs[256], int16 bsums[16]
+ * (tools/lfm2_cpuid_quants.c:76-127). */
+#define ORC_Q4K_BYTES 144u
+#define ORC_Q8K_BYTES 292u
+
+/* Q8_K of n_rows rows of n_cols floats (n_cols % 256 == 0), the AVX2
+ * arithmetic the engine runs: d = max|x| / 127, q = round-half-even(x *
+ * (127 / max|x|)), bsums of the unsaturated values
+ * (lfm2_quantize_row_q8_K_avx2_cpuid, tools/lfm2_cpuid_quants.c:585-635;
+ * per row as lfm2_quantize_batch_q8_K_avx2, tools/lfm2_prefill_batch.c:93-105). */
+void orc_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_cols);
+
+/* One Q4_K row . Q8_K vector, in the order of lfm2_vec_dot_q4_K_q8_K_avx2
+ * (include/lfm2_simd_avx2.h:364-412): exact integer sums per super-block,
+ * then sumf += (d*d8)*dot - (dmin*d8)*mins, super-blocks in order. */
+float orc_dot_q4_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
+
+/* out[t][r] = row r of W . token t of x_q8 (lfm2_matmul_1x4_prequant_mt,
+ * tools/lfm2_decode_1x4.c:795-813, B = 1; the Q4_K branch of
+ * lfm2_matmul_batch_avx2_mt after its quantize step,
+ * tools/lfm2_prefill_batch.c:479-510, 598-634). */
+void orc_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols,
+                     const void *x_q8, uint32_t n_tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -300,3 +300,57 @@ uint32_t ref_kv_shift_sinks_lfm3(uint16_t **k_caches, uint16_t **v_caches, uint3
     free(m);
     return pos;
 }
+
+/* ---- next-row projections -------------------------------------------------- */
+
+static GGUFTensor shim_q4K_tensor(const void *w, uint32_t n_rows, uint32_t n_cols) {
+    GGUFTensor t;
+    memset(&t, 0, sizeof t);
+    t.n_dims = 2;
+    t.ne[0]  = n_cols;
+    t.ne[1]  = n_rows;
+    t.ne[2] = t.ne[3] = 1;
+    t.type   = GGML_TYPE_Q4_K;
+    t.bytes  = (size_t)n_rows * (n_cols / 256u) * sizeof(block_q4_K_t);
+    t.data   = w;
+    return t;
+}
+
+/* lfm2_quantize_batch_q8_K_avx2 (tools/lfm2_prefill_batch.c:93-105): the
+ * engine's kernel table quantizer (lfm2_quantize_row_q8_K_avx2_cpuid). */
+void ref_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_cols) {
+    shim_state st;
+    shim_save(&st);
+    lfm2_quantize_batch_q8_K_avx2(x, (block_q8_K_t *)y, n_rows, n_cols);
+    shim_restore(&st);
+}
+
+/* lfm2_vec_dot_q4_K_q8_K_avx2 (include/lfm2_simd_avx2.h:364-412), one row. */
+float ref_dot_q4_K_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    return lfm2_vec_dot_q4_K_q8_K_avx2((const block_q4_K_t *)w_row, (const block_q8_K_t *)x_q8, n_cols);
+}
+
+/* lfm2_matmul_1x4_prequant_mt (tools/lfm2_decode_1x4.c:795-813) without a
+ * pool: the engine's decode-step projection from a prequantized vector. */
+void ref_matmul_q4_K_prequant(float *out, const void *w, uint32_t n_rows, uint32_t n_cols,
+                              const void *x_q8) {
+    GGUFTensor t = shim_q4K_tensor(w, n_rows, n_cols);
+    shim_state st;
+    shim_save(&st);
+    lfm2_matmul_1x4_prequant_mt(NULL, out, &t, NULL, (const block_q8_K_t *)x_q8);
+    shim_restore(&st);
+}
+
+/* lfm2_matmul_batch_avx2_mt (tools/lfm2_prefill_batch.c:598-634) without a
+ * pool: quantizes the B <= 8 fp32 tokens, then one row at a time. */
+void ref_matmul_q4_K_batch(float *out, const void *w, uint32_t n_rows, uint32_t n_cols,
+                           const float *x, uint32_t n_tokens) {
+    GGUFTensor t = shim_q4K_tensor(w, n_rows, n_cols);
+    block_q8_K_t *scratch = (block_q8_K_t *)malloc((size_t)n_tokens * (n_cols / 256u) * sizeof(block_q8_K_t));
+    if (!scratch) return;
+    shim_state st;
+    shim_save(&st);
+    lfm2_matmul_batch_avx2_mt(NULL, out, &t, x, n_tokens, scratch);
+    shim_restore(&st);
+    free(scratch);
+}

@@ -43,3 +43,72 @@ def softmax_attention_f64(q, k, v, scale):
     s -= s.max()
     p = np.exp(s)
     return (p @ v.astype(np.float64)) / p.sum()
+
+
+# ---- GGUF Q4_K / Q8_K blocks (packed, as the reference's block_q4_K_t /
+# block_q8_K_t, tools/lfm2_cpuid_quants.c:76-127) -----------------------------
+Q4K_BYTES, Q8K_BYTES = 144, 292
+
+
+def q4k_pattern(n_rows, nb, d, dmin, a, b, c, e):
+    """The reference tests' deterministic Q4_K weights: block i has d, dmin,
+    scales[j] = (i*a + j*b) & 63, qs[j] = (i*c + j*e) & 255."""
+    n = n_rows * nb
+    i = np.arange(n, dtype=np.int64)[:, None]
+    blk = np.zeros((n, Q4K_BYTES), np.uint8)
+    blk[:, 0:2] = np.array([d], np.uint16).view(np.uint8)
+    blk[:, 2:4] = np.array([dmin], np.uint16).view(np.uint8)
+    blk[:, 4:16] = ((i * a + np.arange(12) * b) & 0x3F).astype(np.uint8)
+    blk[:, 16:144] = ((i * c + np.arange(128) * e) & 0xFF).astype(np.uint8)
+    return blk.reshape(n_rows, nb * Q4K_BYTES)
+
+
+def q4k_random(rng, n_rows, n_cols):
+    """Random Q4_K rows: every bit of scales and qs random; d, dmin in
+    [2^-10, 2^-6] as fp16."""
+    nb = n_cols // 256
+    blk = rng.integers(0, 256, size=(n_rows * nb, Q4K_BYTES), dtype=np.uint8)
+    d = rng.uniform(2.0 ** -10, 2.0 ** -6, size=n_rows * nb).astype(np.float16)
+    dm = rng.uniform(2.0 ** -10, 2.0 ** -6, size=n_rows * nb).astype(np.float16)
+    blk[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    blk[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+    return blk.reshape(n_rows, nb * Q4K_BYTES)
+
+
+def _q4k_scale_min(q, j, planted_error=False):
+    if j < 4:
+        return q[:, j] & 63, q[:, j + 4] & 63
+    hi_src = q[:, j] if planted_error else q[:, j - 4]
+    sc = (q[:, j + 4] & 0x0F) | ((hi_src >> 6) << 4)
+    m = (q[:, j + 4] >> 4) | ((q[:, j] >> 6) << 4)
+    return sc, m
+
+
+def q4k_dequant(w, n_cols, planted_error=False):
+    """float64 [n_rows, n_cols]: weight = d*sc*q - dmin*m of its sub-block
+    (sub-block j of a super-block: nibbles of qs[32*(j//2) .. +32], low for
+    even j, high for odd j)."""
+    n_rows = w.shape[0]
+    nb = n_cols // 256
+    blk = w.reshape(n_rows * nb, Q4K_BYTES)
+    d = blk[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    dm = blk[:, 2:4].copy().view(np.float16).astype(np.float64)[:, 0]
+    sc_bytes = blk[:, 4:16].astype(np.int64)
+    qs = blk[:, 16:144].astype(np.int64)
+    out = np.zeros((n_rows * nb, 256))
+    for j in range(8):
+        sc, m = _q4k_scale_min(sc_bytes, j, planted_error)
+        q = qs[:, 32 * (j // 2):32 * (j // 2) + 32]
+        nib = (q & 0x0F) if j % 2 == 0 else (q >> 4)
+        out[:, 32 * j:32 * j + 32] = (d * sc)[:, None] * nib - (dm * m)[:, None]
+    return out.reshape(n_rows, n_cols)
+
+
+def q8k_dequant(q, n_cols):
+    """Q8_K rows -> (float64 values d*q8 [n_rows, n_cols], d [n_rows, nb])."""
+    n_rows = q.shape[0]
+    nb = n_cols // 256
+    blk = q.reshape(n_rows * nb, Q8K_BYTES)
+    d = blk[:, 0:4].copy().view(np.float32).astype(np.float64)[:, 0]
+    qs = blk[:, 4:260].copy().view(np.int8).astype(np.float64)
+    return (qs * d[:, None]).reshape(n_rows, n_cols), d.reshape(n_rows, nb)

@@ -15,7 +15,7 @@ from laii_amd import _lib
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "lfm_attn.h")
 
-E_INVALID, E_RANGE = -1, -2
+E_INVALID, E_RANGE, E_UNSUPPORTED = -1, -2, -3
 FAKE = 4096  # never dereferenced: validation rejects the call first
 
 
@@ -160,3 +160,19 @@ def test_shift_sinks_validation_before_launch():
                   C.byref(p), 4, 150, None) == E_INVALID
     assert p.value == 300
     assert lib.lfm_attn_ctx_shift_sinks(None, C.byref(p), 4, 8) == E_INVALID
+
+
+def test_quant_matmul_validation_before_launch():
+    """Q8_K / Q4_K entry points: empty work is OK, other bad arguments are
+    rejected before any device access."""
+    lib = la.load()
+    q8, mm = lib.lfm_hip_quantize_q8_K, lib.lfm_hip_matmul_q4_K
+    assert q8(None, None, 0, 256, None) == 0                  # nothing to do
+    assert q8(FAKE, None, 1, 256, None) == E_INVALID
+    assert q8(FAKE, FAKE, 1, 300, None) == E_UNSUPPORTED      # n_cols % 256
+    assert q8(FAKE + 2, FAKE, 1, 256, None) == E_INVALID      # misaligned x
+    assert mm(None, None, 0, 256, None, 1, None) == 0
+    assert mm(FAKE, FAKE, 4, 256, None, 1, None) == E_INVALID
+    assert mm(FAKE, FAKE, 4, 384, FAKE, 1, None) == E_UNSUPPORTED
+    assert mm(FAKE, FAKE + 4, 4, 256, FAKE, 1, None) == E_INVALID  # w not 16-byte aligned
+    assert mm(FAKE, FAKE, 4, 256, FAKE + 2, 1, None) == E_INVALID  # x_q8 not 4-byte aligned
