@@ -183,6 +183,65 @@ class KvShiftWorkload:
                                      max_seq, self.pos, self.n_sink, self.n_discard)
 
 
+class FusedQkvWorkload:
+    """LFM2-1.2B fused Q/K/V projection of one decode token: Q4_K 2048 x 2048
+    (Q) and 512 x 2048 (K), Q6_K 512 x 2048 (V, as Q4_K_M files store it), one
+    pass over the same Q8_K activations; rotated weight copies as in
+    QuantProjWorkload."""
+
+    def __init__(self, la, rng, n_tokens=1, copies=80):
+        self.la, self.n_tokens = la, n_tokens
+        self.rows, self.types, n_cols = [2048, 512, 512], [12, 12, 14], 2048
+        self.n_cols = n_cols
+        blk = {12: 144, 14: 210}
+        mats = []
+        for r, t in zip(self.rows, self.types):
+            w = rng.integers(0, 256, size=(r, 8 * blk[t]), dtype=np.uint8)
+            if t == 12:
+                w.reshape(-1, 144)[:, 0:4] = np.array([0x2400, 0x2000], np.uint16).view(np.uint8)
+            else:
+                w.reshape(-1, 210)[:, 208:210] = np.array([0x2000], np.uint16).view(np.uint8)
+            mats.append(w)
+        self.w = [[la.DeviceArray.from_numpy(w) for w in mats] for _ in range(copies)]
+        xd = la.DeviceArray.from_numpy(rng.standard_normal((n_tokens, n_cols)).astype(np.float32))
+        self.xq = la.DeviceArray.zeros((n_tokens, 8 * 292), np.uint8)
+        la.quantize_q8_K(xd, self.xq, n_tokens, n_cols)
+        self.outs = [la.DeviceArray.zeros((n_tokens, r), np.float32) for r in self.rows]
+        self.i = 0
+        self.bytes = sum(m.nbytes for m in mats) + n_tokens * 8 * 292 + n_tokens * sum(self.rows) * 4
+
+    def step(self):
+        self.la.gqa_qkv_fused(self.outs, self.w[self.i], self.types, self.rows, self.n_cols, self.xq,
+                              self.n_tokens)
+        self.i = (self.i + 1) % len(self.w)
+
+
+class QuantProjWorkload:
+    """A Q4_K projection beside the attention path: LFM2-1.2B `wo`
+    (2048 x 2048) applied to n_tokens Q8_K tokens.  Each step reads a
+    different copy of the weights, so the weights (not the 256 MB last-level
+    cache) are streamed from HBM as at decode, where a step reads every
+    layer's weights once."""
+
+    def __init__(self, la, rng, n_rows=2048, n_cols=2048, n_tokens=1, copies=120):
+        self.la, self.n_rows, self.n_cols, self.n_tokens = la, n_rows, n_cols, n_tokens
+        nb = n_cols // 256
+        w = rng.integers(0, 256, size=(n_rows, nb * 144), dtype=np.uint8)
+        w.reshape(-1, 144)[:, 0:4] = np.array([0x2400, 0x2000], np.uint16).view(np.uint8)  # d, dmin
+        self.w = [la.DeviceArray.from_numpy(w) for _ in range(copies)]
+        x = rng.standard_normal((n_tokens, n_cols)).astype(np.float32)
+        xd = la.DeviceArray.from_numpy(x)
+        self.xq = la.DeviceArray.zeros((n_tokens, nb * 292), np.uint8)
+        la.quantize_q8_K(xd, self.xq, n_tokens, n_cols)
+        self.out = la.DeviceArray.zeros((n_tokens, n_rows), np.float32)
+        self.i = 0
+        self.bytes = n_rows * nb * 144 + n_tokens * nb * 292 + n_tokens * n_rows * 4
+
+    def step(self):
+        self.la.matmul_q4_K(self.out, self.w[self.i], self.n_rows, self.n_cols, self.xq, self.n_tokens)
+        self.i = (self.i + 1) % len(self.w)
+
+
 def time_steps(hip, wl, steps, warmup):
     for _ in range(warmup):
         wl.step()
@@ -323,6 +382,21 @@ def main():
             pct_hbm_peak=round(100 * ks.bytes / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
         log(f"kv shift: {kms * 1e3:.1f} us/step")
         del ks
+        for n_tok in (1, 64):
+            qp = QuantProjWorkload(la, rng, n_tokens=n_tok)
+            qms = time_steps(hip, qp, max(20, args.steps), 5)
+            secondary[f"wo_q4K_q8K_lfm2_1p2b_2048x2048_tokens{n_tok}"] = dict(
+                GBps=round(qp.bytes / (qms * 1e-3) / 1e9, 1), us_per_step=round(qms * 1e3, 2),
+                bytes=qp.bytes, pct_hbm_peak=round(100 * qp.bytes / (qms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
+            log(f"wo q4_K tokens {n_tok}: {qms * 1e3:.2f} us/step")
+            del qp
+        fq = FusedQkvWorkload(la, rng)
+        fms = time_steps(hip, fq, max(20, args.steps), 5)
+        secondary["qkv_fused_q4K_q6K_lfm2_1p2b_tokens1"] = dict(
+            GBps=round(fq.bytes / (fms * 1e-3) / 1e9, 1), us_per_step=round(fms * 1e3, 2), bytes=fq.bytes,
+            pct_hbm_peak=round(100 * fq.bytes / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
+        log(f"qkv fused tokens 1: {fms * 1e3:.2f} us/step")
+        del fq
 
     cpu = None
     parity = None

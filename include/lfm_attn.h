@@ -142,6 +142,23 @@ int lfm_hip_quantize_q8_K(const float *x, void *y_q8_K, uint32_t n_rows, uint32_
 int lfm_hip_matmul_q4_K(float *out, const void *w_q4_K, uint32_t n_rows, uint32_t n_cols,
                         const void *x_q8_K, uint32_t n_tokens, lfm_attn_stream_t stream);
 
+/* Fused projections of one Q8_K activation set x_q8_K [n_tokens][n_cols/256]
+ * through the Q, K, V and (optional) gate matrices in one pass: q_out[t][r] =
+ * row r of wq . token t, likewise k, v, g.  Replaces
+ * lfm2_gqa_qkv_fused_1x4_mt (tools/lfm2_decode_1x4.c:885-930; g_out NULL)
+ * and lfm3_gqa_qkvg_1x4_mt (tools/lfm3_engine.c:1545-1598).  types[4] holds
+ * each matrix's GGML type: 12 (Q4_K, 16-byte aligned) or 14 (Q6_K, block_q6_K
+ * 210 B: ql[128], qh[64], int8 scales[16], fp16 d; 2-byte aligned); any other
+ * type gives LFM_ATTN_E_UNSUPPORTED.  Each row is bit-identical to the
+ * reference's AVX2 1x1 dot of its type (include/lfm2_simd_avx2.h:364-412,
+ * 551-634).  The gate output is the raw projection: the attention entry points
+ * take it as logits (gate_is_logit), which applies the reference's sigmoid. */
+int lfm_hip_gqa_qkv_fused(float *q_out, float *k_out, float *v_out, float *g_out, const void *wq,
+                          const void *wk, const void *wv, const void *wg, const uint32_t types[4],
+                          uint32_t q_rows, uint32_t k_rows, uint32_t v_rows, uint32_t g_rows,
+                          uint32_t n_cols, const void *x_q8_K, uint32_t n_tokens,
+                          lfm_attn_stream_t stream);
+
 /* ---- attention ------------------------------------------------------------ */
 /* A1 -- replaces OnlineGQATaskCtx + lfm2_parallel_for(pool, ceil(n_head_q/4), 1,
  * lfm2_online_gqa_f16_worker_simd, &ctx), tools/lfm2_kernels_fast.c:685-697,

@@ -6,11 +6,14 @@ host mirror: ctypes bindings named after the reference's dispatch calls.
 """
 from ._lib import LIB_PATH, LfmAttnError, load  # noqa: F401
 from .attention import (  # noqa: F401
+    GGML_Q4_K,
+    GGML_Q6_K,
     DeviceArray,
     EngineContext,
     device_count,
     gqa_f16_varlen,
     gqa_heads,
+    gqa_qkv_fused,
     kv_cache_shift_sinks,
     lfm3_kv_cache_shift_sinks,
     lfm3_online_gqa_f16_dispatch,

@@ -158,6 +158,26 @@ def matmul_q4_K(out: Ptr, w_q4_K: Ptr, n_rows: int, n_cols: int, x_q8_K: Ptr, n_
                                      stream), "lfm_hip_matmul_q4_K")
 
 
+GGML_Q4_K, GGML_Q6_K = 12, 14
+
+
+def gqa_qkv_fused(outs: Sequence[Ptr], ws: Sequence[Ptr], types: Sequence[int],
+                  rows: Sequence[int], n_cols: int, x_q8_K: Ptr, n_tokens: int, stream=None) -> None:
+    """Q, K, V (and gate, if a fourth matrix is given) projections of the same
+    Q8_K tokens in one pass (lfm2_gqa_qkv_fused_1x4_mt,
+    tools/lfm2_decode_1x4.c:885-930; lfm3_gqa_qkvg_1x4_mt,
+    tools/lfm3_engine.c:1545-1598).  types: GGML ids, 12 (Q4_K) or 14 (Q6_K)."""
+    outs, ws, types, rows = list(outs), list(ws), list(types), list(rows)
+    while len(outs) < 4:
+        outs.append(None)
+        ws.append(None)
+        types.append(GGML_Q4_K)
+        rows.append(0)
+    t = (C.c_uint32 * 4)(*types)
+    check(load().lfm_hip_gqa_qkv_fused(*[_p(o) for o in outs], *[_p(w) for w in ws], t, *rows, n_cols,
+                                       _p(x_q8_K), n_tokens, stream), "lfm_hip_gqa_qkv_fused")
+
+
 def qkv_prologue(q: Ptr, k: Ptr, v: Ptr, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr, n_seq: int,
                  n_rows: int, n_head_q: int, n_head_kv: int, head_dim: int, q_norm_w: Ptr,
                  k_norm_w: Ptr, eps: float, cos_lut: Ptr, sin_lut: Ptr, window_len: int = 0,

@@ -68,8 +68,10 @@ int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *cons
 /* Projections beside the attention path (quant_matmul.hip).  y/x_q8:
  * packed block_q8_K rows; w: packed block_q4_K rows; n_cols % 256 == 0. */
 int launch_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_cols, hipStream_t stream);
-int launch_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols, const void *x_q8,
-                       uint32_t n_tokens, hipStream_t stream);
+/* Up to 4 matrices (GGML type 12 Q4_K or 14 Q6_K, rows[m] each) over the
+ * same Q8_K tokens: outs[m][t][r]. */
+int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, const uint32_t *types,
+                    const uint32_t *rows, uint32_t n_cols, const void *x_q8, uint32_t n_tokens, hipStream_t stream);
 
 /* Attention-sink eviction (kv_shift.hip).  launch_kv_shift moves rows
  * [n_sink + n_discard, n_sink + n_discard + n_keep) down to n_sink and

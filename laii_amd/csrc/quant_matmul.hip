@@ -23,7 +23,7 @@
  *             order (lfm2_vec_dot_q4_K_q8_K_avx2, include/lfm2_simd_avx2.h:364-412).
  * So results are bit-identical to that reference kernel.
  *
- * Work decomposition of the product: one wave per R consecutive rows; the 8
+ * Work decomposition of the product: one wave per RPW consecutive rows; the 8
  * lanes of a lane group take the 8 16-byte parts of one super-block's qs
  * (part p holds 16 weights of sub-block 2*(p/2) in its low nibbles and 16 of
  * sub-block 2*(p/2)+1 in its high nibbles), so a wave covers 8 super-blocks
@@ -40,7 +40,6 @@ namespace lfm {
 namespace {
 
 constexpr uint32_t kQ4K = 144u, kQ8K = 292u;
-constexpr int kRows = 4; /* rows per wave */
 
 __device__ __forceinline__ uint32_t ld32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
 
@@ -93,102 +92,248 @@ __device__ __forceinline__ void scale_min(uint32_t j, const uint8_t *sc12, int32
     }
 }
 
-/* One super-block's term: (d*d8)*dot - (dmin*d8)*mins, each step rounded. */
-__device__ __forceinline__ float block_term(float d, float dmin, float d8, int32_t dot, int32_t mins) {
-#pragma clang fp contract(off)
-    const float dd = d * d8, dm = dmin * d8;
-    return dd * (float)dot - dm * (float)mins;
-}
+__device__ __forceinline__ float fp16_bits(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
 __device__ __forceinline__ float add_rounded(float a, float b) {
 #pragma clang fp contract(off)
     return a + b;
 }
 
-/* ---- Q4_K x Q8_K: out[t][r] --------------------------------------------------- */
-__global__ __launch_bounds__(256) void k_matmul_q4K(float *__restrict__ out, const uint8_t *__restrict__ w,
-                                                    const uint8_t *__restrict__ xq, uint32_t n_rows,
-                                                    uint32_t nb, uint32_t n_tokens) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t r0   = (blockIdx.x * 4u + (threadIdx.x >> 6)) * kRows;
-    if (r0 >= n_rows) return;
-    const uint32_t p  = lane & 7u;  /* 16-byte part of qs              */
-    const uint32_t g  = lane >> 3;  /* super-block slot of this step   */
-    const uint32_t jp = p >> 1;     /* sub-block pair                  */
-    const uint32_t h  = p & 1u;     /* first or second 16 of each half */
-    /* q8 offsets of this part's 16 low-nibble and 16 high-nibble partners */
-    const uint32_t qlo = 4u + 64u * jp + 16u * h, qhi = qlo + 32u;
-    const uint32_t bslo = 260u + 2u * (4u * jp + h), bshi = bslo + 4u;
-    const size_t row_bytes = (size_t)nb * kQ4K;
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
 
-    for (uint32_t t = 0; t < n_tokens; ++t) {
-        const uint8_t *xt = xq + (size_t)t * nb * kQ8K;
-        float sumf[kRows];
+/* Per weight type: what lane p (0..7) of a super-block's lane group loads and
+ * computes.  Both give two exact integer partials (a, b) that sum over the
+ * 8 lanes, and the super-block's fp32 term in the reference's rounding order. */
+template <int TYPE> struct QType;
+
+/* Q4_K: part p = qs bytes 16p..16p+15: 16 weights of sub-block 2*(p/2) (low
+ * nibbles) and of sub-block 2*(p/2)+1 (high nibbles); a = sum(sc*q4*q8),
+ * b = sum(m*bsum); term = (d*d8)*a - (dmin*d8)*b
+ * (include/lfm2_simd_avx2.h:364-412). */
+template <> struct QType<12> {
+    static constexpr uint32_t kBytes = 144u;
+    struct W { uint32_t q[4]; int32_t sc1, m1, sc2, m2; float d, dmin; };
+    struct X { float d8; uint32_t lo[4], hi[4]; int32_t bl, bh; };
+    static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qs  = *reinterpret_cast<const uint4 *>(blk + 16u + 16u * p);
+        w.q[0] = qs.x;
+        w.q[1] = qs.y;
+        w.q[2] = qs.z;
+        w.q[3] = qs.w;
+        uint8_t sc12[12];
+        __builtin_memcpy(sc12, reinterpret_cast<const uint8_t *>(&hdr) + 4, 12);
+        scale_min(2u * (p >> 1), sc12, &w.sc1, &w.m1);
+        scale_min(2u * (p >> 1) + 1u, sc12, &w.sc2, &w.m2);
+        w.d    = fp16_bits(hdr.x & 0xFFFFu);
+        w.dmin = fp16_bits(hdr.x >> 16);
+    }
+    static __device__ __forceinline__ void load_x(X &x, const uint8_t *xb, uint32_t p) {
+        const uint32_t jp = p >> 1, h = p & 1u;
+        const uint32_t qlo = 4u + 64u * jp + 16u * h, qhi = qlo + 32u;
+        x.d8 = *reinterpret_cast<const float *>(xb);
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) sumf[r] = 0.0f;
-        for (uint32_t b0 = 0; b0 < nb; b0 += 8u) {
-            const uint32_t b   = b0 + g;
-            const bool live    = b < nb;
-            const uint8_t *xb  = xt + (size_t)(live ? b : 0u) * kQ8K;
-            const float d8     = *reinterpret_cast<const float *>(xb);
-            uint32_t xl[4], xh[4];
+        for (int i = 0; i < 4; ++i) {
+            x.lo[i] = ld32(xb + qlo + 4u * i);
+            x.hi[i] = ld32(xb + qhi + 4u * i);
+        }
+        x.bl = *reinterpret_cast<const int16_t *>(xb + 260u + 2u * (4u * jp + h));
+        x.bh = *reinterpret_cast<const int16_t *>(xb + 260u + 2u * (4u * jp + 2u + h));
+    }
+    static __device__ __forceinline__ void partials(const W &w, const X &x, uint32_t, int32_t &a, int32_t &b) {
+        int32_t lo = 0, hi = 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                xl[i] = ld32(xb + qlo + 4u * i);
-                xh[i] = ld32(xb + qhi + 4u * i);
-            }
-            const int32_t bsl = *reinterpret_cast<const int16_t *>(xb + bslo);
-            const int32_t bsh = *reinterpret_cast<const int16_t *>(xb + bshi);
-            float term[kRows];
+        for (int i = 0; i < 4; ++i) {
+            lo = dot4(w.q[i] & 0x0F0F0F0Fu, x.lo[i], lo);
+            hi = dot4((w.q[i] >> 4) & 0x0F0F0F0Fu, x.hi[i], hi);
+        }
+        a = w.sc1 * lo + w.sc2 * hi;
+        b = w.m1 * x.bl + w.m2 * x.bh;
+    }
+    static __device__ __forceinline__ float term(const W &w, float d8, int32_t a, int32_t b) {
+#pragma clang fp contract(off)
+        const float dd = w.d * d8, dm = w.dmin * d8;
+        return dd * (float)a - dm * (float)b;
+    }
+};
+
+/* Q6_K (ql[128], qh[64], int8 scales[16], fp16 d; 210 bytes, so blocks are
+ * only 2-byte aligned): part p = half p/4, columns l in 8(p%4)..+8 of the
+ * half's four 32-groups; a = sum(sc*u*q8), b = sc[2p]*bsum[2p] +
+ * sc[2p+1]*bsum[2p+1]; term = (d*d8) * (float)(a - 32*b)
+ * (include/lfm2_simd_avx2.h:551-634). */
+template <> struct QType<14> {
+    static constexpr uint32_t kBytes = 210u;
+    struct W { uint32_t l0[2], l1[2], qh[2]; int32_t s[4], so0, so1; float d; };
+    struct X { float d8; uint32_t x[4][2]; int32_t b0, b1; };
+    static __device__ __forceinline__ uint32_t ld16x2(const uint8_t *p) { /* 2-byte aligned */
+        const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+        return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    }
+    static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
+        const uint32_t half = p >> 2, q = p & 3u;
+        const uint8_t *ql = blk + 64u * half + 8u * q, *qh = blk + 128u + 32u * half + 8u * q;
 #pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                const uint32_t row = min(r0 + (uint32_t)r, n_rows - 1u);
-                const uint8_t *wb  = w + row * row_bytes + (size_t)(live ? b : 0u) * kQ4K;
-                const uint4 hdr    = *reinterpret_cast<const uint4 *>(wb);
-                const uint4 qs     = *reinterpret_cast<const uint4 *>(wb + 16u + 16u * p);
-                uint8_t sc12[12];
-                __builtin_memcpy(sc12, reinterpret_cast<const uint8_t *>(&hdr) + 4, 12);
-                int32_t sc1, m1, sc2, m2;
-                scale_min(2u * jp, sc12, &sc1, &m1);
-                scale_min(2u * jp + 1u, sc12, &sc2, &m2);
-                const uint32_t qv[4] = {qs.x, qs.y, qs.z, qs.w};
-                int32_t lo = 0, hi = 0;
+        for (int i = 0; i < 2; ++i) {
+            w.l0[i] = ld16x2(ql + 4u * i);
+            w.l1[i] = ld16x2(ql + 32u + 4u * i);
+            w.qh[i] = ld16x2(qh + 4u * i);
+        }
+        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192u + 8u * half + (q >> 1));
+        w.s[0] = sc[0];
+        w.s[1] = sc[2];
+        w.s[2] = sc[4];
+        w.s[3] = sc[6];
+        const int8_t *so = reinterpret_cast<const int8_t *>(blk + 192u + 2u * p);
+        w.so0 = so[0];
+        w.so1 = so[1];
+        w.d   = fp16_bits(*reinterpret_cast<const uint16_t *>(blk + 208u));
+    }
+    static __device__ __forceinline__ void load_x(X &x, const uint8_t *xb, uint32_t p) {
+        const uint32_t half = p >> 2, q = p & 3u;
+        x.d8 = *reinterpret_cast<const float *>(xb);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    lo = __builtin_amdgcn_sdot4((int)(qv[i] & 0x0F0F0F0Fu), (int)xl[i], lo, false);
-                    hi = __builtin_amdgcn_sdot4((int)((qv[i] >> 4) & 0x0F0F0F0Fu), (int)xh[i], hi, false);
-                }
-                int32_t dot  = sc1 * lo + sc2 * hi;
-                int32_t mins = m1 * bsl + m2 * bsh;
+        for (int k = 0; k < 4; ++k) {
+            const uint8_t *g = xb + 4u + 128u * half + 32u * k + 8u * q;
+            x.x[k][0] = ld32(g);
+            x.x[k][1] = ld32(g + 4u);
+        }
+        const uint32_t bs = ld32(xb + 260u + 4u * p); /* bsums 2p, 2p+1 */
+        x.b0 = (int16_t)(bs & 0xFFFFu);
+        x.b1 = (int16_t)(bs >> 16);
+    }
+    static __device__ __forceinline__ void partials(const W &w, const X &x, uint32_t, int32_t &a, int32_t &b) {
+        int32_t acc = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t u1 = (w.l0[i] & 0x0F0F0F0Fu) | ((w.qh[i] & 0x03030303u) << 4);
+            const uint32_t u2 = (w.l1[i] & 0x0F0F0F0Fu) | ((w.qh[i] & 0x0C0C0C0Cu) << 2);
+            const uint32_t u3 = ((w.l0[i] >> 4) & 0x0F0F0F0Fu) | (w.qh[i] & 0x30303030u);
+            const uint32_t u4 = ((w.l1[i] >> 4) & 0x0F0F0F0Fu) | ((w.qh[i] >> 2) & 0x30303030u);
+            acc += w.s[0] * dot4(u1, x.x[0][i], 0) + w.s[1] * dot4(u2, x.x[1][i], 0) +
+                   w.s[2] * dot4(u3, x.x[2][i], 0) + w.s[3] * dot4(u4, x.x[3][i], 0);
+        }
+        a = acc;
+        b = w.so0 * x.b0 + w.so1 * x.b1;
+    }
+    static __device__ __forceinline__ float term(const W &w, float d8, int32_t a, int32_t b) {
+#pragma clang fp contract(off)
+        const float dd = w.d * d8;
+        return dd * (float)(a - 32 * b);
+    }
+};
+
+/* Up to four matrices over the same activations (Q, K, V, gate); waves
+ * [wave0[m], wave0[m+1]) cover matrix m, RPW rows each. */
+struct MatSet {
+    const uint8_t *w[4];
+    float *out[4];
+    uint32_t rows[4];
+    uint32_t wave0[5];
+    uint32_t n;
+};
+
+/* ---- quantized weights x Q8_K: out[t][r] ----------------------------------------
+ * RPW rows of one matrix and a chunk of TCH tokens per wave (grid y = token
+ * chunks): per 8-super-block step a lane loads its part of the RPW rows'
+ * weights and of the TCH tokens' activations in one batch, then forms the
+ * RPW x TCH partials, sums them over its lane group, and adds the
+ * super-blocks' terms to the row sums in order. */
+template <int TYPE, int RPW, int TCH>
+__global__ __launch_bounds__(256) void k_matmul_q(const MatSet S, const uint8_t *__restrict__ xq, uint32_t nb,
+                                                  uint32_t n_tokens) {
+    using Q = QType<TYPE>;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wv   = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (wv >= S.wave0[S.n]) return;
+    uint32_t m = 0;
+    while (m + 1u < S.n && wv >= S.wave0[m + 1u]) ++m;
+    const uint32_t n_rows = S.rows[m];
+    const uint32_t r0     = (wv - S.wave0[m]) * RPW;
+    const uint8_t *w      = S.w[m];
+    float *out            = S.out[m];
+    const uint32_t p = lane & 7u; /* part within the super-block    */
+    const uint32_t g = lane >> 3; /* super-block slot of this step  */
+    const size_t row_bytes = (size_t)nb * Q::kBytes;
+    const uint32_t t0      = blockIdx.y * TCH;
+
+    float sumf[TCH][RPW];
+#pragma unroll
+    for (int tt = 0; tt < TCH; ++tt)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) sumf[tt][r] = 0.0f;
+    for (uint32_t b0 = 0; b0 < nb; b0 += 8u) {
+        const uint32_t b = min(b0 + g, nb - 1u); /* slots past the end repeat a block, unused */
+        typename Q::W wr[RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const uint32_t row = min(r0 + (uint32_t)r, n_rows - 1u);
+            Q::load_w(wr[r], w + row * row_bytes + (size_t)b * Q::kBytes, p);
+        }
+        typename Q::X xt[TCH];
+#pragma unroll
+        for (int tt = 0; tt < TCH; ++tt) {
+            const uint32_t t = min(t0 + (uint32_t)tt, n_tokens - 1u);
+            Q::load_x(xt[tt], xq + ((size_t)t * nb + b) * kQ8K, p);
+        }
+        float term[TCH][RPW];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int tt = 0; tt < TCH; ++tt) {
+                int32_t a, c;
+                Q::partials(wr[r], xt[tt], p, a, c);
 #pragma unroll
                 for (int o = 1; o < 8; o <<= 1) {
-                    dot += __shfl_xor(dot, o);
-                    mins += __shfl_xor(mins, o);
+                    a += __shfl_xor(a, o);
+                    c += __shfl_xor(c, o);
                 }
-                const float d    = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x & 0xFFFFu));
-                const float dmin = (float)__builtin_bit_cast(_Float16, (uint16_t)(hdr.x >> 16));
-                term[r]          = block_term(d, dmin, d8, dot, mins);
+                term[tt][r] = Q::term(wr[r], xt[tt].d8, a, c);
             }
-            /* super-blocks b0 .. b0+7 in order; a block whose d8 is 0 adds nothing */
+        /* super-blocks b0 .. b0+7 in order; a block whose d8 is 0 adds nothing */
 #pragma unroll
-            for (uint32_t i = 0; i < 8u; ++i) {
-                if (b0 + i >= nb) break;
-                const float d8i = __shfl(d8, (int)(8u * i));
+        for (uint32_t i = 0; i < 8u; ++i) {
+            if (b0 + i >= nb) break;
 #pragma unroll
-                for (int r = 0; r < kRows; ++r) {
-                    const float ti = __shfl(term[r], (int)(8u * i));
-                    if (d8i != 0.0f) sumf[r] = add_rounded(sumf[r], ti);
+            for (int tt = 0; tt < TCH; ++tt) {
+                const float d8i = __shfl(xt[tt].d8, (int)(8u * i));
+#pragma unroll
+                for (int r = 0; r < RPW; ++r) {
+                    const float ti = __shfl(term[tt][r], (int)(8u * i));
+                    if (d8i != 0.0f) sumf[tt][r] = add_rounded(sumf[tt][r], ti);
                 }
             }
-        }
-        if (lane < (uint32_t)kRows && r0 + lane < n_rows) {
-            float v = sumf[0];
-#pragma unroll
-            for (int r = 1; r < kRows; ++r)
-                if (lane == (uint32_t)r) v = sumf[r];
-            out[(size_t)t * n_rows + r0 + lane] = v;
         }
     }
+    /* lane tt * RPW + r writes token t0 + tt, row r0 + r */
+#pragma unroll
+    for (int tt = 0; tt < TCH; ++tt)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+            if (lane == (uint32_t)(tt * RPW + r) && t0 + tt < n_tokens && r0 + r < n_rows)
+                out[(size_t)(t0 + tt) * n_rows + r0 + r] = sumf[tt][r];
+}
+
+template <int TYPE, int RPW, int TCH>
+hipError_t launch_set(MatSet S, const void *x_q8, uint32_t nb, uint32_t n_tokens, hipStream_t stream) {
+    S.wave0[0] = 0;
+    for (uint32_t m = 0; m < S.n; ++m) S.wave0[m + 1] = S.wave0[m] + (S.rows[m] + RPW - 1u) / RPW;
+    if (S.wave0[S.n] == 0u) return hipSuccess;
+    hipLaunchKernelGGL((k_matmul_q<TYPE, RPW, TCH>), dim3((S.wave0[S.n] + 3u) / 4u, (n_tokens + TCH - 1u) / TCH),
+                       dim3(256), 0, stream, S, static_cast<const uint8_t *>(x_q8), nb, n_tokens);
+    return hipGetLastError();
+}
+
+/* one token: a row per wave (most waves in flight); more: two rows and up to
+ * eight tokens per wave share each weight and activation load */
+template <int TYPE>
+hipError_t launch_type(const MatSet &S, const void *x_q8, uint32_t nb, uint32_t n_tokens, hipStream_t stream) {
+    if (n_tokens == 1u) return launch_set<TYPE, 1, 1>(S, x_q8, nb, n_tokens, stream);
+    if (n_tokens == 2u) return launch_set<TYPE, 2, 2>(S, x_q8, nb, n_tokens, stream);
+    if (n_tokens <= 4u) return launch_set<TYPE, 2, 4>(S, x_q8, nb, n_tokens, stream);
+    return launch_set<TYPE, 2, 8>(S, x_q8, nb, n_tokens, stream);
 }
 
 } // namespace
@@ -202,14 +347,26 @@ int launch_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_co
     return hip_status(hipGetLastError());
 }
 
-int launch_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols, const void *x_q8,
-                       uint32_t n_tokens, hipStream_t stream) {
-    if (n_rows == 0u || n_tokens == 0u) return LFM_ATTN_OK;
-    const uint32_t waves = (n_rows + kRows - 1u) / kRows;
-    hipLaunchKernelGGL(k_matmul_q4K, dim3((waves + 3u) / 4u), dim3(256), 0, stream, out,
-                       static_cast<const uint8_t *>(w), static_cast<const uint8_t *>(x_q8), n_rows,
-                       n_cols / 256u, n_tokens);
-    return hip_status(hipGetLastError());
+int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, const uint32_t *types,
+                    const uint32_t *rows, uint32_t n_cols, const void *x_q8, uint32_t n_tokens, hipStream_t stream) {
+    if (n_tokens == 0u) return LFM_ATTN_OK;
+    const uint32_t nb = n_cols / 256u;
+    /* one launch per weight type present, each over its matrices */
+    for (uint32_t type : {12u, 14u}) {
+        MatSet S{};
+        for (uint32_t m = 0; m < n_mats; ++m) {
+            if (types[m] != type || rows[m] == 0u) continue;
+            S.w[S.n]    = static_cast<const uint8_t *>(ws[m]);
+            S.out[S.n]  = outs[m];
+            S.rows[S.n] = rows[m];
+            ++S.n;
+        }
+        if (S.n == 0u) continue;
+        const hipError_t e = type == 12u ? launch_type<12>(S, x_q8, nb, n_tokens, stream)
+                                         : launch_type<14>(S, x_q8, nb, n_tokens, stream);
+        if (e != hipSuccess) return hip_status(e);
+    }
+    return LFM_ATTN_OK;
 }
 
 } // namespace lfm

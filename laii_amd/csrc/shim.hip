@@ -219,7 +219,33 @@ int lfm_hip_matmul_q4_K(float *out, const void *w_q4_K, uint32_t n_rows, uint32_
     if (!out || !w_q4_K || !x_q8_K || n_cols == 0u) return LFM_ATTN_E_INVALID;
     if (n_cols % 256u) return LFM_ATTN_E_UNSUPPORTED;
     if (!aligned(w_q4_K, 16) || !aligned(x_q8_K, 4) || !aligned(out, 4)) return LFM_ATTN_E_INVALID;
-    return lfm::launch_matmul_q4_K(out, w_q4_K, n_rows, n_cols, x_q8_K, n_tokens, to_stream(stream));
+    const uint32_t type = 12u;
+    return lfm::launch_matmul_q(1u, &out, &w_q4_K, &type, &n_rows, n_cols, x_q8_K, n_tokens, to_stream(stream));
+}
+
+int lfm_hip_gqa_qkv_fused(float *q_out, float *k_out, float *v_out, float *g_out, const void *wq,
+                          const void *wk, const void *wv, const void *wg, const uint32_t types[4],
+                          uint32_t q_rows, uint32_t k_rows, uint32_t v_rows, uint32_t g_rows, uint32_t n_cols,
+                          const void *x_q8_K, uint32_t n_tokens, lfm_attn_stream_t stream) {
+    if (!types) return LFM_ATTN_E_INVALID;
+    float *outs[4]       = {q_out, k_out, v_out, g_out};
+    const void *ws[4]    = {wq, wk, wv, wg};
+    const uint32_t rows[4] = {q_rows, k_rows, v_rows, g_out ? g_rows : 0u};
+    if (n_tokens == 0u) return LFM_ATTN_OK;
+    if (!x_q8_K || n_cols == 0u || !aligned(x_q8_K, 4)) return LFM_ATTN_E_INVALID;
+    if (n_cols % 256u) return LFM_ATTN_E_UNSUPPORTED;
+    for (int m = 0; m < 4; ++m) {
+        if (rows[m] == 0u) continue;
+        if (!outs[m] || !ws[m] || !aligned(outs[m], 4)) return LFM_ATTN_E_INVALID;
+        if (types[m] == 12u) {
+            if (!aligned(ws[m], 16)) return LFM_ATTN_E_INVALID;
+        } else if (types[m] == 14u) {
+            if (!aligned(ws[m], 2)) return LFM_ATTN_E_INVALID;
+        } else {
+            return LFM_ATTN_E_UNSUPPORTED;
+        }
+    }
+    return lfm::launch_matmul_q(4u, outs, ws, types, rows, n_cols, x_q8_K, n_tokens, to_stream(stream));
 }
 
 /* ---- attention -------------------------------------------------------------- */

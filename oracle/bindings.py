@@ -76,6 +76,9 @@ class Oracle:
         L.orc_dot_q4_K_q8_K.restype = _f32
         L.orc_dot_q4_K_q8_K.argtypes = [_u8p, _u8p, _u32]
         L.orc_matmul_q4_K.argtypes = [_f32p, _u8p, _u32, _u32, _u8p, _u32]
+        L.orc_dot_q6_K_q8_K.restype = _f32
+        L.orc_dot_q6_K_q8_K.argtypes = [_u8p, _u8p, _u32]
+        L.orc_matmul_q.argtypes = [_f32p, _u8p, _u32, _u32, _u32, _u8p, _u32]
         L.orc_f16_to_f32.restype = _f32
         L.orc_f16_to_f32.argtypes = [C.c_uint16]
         L.orc_f32_to_f16.restype = C.c_uint16
@@ -256,8 +259,24 @@ def _orc_matmul(self, w, x_q8, n_cols):
     return out
 
 
+def _orc_dot6(self, w_row, x_q8, n_cols):
+    return float(self.lib.orc_dot_q6_K_q8_K(np.ascontiguousarray(w_row, np.uint8),
+                                             np.ascontiguousarray(x_q8, np.uint8), n_cols))
+
+
+def _orc_matmul_q(self, w, qtype, x_q8, n_cols):
+    """GGML type 12 (Q4_K) or 14 (Q6_K) rows: w uint8 [n_rows, row bytes] -> float32 [B, n_rows]."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x_q8 = np.ascontiguousarray(x_q8, np.uint8)
+    out = np.zeros((x_q8.shape[0], w.shape[0]), np.float32)
+    self.lib.orc_matmul_q(out, w, qtype, w.shape[0], n_cols, x_q8, x_q8.shape[0])
+    return out
+
+
 Oracle.dot_q4_K = _orc_dot
 Oracle.matmul_q4_K = _orc_matmul
+Oracle.dot_q6_K = _orc_dot6
+Oracle.matmul_q = _orc_matmul_q
 
 
 class Reference:
@@ -299,6 +318,8 @@ class Reference:
         L.ref_dot_q4_K_avx2.argtypes = [_u8p, _u8p, _u32]
         L.ref_matmul_q4_K_prequant.argtypes = [_f32p, _u8p, _u32, _u32, _u8p]
         L.ref_matmul_q4_K_batch.argtypes = [_f32p, _u8p, _u32, _u32, _f32p, _u32]
+        L.ref_dot_q6_K_avx2.restype = _f32
+        L.ref_dot_q6_K_avx2.argtypes = [_u8p, _u8p, _u32]
         self.has_avx2 = bool(L.ref_has_avx2())
 
     def kv_shift_sinks_lfm2(self, k_caches, v_caches, n_head_kv, head_dim, lut, pos, n_sink,
@@ -421,3 +442,11 @@ Reference.quantize_q8_K = _quantize_q8_K
 Reference.dot_q4_K = _ref_dot
 Reference.matmul_q4_K_prequant = _ref_matmul_prequant
 Reference.matmul_q4_K_batch = _ref_matmul_batch
+
+
+def _ref_dot6(self, w_row, x_q8, n_cols):
+    return float(self.lib.ref_dot_q6_K_avx2(np.ascontiguousarray(w_row, np.uint8),
+                                             np.ascontiguousarray(x_q8, np.uint8), n_cols))
+
+
+Reference.dot_q6_K = _ref_dot6

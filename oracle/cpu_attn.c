@@ -704,3 +704,56 @@ void orc_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols
                 orc_dot_q4_K_q8_K((const uint8_t *)w + (size_t)r * nb * ORC_Q4K_BYTES,
                                   (const uint8_t *)x_q8 + (size_t)t * nb * ORC_Q8K_BYTES, n_cols);
 }
+
+float orc_dot_q6_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    const uint8_t *w  = (const uint8_t *)w_row;
+    const uint8_t *xq = (const uint8_t *)x_q8;
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *wb = w + (size_t)b * ORC_Q6K_BYTES;
+        const uint8_t *xb = xq + (size_t)b * ORC_Q8K_BYTES;
+        float d8;
+        memcpy(&d8, xb, 4);
+        if (d8 == 0.0f) continue;
+        uint16_t dh;
+        memcpy(&dh, wb + 208, 2);
+        const float d = orc_f16_to_f32(dh) * d8;
+        const uint8_t *ql = wb, *qh = wb + 128;
+        const int8_t *sc  = (const int8_t *)(wb + 192);
+        const int8_t *q8  = (const int8_t *)(xb + 4);
+        int16_t bs[16];
+        memcpy(bs, xb + 260, sizeof bs);
+        int32_t offset = 0;
+        for (int is = 0; is < 16; ++is) offset += (int32_t)sc[is] * bs[is];
+        int32_t acc = 0;
+        for (int half = 0; half < 2; ++half) {
+            const uint8_t *l_ = ql + 64 * half, *h_ = qh + 32 * half;
+            const int8_t *s_ = sc + 8 * half, *x_ = q8 + 128 * half;
+            for (int l = 0; l < 32; ++l) {
+                const int32_t u1 = (l_[l] & 0x0F) | ((h_[l] & 0x03) << 4);
+                const int32_t u2 = (l_[l + 32] & 0x0F) | ((h_[l] & 0x0C) << 2);
+                const int32_t u3 = (l_[l] >> 4) | (h_[l] & 0x30);
+                const int32_t u4 = (l_[l + 32] >> 4) | ((h_[l] & 0xC0) >> 2);
+                const int g = l / 16;
+                acc += u1 * x_[l] * s_[g] + u2 * x_[l + 32] * s_[2 + g] + u3 * x_[l + 64] * s_[4 + g] +
+                       u4 * x_[l + 96] * s_[6 + g];
+            }
+        }
+        sumf += d * (float)(acc - 32 * offset);
+    }
+    return sumf;
+}
+
+void orc_matmul_q(float *out, const void *w, uint32_t type, uint32_t n_rows, uint32_t n_cols,
+                  const void *x_q8, uint32_t n_tokens) {
+    const uint32_t nb   = n_cols / 256u;
+    const size_t rowb   = (size_t)nb * (type == 14u ? ORC_Q6K_BYTES : ORC_Q4K_BYTES);
+    for (uint32_t t = 0; t < n_tokens; ++t)
+        for (uint32_t r = 0; r < n_rows; ++r) {
+            const void *wr = (const uint8_t *)w + (size_t)r * rowb;
+            const void *xt = (const uint8_t *)x_q8 + (size_t)t * nb * ORC_Q8K_BYTES;
+            out[(size_t)t * n_rows + r] = type == 14u ? orc_dot_q6_K_q8_K(wr, xt, n_cols)
+                                                      : orc_dot_q4_K_q8_K(wr, xt, n_cols);
+        }
+}

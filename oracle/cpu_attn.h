@@ -128,6 +128,17 @@ float orc_dot_q4_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
 void orc_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols,
                      const void *x_q8, uint32_t n_tokens);
 
+/* block_q6_K (210 B): ql[128], qh[64], int8 scales[16], fp16 d.  One row .
+ * Q8_K vector in the order of lfm2_vec_dot_q6_K_q8_K_avx2
+ * (include/lfm2_simd_avx2.h:551-634): exact sum(sc*u*q8) and sum(sc*bsum)
+ * per super-block, then sumf += (d*d8) * (float)(sum - 32*offset). */
+#define ORC_Q6K_BYTES 210u
+float orc_dot_q6_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
+
+/* out[t][r] for a matrix of GGML type 12 (Q4_K) or 14 (Q6_K). */
+void orc_matmul_q(float *out, const void *w, uint32_t type, uint32_t n_rows, uint32_t n_cols,
+                  const void *x_q8, uint32_t n_tokens);
+
 #ifdef __cplusplus
 }
 #endif

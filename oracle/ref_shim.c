@@ -354,3 +354,8 @@ void ref_matmul_q4_K_batch(float *out, const void *w, uint32_t n_rows, uint32_t 
     shim_restore(&st);
     free(scratch);
 }
+
+/* lfm2_vec_dot_q6_K_q8_K_avx2 (include/lfm2_simd_avx2.h:551-634), one row. */
+float ref_dot_q6_K_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    return lfm2_vec_dot_q6_K_q8_K_avx2((const block_q6_K_t *)w_row, (const block_q8_K_t *)x_q8, n_cols);
+}

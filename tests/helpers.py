@@ -112,3 +112,38 @@ def q8k_dequant(q, n_cols):
     d = blk[:, 0:4].copy().view(np.float32).astype(np.float64)[:, 0]
     qs = blk[:, 4:260].copy().view(np.int8).astype(np.float64)
     return (qs * d[:, None]).reshape(n_rows, n_cols), d.reshape(n_rows, nb)
+
+
+Q6K_BYTES = 210
+
+
+def q6k_random(rng, n_rows, n_cols):
+    """Random Q6_K rows: ql, qh random; int8 scales in [-64, 63]; d in [2^-12, 2^-8]."""
+    nb = n_cols // 256
+    blk = rng.integers(0, 256, size=(n_rows * nb, Q6K_BYTES), dtype=np.uint8)
+    blk[:, 192:208] = rng.integers(-64, 64, size=(n_rows * nb, 16)).astype(np.int8).view(np.uint8)
+    d = rng.uniform(2.0 ** -12, 2.0 ** -8, size=n_rows * nb).astype(np.float16)
+    blk[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return blk.reshape(n_rows, nb * Q6K_BYTES)
+
+
+def q6k_dequant(w, n_cols):
+    """float64 [n_rows, n_cols]: weight = d * sc * (u - 32), u the 6-bit value
+    (low 4 bits from ql, high 2 from qh), sc the int8 scale of its 16-group."""
+    n_rows = w.shape[0]
+    nb = n_cols // 256
+    blk = w.reshape(n_rows * nb, Q6K_BYTES).astype(np.int64)
+    d = w.reshape(n_rows * nb, Q6K_BYTES)[:, 208:210].copy().view(np.float16).astype(np.float64)[:, 0]
+    sc = w.reshape(n_rows * nb, Q6K_BYTES)[:, 192:208].copy().view(np.int8).astype(np.float64)
+    out = np.zeros((n_rows * nb, 256))
+    for half in range(2):
+        ql = blk[:, 64 * half:64 * half + 64]
+        qh = blk[:, 128 + 32 * half:128 + 32 * half + 32]
+        base = 128 * half
+        for l in range(32):
+            us = [(ql[:, l] & 0xF) | ((qh[:, l] & 3) << 4), (ql[:, l + 32] & 0xF) | ((qh[:, l] & 0xC) << 2),
+                  (ql[:, l] >> 4) | (qh[:, l] & 0x30), (ql[:, l + 32] >> 4) | ((qh[:, l] & 0xC0) >> 2)]
+            for k, u in enumerate(us):
+                idx = base + 32 * k + l
+                out[:, idx] = d * sc[:, idx // 16] * (u - 32)
+    return out.reshape(n_rows, n_cols)

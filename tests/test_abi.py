@@ -176,3 +176,18 @@ def test_quant_matmul_validation_before_launch():
     assert mm(FAKE, FAKE, 4, 384, FAKE, 1, None) == E_UNSUPPORTED
     assert mm(FAKE, FAKE + 4, 4, 256, FAKE, 1, None) == E_INVALID  # w not 16-byte aligned
     assert mm(FAKE, FAKE, 4, 256, FAKE + 2, 1, None) == E_INVALID  # x_q8 not 4-byte aligned
+
+
+def test_qkv_fused_validation_before_launch():
+    lib = la.load()
+    f = lib.lfm_hip_gqa_qkv_fused
+    t = (C.c_uint32 * 4)(12, 12, 14, 12)
+    bad = (C.c_uint32 * 4)(12, 12, 8, 12)  # Q8_0: no kernel here
+    args = lambda types, cols=2048, wv=FAKE: (FAKE, FAKE, FAKE, None, FAKE, FAKE, wv, None, types, 8, 8, 8,
+                                              4, cols, FAKE, 1, None)
+    assert f(*args(None)) == E_INVALID
+    assert f(*args(bad)) == E_UNSUPPORTED
+    assert f(*args(t, cols=300)) == E_UNSUPPORTED
+    assert f(*args(t, wv=FAKE + 1)) == E_INVALID            # Q6_K rows need 2-byte alignment
+    assert f(FAKE, FAKE, FAKE, None, FAKE + 8, FAKE, FAKE, None, t, 8, 8, 8, 0, 2048, FAKE, 1,
+             None) == E_INVALID                             # Q4_K rows need 16-byte alignment

@@ -8,7 +8,7 @@ the reference's fp32 order."""
 import numpy as np
 import pytest
 
-from helpers import parity, q4k_pattern, q4k_random
+from helpers import parity, q4k_pattern, q4k_random, q6k_random
 
 pytestmark = pytest.mark.gpu
 
@@ -117,3 +117,35 @@ def test_attention_output_to_wo_projection(gpu, orc):
     parity(xb_h, want_xb, what="attention")
     want = orc.matmul_q4_K(w, orc.quantize_q8_K(want_xb[None]), nq * hd)
     parity(out.numpy(), want, max_abs=2e-3 * max(1.0, float(np.abs(want).max())), what="wo")
+
+
+@pytest.mark.parametrize("n_rows,n_cols,B", [(8, 256, 1), (512, 2048, 1), (130, 2304, 5), (64, 2048, 64)])
+def test_q6K_matmul_bit_exact(gpu, orc, n_rows, n_cols, B):
+    """Q6_K rows (210-byte blocks, 2-byte aligned) through the fused entry."""
+    la = gpu
+    rng = np.random.default_rng(n_rows + B)
+    w = q6k_random(rng, n_rows, n_cols)
+    xq = orc.quantize_q8_K(rng.standard_normal((B, n_cols)).astype(np.float32))
+    out = la.DeviceArray.zeros((B, n_rows), np.float32)
+    la.gqa_qkv_fused([out], [dev(la, w)], [la.GGML_Q6_K], [n_rows], n_cols, dev(la, xq), B)
+    want = orc.matmul_q(w, 14, xq, n_cols)
+    assert np.array_equal(out.numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("B,gate,v_type", [(1, False, 12), (1, True, 14), (8, True, 14), (3, False, 14)])
+def test_qkv_fused_lfm2_lfm3_shapes(gpu, orc, B, gate, v_type):
+    """LFM2-1.2B Q/K/V (2048 -> 2048 / 512 / 512) and LFM3 with the gate
+    (16 rows): every output bit-exact against the oracle row by row, V in
+    Q4_K or Q6_K (Q4_K_M files store some `wv` as Q6_K)."""
+    la = gpu
+    rng = np.random.default_rng(B * 3 + gate)
+    n_cols, rows = 2048, [2048, 512, 512] + ([16] if gate else [])
+    types = [12, 12, v_type] + ([12] if gate else [])
+    ws = [q6k_random(rng, r, n_cols) if t == 14 else q4k_random(rng, r, n_cols)
+          for r, t in zip(rows, types)]
+    xq = orc.quantize_q8_K(rng.standard_normal((B, n_cols)).astype(np.float32))
+    outs = [la.DeviceArray.zeros((B, r), np.float32) for r in rows]
+    la.gqa_qkv_fused(outs, [dev(la, w) for w in ws], types, rows, n_cols, dev(la, xq), B)
+    for o, w, t in zip(outs, ws, types):
+        want = orc.matmul_q(w, t, xq, n_cols)
+        assert np.array_equal(o.numpy().view(np.uint32), want.view(np.uint32))

@@ -17,7 +17,7 @@ tests/test_cpuid_quants.c:69-112 of the reference."""
 import numpy as np
 import pytest
 
-from helpers import q4k_dequant, q4k_pattern, q4k_random, q8k_dequant
+from helpers import q4k_dequant, q4k_pattern, q4k_random, q6k_dequant, q6k_random, q8k_dequant
 
 
 def test_quantize_matches_reference_test_inputs(orc, ref):
@@ -141,3 +141,26 @@ def test_planted_scale_unpack_error_breaks_closed_form(orc):
     got = orc.matmul_q4_K(w, xq, 512)
     assert np.abs(got - good).max() < 1e-3 * np.abs(good).max()
     assert np.abs(got - bad).max() > 0.05 * np.abs(good).max()
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_q6K_dot_matches_reference(orc, ref, seed):
+    """Q6_K rows (the `wv` type of Q4_K_M files) bit-exact against
+    lfm2_vec_dot_q6_K_q8_K_avx2 (include/lfm2_simd_avx2.h:551-634)."""
+    rng = np.random.default_rng(seed)
+    w = q6k_random(rng, 16, 2048)
+    xq = orc.quantize_q8_K(rng.standard_normal((1, 2048)).astype(np.float32))
+    for r in range(16):
+        got = orc.dot_q6_K(w[r], xq[0], 2048)
+        assert np.float32(got).tobytes() == np.float32(ref.dot_q6_K(w[r], xq[0], 2048)).tobytes()
+
+
+def test_q6K_closed_form(orc):
+    rng = np.random.default_rng(3)
+    w = q6k_random(rng, 24, 1024)
+    xq = orc.quantize_q8_K(rng.standard_normal((3, 1024)).astype(np.float32))
+    xd, _ = q8k_dequant(xq, 1024)
+    wd = q6k_dequant(w, 1024)
+    got = orc.matmul_q(w, 14, xq, 1024)
+    assert np.all(np.abs(got - xd @ wd.T) <= 1e-5 * (np.abs(xd) @ np.abs(wd).T))
+    assert np.array_equal(orc.matmul_q(q4k_random(rng, 8, 1024), 12, xq, 1024).shape, (3, 8))
