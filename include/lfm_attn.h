@@ -40,6 +40,7 @@ extern "C" {
 #define LFM_ATTN_E_UNSUPPORTED -3 /* shape this build has no kernel for            */
 #define LFM_ATTN_E_DEVICE     -4 /* HIP runtime error (see lfm_attn_last_error)    */
 #define LFM_ATTN_E_NOMEM      -5 /* device allocation failed                       */
+#define LFM_ATTN_E_IO         -6 /* a file could not be written                     */
 
 typedef void *lfm_attn_stream_t; /* hipStream_t */
 
@@ -336,6 +337,63 @@ int lfm_attn_ctx_kv_import(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uin
  * lfm_hip_lfm3_kv_cache_shift_sinks. */
 int lfm_attn_ctx_shift_sinks(lfm_attn_ctx *ctx, uint32_t *inout_pos, uint32_t n_sink,
                              uint32_t n_discard);
+/* ---- prompt cache files (.lfmcache v1) ----------------------------------------
+ * The engine's disk-backed prompt cache (tools/lfm2_sys_cache.c:354-799):
+ * a 64-byte header (magic "01LFM2PC", version 1, token count, model
+ * fingerprint, layer count, n_embd, n_head_q, ShortConv cache length, payload
+ * bytes), the token ids, then per model layer either the ShortConv state
+ * (float [(l_cache - 1)][n_embd], ring linearized) or the fp16 K rows then V
+ * rows (full layers: positions 0 .. n-1; sliding-window layers: the last
+ * min(n, window) positions in order), and a trailing FNV-1a 64 checksum of
+ * everything after the header.  Files are byte-identical to the reference's.
+ * The fields only the engine knows come in lfm_attn_cache_model. */
+typedef struct {
+    uint64_t model_fingerprint; /* lfm2_compute_model_fingerprint (tools/lfm2_sys_cache.c:394-422) */
+    uint32_t n_model_layers;    /* ShortConv + attention layers (cfg.n_layers)      */
+    uint32_t n_embd;            /* cfg.n_embd                                       */
+    uint32_t n_head_q;          /* cfg.n_head_q (a header field)                    */
+    uint32_t shortconv_l_cache; /* cfg.shortconv_l_cache                            */
+    const int32_t *ctx_layer;   /* [n_model_layers]: this context's layer index of an
+                                   attention layer, -1 for a ShortConv layer         */
+} lfm_attn_cache_model;
+
+/* Write a prompt cache of the first n_tokens positions
+ * (lfm2_prompt_cache_save_ex, tools/lfm2_sys_cache.c:504-627): the
+ * context's KV rows come from the device; conv_states[l] (host, ShortConv
+ * layers) are linearized from their ring with conv_ring_heads (NULL: already
+ * linear).  Written to "<path>.tmp.<pid>" and renamed over path.
+ * LFM_ATTN_E_IO when the file cannot be written. */
+int lfm_attn_ctx_cache_save(lfm_attn_ctx *ctx, const char *path, const lfm_attn_cache_model *model,
+                            const uint32_t *tokens, uint32_t n_tokens, float *const *conv_states,
+                            const uint32_t *conv_ring_heads);
+/* Restore a prompt cache whose tokens are an exact prefix of prompt_tokens
+ * (lfm2_prompt_cache_try_load_prefix_ex, tools/lfm2_sys_cache.c:650-797):
+ * on success *matched_pos = the file's token count, the KV rows are in the
+ * context's device caches, and conv_states[l] (when non-NULL) hold the
+ * ShortConv states with out_conv_heads[l] = 0.  A file that does not apply
+ * (missing, other model, longer than the prompt or max_seq, prefix mismatch,
+ * truncated, bad checksum) returns LFM_ATTN_OK with *matched_pos = 0, as the
+ * reference returns false; unlike the reference, the whole file is verified
+ * before any cache or state is written, so a rejected file leaves them
+ * untouched. */
+int lfm_attn_ctx_cache_load_prefix(lfm_attn_ctx *ctx, const char *path,
+                                   const lfm_attn_cache_model *model, const uint32_t *prompt_tokens,
+                                   uint32_t n_prompt, float *const *conv_states,
+                                   uint32_t *out_conv_heads, uint32_t *matched_pos);
+
+/* ---- checkpoint SWA ring slab ------------------------------------------------
+ * LFM2Checkpoint keeps, beside the ShortConv states and the position, a slab
+ * of every sliding-window layer's whole ring: K [swa_cap][kv_dim] then V,
+ * layer after layer in order (lfm2_checkpoint_save_ex / restore_ex,
+ * tools/lfm2_moe_checkpoint.c:472-560; the slab is sized at :399-440 with
+ * swa_cap = window + 8, which is what the engines use).  Here the rings are
+ * the context's (swa_cap of the geometry).  The slab may be host or device
+ * memory: a device slab makes a rollback an HBM-to-HBM copy.  Full-attention
+ * layers need no snapshot: rewinding the position is enough. */
+int lfm_attn_ctx_swa_slab_bytes(const lfm_attn_ctx *ctx, size_t *bytes);
+int lfm_attn_ctx_swa_slab_save(lfm_attn_ctx *ctx, void *slab);
+int lfm_attn_ctx_swa_slab_restore(lfm_attn_ctx *ctx, const void *slab);
+
 /* Device address of a layer's caches (for callers that drive lfm_hip_* directly). */
 int lfm_attn_ctx_kv_device(lfm_attn_ctx *ctx, uint32_t layer, uint16_t **k_dev, uint16_t **v_dev,
                            uint32_t *n_slots);

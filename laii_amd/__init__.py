@@ -8,6 +8,7 @@ from ._lib import LIB_PATH, LfmAttnError, load  # noqa: F401
 from .attention import (  # noqa: F401
     GGML_Q4_K,
     GGML_Q6_K,
+    CacheModel,
     DeviceArray,
     EngineContext,
     device_count,

@@ -71,7 +71,20 @@ class Geom(C.Structure):
                 ("n_rope_freqs", _u32), ("lfm3", _int)]
 
 
+class CacheModelC(C.Structure):
+    """lfm_attn_cache_model of include/lfm_attn.h."""
+    _fields_ = [("model_fingerprint", C.c_uint64), ("n_model_layers", _u32), ("n_embd", _u32),
+                ("n_head_q", _u32), ("shortconv_l_cache", _u32),
+                ("ctx_layer", C.POINTER(C.c_int32))]
+
+
 SIGNATURES.update({
+    "lfm_attn_ctx_cache_save": (_int, [_vp, C.c_char_p, C.POINTER(CacheModelC), _vp, _u32, _vp, _vp]),
+    "lfm_attn_ctx_cache_load_prefix": (_int, [_vp, C.c_char_p, C.POINTER(CacheModelC), _vp, _u32, _vp,
+                                              _vp, C.POINTER(_u32)]),
+    "lfm_attn_ctx_swa_slab_bytes": (_int, [_vp, C.POINTER(C.c_size_t)]),
+    "lfm_attn_ctx_swa_slab_save": (_int, [_vp, _vp]),
+    "lfm_attn_ctx_swa_slab_restore": (_int, [_vp, _vp]),
     "lfm_attn_ctx_create": (_int, [C.POINTER(_vp), C.POINTER(Geom)]),
     "lfm_attn_ctx_destroy": (None, [_vp]),
     "lfm_attn_ctx_set_norms": (_int, [_vp, _u32, _vp, _vp]),

@@ -15,11 +15,12 @@ the CPU.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from typing import Optional, Sequence, Union
 
 import numpy as np
 
-from ._lib import Geom, check, load
+from ._lib import CacheModelC, Geom, check, load
 
 Ptr = Union["DeviceArray", int, None]
 
@@ -283,6 +284,17 @@ def pointer_table(arrays: Sequence[Union["DeviceArray", int]]) -> DeviceArray:
     return DeviceArray.from_numpy(np.array([int(a) for a in arrays], dtype=np.uint64))
 
 
+class CacheModel:
+    """What a .lfmcache file records of the model beside the caches
+    (lfm_attn_cache_model): the engine's fingerprint, its layer count (as the
+    length of ctx_layer: the context layer of each attention layer, -1 for a
+    ShortConv layer), n_embd, n_head_q and the ShortConv cache length."""
+
+    def __init__(self, fingerprint, ctx_layer, n_embd, n_head_q, l_cache=3):
+        self.fingerprint, self.ctx_layer = int(fingerprint), [int(x) for x in ctx_layer]
+        self.n_embd, self.n_head_q, self.l_cache = n_embd, n_head_q, l_cache
+
+
 class EngineContext:
     """Device-resident KV + RoPE tables for the attention layers of one model
     (lfm_attn_ctx of include/lfm_attn.h).  forward() is the per-layer
@@ -352,6 +364,81 @@ class EngineContext:
         check(load().lfm_attn_ctx_shift_sinks(self.h, C.byref(p), n_sink, n_discard),
               "lfm_attn_ctx_shift_sinks")
         return p.value
+
+    def slots(self, layer):
+        """Cache slots of a layer: max_seq, or the ring size of an SWA layer."""
+        n = C.c_uint32(0)
+        check(load().lfm_attn_ctx_kv_device(self.h, layer, None, None, C.byref(n)),
+              "lfm_attn_ctx_kv_device")
+        return n.value
+
+    # -- KV persistence --------------------------------------------------------
+    @staticmethod
+    def _cache_model(model):
+        cm = CacheModelC()
+        cm.model_fingerprint, cm.n_model_layers = model.fingerprint, len(model.ctx_layer)
+        cm.n_embd, cm.n_head_q, cm.shortconv_l_cache = model.n_embd, model.n_head_q, model.l_cache
+        arr = np.ascontiguousarray(model.ctx_layer, np.int32)
+        cm.ctx_layer = arr.ctypes.data_as(C.POINTER(C.c_int32))
+        return cm, arr
+
+    def cache_save(self, path, model, tokens, conv_states=None, conv_ring_heads=None):
+        """Write a .lfmcache v1 file of the first len(tokens) positions
+        (lfm2_prompt_cache_save_ex, tools/lfm2_sys_cache.c:504-627).
+        conv_states: per model layer float32 [hist, n_embd] or None."""
+        cm, keep = self._cache_model(model)
+        tok = np.ascontiguousarray(tokens, np.uint32)
+        n = cm.n_model_layers
+        conv = [None if c is None else np.ascontiguousarray(c, np.float32)
+                for c in (conv_states or [None] * n)]
+        cp = (C.c_void_p * n)(*[None if c is None else c.ctypes.data for c in conv])
+        heads = None if conv_ring_heads is None else np.ascontiguousarray(conv_ring_heads, np.uint32)
+        check(load().lfm_attn_ctx_cache_save(self.h, os.fsencode(path), C.byref(cm), tok.ctypes.data,
+                                             tok.size, cp, None if heads is None else heads.ctypes.data),
+              "lfm_attn_ctx_cache_save")
+        del keep
+
+    def cache_load_prefix(self, path, model, prompt, conv_states=None):
+        """Restore a .lfmcache whose tokens prefix `prompt`
+        (lfm2_prompt_cache_try_load_prefix_ex, tools/lfm2_sys_cache.c:650-797).
+        conv_states (filled in place) as in cache_save.  Returns (matched
+        position, conv ring heads); 0 when the file does not apply."""
+        cm, keep = self._cache_model(model)
+        pr = np.ascontiguousarray(prompt, np.uint32)
+        n = cm.n_model_layers
+        conv = list(conv_states) if conv_states is not None else [None] * n
+        for c in conv:
+            assert c is None or (c.dtype == np.float32 and c.flags.c_contiguous)
+        cp = (C.c_void_p * n)(*[None if c is None else c.ctypes.data for c in conv])
+        heads = np.full(n, 0xFFFFFFFF, np.uint32)
+        matched = C.c_uint32(0)
+        check(load().lfm_attn_ctx_cache_load_prefix(self.h, os.fsencode(path), C.byref(cm), pr.ctypes.data,
+                                                    pr.size, cp, heads.ctypes.data, C.byref(matched)),
+              "lfm_attn_ctx_cache_load_prefix")
+        del keep
+        return matched.value, heads
+
+    def swa_slab_bytes(self):
+        b = C.c_size_t(0)
+        check(load().lfm_attn_ctx_swa_slab_bytes(self.h, C.byref(b)), "lfm_attn_ctx_swa_slab_bytes")
+        return b.value
+
+    def swa_slab_save(self, slab=None):
+        """Checkpoint slab of the SWA rings (tools/lfm2_moe_checkpoint.c:472-506)
+        into a host uint16 array (a new one when slab is None) or a DeviceArray."""
+        if slab is None:
+            slab = np.zeros(self.swa_slab_bytes() // 2, np.uint16)
+        ptr = int(slab) if isinstance(slab, DeviceArray) else slab.ctypes.data
+        check(load().lfm_attn_ctx_swa_slab_save(self.h, ptr), "lfm_attn_ctx_swa_slab_save")
+        return slab
+
+    def swa_slab_restore(self, slab):
+        if isinstance(slab, DeviceArray):
+            ptr = int(slab)
+        else:
+            slab = np.ascontiguousarray(slab, np.uint16)
+            ptr = slab.ctypes.data
+        check(load().lfm_attn_ctx_swa_slab_restore(self.h, ptr), "lfm_attn_ctx_swa_slab_restore")
 
     def close(self):
         if getattr(self, "h", None):

@@ -9,10 +9,13 @@
  * attention kernel, and returns the output with a single device-to-host copy,
  * all on the context's stream.
  */
+#define _POSIX_C_SOURCE 200809L /* getpid, fsync, fileno */
 #include <hip/hip_runtime_api.h>
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include "lfm_attn.h"
 
@@ -314,5 +317,271 @@ int lfm_attn_ctx_shift_sinks(lfm_attn_ctx *c, uint32_t *inout_pos, uint32_t n_si
     free(nkv);
     free(kind);
     if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    return st;
+}
+
+/* ==== checkpoint SWA ring slab (tools/lfm2_moe_checkpoint.c:472-560) ========== */
+int lfm_attn_ctx_swa_slab_bytes(const lfm_attn_ctx *c, size_t *bytes) {
+    if (!c || !bytes) return LFM_ATTN_E_INVALID;
+    const size_t row = (size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t);
+    size_t b         = 0;
+    for (uint32_t l = 0; l < c->g.n_layers; ++l)
+        if (c->is_swa[l]) b += 2u * (size_t)c->slots[l] * row;
+    *bytes = b;
+    return LFM_ATTN_OK;
+}
+
+static int swa_slab_copy(lfm_attn_ctx *c, uint8_t *slab, const uint8_t *src_slab) {
+    const size_t row = (size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t);
+    size_t off       = 0;
+    int st           = LFM_ATTN_OK;
+    for (uint32_t l = 0; l < c->g.n_layers && st == LFM_ATTN_OK; ++l) {
+        if (!c->is_swa[l]) continue;
+        const size_t ring = (size_t)c->slots[l] * row;
+        if (slab) {
+            st = st_of(hipMemcpyAsync(slab + off, c->k_cache[l], ring, hipMemcpyDefault, c->stream));
+            if (st == LFM_ATTN_OK)
+                st = st_of(hipMemcpyAsync(slab + off + ring, c->v_cache[l], ring, hipMemcpyDefault, c->stream));
+        } else {
+            st = st_of(hipMemcpyAsync(c->k_cache[l], src_slab + off, ring, hipMemcpyDefault, c->stream));
+            if (st == LFM_ATTN_OK)
+                st = st_of(hipMemcpyAsync(c->v_cache[l], src_slab + off + ring, ring, hipMemcpyDefault, c->stream));
+        }
+        off += 2u * ring;
+    }
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    return st;
+}
+
+int lfm_attn_ctx_swa_slab_save(lfm_attn_ctx *c, void *slab) {
+    if (!c || !slab) return LFM_ATTN_E_INVALID;
+    return swa_slab_copy(c, (uint8_t *)slab, NULL);
+}
+
+int lfm_attn_ctx_swa_slab_restore(lfm_attn_ctx *c, const void *slab) {
+    if (!c || !slab) return LFM_ATTN_E_INVALID;
+    return swa_slab_copy(c, NULL, (const uint8_t *)slab);
+}
+
+/* ==== prompt cache files (.lfmcache v1) ======================================
+ * Layout and rules of tools/lfm2_sys_cache.c:354-799 (header struct :368-380,
+ * FNV-1a :382-389, save :504-627, load :650-797). */
+#define LFM_CACHE_MAGIC   0x4350324D464C3130ULL /* "01LFM2PC" little-endian */
+#define LFM_CACHE_VERSION 1u
+#define FNV_OFFSET        14695981039346656037ULL
+#define FNV_PRIME         1099511628211ULL
+
+typedef struct {
+    uint64_t magic;
+    uint32_t version;
+    uint32_t n_tokens;
+    uint64_t model_fingerprint;
+    uint32_t n_layers;
+    uint32_t n_embd;
+    uint32_t n_head_q;
+    uint32_t shortconv_l_cache;
+    uint64_t total_payload_bytes;
+    uint8_t reserved[16];
+} cache_header;
+_Static_assert(sizeof(cache_header) == 64, "cache header is 64 bytes");
+
+static uint64_t fnv1a(uint64_t h, const void *data, size_t len) {
+    const uint8_t *p = (const uint8_t *)data;
+    for (size_t i = 0; i < len; ++i) {
+        h ^= p[i];
+        h *= FNV_PRIME;
+    }
+    return h;
+}
+
+/* Per-layer sizes shared by save and load. */
+typedef struct {
+    uint32_t hist_len, swa_win, cap;
+    size_t conv_bytes;
+} cache_dims;
+
+static int cache_check(const lfm_attn_ctx *c, const lfm_attn_cache_model *m, cache_dims *d) {
+    if (!m || !m->ctx_layer || m->n_model_layers == 0u || m->n_embd == 0u) return LFM_ATTN_E_INVALID;
+    for (uint32_t l = 0; l < m->n_model_layers; ++l)
+        if (m->ctx_layer[l] >= (int32_t)c->g.n_layers || m->ctx_layer[l] < -1) return LFM_ATTN_E_INVALID;
+    d->hist_len   = m->shortconv_l_cache > 1u ? m->shortconv_l_cache - 1u : 2u;
+    d->swa_win    = c->g.sliding_window ? c->g.sliding_window : 256u;
+    d->cap        = c->g.swa_cap ? c->g.swa_cap : d->swa_win + 8u;
+    d->conv_bytes = (size_t)d->hist_len * m->n_embd * sizeof(float);
+    return LFM_ATTN_OK;
+}
+
+/* Bytes of one attention layer's rows for n positions: K then V. */
+static size_t cache_kv_rows(const lfm_attn_ctx *c, uint32_t layer, uint32_t n, const cache_dims *d) {
+    const uint32_t rows = c->is_swa[layer] ? (n < d->swa_win ? n : d->swa_win) : n;
+    return (size_t)rows * c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t);
+}
+
+/* Rows of positions [t0, t1) between a layer's device cache and host rows in
+ * position order; ring layers map position t to slot t % cap, in at most
+ * two contiguous runs. */
+static int cache_rows_xfer(lfm_attn_ctx *c, uint32_t layer, uint32_t t0, uint32_t t1, uint16_t *k, uint16_t *v,
+                           const cache_dims *d, int to_device) {
+    const size_t row = (size_t)c->g.n_head_kv * c->g.head_dim;
+    uint32_t t = t0;
+    while (t < t1) {
+        uint32_t slot = t, n = t1 - t;
+        if (c->is_swa[layer]) {
+            slot = t % d->cap;
+            if (n > d->cap - slot) n = d->cap - slot;
+        }
+        const size_t o = (size_t)(t - t0) * row;
+        const int st = to_device ? lfm_attn_ctx_kv_import(c, layer, slot, n, k + o, v + o)
+                                 : lfm_attn_ctx_kv_export(c, layer, slot, n, k + o, v + o);
+        if (st != LFM_ATTN_OK) return st;
+        t += n;
+    }
+    return LFM_ATTN_OK;
+}
+
+int lfm_attn_ctx_cache_save(lfm_attn_ctx *c, const char *path, const lfm_attn_cache_model *m,
+                            const uint32_t *tokens, uint32_t n_tokens, float *const *conv_states,
+                            const uint32_t *conv_ring_heads) {
+    if (!c || !path || !tokens || n_tokens == 0u) return LFM_ATTN_E_INVALID;
+    cache_dims d;
+    int st = cache_check(c, m, &d);
+    if (st != LFM_ATTN_OK) return st;
+    if (n_tokens > c->g.max_seq) return LFM_ATTN_E_RANGE;
+    uint64_t payload = (uint64_t)n_tokens * sizeof(uint32_t);
+    size_t max_kv = 0;
+    for (uint32_t l = 0; l < m->n_model_layers; ++l) {
+        if (m->ctx_layer[l] < 0) {
+            if (!conv_states || !conv_states[l]) return LFM_ATTN_E_INVALID;
+            payload += d.conv_bytes;
+        } else {
+            const size_t b = cache_kv_rows(c, (uint32_t)m->ctx_layer[l], n_tokens, &d);
+            payload += 2u * (uint64_t)b;
+            if (b > max_kv) max_kv = b;
+        }
+    }
+    cache_header h;
+    memset(&h, 0, sizeof h);
+    h.magic               = LFM_CACHE_MAGIC;
+    h.version             = LFM_CACHE_VERSION;
+    h.n_tokens            = n_tokens;
+    h.model_fingerprint   = m->model_fingerprint;
+    h.n_layers            = m->n_model_layers;
+    h.n_embd              = m->n_embd;
+    h.n_head_q            = m->n_head_q;
+    h.shortconv_l_cache   = m->shortconv_l_cache;
+    h.total_payload_bytes = payload;
+
+    uint16_t *k = max_kv ? (uint16_t *)malloc(max_kv) : NULL;
+    uint16_t *v = max_kv ? (uint16_t *)malloc(max_kv) : NULL;
+    float *lin  = (float *)malloc(d.conv_bytes);
+    char tmp[4096];
+    if ((max_kv && (!k || !v)) || !lin ||
+        snprintf(tmp, sizeof tmp, "%s.tmp.%d", path, (int)getpid()) >= (int)sizeof tmp) {
+        free(k);
+        free(v);
+        free(lin);
+        return LFM_ATTN_E_INVALID;
+    }
+    FILE *f       = fopen(tmp, "wb");
+    uint64_t csum = FNV_OFFSET;
+    st            = f ? LFM_ATTN_OK : LFM_ATTN_E_IO;
+#define PUT(buf, len)                                                              \
+    do {                                                                           \
+        if (st == LFM_ATTN_OK) {                                                   \
+            if (fwrite((buf), 1, (len), f) != (len)) st = LFM_ATTN_E_IO;           \
+            else csum = fnv1a(csum, (buf), (len));                                 \
+        }                                                                          \
+    } while (0)
+    if (st == LFM_ATTN_OK && fwrite(&h, sizeof h, 1, f) != 1) st = LFM_ATTN_E_IO;
+    PUT(tokens, (size_t)n_tokens * sizeof(uint32_t));
+    for (uint32_t l = 0; l < m->n_model_layers && st == LFM_ATTN_OK; ++l) {
+        if (m->ctx_layer[l] < 0) {
+            const float *src = conv_states[l];
+            if (conv_ring_heads && d.hist_len > 1u) {
+                for (uint32_t sidx = 0; sidx < d.hist_len; ++sidx) {
+                    const uint32_t slot = (conv_ring_heads[l] + sidx) % d.hist_len;
+                    memcpy(lin + (size_t)sidx * m->n_embd, src + (size_t)slot * m->n_embd,
+                           (size_t)m->n_embd * sizeof(float));
+                }
+                src = lin;
+            }
+            PUT(src, d.conv_bytes);
+        } else {
+            const uint32_t layer = (uint32_t)m->ctx_layer[l];
+            const size_t b       = cache_kv_rows(c, layer, n_tokens, &d);
+            const uint32_t rows  = (uint32_t)(b / ((size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t)));
+            st = cache_rows_xfer(c, layer, n_tokens - rows, n_tokens, k, v, &d, 0);
+            PUT(k, b);
+            PUT(v, b);
+        }
+    }
+#undef PUT
+    if (st == LFM_ATTN_OK && fwrite(&csum, sizeof csum, 1, f) != 1) st = LFM_ATTN_E_IO;
+    if (st == LFM_ATTN_OK && fflush(f) != 0) st = LFM_ATTN_E_IO;
+    if (st == LFM_ATTN_OK) (void)fsync(fileno(f));
+    if (f && fclose(f) != 0 && st == LFM_ATTN_OK) st = LFM_ATTN_E_IO;
+    if (st == LFM_ATTN_OK && rename(tmp, path) != 0) st = LFM_ATTN_E_IO;
+    if (st != LFM_ATTN_OK && f) (void)unlink(tmp);
+    free(k);
+    free(v);
+    free(lin);
+    return st;
+}
+
+int lfm_attn_ctx_cache_load_prefix(lfm_attn_ctx *c, const char *path, const lfm_attn_cache_model *m,
+                                   const uint32_t *prompt, uint32_t n_prompt, float *const *conv_states,
+                                   uint32_t *out_conv_heads, uint32_t *matched_pos) {
+    if (!matched_pos) return LFM_ATTN_E_INVALID;
+    *matched_pos = 0;
+    if (!c || !path || !prompt) return LFM_ATTN_E_INVALID;
+    cache_dims d;
+    int st = cache_check(c, m, &d);
+    if (st != LFM_ATTN_OK) return st;
+    FILE *f = fopen(path, "rb");
+    if (!f) return LFM_ATTN_OK;
+    cache_header h;
+    if (fread(&h, sizeof h, 1, f) != 1 || h.magic != LFM_CACHE_MAGIC || h.version != LFM_CACHE_VERSION ||
+        h.model_fingerprint != m->model_fingerprint || h.n_layers != m->n_model_layers ||
+        h.n_embd != m->n_embd || h.n_tokens == 0u || h.n_tokens > n_prompt || h.n_tokens > c->g.max_seq) {
+        fclose(f);
+        return LFM_ATTN_OK;
+    }
+    const uint32_t n = h.n_tokens;
+    /* stage the whole payload, verify, then write states and caches */
+    size_t total = (size_t)n * sizeof(uint32_t);
+    for (uint32_t l = 0; l < m->n_model_layers; ++l)
+        total += m->ctx_layer[l] < 0 ? d.conv_bytes : 2u * cache_kv_rows(c, (uint32_t)m->ctx_layer[l], n, &d);
+    uint8_t *buf = (uint8_t *)malloc(total ? total : 1u);
+    if (!buf) {
+        fclose(f);
+        return LFM_ATTN_E_NOMEM;
+    }
+    uint64_t file_csum = 0;
+    const int ok = fread(buf, 1, total, f) == total && fread(&file_csum, sizeof file_csum, 1, f) == 1 &&
+                   file_csum == fnv1a(FNV_OFFSET, buf, total) &&
+                   memcmp(buf, prompt, (size_t)n * sizeof(uint32_t)) == 0;
+    fclose(f);
+    if (!ok) {
+        free(buf);
+        return LFM_ATTN_OK;
+    }
+    size_t off = (size_t)n * sizeof(uint32_t);
+    for (uint32_t l = 0; l < m->n_model_layers && st == LFM_ATTN_OK; ++l) {
+        if (m->ctx_layer[l] < 0) {
+            if (conv_states && conv_states[l]) {
+                memcpy(conv_states[l], buf + off, d.conv_bytes);
+                if (out_conv_heads) out_conv_heads[l] = 0u;
+            }
+            off += d.conv_bytes;
+        } else {
+            const uint32_t layer = (uint32_t)m->ctx_layer[l];
+            const size_t b       = cache_kv_rows(c, layer, n, &d);
+            const uint32_t rows  = (uint32_t)(b / ((size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t)));
+            st = cache_rows_xfer(c, layer, n - rows, n, (uint16_t *)(buf + off), (uint16_t *)(buf + off + b), &d, 1);
+            off += 2u * b;
+        }
+    }
+    free(buf);
+    if (st == LFM_ATTN_OK) *matched_pos = n;
     return st;
 }

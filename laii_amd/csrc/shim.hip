@@ -88,6 +88,7 @@ const char *lfm_attn_status_string(int status) {
     case LFM_ATTN_E_UNSUPPORTED: return "unsupported shape";
     case LFM_ATTN_E_DEVICE: return "device error";
     case LFM_ATTN_E_NOMEM: return "out of device memory";
+    case LFM_ATTN_E_IO: return "file could not be written";
     default: return "unknown status";
     }
 }

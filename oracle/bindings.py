@@ -450,3 +450,189 @@ def _ref_dot6(self, w_row, x_q8, n_cols):
 
 
 Reference.dot_q6_K = _ref_dot6
+
+
+# -- KV persistence: .lfmcache v1 prompt cache and the checkpoint SWA slab ----------
+class CacheModel:
+    """The model fields the .lfmcache format and the fingerprint read
+    (LFM2Config of the reference): layer_kind 0 ShortConv, 1 full attention,
+    2 sliding-window attention; n_head_kv per layer (0 for ShortConv)."""
+
+    def __init__(self, layer_kind, n_head_kv, head_dim, n_embd, n_head_q, l_cache=3,
+                 sliding_window=0, is_lfm3=False, n_vocab=65536):
+        self.layer_kind = np.ascontiguousarray(layer_kind, np.uint8)
+        self.n_head_kv = np.ascontiguousarray(n_head_kv, np.uint32)
+        self.n_layers = int(self.layer_kind.size)
+        self.head_dim, self.n_embd, self.n_head_q = head_dim, n_embd, n_head_q
+        self.l_cache, self.sliding_window, self.is_lfm3 = l_cache, sliding_window, bool(is_lfm3)
+        self.n_vocab = n_vocab
+
+    @property
+    def hist_len(self):
+        return self.l_cache - 1 if self.l_cache > 1 else 2
+
+    def args(self):
+        return (self.n_layers, self.n_head_kv, self.layer_kind, self.head_dim, self.n_embd,
+                self.n_head_q, self.l_cache, self.sliding_window)
+
+
+def _f32_ptrs(arrs):
+    for a in arrs:
+        assert a is None or (a.dtype == np.float32 and a.flags.c_contiguous)
+    return (C.c_void_p * len(arrs))(*[None if a is None else a.ctypes.data for a in arrs])
+
+
+def _heads_arr(heads, n):
+    return None if heads is None else np.ascontiguousarray(heads, np.uint32)
+
+
+_CACHE_GEOM = [_u32, _u32p, _u8p, _u32, _u32, _u32, _u32, _u32]
+
+
+def _bind_cache(L, prefix, fp_arg):
+    fp = [C.c_uint64] if fp_arg else []
+    save = getattr(L, prefix + "prompt_cache_save")
+    save.restype = C.c_int
+    load = getattr(L, prefix + "prompt_cache_load")
+    load.restype = _u32
+    if fp_arg:  # oracle: (path, fingerprint, geometry...)
+        save.argtypes = [C.c_char_p] + fp + _CACHE_GEOM + [_u32p, _u32, C.c_void_p, C.c_void_p,
+                                                           C.c_void_p, C.c_void_p, _u32]
+        load.argtypes = [C.c_char_p] + fp + _CACHE_GEOM + [_u32p, _u32, _u32, C.c_void_p, C.c_void_p,
+                                                           C.c_void_p, C.c_void_p, _u32]
+    else:  # reference: (path, geometry..., is_lfm3, ...)
+        save.argtypes = [C.c_char_p] + _CACHE_GEOM + [C.c_int, _u32p, _u32, C.c_void_p, C.c_void_p,
+                                                      C.c_void_p, C.c_void_p, _u32]
+        load.argtypes = [C.c_char_p] + _CACHE_GEOM + [C.c_int, _u32p, _u32, _u32, C.c_void_p,
+                                                      C.c_void_p, C.c_void_p, C.c_void_p, _u32]
+
+
+def _pc_save(self, path, model, tokens, conv, k, v, conv_heads=None, swa_cap=0, fingerprint=None):
+    """Write a prompt cache; conv/k/v are per-layer lists (None where a layer has none)."""
+    tokens = np.ascontiguousarray(tokens, np.uint32)
+    n = model.n_layers
+    conv = list(conv) + [None] * (n - len(conv))
+    heads = _heads_arr(conv_heads, n)
+    hp = None if heads is None else heads.ctypes.data
+    if isinstance(self, Oracle):
+        fp = self.model_fingerprint(model) if fingerprint is None else fingerprint
+        ok = self.lib.orc_prompt_cache_save(path.encode(), fp, *model.args(), tokens, tokens.size,
+                                            _f32_ptrs(conv), hp, _cache_ptrs(k), _cache_ptrs(v), swa_cap)
+    else:
+        ok = self.lib.ref_prompt_cache_save(path.encode(), *model.args(), int(model.is_lfm3), tokens,
+                                            tokens.size, _f32_ptrs(conv), hp, _cache_ptrs(k),
+                                            _cache_ptrs(v), swa_cap)
+    return bool(ok)
+
+
+def _pc_load(self, path, model, prompt, max_seq, conv, k, v, swa_cap=0, fingerprint=None):
+    """Load into the given buffers (modified in place); returns (matched, conv_heads)."""
+    prompt = np.ascontiguousarray(prompt, np.uint32)
+    n = model.n_layers
+    conv = list(conv) + [None] * (n - len(conv))
+    heads = np.full(n, 0xFFFFFFFF, np.uint32)
+    if isinstance(self, Oracle):
+        fp = self.model_fingerprint(model) if fingerprint is None else fingerprint
+        m = self.lib.orc_prompt_cache_load(path.encode(), fp, *model.args(), prompt, prompt.size,
+                                           max_seq, _f32_ptrs(conv), heads.ctypes.data,
+                                           _cache_ptrs(k), _cache_ptrs(v), swa_cap)
+    else:
+        m = self.lib.ref_prompt_cache_load(path.encode(), *model.args(), int(model.is_lfm3), prompt,
+                                           prompt.size, max_seq, _f32_ptrs(conv), heads.ctypes.data,
+                                           _cache_ptrs(k), _cache_ptrs(v), swa_cap)
+    return int(m), heads
+
+
+def _orc_fingerprint(self, model, arch=None):
+    arch = arch or ("lfm3" if model.is_lfm3 else "lfm2")
+    is_swa = np.ascontiguousarray(model.layer_kind == 2, np.uint8)
+    return int(self.lib.orc_model_fingerprint(arch.encode(), model.n_layers, model.n_embd, model.n_vocab,
+                                              model.n_head_q, model.l_cache, model.n_head_kv,
+                                              int(model.is_lfm3), model.head_dim,
+                                              model.sliding_window, is_swa))
+
+
+def _ref_fingerprint(self, model):
+    return int(self.lib.ref_model_fingerprint(model.n_layers, model.n_head_kv, model.layer_kind,
+                                              model.head_dim, model.n_embd, model.n_head_q,
+                                              model.l_cache, model.sliding_window,
+                                              int(model.is_lfm3)))
+
+
+def _orc_fnv1a(self, data, h=14695981039346656037):
+    b = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else data
+    b = np.ascontiguousarray(b).view(np.uint8)
+    return int(self.lib.orc_fnv1a(h, b.ctypes.data, b.size))
+
+
+def _orc_slab(self, model, swa_cap, k, v, slab=None):
+    """Checkpoint SWA slab of the caches (slab=None: a new one), or restore
+    the caches from `slab` when it is given."""
+    n = self.lib.orc_checkpoint_swa_slab(None, model.n_layers, model.n_head_kv, model.layer_kind,
+                                         model.head_dim, swa_cap, _cache_ptrs(k), _cache_ptrs(v), 0)
+    restore = slab is not None
+    out = np.ascontiguousarray(slab, np.uint16) if restore else np.zeros(n, np.uint16)
+    assert out.size == n
+    self.lib.orc_checkpoint_swa_slab(out.ctypes.data, model.n_layers, model.n_head_kv,
+                                     model.layer_kind, model.head_dim, swa_cap, _cache_ptrs(k),
+                                     _cache_ptrs(v), int(restore))
+    return out
+
+
+def _ref_slab_save(self, model, k, v):
+    n = self.lib.ref_checkpoint_swa_save(None, *model.args(), _cache_ptrs(k), _cache_ptrs(v))
+    out = np.zeros(n, np.uint16)
+    self.lib.ref_checkpoint_swa_save(out.ctypes.data, *model.args(), _cache_ptrs(k), _cache_ptrs(v))
+    return out
+
+
+def _ref_slab_restore(self, model, slab, k, v):
+    slab = np.ascontiguousarray(slab, np.uint16)
+    return bool(self.lib.ref_checkpoint_swa_restore(slab.ctypes.data, *model.args(), _cache_ptrs(k),
+                                                    _cache_ptrs(v)))
+
+
+def _orc_cache_init(self):
+    L = self.lib
+    _bind_cache(L, "orc_", True)
+    L.orc_fnv1a.restype = C.c_uint64
+    L.orc_fnv1a.argtypes = [C.c_uint64, C.c_void_p, C.c_size_t]
+    L.orc_model_fingerprint.restype = C.c_uint64
+    L.orc_model_fingerprint.argtypes = [C.c_char_p, _u32, _u32, _u32, _u32, _u32, _u32p, C.c_int, _u32,
+                                        _u32, _u8p]
+    L.orc_checkpoint_swa_slab.restype = C.c_size_t
+    L.orc_checkpoint_swa_slab.argtypes = [C.c_void_p, _u32, _u32p, _u8p, _u32, _u32, C.c_void_p,
+                                          C.c_void_p, C.c_int]
+
+
+def _ref_cache_init(self):
+    L = self.lib
+    _bind_cache(L, "ref_", False)
+    L.ref_model_fingerprint.restype = C.c_uint64
+    L.ref_model_fingerprint.argtypes = _CACHE_GEOM + [C.c_int]
+    L.ref_checkpoint_swa_save.restype = C.c_size_t
+    L.ref_checkpoint_swa_save.argtypes = [C.c_void_p] + _CACHE_GEOM + [C.c_void_p, C.c_void_p]
+    L.ref_checkpoint_swa_restore.restype = C.c_int
+    L.ref_checkpoint_swa_restore.argtypes = [C.c_void_p] + _CACHE_GEOM + [C.c_void_p, C.c_void_p]
+
+
+def _wrap_init(cls, extra):
+    base = cls.__init__
+
+    def __init__(self, *a, **kw):
+        base(self, *a, **kw)
+        extra(self)
+
+    cls.__init__ = __init__
+
+
+_wrap_init(Oracle, _orc_cache_init)
+_wrap_init(Reference, _ref_cache_init)
+Oracle.prompt_cache_save = Reference.prompt_cache_save = _pc_save
+Oracle.prompt_cache_load = Reference.prompt_cache_load = _pc_load
+Oracle.model_fingerprint = _orc_fingerprint
+Oracle.fnv1a = _orc_fnv1a
+Oracle.checkpoint_swa_slab = _orc_slab
+Reference.model_fingerprint = _ref_fingerprint
+Reference.checkpoint_swa_save = _ref_slab_save
+Reference.checkpoint_swa_restore = _ref_slab_restore

@@ -139,6 +139,26 @@ float orc_dot_q6_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
 void orc_matmul_q(float *out, const void *w, uint32_t type, uint32_t n_rows, uint32_t n_cols,
                   const void *x_q8, uint32_t n_tokens);
 
+/* ---- KV persistence (cpu_cache.c): .lfmcache v1 and the checkpoint slab -- */
+/* layer_kind: 0 ShortConv, 1 full attention, 2 sliding-window attention */
+uint64_t orc_fnv1a(uint64_t h, const void *data, size_t len);
+uint64_t orc_model_fingerprint(const char *arch, uint32_t n_layers, uint32_t n_embd, uint32_t n_vocab,
+                               uint32_t n_head_q, uint32_t l_cache, const uint32_t *n_head_kv, int is_lfm3,
+                               uint32_t head_dim, uint32_t sliding_window, const uint8_t *is_swa);
+int orc_prompt_cache_save(const char *path, uint64_t fingerprint, uint32_t n_layers, const uint32_t *n_head_kv,
+                          const uint8_t *layer_kind, uint32_t head_dim, uint32_t n_embd, uint32_t n_head_q,
+                          uint32_t l_cache, uint32_t sliding_window, const uint32_t *tokens, uint32_t n_tokens,
+                          float *const *conv, const uint32_t *conv_heads, uint16_t *const *k, uint16_t *const *v,
+                          uint32_t swa_cap);
+uint32_t orc_prompt_cache_load(const char *path, uint64_t fingerprint, uint32_t n_layers,
+                               const uint32_t *n_head_kv, const uint8_t *layer_kind, uint32_t head_dim,
+                               uint32_t n_embd, uint32_t n_head_q, uint32_t l_cache, uint32_t sliding_window,
+                               const uint32_t *prompt, uint32_t n_prompt, uint32_t max_seq, float *const *conv,
+                               uint32_t *conv_heads, uint16_t *const *k, uint16_t *const *v, uint32_t swa_cap);
+size_t orc_checkpoint_swa_slab(uint16_t *slab, uint32_t n_layers, const uint32_t *n_head_kv,
+                               const uint8_t *layer_kind, uint32_t head_dim, uint32_t swa_cap,
+                               uint16_t *const *k, uint16_t *const *v, int restore);
+
 #ifdef __cplusplus
 }
 #endif

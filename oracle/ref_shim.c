@@ -22,8 +22,12 @@
 #define LFM2_SPECULATIVE_PLD_NO_MAIN 1
 #define LFM3_ENGINE_NO_MAIN 1
 #define LFM2_RUNTIME_FEATURES_NO_MAIN 1
+#define LFM2_SYS_CACHE_NO_MAIN 1
+#define LFM2_MOE_CHECKPOINT_NO_MAIN 1
 #include "tools/lfm3_engine.c"
 #include "tools/lfm2_runtime_features.c"
+#include "tools/lfm2_sys_cache.c"
+#include "tools/lfm2_moe_checkpoint.c"
 
 #include <sched.h>
 #include <time.h>
@@ -358,4 +362,119 @@ void ref_matmul_q4_K_batch(float *out, const void *w, uint32_t n_rows, uint32_t 
 /* lfm2_vec_dot_q6_K_q8_K_avx2 (include/lfm2_simd_avx2.h:551-634), one row. */
 float ref_dot_q6_K_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
     return lfm2_vec_dot_q6_K_q8_K_avx2((const block_q6_K_t *)w_row, (const block_q8_K_t *)x_q8, n_cols);
+}
+
+/* ---- prompt cache (.lfmcache v1) ------------------------------------------------ */
+
+static LFM2Model *shim_cache_model(uint32_t n_layers, const uint32_t *n_head_kv, const uint8_t *layer_kind,
+                                   uint32_t head_dim, uint32_t n_embd, uint32_t n_head_q,
+                                   uint32_t l_cache, uint32_t sliding_window, int is_lfm3) {
+    LFM2Model *m = shim_model(n_layers, n_head_kv, layer_kind, head_dim, sliding_window);
+    if (!m) return NULL;
+    snprintf(m->cfg.arch, sizeof m->cfg.arch, "%s", is_lfm3 ? "lfm3" : "lfm2");
+    m->cfg.is_lfm3           = is_lfm3 != 0;
+    m->cfg.n_embd            = n_embd;
+    m->cfg.n_head_q          = n_head_q;
+    m->cfg.shortconv_l_cache = l_cache;
+    m->cfg.n_vocab           = 65536;
+    for (uint32_t l = 0; l < n_layers; ++l) m->cfg.is_swa_layer[l] = layer_kind && layer_kind[l] == 2u;
+    return m;
+}
+
+/* lfm2_compute_model_fingerprint (tools/lfm2_sys_cache.c:394-422) of that model */
+uint64_t ref_model_fingerprint(uint32_t n_layers, const uint32_t *n_head_kv, const uint8_t *layer_kind,
+                               uint32_t head_dim, uint32_t n_embd, uint32_t n_head_q, uint32_t l_cache,
+                               uint32_t sliding_window, int is_lfm3) {
+    LFM2Model *m = shim_cache_model(n_layers, n_head_kv, layer_kind, head_dim, n_embd, n_head_q, l_cache,
+                                    sliding_window, is_lfm3);
+    if (!m) return 0;
+    const uint64_t h = lfm2_compute_model_fingerprint(m);
+    free(m);
+    return h;
+}
+
+/* lfm2_prompt_cache_save_ex (tools/lfm2_sys_cache.c:504-627) */
+int ref_prompt_cache_save(const char *path, uint32_t n_layers, const uint32_t *n_head_kv,
+                          const uint8_t *layer_kind, uint32_t head_dim, uint32_t n_embd, uint32_t n_head_q,
+                          uint32_t l_cache, uint32_t sliding_window, int is_lfm3, const uint32_t *tokens,
+                          uint32_t n_tokens, float **conv, const uint32_t *conv_heads, uint16_t **k,
+                          uint16_t **v, uint32_t swa_cap) {
+    LFM2Model *m = shim_cache_model(n_layers, n_head_kv, layer_kind, head_dim, n_embd, n_head_q, l_cache,
+                                    sliding_window, is_lfm3);
+    if (!m) return 0;
+    float *cs[LFM2_MAX_LAYERS]    = {0};
+    uint16_t *kc[LFM2_MAX_LAYERS] = {0}, *vc[LFM2_MAX_LAYERS] = {0};
+    for (uint32_t l = 0; l < n_layers; ++l) { cs[l] = conv[l]; kc[l] = k[l]; vc[l] = v[l]; }
+    const bool ok = lfm2_prompt_cache_save_ex(path, m, tokens, n_tokens, cs, conv_heads, kc, vc, swa_cap);
+    free(m);
+    return ok ? 1 : 0;
+}
+
+/* lfm2_prompt_cache_try_load_prefix_ex (tools/lfm2_sys_cache.c:650-797); returns the matched
+ * position (0: not applied) */
+uint32_t ref_prompt_cache_load(const char *path, uint32_t n_layers, const uint32_t *n_head_kv,
+                               const uint8_t *layer_kind, uint32_t head_dim, uint32_t n_embd,
+                               uint32_t n_head_q, uint32_t l_cache, uint32_t sliding_window, int is_lfm3,
+                               const uint32_t *prompt, uint32_t n_prompt, uint32_t max_seq, float **conv,
+                               uint32_t *conv_heads, uint16_t **k, uint16_t **v, uint32_t swa_cap) {
+    LFM2Model *m = shim_cache_model(n_layers, n_head_kv, layer_kind, head_dim, n_embd, n_head_q, l_cache,
+                                    sliding_window, is_lfm3);
+    if (!m) return 0;
+    float *cs[LFM2_MAX_LAYERS]    = {0};
+    uint16_t *kc[LFM2_MAX_LAYERS] = {0}, *vc[LFM2_MAX_LAYERS] = {0};
+    for (uint32_t l = 0; l < n_layers; ++l) { cs[l] = conv[l]; kc[l] = k[l]; vc[l] = v[l]; }
+    uint32_t pos = 0;
+    (void)lfm2_prompt_cache_try_load_prefix_ex(path, m, prompt, n_prompt, max_seq, cs, conv_heads, kc, vc,
+                                               swa_cap, &pos);
+    free(m);
+    return pos;
+}
+
+/* ---- checkpoint SWA slab ------------------------------------------------------ */
+
+/* lfm2_checkpoint_init + lfm2_checkpoint_save_ex (tools/lfm2_moe_checkpoint.c:399-505)
+ * of the caches; the slab (swa_total_u16 elements, returned) is copied to slab_out
+ * when it is non-NULL. */
+size_t ref_checkpoint_swa_save(uint16_t *slab_out, uint32_t n_layers, const uint32_t *n_head_kv,
+                               const uint8_t *layer_kind, uint32_t head_dim, uint32_t n_embd,
+                               uint32_t n_head_q, uint32_t l_cache, uint32_t sliding_window,
+                               uint16_t **k, uint16_t **v) {
+    LFM2Model *m = shim_cache_model(n_layers, n_head_kv, layer_kind, head_dim, n_embd, n_head_q, l_cache,
+                                    sliding_window, 1);
+    if (!m) return 0;
+    LFM2Checkpoint cp;
+    size_t n = 0;
+    if (lfm2_checkpoint_init(&cp, m, 0U)) {
+        uint16_t *kc[LFM2_MAX_LAYERS] = {0}, *vc[LFM2_MAX_LAYERS] = {0};
+        for (uint32_t l = 0; l < n_layers; ++l) { kc[l] = k[l]; vc[l] = v[l]; }
+        lfm2_checkpoint_save_ex(&cp, m, NULL, NULL, kc, vc, 0U, 0ULL, NULL, 0U);
+        n = cp.swa_total_u16;
+        if (slab_out && n) memcpy(slab_out, cp.swa_kv_slab, n * sizeof(uint16_t));
+        lfm2_checkpoint_destroy(&cp);
+    }
+    free(m);
+    return n;
+}
+
+/* lfm2_checkpoint_restore_ex (tools/lfm2_moe_checkpoint.c:508-560) from a slab. */
+int ref_checkpoint_swa_restore(const uint16_t *slab, uint32_t n_layers, const uint32_t *n_head_kv,
+                               const uint8_t *layer_kind, uint32_t head_dim, uint32_t n_embd,
+                               uint32_t n_head_q, uint32_t l_cache, uint32_t sliding_window,
+                               uint16_t **k, uint16_t **v) {
+    LFM2Model *m = shim_cache_model(n_layers, n_head_kv, layer_kind, head_dim, n_embd, n_head_q, l_cache,
+                                    sliding_window, 1);
+    if (!m) return 0;
+    LFM2Checkpoint cp;
+    int ok = 0;
+    if (lfm2_checkpoint_init(&cp, m, 0U)) {
+        if (cp.swa_total_u16) memcpy(cp.swa_kv_slab, slab, cp.swa_total_u16 * sizeof(uint16_t));
+        cp.is_valid                   = true;
+        uint16_t *kc[LFM2_MAX_LAYERS] = {0}, *vc[LFM2_MAX_LAYERS] = {0};
+        for (uint32_t l = 0; l < n_layers; ++l) { kc[l] = k[l]; vc[l] = v[l]; }
+        uint32_t pos = 0;
+        ok = lfm2_checkpoint_restore_ex(&cp, m, NULL, NULL, kc, vc, &pos, NULL, NULL, NULL) ? 1 : 0;
+        lfm2_checkpoint_destroy(&cp);
+    }
+    free(m);
+    return ok;
 }

@@ -191,3 +191,23 @@ def test_qkv_fused_validation_before_launch():
     assert f(*args(t, wv=FAKE + 1)) == E_INVALID            # Q6_K rows need 2-byte alignment
     assert f(FAKE, FAKE, FAKE, None, FAKE + 8, FAKE, FAKE, None, t, 8, 8, 8, 0, 2048, FAKE, 1,
              None) == E_INVALID                             # Q4_K rows need 16-byte alignment
+
+
+def test_cache_entry_points_validate_without_device():
+    """The persistence entry points reject a missing context / output before
+    any device work (the context itself needs a GPU)."""
+    lib = la.load()
+    m = _lib.CacheModelC()
+    tok = (C.c_uint32 * 4)(1, 2, 3, 4)
+    matched = C.c_uint32(7)
+    assert lib.lfm_attn_ctx_cache_save(None, b"/tmp/x", C.byref(m), tok, 4, None, None) == E_INVALID
+    assert lib.lfm_attn_ctx_cache_load_prefix(None, b"/tmp/x", C.byref(m), tok, 4, None, None,
+                                              C.byref(matched)) == E_INVALID
+    assert matched.value == 0
+    assert lib.lfm_attn_ctx_cache_load_prefix(None, b"/tmp/x", C.byref(m), tok, 4, None, None,
+                                              None) == E_INVALID
+    n = C.c_size_t(0)
+    assert lib.lfm_attn_ctx_swa_slab_bytes(None, C.byref(n)) == E_INVALID
+    assert lib.lfm_attn_ctx_swa_slab_save(None, FAKE) == E_INVALID
+    assert lib.lfm_attn_ctx_swa_slab_restore(None, FAKE) == E_INVALID
+    assert lib.lfm_attn_status_string(-6) == b"file could not be written"
