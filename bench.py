@@ -242,6 +242,60 @@ class QuantProjWorkload:
         self.i = (self.i + 1) % len(self.w)
 
 
+def bench_prompt_cache(la, rng, n_tokens=4096, reps=5):
+    """.lfmcache v1 save and prefix load of an LFM2-1.2B session (16 layers:
+    ShortConv states of 10, fp16 K/V of the 6 attention layers, 32q/8kv d64)
+    at n_tokens positions, through the engine context; and the device FNV-1a
+    64 over a payload of that size.  Times are wall clock around the host
+    calls (file in the temp directory, fsync included)."""
+    import tempfile
+
+    kinds = [0] * 16
+    for l in (2, 5, 8, 10, 12, 14):
+        kinds[l] = 1
+    ctx = la.EngineContext(6, 32, 8, 64, n_tokens)
+    for l in range(6):
+        ctx.kv_import(l, 0, rng.integers(0, 1 << 16, (n_tokens, 512), dtype=np.uint16),
+                      rng.integers(0, 1 << 16, (n_tokens, 512), dtype=np.uint16))
+    ctx_layer, i = [], 0
+    for k in kinds:
+        ctx_layer.append(i if k else -1)
+        i += 1 if k else 0
+    model = la.CacheModel(0x4C464D32315A4232, ctx_layer, 2048, 32, 3)  # the engine's fingerprint
+    conv = [rng.standard_normal(2 * 2048).astype(np.float32) if k == 0 else None for k in kinds]
+    tok = rng.integers(0, 65536, n_tokens, dtype=np.uint32)
+    fd, path = tempfile.mkstemp(suffix=".lfmcache")
+    os.close(fd)
+    try:
+        ctx.cache_save(path, model, tok, conv)
+        size = os.path.getsize(path)
+        dst = [None if c is None else np.zeros_like(c) for c in conv]
+        saves, loads = [], []
+        for _ in range(reps):
+            t = time.perf_counter()
+            ctx.cache_save(path, model, tok, conv)
+            saves.append(time.perf_counter() - t)
+            t = time.perf_counter()
+            matched, _ = ctx.cache_load_prefix(path, model, tok, dst)
+            loads.append(time.perf_counter() - t)
+            assert matched == n_tokens
+    finally:
+        os.unlink(path)
+        ctx.close()
+    payload = size - 72
+    buf = la.DeviceArray.from_numpy(rng.integers(0, 256, payload, dtype=np.uint8))
+    la.fnv1a64(buf, payload)
+    t = time.perf_counter()
+    for _ in range(20):
+        la.fnv1a64(buf, payload)
+    h_s = (time.perf_counter() - t) / 20
+    del buf
+    ts, tl = float(np.median(saves)), float(np.median(loads))
+    return dict(file_bytes=size, save_ms=round(ts * 1e3, 2), load_ms=round(tl * 1e3, 2),
+                save_GBps=round(size / ts / 1e9, 2), load_GBps=round(size / tl / 1e9, 2),
+                fnv1a64_device_ms=round(h_s * 1e3, 3), fnv1a64_device_GBps=round(payload / h_s / 1e9, 1))
+
+
 def time_steps(hip, wl, steps, warmup):
     for _ in range(warmup):
         wl.step()
@@ -294,6 +348,39 @@ def cpu_baseline(wl, n_threads, max_seconds=8.0):
     return dict(value=round(sample_bytes / dt / 1e9, 3), unit="GB/s", cores=int(used), kind=kind,
                 sample=f"{n} of {wl.n_seq} sequences x ctx {int(wl.keys[0])}, 32q/8kv d64, "
                        f"best of repeated passes, {dt * 1e3:.1f} ms per pass"), out.reshape(n, wl.nq, wl.hd)
+
+
+def cpu_prompt_cache(rng, n_tokens=4096, reps=3):
+    """The reference's .lfmcache writer and prefix loader (oracle/_ref; the C
+    restatement when absent) on host caches of the bench_prompt_cache layout."""
+    import tempfile
+
+    from oracle.bindings import CacheModel, Oracle, Reference
+
+    kinds = [0] * 16
+    for l in (2, 5, 8, 10, 12, 14):
+        kinds[l] = 1
+    m = CacheModel(kinds, [8 if k else 0 for k in kinds], 64, 2048, 32, 3)
+    lib, kind = (Reference(), "reference") if Reference.available() else (Oracle(), "port")
+    conv = [rng.standard_normal(2 * 2048).astype(np.float32) if k == 0 else None for k in kinds]
+    k = [rng.integers(0, 1 << 16, n_tokens * 512, dtype=np.uint16) if x else None for x in kinds]
+    v = [rng.integers(0, 1 << 16, n_tokens * 512, dtype=np.uint16) if x else None for x in kinds]
+    tok = rng.integers(0, 65536, n_tokens, dtype=np.uint32)
+    fd, path = tempfile.mkstemp(suffix=".lfmcache")
+    os.close(fd)
+    saves, loads = [], []
+    try:
+        for _ in range(reps):
+            t = time.perf_counter()
+            assert lib.prompt_cache_save(path, m, tok, conv, k, v)
+            saves.append(time.perf_counter() - t)
+            t = time.perf_counter()
+            assert lib.prompt_cache_load(path, m, tok, n_tokens, conv, k, v)[0] == n_tokens
+            loads.append(time.perf_counter() - t)
+    finally:
+        os.unlink(path)
+    return dict(save_ms=round(float(np.median(saves)) * 1e3, 2), load_ms=round(float(np.median(loads)) * 1e3, 2),
+                cores=1, kind=kind, sample=f"LFM2-1.2B session at {n_tokens} tokens, median of {reps}")
 
 
 def run_prefill(hip, la, rng, steps):
@@ -397,6 +484,10 @@ def main():
             pct_hbm_peak=round(100 * fq.bytes / (fms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
         log(f"qkv fused tokens 1: {fms * 1e3:.2f} us/step")
         del fq
+        pc = bench_prompt_cache(la, rng)
+        secondary["lfmcache_save_load_lfm2_1p2b_n4096"] = pc
+        log(f"prompt cache: save {pc['save_ms']} ms, load {pc['load_ms']} ms, "
+            f"device FNV-1a {pc['fnv1a64_device_GBps']} GB/s")
 
     cpu = None
     parity = None
@@ -404,6 +495,8 @@ def main():
         n_thr = max(1, min(16, os.cpu_count() or 1) - 1)  # reference policy: N_phys - 1
         log(f"cpu baseline with {n_thr} threads")
         cpu, cpu_out = cpu_baseline(head, n_thr)
+        if not args.quick:
+            cpu["rows"] = {"lfmcache_save_load_lfm2_1p2b_n4096": cpu_prompt_cache(rng)}
         g = gpu_out[:cpu_out.shape[0], 0]
         parity = dict(max_abs=float(np.abs(g - cpu_out).max()),
                       rel_l2=float(np.linalg.norm(g - cpu_out) / np.linalg.norm(cpu_out)),

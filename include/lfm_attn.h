@@ -337,6 +337,14 @@ int lfm_attn_ctx_kv_import(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uin
  * lfm_hip_lfm3_kv_cache_shift_sinks. */
 int lfm_attn_ctx_shift_sinks(lfm_attn_ctx *ctx, uint32_t *inout_pos, uint32_t n_sink,
                              uint32_t n_discard);
+/* FNV-1a 64 of n_bytes of device memory (16-byte aligned), continuing from
+ * h_in (the offset basis 14695981039346656037 for a fresh hash): the value
+ * lfm2_fnv1a_update (tools/lfm2_sys_cache.c:382-389) returns for the same
+ * bytes, computed in parallel on the device.  Synchronous: *h_out is set on
+ * return.  n_bytes == 0 returns h_in. */
+int lfm_hip_fnv1a64(const void *data, size_t n_bytes, uint64_t h_in, uint64_t *h_out,
+                    lfm_attn_stream_t stream);
+
 /* ---- prompt cache files (.lfmcache v1) ----------------------------------------
  * The engine's disk-backed prompt cache (tools/lfm2_sys_cache.c:354-799):
  * a 64-byte header (magic "01LFM2PC", version 1, token count, model

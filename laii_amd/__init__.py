@@ -12,6 +12,7 @@ from .attention import (  # noqa: F401
     DeviceArray,
     EngineContext,
     device_count,
+    fnv1a64,
     gqa_f16_varlen,
     gqa_heads,
     gqa_qkv_fused,

@@ -279,6 +279,16 @@ def lfm3_kv_cache_shift_sinks(k_caches, v_caches, n_head_kv, layer_kind, head_di
     return p.value
 
 
+FNV_OFFSET_BASIS = 14695981039346656037
+
+
+def fnv1a64(data: Ptr, n_bytes: int, h_in: int = FNV_OFFSET_BASIS, stream=None) -> int:
+    """FNV-1a 64 of device bytes (lfm2_fnv1a_update, tools/lfm2_sys_cache.c:382-389)."""
+    out = C.c_uint64(0)
+    check(load().lfm_hip_fnv1a64(_p(data), n_bytes, h_in, C.byref(out), stream), "lfm_hip_fnv1a64")
+    return out.value
+
+
 def pointer_table(arrays: Sequence[Union["DeviceArray", int]]) -> DeviceArray:
     """Device array of device pointers (the k_seq / v_seq arguments)."""
     return DeviceArray.from_numpy(np.array([int(a) for a in arrays], dtype=np.uint64))

@@ -23,7 +23,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["shim.hip", "decode_splitkv.hip", "generic.hip", "prologue.hip", "prefill_fa.hip",
-               "kv_shift.hip", "quant_matmul.hip"]
+               "kv_shift.hip", "quant_matmul.hip", "fnv_hash.hip"]
 C_SOURCES = ["lfm_attn_host.c", "lfm_attn_ctx.c"]
 
 HIP_FLAGS = [

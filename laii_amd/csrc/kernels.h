@@ -91,6 +91,11 @@ void profile_events(hipEvent_t *before, hipEvent_t *after);
 /* Record a HIP error for lfm_attn_last_error and map it to a status. */
 int hip_status(hipError_t e);
 
+/* FNV-1a 64 of a device buffer (fnv_hash.hip). */
+size_t fnv1a64_workspace_bytes(uint64_t len);
+int launch_fnv1a64(const void *data, uint64_t len, uint64_t h_in, void *ws, hipStream_t stream);
+uint64_t fnv1a64_finish(uint64_t h_in, uint64_t len, uint64_t acc);
+
 } // namespace lfm
 
 #endif

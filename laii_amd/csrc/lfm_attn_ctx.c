@@ -34,6 +34,9 @@ struct lfm_attn_ctx {
     unsigned char *stage_host;  /* pinned: q | k | v | gate | pos | out */
     unsigned char *stage_dev;
     size_t off_k, off_v, off_g, off_pos, off_out, stage_in_bytes, out_bytes;
+    unsigned char *file_host;   /* pinned: a whole .lfmcache file (grown on demand) */
+    unsigned char *file_dev;    /* its payload in device memory */
+    size_t file_host_bytes, file_dev_bytes;
     hipStream_t stream;
 };
 
@@ -60,6 +63,8 @@ void lfm_attn_ctx_destroy(lfm_attn_ctx *c) {
     (void)hipFree(c->sin_swa);
     (void)hipFree(c->stage_dev);
     if (c->stage_host) (void)hipHostFree(c->stage_host);
+    (void)hipFree(c->file_dev);
+    if (c->file_host) (void)hipHostFree(c->file_host);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     free(c->is_swa);
     free(c->slots);
@@ -369,7 +374,6 @@ int lfm_attn_ctx_swa_slab_restore(lfm_attn_ctx *c, const void *slab) {
 #define LFM_CACHE_MAGIC   0x4350324D464C3130ULL /* "01LFM2PC" little-endian */
 #define LFM_CACHE_VERSION 1u
 #define FNV_OFFSET        14695981039346656037ULL
-#define FNV_PRIME         1099511628211ULL
 
 typedef struct {
     uint64_t magic;
@@ -384,15 +388,6 @@ typedef struct {
     uint8_t reserved[16];
 } cache_header;
 _Static_assert(sizeof(cache_header) == 64, "cache header is 64 bytes");
-
-static uint64_t fnv1a(uint64_t h, const void *data, size_t len) {
-    const uint8_t *p = (const uint8_t *)data;
-    for (size_t i = 0; i < len; ++i) {
-        h ^= p[i];
-        h *= FNV_PRIME;
-    }
-    return h;
-}
 
 /* Per-layer sizes shared by save and load. */
 typedef struct {
@@ -417,28 +412,66 @@ static size_t cache_kv_rows(const lfm_attn_ctx *c, uint32_t layer, uint32_t n, c
     return (size_t)rows * c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t);
 }
 
-/* Rows of positions [t0, t1) between a layer's device cache and host rows in
- * position order; ring layers map position t to slot t % cap, in at most
- * two contiguous runs. */
-static int cache_rows_xfer(lfm_attn_ctx *c, uint32_t layer, uint32_t t0, uint32_t t1, uint16_t *k, uint16_t *v,
-                           const cache_dims *d, int to_device) {
-    const size_t row = (size_t)c->g.n_head_kv * c->g.head_dim;
-    uint32_t t = t0;
-    while (t < t1) {
+/* Pinned host buffer for a whole file and a device buffer for its payload. */
+static int file_buffers(lfm_attn_ctx *c, size_t host_bytes, size_t dev_bytes) {
+    int st = LFM_ATTN_OK;
+    if (c->file_host_bytes < host_bytes) {
+        if (c->file_host) (void)hipHostFree(c->file_host);
+        c->file_host       = NULL;
+        c->file_host_bytes = 0;
+        st = st_of(hipHostMalloc((void **)&c->file_host, host_bytes, hipHostMallocDefault));
+        if (st != LFM_ATTN_OK) return st;
+        c->file_host_bytes = host_bytes;
+    }
+    if (c->file_dev_bytes < dev_bytes) {
+        (void)hipFree(c->file_dev);
+        c->file_dev       = NULL;
+        c->file_dev_bytes = 0;
+        st = st_of(hipMalloc((void **)&c->file_dev, dev_bytes));
+        if (st != LFM_ATTN_OK) return st;
+        c->file_dev_bytes = dev_bytes;
+    }
+    return st;
+}
+
+/* Device-to-device copies of positions [t0, t1) of a layer between its
+ * caches and position-ordered K rows at k_rows, V rows at v_rows; ring
+ * layers map position t to slot t % cap, in at most two contiguous runs. */
+static int cache_rows_d2d(lfm_attn_ctx *c, uint32_t layer, uint32_t t0, uint32_t t1, unsigned char *k_rows,
+                          unsigned char *v_rows, const cache_dims *d, int to_cache) {
+    const size_t row = (size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t);
+    int st           = LFM_ATTN_OK;
+    for (uint32_t t = t0; t < t1 && st == LFM_ATTN_OK;) {
         uint32_t slot = t, n = t1 - t;
         if (c->is_swa[layer]) {
             slot = t % d->cap;
             if (n > d->cap - slot) n = d->cap - slot;
         }
-        const size_t o = (size_t)(t - t0) * row;
-        const int st = to_device ? lfm_attn_ctx_kv_import(c, layer, slot, n, k + o, v + o)
-                                 : lfm_attn_ctx_kv_export(c, layer, slot, n, k + o, v + o);
-        if (st != LFM_ATTN_OK) return st;
+        const size_t o = (size_t)(t - t0) * row, bytes = (size_t)n * row;
+        unsigned char *kc = (unsigned char *)c->k_cache[layer] + (size_t)slot * row;
+        unsigned char *vc = (unsigned char *)c->v_cache[layer] + (size_t)slot * row;
+        st = st_of(hipMemcpyAsync(to_cache ? kc : k_rows + o, to_cache ? k_rows + o : kc, bytes,
+                                  hipMemcpyDeviceToDevice, c->stream));
+        if (st == LFM_ATTN_OK)
+            st = st_of(hipMemcpyAsync(to_cache ? vc : v_rows + o, to_cache ? v_rows + o : vc, bytes,
+                                      hipMemcpyDeviceToDevice, c->stream));
         t += n;
     }
-    return LFM_ATTN_OK;
+    return st;
 }
 
+/* Payload bytes of an n-token file. */
+static size_t cache_payload(const lfm_attn_ctx *c, const lfm_attn_cache_model *m, uint32_t n, const cache_dims *d) {
+    size_t total = (size_t)n * sizeof(uint32_t);
+    for (uint32_t l = 0; l < m->n_model_layers; ++l)
+        total += m->ctx_layer[l] < 0 ? d->conv_bytes : 2u * cache_kv_rows(c, (uint32_t)m->ctx_layer[l], n, d);
+    return total;
+}
+
+/* Save: the payload is assembled in device memory in file order (token ids
+ * and ShortConv states uploaded, KV rows copied from the caches), hashed
+ * there (lfm_hip_fnv1a64), copied out once and written with the header and
+ * checksum in one write. */
 int lfm_attn_ctx_cache_save(lfm_attn_ctx *c, const char *path, const lfm_attn_cache_model *m,
                             const uint32_t *tokens, uint32_t n_tokens, float *const *conv_states,
                             const uint32_t *conv_ring_heads) {
@@ -447,18 +480,43 @@ int lfm_attn_ctx_cache_save(lfm_attn_ctx *c, const char *path, const lfm_attn_ca
     int st = cache_check(c, m, &d);
     if (st != LFM_ATTN_OK) return st;
     if (n_tokens > c->g.max_seq) return LFM_ATTN_E_RANGE;
-    uint64_t payload = (uint64_t)n_tokens * sizeof(uint32_t);
-    size_t max_kv = 0;
-    for (uint32_t l = 0; l < m->n_model_layers; ++l) {
+    for (uint32_t l = 0; l < m->n_model_layers; ++l)
+        if (m->ctx_layer[l] < 0 && (!conv_states || !conv_states[l])) return LFM_ATTN_E_INVALID;
+    char tmp[4096];
+    if (snprintf(tmp, sizeof tmp, "%s.tmp.%d", path, (int)getpid()) >= (int)sizeof tmp) return LFM_ATTN_E_INVALID;
+    const size_t payload = cache_payload(c, m, n_tokens, &d);
+    st = file_buffers(c, sizeof(cache_header) + payload + sizeof(uint64_t), align256(payload));
+    if (st != LFM_ATTN_OK) return st;
+    unsigned char *hp = c->file_host + sizeof(cache_header), *dp = c->file_dev;
+
+    size_t off = (size_t)n_tokens * sizeof(uint32_t);
+    memcpy(hp, tokens, off);
+    st = st_of(hipMemcpyAsync(dp, hp, off, hipMemcpyHostToDevice, c->stream));
+    for (uint32_t l = 0; l < m->n_model_layers && st == LFM_ATTN_OK; ++l) {
         if (m->ctx_layer[l] < 0) {
-            if (!conv_states || !conv_states[l]) return LFM_ATTN_E_INVALID;
-            payload += d.conv_bytes;
+            const float *src = conv_states[l];
+            for (uint32_t sidx = 0; sidx < d.hist_len; ++sidx) {
+                const uint32_t slot = conv_ring_heads && d.hist_len > 1u ? (conv_ring_heads[l] + sidx) % d.hist_len
+                                                                         : sidx;
+                memcpy(hp + off + (size_t)sidx * m->n_embd * sizeof(float), src + (size_t)slot * m->n_embd,
+                       (size_t)m->n_embd * sizeof(float));
+            }
+            st = st_of(hipMemcpyAsync(dp + off, hp + off, d.conv_bytes, hipMemcpyHostToDevice, c->stream));
+            off += d.conv_bytes;
         } else {
-            const size_t b = cache_kv_rows(c, (uint32_t)m->ctx_layer[l], n_tokens, &d);
-            payload += 2u * (uint64_t)b;
-            if (b > max_kv) max_kv = b;
+            const uint32_t layer = (uint32_t)m->ctx_layer[l];
+            const size_t b       = cache_kv_rows(c, layer, n_tokens, &d);
+            const uint32_t rows  = (uint32_t)(b / ((size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t)));
+            st = cache_rows_d2d(c, layer, n_tokens - rows, n_tokens, dp + off, dp + off + b, &d, 0);
+            off += 2u * b;
         }
     }
+    uint64_t csum = 0;
+    if (st == LFM_ATTN_OK) st = lfm_hip_fnv1a64(dp, payload, FNV_OFFSET, &csum, c->stream);
+    if (st == LFM_ATTN_OK) st = st_of(hipMemcpyAsync(hp, dp, payload, hipMemcpyDeviceToHost, c->stream));
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    if (st != LFM_ATTN_OK) return st;
+
     cache_header h;
     memset(&h, 0, sizeof h);
     h.magic               = LFM_CACHE_MAGIC;
@@ -470,64 +528,24 @@ int lfm_attn_ctx_cache_save(lfm_attn_ctx *c, const char *path, const lfm_attn_ca
     h.n_head_q            = m->n_head_q;
     h.shortconv_l_cache   = m->shortconv_l_cache;
     h.total_payload_bytes = payload;
+    memcpy(c->file_host, &h, sizeof h);
+    memcpy(hp + payload, &csum, sizeof csum);
 
-    uint16_t *k = max_kv ? (uint16_t *)malloc(max_kv) : NULL;
-    uint16_t *v = max_kv ? (uint16_t *)malloc(max_kv) : NULL;
-    float *lin  = (float *)malloc(d.conv_bytes);
-    char tmp[4096];
-    if ((max_kv && (!k || !v)) || !lin ||
-        snprintf(tmp, sizeof tmp, "%s.tmp.%d", path, (int)getpid()) >= (int)sizeof tmp) {
-        free(k);
-        free(v);
-        free(lin);
-        return LFM_ATTN_E_INVALID;
-    }
-    FILE *f       = fopen(tmp, "wb");
-    uint64_t csum = FNV_OFFSET;
-    st            = f ? LFM_ATTN_OK : LFM_ATTN_E_IO;
-#define PUT(buf, len)                                                              \
-    do {                                                                           \
-        if (st == LFM_ATTN_OK) {                                                   \
-            if (fwrite((buf), 1, (len), f) != (len)) st = LFM_ATTN_E_IO;           \
-            else csum = fnv1a(csum, (buf), (len));                                 \
-        }                                                                          \
-    } while (0)
-    if (st == LFM_ATTN_OK && fwrite(&h, sizeof h, 1, f) != 1) st = LFM_ATTN_E_IO;
-    PUT(tokens, (size_t)n_tokens * sizeof(uint32_t));
-    for (uint32_t l = 0; l < m->n_model_layers && st == LFM_ATTN_OK; ++l) {
-        if (m->ctx_layer[l] < 0) {
-            const float *src = conv_states[l];
-            if (conv_ring_heads && d.hist_len > 1u) {
-                for (uint32_t sidx = 0; sidx < d.hist_len; ++sidx) {
-                    const uint32_t slot = (conv_ring_heads[l] + sidx) % d.hist_len;
-                    memcpy(lin + (size_t)sidx * m->n_embd, src + (size_t)slot * m->n_embd,
-                           (size_t)m->n_embd * sizeof(float));
-                }
-                src = lin;
-            }
-            PUT(src, d.conv_bytes);
-        } else {
-            const uint32_t layer = (uint32_t)m->ctx_layer[l];
-            const size_t b       = cache_kv_rows(c, layer, n_tokens, &d);
-            const uint32_t rows  = (uint32_t)(b / ((size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t)));
-            st = cache_rows_xfer(c, layer, n_tokens - rows, n_tokens, k, v, &d, 0);
-            PUT(k, b);
-            PUT(v, b);
-        }
-    }
-#undef PUT
-    if (st == LFM_ATTN_OK && fwrite(&csum, sizeof csum, 1, f) != 1) st = LFM_ATTN_E_IO;
-    if (st == LFM_ATTN_OK && fflush(f) != 0) st = LFM_ATTN_E_IO;
+    const size_t total = sizeof h + payload + sizeof csum;
+    FILE *f            = fopen(tmp, "wb");
+    if (!f) return LFM_ATTN_E_IO;
+    st = fwrite(c->file_host, 1, total, f) == total && fflush(f) == 0 ? LFM_ATTN_OK : LFM_ATTN_E_IO;
     if (st == LFM_ATTN_OK) (void)fsync(fileno(f));
-    if (f && fclose(f) != 0 && st == LFM_ATTN_OK) st = LFM_ATTN_E_IO;
+    if (fclose(f) != 0) st = LFM_ATTN_E_IO;
     if (st == LFM_ATTN_OK && rename(tmp, path) != 0) st = LFM_ATTN_E_IO;
-    if (st != LFM_ATTN_OK && f) (void)unlink(tmp);
-    free(k);
-    free(v);
-    free(lin);
+    if (st != LFM_ATTN_OK) (void)unlink(tmp);
     return st;
 }
 
+/* Load: header checks, the whole payload read into pinned memory, the token
+ * prefix compared, the payload uploaded and its checksum verified on the
+ * device; only then are the states and caches written (caches by
+ * device-to-device copies from the uploaded payload). */
 int lfm_attn_ctx_cache_load_prefix(lfm_attn_ctx *c, const char *path, const lfm_attn_cache_model *m,
                                    const uint32_t *prompt, uint32_t n_prompt, float *const *conv_states,
                                    uint32_t *out_conv_heads, uint32_t *matched_pos) {
@@ -546,30 +564,28 @@ int lfm_attn_ctx_cache_load_prefix(lfm_attn_ctx *c, const char *path, const lfm_
         fclose(f);
         return LFM_ATTN_OK;
     }
-    const uint32_t n = h.n_tokens;
-    /* stage the whole payload, verify, then write states and caches */
-    size_t total = (size_t)n * sizeof(uint32_t);
-    for (uint32_t l = 0; l < m->n_model_layers; ++l)
-        total += m->ctx_layer[l] < 0 ? d.conv_bytes : 2u * cache_kv_rows(c, (uint32_t)m->ctx_layer[l], n, &d);
-    uint8_t *buf = (uint8_t *)malloc(total ? total : 1u);
-    if (!buf) {
+    const uint32_t n      = h.n_tokens;
+    const size_t payload  = cache_payload(c, m, n, &d);
+    st = file_buffers(c, sizeof h + payload + sizeof(uint64_t), align256(payload));
+    if (st != LFM_ATTN_OK) {
         fclose(f);
-        return LFM_ATTN_E_NOMEM;
+        return st;
     }
-    uint64_t file_csum = 0;
-    const int ok = fread(buf, 1, total, f) == total && fread(&file_csum, sizeof file_csum, 1, f) == 1 &&
-                   file_csum == fnv1a(FNV_OFFSET, buf, total) &&
-                   memcmp(buf, prompt, (size_t)n * sizeof(uint32_t)) == 0;
+    unsigned char *hp = c->file_host + sizeof h, *dp = c->file_dev;
+    const int whole   = fread(hp, 1, payload + sizeof(uint64_t), f) == payload + sizeof(uint64_t);
     fclose(f);
-    if (!ok) {
-        free(buf);
-        return LFM_ATTN_OK;
-    }
+    if (!whole || memcmp(hp, prompt, (size_t)n * sizeof(uint32_t)) != 0) return LFM_ATTN_OK;
+    uint64_t stored = 0, csum = 0;
+    memcpy(&stored, hp + payload, sizeof stored);
+    st = st_of(hipMemcpyAsync(dp, hp, payload, hipMemcpyHostToDevice, c->stream));
+    if (st == LFM_ATTN_OK) st = lfm_hip_fnv1a64(dp, payload, FNV_OFFSET, &csum, c->stream);
+    if (st != LFM_ATTN_OK || csum != stored) return st;
+
     size_t off = (size_t)n * sizeof(uint32_t);
     for (uint32_t l = 0; l < m->n_model_layers && st == LFM_ATTN_OK; ++l) {
         if (m->ctx_layer[l] < 0) {
             if (conv_states && conv_states[l]) {
-                memcpy(conv_states[l], buf + off, d.conv_bytes);
+                memcpy(conv_states[l], hp + off, d.conv_bytes);
                 if (out_conv_heads) out_conv_heads[l] = 0u;
             }
             off += d.conv_bytes;
@@ -577,11 +593,11 @@ int lfm_attn_ctx_cache_load_prefix(lfm_attn_ctx *c, const char *path, const lfm_
             const uint32_t layer = (uint32_t)m->ctx_layer[l];
             const size_t b       = cache_kv_rows(c, layer, n, &d);
             const uint32_t rows  = (uint32_t)(b / ((size_t)c->g.n_head_kv * c->g.head_dim * sizeof(uint16_t)));
-            st = cache_rows_xfer(c, layer, n - rows, n, (uint16_t *)(buf + off), (uint16_t *)(buf + off + b), &d, 1);
+            st = cache_rows_d2d(c, layer, n - rows, n, dp + off, dp + off + b, &d, 1);
             off += 2u * b;
         }
     }
-    free(buf);
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
     if (st == LFM_ATTN_OK) *matched_pos = n;
     return st;
 }

@@ -202,6 +202,27 @@ int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *con
                                     cap, to_stream(stream));
 }
 
+/* ---- FNV-1a 64 of a device buffer ------------------------------------------- */
+int lfm_hip_fnv1a64(const void *data, size_t n_bytes, uint64_t h_in, uint64_t *h_out, lfm_attn_stream_t stream) {
+    if (!h_out) return LFM_ATTN_E_INVALID;
+    if (n_bytes == 0u) {
+        *h_out = h_in;
+        return LFM_ATTN_OK;
+    }
+    if (!data || ((uintptr_t)data & 15u)) return LFM_ATTN_E_INVALID;
+    const hipStream_t s = to_stream(stream);
+    int st              = LFM_ATTN_OK;
+    void *ws            = lfm::workspace(lfm::fnv1a64_workspace_bytes(n_bytes), s, &st);
+    if (!ws) return st;
+    if (lfm::launch_fnv1a64(data, n_bytes, h_in, ws, s) != 0) return lfm::hip_status(hipGetLastError());
+    uint64_t acc = 0;
+    hipError_t e = hipMemcpyAsync(&acc, ws, sizeof acc, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return lfm::hip_status(e);
+    *h_out = lfm::fnv1a64_finish(h_in, n_bytes, acc);
+    return LFM_ATTN_OK;
+}
+
 /* ---- projections beside the path ------------------------------------------- */
 static inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1u)) == 0u; }
 

@@ -229,3 +229,53 @@ def test_checkpoint_swa_slab_matches_reference(orc, ref):
         assert np.array_equal(k2[l], k[l]) and np.array_equal(v2[l], v[l])
         assert np.array_equal(k3[l], k[l]) and np.array_equal(v3[l], v[l])
     assert not k2[2].any() and not k3[2].any()  # full layers are not in the slab
+
+
+def _fnv_chunked(data, h0, chunk=64, fan=4):
+    """numpy emulation of the device decomposition of FNV-1a 64: per-chunk
+    256-state maps of the low byte, composed in groups into prefix tables,
+    then each chunk's polynomial from its start state, weighted by
+    P^(bytes after it)."""
+    P, M = 0x100000001B3, (1 << 64) - 1
+    states = np.arange(256, dtype=np.int64)
+    n = (len(data) + chunk - 1) // chunk
+    maps = []
+    for c in range(n):
+        s = states.copy()
+        for b in data[c * chunk:(c + 1) * chunk]:
+            s = ((s ^ int(b)) * 179) & 255
+        maps.append(s)
+    levels, cur = [], maps
+    while len(cur) > 1:
+        pre, up = [], []
+        for g in range(0, len(cur), fan):
+            s = states.copy()
+            for m in cur[g:g + fan]:
+                pre.append(s.copy())
+                s = m[s]
+            up.append(s)
+        levels.append(pre)
+        cur = up
+    acc = 0
+    for i in range(n):
+        s = h0 & 255
+        for l in range(len(levels) - 1, -1, -1):
+            s = int(levels[l][i // fan ** l][s])
+        a = 0
+        seg = data[i * chunk:(i + 1) * chunk]
+        for b in seg:
+            x = s ^ int(b)
+            a = ((a + (x - s)) * P) & M
+            s = (x * 179) & 255
+        acc = (acc + a * pow(P, len(data) - i * chunk - len(seg), 1 << 64)) & M
+    return (h0 * pow(P, len(data), 1 << 64) + acc) & M
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 64 * 4 * 4 + 7, 1500])
+def test_parallel_fnv_decomposition(orc, n):
+    """The identity the device hash relies on, checked against the sequential
+    FNV-1a on small buffers and uneven chunk counts (several levels)."""
+    rng = np.random.default_rng(n)
+    data = rng.integers(0, 256, n, dtype=np.uint8)
+    for h0 in (14695981039346656037, 0x1234567890ABCDEF):
+        assert _fnv_chunked(data, h0) == orc.fnv1a(data, h0)
