@@ -16,10 +16,12 @@
  *      states s_j are known.
  *
  * Kernels:
- *  k_fnv_maps     one workgroup per 1 KiB chunk: the chunk's 256-state map,
- *                 two states per lane in 16-bit halves (v_pk_mul_lo_u16; the
- *                 low byte of a 16-bit product depends only on low bytes, so
- *                 masking waits until the end).
+ *  k_fnv_maps     one wave per 1 KiB chunk: the chunk's 256-state map.
+ *                 Flipping bit 7 of s flips bit 7 of s' and nothing else
+ *                 (128 * 179 = 128 mod 256), so map(s ^ 128) = map(s) ^ 128
+ *                 and only states 0..127 are run: two per lane in 16-bit
+ *                 halves (v_pk_mul_lo_u16; the low byte of a 16-bit product
+ *                 depends only on low bytes, so masking waits until the end).
  *  k_fnv_compose  groups of 64 maps: per group-start state, the state at the
  *                 start of every member (written over the member maps) and
  *                 the group's map (input to the next level).
@@ -57,8 +59,9 @@ __device__ uint64_t pow_p(uint64_t e) {
 }
 
 /* 256-state map of each 1 KiB chunk: maps[c][s] = low byte after the chunk
- * starting from low byte s.  128 lanes, states (2t, 2t+1). */
-__global__ __launch_bounds__(128) void k_fnv_maps(const uint8_t *__restrict__ data, uint64_t len,
+ * starting from low byte s.  64 lanes run states (2t, 2t+1); states
+ * 128 + (2t, 2t+1) follow by the bit-7 symmetry. */
+__global__ __launch_bounds__(64) void k_fnv_maps(const uint8_t *__restrict__ data, uint64_t len,
                                                   uint8_t *__restrict__ maps, uint64_t *__restrict__ acc_out) {
     const uint64_t c0 = (uint64_t)blockIdx.x * kChunk;
     const uint32_t n  = (uint32_t)(len - c0 < kChunk ? len - c0 : kChunk);
@@ -82,7 +85,9 @@ __global__ __launch_bounds__(128) void k_fnv_maps(const uint8_t *__restrict__ da
         s                      = (s ^ (u16x2){b, b}) * m;
     }
     const uint32_t out = (uint32_t)(s.x & 0xffu) | ((uint32_t)(s.y & 0xffu) << 8);
-    ((uint16_t *)(maps + (size_t)blockIdx.x * 256u))[t] = (uint16_t)out;
+    uint16_t *row      = (uint16_t *)(maps + (size_t)blockIdx.x * 256u);
+    row[t]             = (uint16_t)out;
+    row[64u + t]       = (uint16_t)(out ^ 0x8080u);
 }
 
 /* Group of up to 64 maps: member maps become prefix tables (state at the
@@ -179,7 +184,7 @@ int launch_fnv1a64(const void *data, uint64_t len, uint64_t h_in, void *ws, hipS
     p.n_chunks    = n;
     p.start_state = (uint32_t)(h_in & 0xffu);
     p.acc         = acc_dev;
-    hipLaunchKernelGGL(k_fnv_maps, dim3(n), dim3(128), 0, stream, (const uint8_t *)data, len, w, acc_dev);
+    hipLaunchKernelGGL(k_fnv_maps, dim3(n), dim3(64), 0, stream, (const uint8_t *)data, len, w, acc_dev);
     uint32_t lv = 0;
     while (n > 1u) {
         if (lv == kMaxLvls) return -1;

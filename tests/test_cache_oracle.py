@@ -271,6 +271,19 @@ def _fnv_chunked(data, h0, chunk=64, fan=4):
     return (h0 * pow(P, len(data), 1 << 64) + acc) & M
 
 
+def test_low_byte_map_bit7_symmetry():
+    """map(s ^ 128) = map(s) ^ 128 for any byte run, so the device runs only
+    states 0..127 (128 * 179 = 128 mod 256)."""
+    rng = np.random.default_rng(4)
+    states = np.arange(256, dtype=np.int64)
+    for n in (1, 7, 300):
+        s = states.copy()
+        for b in rng.integers(0, 256, n):
+            s = ((s ^ int(b)) * 179) & 255
+        assert np.array_equal(s[128:], s[:128] ^ 128)
+        assert sorted(s.tolist()) == list(range(256))  # a permutation
+
+
 @pytest.mark.parametrize("n", [1, 63, 64, 65, 64 * 4 * 4 + 7, 1500])
 def test_parallel_fnv_decomposition(orc, n):
     """The identity the device hash relies on, checked against the sequential
