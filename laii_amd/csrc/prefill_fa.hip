@@ -27,8 +27,11 @@
  *                            only when a step exceeds it by more than
  *                            8 ln 2 (P <= 2^8, fp16 P stays finite), which
  *                            rescales O and l in a rare uniform branch
- *   l += p                   v_dot2_f32_f16 over the fp16 P fed to the MFMA
  *   O^T += V^T . P^T(k)      V^T fragments read transposed from row-major V
+ *   l += 1 . P^T(k)          one more MFMA with an all-ones A operand: the
+ *                            column sums of the same fp16 P, in fp32, on
+ *                            the matrix pipe (v_dot2 on the VALU cannot
+ *                            co-issue with MFMA)
  * Causal masking only touches steps that cross the diagonal; steps above it
  * are skipped.  Workgroups run heaviest-first (late query tiles first).
  */
@@ -194,15 +197,15 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
 
     float4_t oacc[NM][NT];
     float4_t negm[NT]; /* -m splat: initial value of the score accumulator */
-    float l[NT];
+    float4_t lacc[NT]; /* column sums of P (every element holds the column's sum) */
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         negm[nt] = (float4_t)0.0f;
-        l[nt]    = 0.0f;
+        lacc[nt] = (float4_t)0.0f;
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
     }
-    const half2_t ones = {(_Float16)1.0f, (_Float16)1.0f};
+    const half8_t ones8 = (half8_t)(_Float16)1.0f;
 
     /* S^T of step k: two 16-key tiles x NT column tiles */
     auto scores = [&](auto mask_tag, uint32_t k, float4_t (&sc)[2][NT]) {
@@ -256,7 +259,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 const float inc   = raise ? v : 0.0f;
                 const float alpha = __builtin_amdgcn_exp2f(-inc * kLog2e);
                 negm[nt] -= inc;
-                l[nt] *= alpha;
+                lacc[nt] *= alpha;
                 sc[0][nt] -= inc;
                 sc[1][nt] -= inc;
 #pragma unroll
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
         }
     };
 
-    /* P^T(k) = exp2(S^T(k)), l += P, O^T += V^T(k) . P^T(k) */
+    /* P^T(k) = exp2(S^T(k)), O^T += V^T(k) . P^T(k), l += 1 . P^T(k) */
     auto accumulate = [&](uint32_t k, const float4_t (&sc)[2][NT]) {
         u32x4_t pf[NT];
 #pragma unroll
@@ -277,12 +280,6 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
             const half2_t h1 = exp_pk(a[2], a[3]);
             const half2_t h2 = exp_pk(c[0], c[1]);
             const half2_t h3 = exp_pk(c[2], c[3]);
-            float lsum = l[nt];
-            lsum = __builtin_amdgcn_fdot2(h0, ones, lsum, false);
-            lsum = __builtin_amdgcn_fdot2(h1, ones, lsum, false);
-            lsum = __builtin_amdgcn_fdot2(h2, ones, lsum, false);
-            lsum = __builtin_amdgcn_fdot2(h3, ones, lsum, false);
-            l[nt] = lsum;
             u32x4_t w;
             w[0] = __builtin_bit_cast(uint32_t, h0);
             w[1] = __builtin_bit_cast(uint32_t, h1);
@@ -299,6 +296,8 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
         }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
     };
 
     /* entering LDS block b: block b (stored at the previous entry) becomes
@@ -346,8 +345,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     /* ---- epilogue: O / l ------------------------------------------------- */
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-        float lt = l[nt] + __shfl_xor(l[nt], 16);
-        lt += __shfl_xor(lt, 32);
+        const float lt = lacc[nt][0];
         if (!col_ok[nt]) continue;
         const uint32_t c = (uint32_t)(wave * 64 + nt * 16 + l16);
         const uint32_t j = c / P.tq, t = t0 + c % P.tq;
