@@ -266,8 +266,11 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                     }
         }
 
-        /* online softmax; P^T fragments (hi, lo) */
+        /* online softmax; P^T fragments (hi, lo).  O is rescaled only when
+         * some column's running max rose (alpha == 1 exactly otherwise) */
         half8_t ph[NT], pl[NT];
+        float alpha_nt[NT];
+        bool rose = false;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             float mx = fmaxf(fmaxf(fmaxf(sacc[0][nt][0], sacc[0][nt][1]), fmaxf(sacc[0][nt][2], sacc[0][nt][3])),
@@ -276,6 +279,8 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float mnew  = fmaxf(mrun[nt], mx);
             const float alpha = __builtin_amdgcn_exp2f(mrun[nt] - mnew);
+            rose             |= mnew > mrun[nt];
+            alpha_nt[nt]      = alpha;
             mrun[nt]          = mnew;
             float psum        = 0.0f;
 #pragma unroll
@@ -289,8 +294,12 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                     pl[nt][4 * kt + i] = (_Float16)(p - (float)hi);
                 }
             lrun[nt] = lrun[nt] * alpha + psum;
+        }
+        if (__builtin_amdgcn_ballot_w64(rose) != 0ull) {
 #pragma unroll
-            for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha_nt[nt];
         }
 
         wave_lds_sync(); /* V^T of this sub-tile is in LDS */
