@@ -132,6 +132,18 @@ int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *con
 int lfm_hip_quantize_q8_K(const float *x, void *y_q8_K, uint32_t n_rows, uint32_t n_cols,
                           lfm_attn_stream_t stream);
 
+/* Weight types of the projections (GGML ids; blocks as in
+ * tools/lfm2_cpuid_quants.c:55-127, include/lfm2_simd_avx2.h:120-158), the
+ * alignment a matrix needs, and the reference dot each row equals bit for bit:
+ *   2  Q4_0   18 B / 32 weights (fp16 d, qs[16])             2  lfm2_vec_dot_q4_0_q8_K_avx2
+ *   8  Q8_0   34 B / 32 weights (fp16 d, int8 qs[32])        2  lfm2_vec_dot_q8_0_q8_K_avx2
+ *   12 Q4_K  144 B / 256 (d, dmin, scales[12], qs[128])     16  lfm2_vec_dot_q4_K_q8_K_avx2
+ *   13 Q5_K  176 B / 256 (d, dmin, scales[12], qh[32], qs) 16  lfm2_vec_dot_q5_K_q8_K_avx2
+ *   14 Q6_K  210 B / 256 (ql[128], qh[64], scales[16], d)    2  lfm2_vec_dot_q6_K_q8_K_avx2
+ *   23 IQ4_XS 136 B / 256 (d, scales_h, scales_l[4], qs)     8  lfm2_vec_dot_iq4_xs_q8_K_avx2
+ * n_cols must be a multiple of 256 (the Q8_K activations'). */
+#define LFM_Q_TYPES {2u, 8u, 12u, 13u, 14u, 23u}
+
 /* out[t][r] = (row r of the Q4_K matrix w_q4_K [n_rows][n_cols/256]) .
  * (token t of x_q8_K [n_tokens][n_cols/256]), bit-identical to
  * lfm2_vec_dot_q4_K_q8_K_avx2 (include/lfm2_simd_avx2.h:364-412) per row.
@@ -148,12 +160,19 @@ int lfm_hip_matmul_q4_K(float *out, const void *w_q4_K, uint32_t n_rows, uint32_
  * row r of wq . token t, likewise k, v, g.  Replaces
  * lfm2_gqa_qkv_fused_1x4_mt (tools/lfm2_decode_1x4.c:885-930; g_out NULL)
  * and lfm3_gqa_qkvg_1x4_mt (tools/lfm3_engine.c:1545-1598).  types[4] holds
- * each matrix's GGML type: 12 (Q4_K, 16-byte aligned) or 14 (Q6_K, block_q6_K
- * 210 B: ql[128], qh[64], int8 scales[16], fp16 d; 2-byte aligned); any other
- * type gives LFM_ATTN_E_UNSUPPORTED.  Each row is bit-identical to the
- * reference's AVX2 1x1 dot of its type (include/lfm2_simd_avx2.h:364-412,
- * 551-634).  The gate output is the raw projection: the attention entry points
- * take it as logits (gate_is_logit), which applies the reference's sigmoid. */
+ * each matrix's GGML type (LFM_Q_TYPES below); any other type gives
+ * LFM_ATTN_E_UNSUPPORTED.  Each row is bit-identical to the reference's AVX2
+ * 1x1 dot of its type.  The gate output is the raw projection: the attention
+ * entry points take it as logits (gate_is_logit), which applies the
+ * reference's sigmoid. */
+/* out[t][r] = (row r of w, GGML type w_type, [n_rows][n_cols]) . (token t of
+ * x_q8_K): lfm2_matmul_1x4_prequant_mt (tools/lfm2_decode_1x4.c:795-813) for
+ * every weight type its kernel table serves (tools/lfm2_decode_1x4.c:597-690),
+ * and those branches of lfm2_matmul_batch_avx2_mt after its quantize step.
+ * Types and alignment as LFM_Q_TYPES; out and x_q8_K 4-byte aligned. */
+int lfm_hip_matmul_prequant(float *out, const void *w, uint32_t w_type, uint32_t n_rows, uint32_t n_cols,
+                            const void *x_q8_K, uint32_t n_tokens, lfm_attn_stream_t stream);
+
 int lfm_hip_gqa_qkv_fused(float *q_out, float *k_out, float *v_out, float *g_out, const void *wq,
                           const void *wk, const void *wv, const void *wg, const uint32_t types[4],
                           uint32_t q_rows, uint32_t k_rows, uint32_t v_rows, uint32_t g_rows,

@@ -6,8 +6,12 @@ host mirror: ctypes bindings named after the reference's dispatch calls.
 """
 from ._lib import LIB_PATH, LfmAttnError, load  # noqa: F401
 from .attention import (  # noqa: F401
+    GGML_IQ4_XS,
+    GGML_Q4_0,
     GGML_Q4_K,
+    GGML_Q5_K,
     GGML_Q6_K,
+    GGML_Q8_0,
     CacheModel,
     DeviceArray,
     EngineContext,
@@ -19,6 +23,7 @@ from .attention import (  # noqa: F401
     kv_cache_shift_sinks,
     lfm3_kv_cache_shift_sinks,
     lfm3_online_gqa_f16_dispatch,
+    matmul_prequant,
     matmul_q4_K,
     online_gqa_f16,
     pointer_table,

@@ -40,6 +40,7 @@ SIGNATURES = {
     "lfm_hip_store_fp32_to_fp16": (_int, [_vp, _vp, _u32, _vp]),
     "lfm_hip_quantize_q8_K": (_int, [_vp, _vp, _u32, _u32, _vp]),
     "lfm_hip_matmul_q4_K": (_int, [_vp, _vp, _u32, _u32, _vp, _u32, _vp]),
+    "lfm_hip_matmul_prequant": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _u32, _vp]),
     "lfm_hip_gqa_qkv_fused": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                      _u32, _u32, _vp, _u32, _vp]),
     "lfm_hip_qkv_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,

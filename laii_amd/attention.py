@@ -159,7 +159,15 @@ def matmul_q4_K(out: Ptr, w_q4_K: Ptr, n_rows: int, n_cols: int, x_q8_K: Ptr, n_
                                      stream), "lfm_hip_matmul_q4_K")
 
 
-GGML_Q4_K, GGML_Q6_K = 12, 14
+GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_IQ4_XS = 2, 8, 12, 13, 14, 23
+
+
+def matmul_prequant(out: Ptr, w: Ptr, w_type: int, n_rows: int, n_cols: int, x_q8_K: Ptr,
+                    n_tokens: int, stream=None) -> None:
+    """out[t][r] = row r of w (GGML type w_type) . token t of the Q8_K
+    activations (lfm2_matmul_1x4_prequant_mt, tools/lfm2_decode_1x4.c:795-813)."""
+    check(load().lfm_hip_matmul_prequant(_p(out), _p(w), w_type, n_rows, n_cols, _p(x_q8_K), n_tokens,
+                                         stream), "lfm_hip_matmul_prequant")
 
 
 def gqa_qkv_fused(outs: Sequence[Ptr], ws: Sequence[Ptr], types: Sequence[int],
@@ -167,7 +175,8 @@ def gqa_qkv_fused(outs: Sequence[Ptr], ws: Sequence[Ptr], types: Sequence[int],
     """Q, K, V (and gate, if a fourth matrix is given) projections of the same
     Q8_K tokens in one pass (lfm2_gqa_qkv_fused_1x4_mt,
     tools/lfm2_decode_1x4.c:885-930; lfm3_gqa_qkvg_1x4_mt,
-    tools/lfm3_engine.c:1545-1598).  types: GGML ids, 12 (Q4_K) or 14 (Q6_K)."""
+    tools/lfm3_engine.c:1545-1598).  types: GGML ids 2 (Q4_0), 8 (Q8_0),
+    12 (Q4_K), 13 (Q5_K), 14 (Q6_K) or 23 (IQ4_XS)."""
     outs, ws, types, rows = list(outs), list(ws), list(types), list(rows)
     while len(outs) < 4:
         outs.append(None)

@@ -99,8 +99,19 @@ __device__ __forceinline__ float add_rounded(float a, float b) {
     return a + b;
 }
 
+__device__ __forceinline__ float mul_rounded(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+
 __device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+/* 4 bytes from a 2-byte aligned address */
+__device__ __forceinline__ uint32_t ld16x2(const uint8_t *p) {
+    const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
+    return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
 }
 
 /* Per weight type: what lane p (0..7) of a super-block's lane group loads and
@@ -108,12 +119,17 @@ __device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
  * 8 lanes, and the super-block's fp32 term in the reference's rounding order. */
 template <int TYPE> struct QType;
 
+/* Integer-partial types (Q4_K, Q5_K, Q6_K, IQ4_XS) combine their exact lane
+ * sums in one fp32 term per super-block; the 32-weight block types (Q4_0,
+ * Q8_0) give a float per lane (one block each) that the reference sums in
+ * block order before scaling by d8 (kFloatParts). */
 /* Q4_K: part p = qs bytes 16p..16p+15: 16 weights of sub-block 2*(p/2) (low
  * nibbles) and of sub-block 2*(p/2)+1 (high nibbles); a = sum(sc*q4*q8),
  * b = sum(m*bsum); term = (d*d8)*a - (dmin*d8)*b
  * (include/lfm2_simd_avx2.h:364-412). */
 template <> struct QType<12> {
     static constexpr uint32_t kBytes = 144u;
+    static constexpr bool kFloatParts = false;
     struct W { uint32_t q[4]; int32_t sc1, m1, sc2, m2; float d, dmin; };
     struct X { float d8; uint32_t lo[4], hi[4]; int32_t bl, bh; };
     static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
@@ -166,12 +182,9 @@ template <> struct QType<12> {
  * (include/lfm2_simd_avx2.h:551-634). */
 template <> struct QType<14> {
     static constexpr uint32_t kBytes = 210u;
+    static constexpr bool kFloatParts = false;
     struct W { uint32_t l0[2], l1[2], qh[2]; int32_t s[4], so0, so1; float d; };
     struct X { float d8; uint32_t x[4][2]; int32_t b0, b1; };
-    static __device__ __forceinline__ uint32_t ld16x2(const uint8_t *p) { /* 2-byte aligned */
-        const uint16_t *h = reinterpret_cast<const uint16_t *>(p);
-        return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
-    }
     static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
         const uint32_t half = p >> 2, q = p & 3u;
         const uint8_t *ql = blk + 64u * half + 8u * q, *qh = blk + 128u + 32u * half + 8u * q;
@@ -222,6 +235,167 @@ template <> struct QType<14> {
 #pragma clang fp contract(off)
         const float dd = w.d * d8;
         return dd * (float)(a - 32 * b);
+    }
+};
+
+/* Q5_K (fp16 d, fp16 dmin, scales[12] as Q4_K, qh[32], qs[128]; 176 bytes):
+ * part p = qs bytes 16p..16p+15 of 64-chunk c = p/2 with qh bytes
+ * 16(p%2)..+15: low nibbles + 16 * qh bit 2c are sub-block 2c, high nibbles
+ * + 16 * bit 2c+1 sub-block 2c+1; a, b and the term as Q4_K
+ * (lfm2_vec_dot_q5_K_q8_K_avx2, tools/lfm2_cpuid_quants.c:690-740). */
+template <> struct QType<13> {
+    static constexpr uint32_t kBytes = 176u;
+    static constexpr bool kFloatParts = false;
+    using X = QType<12>::X;
+    struct W { uint32_t lo[4], hi[4]; int32_t sc1, m1, sc2, m2; float d, dmin; };
+    static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(blk);
+        const uint4 qs  = *reinterpret_cast<const uint4 *>(blk + 48u + 16u * p);
+        const uint4 qh  = *reinterpret_cast<const uint4 *>(blk + 16u + 16u * (p & 1u));
+        const uint32_t c = p >> 1;
+        const uint32_t q[4] = {qs.x, qs.y, qs.z, qs.w}, h[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w.lo[i] = (q[i] & 0x0F0F0F0Fu) | (((h[i] >> (2u * c)) & 0x01010101u) << 4);
+            w.hi[i] = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (2u * c + 1u)) & 0x01010101u) << 4);
+        }
+        uint8_t sc12[12];
+        __builtin_memcpy(sc12, reinterpret_cast<const uint8_t *>(&hdr) + 4, 12);
+        scale_min(2u * c, sc12, &w.sc1, &w.m1);
+        scale_min(2u * c + 1u, sc12, &w.sc2, &w.m2);
+        w.d    = fp16_bits(hdr.x & 0xFFFFu);
+        w.dmin = fp16_bits(hdr.x >> 16);
+    }
+    static __device__ __forceinline__ void load_x(X &x, const uint8_t *xb, uint32_t p) { QType<12>::load_x(x, xb, p); }
+    static __device__ __forceinline__ void partials(const W &w, const X &x, uint32_t, int32_t &a, int32_t &b) {
+        int32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo = dot4(w.lo[i], x.lo[i], lo);
+            hi = dot4(w.hi[i], x.hi[i], hi);
+        }
+        a = w.sc1 * lo + w.sc2 * hi;
+        b = w.m1 * x.bl + w.m2 * x.bh;
+    }
+    static __device__ __forceinline__ float term(const W &w, float d8, int32_t a, int32_t b) {
+#pragma clang fp contract(off)
+        const float dd = w.d * d8, dm = w.dmin * d8;
+        return dd * (float)a - dm * (float)b;
+    }
+};
+
+/* IQ4_XS (fp16 d, scales_h, scales_l[4], qs[128]; 136 bytes): part p =
+ * sub-block p, qs bytes 16p..16p+15 (low nibbles elements 0..15, high
+ * 16..31) mapped through the IQ4_NL grid with v_perm_b32; a = ls * dot, b = 0;
+ * term = (d*d8) * a (lfm2_vec_dot_iq4_xs_q8_K_avx2, tools/lfm2_cpuid_quants.c:832-880). */
+template <> struct QType<23> {
+    static constexpr uint32_t kBytes = 136u;
+    static constexpr bool kFloatParts = false;
+    struct W { uint32_t lo[4], hi[4]; int32_t ls; float d; };
+    struct X { float d8; uint32_t lo[4], hi[4]; };
+    /* the 16 grid values as int8 bytes, four per dword */
+    static constexpr uint32_t kG0 = 0xBFAD9881u, kG1 = 0xF6EADDCFu, kG2 = 0x26190D01u, kG3 = 0x71594535u;
+    static __device__ __forceinline__ uint32_t grid4(uint32_t nib) { /* 4 nibbles (one per byte) */
+        const uint32_t sel = nib & 0x07070707u;
+        const uint32_t lo  = __builtin_amdgcn_perm(kG1, kG0, sel);
+        const uint32_t hi  = __builtin_amdgcn_perm(kG3, kG2, sel);
+        const uint32_t m   = ((nib >> 3) & 0x01010101u) * 0xFFu;
+        return (lo & ~m) | (hi & m);
+    }
+    static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
+        const uint2 hdr = *reinterpret_cast<const uint2 *>(blk);
+        const uint2 q0  = *reinterpret_cast<const uint2 *>(blk + 8u + 16u * p);
+        const uint2 q1  = *reinterpret_cast<const uint2 *>(blk + 16u + 16u * p);
+        const uint32_t q[4] = {q0.x, q0.y, q1.x, q1.y};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w.lo[i] = grid4(q[i] & 0x0F0F0F0Fu);
+            w.hi[i] = grid4((q[i] >> 4) & 0x0F0F0F0Fu);
+        }
+        const uint32_t sh = hdr.x >> 16, sl = hdr.y;
+        w.ls = (int32_t)(((sl >> (8u * (p >> 1) + 4u * (p & 1u))) & 0x0Fu) | (((sh >> (2u * p)) & 3u) << 4)) - 32;
+        w.d  = fp16_bits(hdr.x & 0xFFFFu);
+    }
+    static __device__ __forceinline__ void load_x(X &x, const uint8_t *xb, uint32_t p) {
+        x.d8 = *reinterpret_cast<const float *>(xb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x.lo[i] = ld32(xb + 4u + 32u * p + 4u * i);
+            x.hi[i] = ld32(xb + 20u + 32u * p + 4u * i);
+        }
+    }
+    static __device__ __forceinline__ void partials(const W &w, const X &x, uint32_t, int32_t &a, int32_t &b) {
+        int32_t acc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = dot4(w.hi[i], x.hi[i], dot4(w.lo[i], x.lo[i], acc));
+        a = w.ls * acc;
+        b = 0;
+    }
+    static __device__ __forceinline__ float term(const W &w, float d8, int32_t a, int32_t) {
+#pragma clang fp contract(off)
+        const float dd = w.d * d8;
+        return dd * (float)a;
+    }
+};
+
+/* Q4_0 (fp16 d, qs[16]; 18 bytes per 32 weights, 2-byte aligned): part p =
+ * block p of the super-block; its float d * (sum(u4*q8) - 8 * bsums) is
+ * summed in block order (lfm2_vec_dot_q4_0_q8_K_avx2,
+ * tools/lfm2_cpuid_quants.c:634-672). */
+template <> struct QType<2> {
+    static constexpr uint32_t kBytes = 144u; /* 8 blocks */
+    static constexpr bool kFloatParts = true;
+    struct W { uint32_t q[4]; float d; };
+    struct X { float d8; uint32_t lo[4], hi[4]; int32_t s8; };
+    static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
+        const uint8_t *b = blk + 18u * p;
+        w.d = fp16_bits(*reinterpret_cast<const uint16_t *>(b));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.q[i] = ld16x2(b + 2u + 4u * i);
+    }
+    static __device__ __forceinline__ void load_x(X &x, const uint8_t *xb, uint32_t p) {
+        x.d8 = *reinterpret_cast<const float *>(xb);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x.lo[i] = ld32(xb + 4u + 32u * p + 4u * i);
+            x.hi[i] = ld32(xb + 20u + 32u * p + 4u * i);
+        }
+        const uint32_t bs = ld32(xb + 260u + 4u * p);
+        x.s8 = (int32_t)(int16_t)(bs & 0xFFFFu) + (int32_t)(int16_t)(bs >> 16);
+    }
+    static __device__ __forceinline__ float part_float(const W &w, const X &x) {
+#pragma clang fp contract(off)
+        int32_t acc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc = dot4((w.q[i] >> 4) & 0x0F0F0F0Fu, x.hi[i], dot4(w.q[i] & 0x0F0F0F0Fu, x.lo[i], acc));
+        return w.d * (float)(acc - 8 * x.s8);
+    }
+};
+
+/* Q8_0 (fp16 d, int8 qs[32]; 34 bytes per 32 weights, 2-byte aligned): as
+ * Q4_0 with d * sum(q*q8) (lfm2_vec_dot_q8_0_q8_K_avx2, include/lfm2_simd_avx2.h:639-674). */
+template <> struct QType<8> {
+    static constexpr uint32_t kBytes = 272u; /* 8 blocks */
+    static constexpr bool kFloatParts = true;
+    struct W { uint32_t q[8]; float d; };
+    struct X { float d8; uint32_t v[8]; };
+    static __device__ __forceinline__ void load_w(W &w, const uint8_t *blk, uint32_t p) {
+        const uint8_t *b = blk + 34u * p;
+        w.d = fp16_bits(*reinterpret_cast<const uint16_t *>(b));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w.q[i] = ld16x2(b + 2u + 4u * i);
+    }
+    static __device__ __forceinline__ void load_x(X &x, const uint8_t *xb, uint32_t p) {
+        x.d8 = *reinterpret_cast<const float *>(xb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x.v[i] = ld32(xb + 4u + 32u * p + 4u * i);
+    }
+    static __device__ __forceinline__ float part_float(const W &w, const X &x) {
+#pragma clang fp contract(off)
+        int32_t acc = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = dot4(w.q[i], x.v[i], acc);
+        return w.d * (float)acc;
     }
 };
 
@@ -283,14 +457,24 @@ __global__ __launch_bounds__(256) void k_matmul_q(const MatSet S, const uint8_t 
         for (int r = 0; r < RPW; ++r)
 #pragma unroll
             for (int tt = 0; tt < TCH; ++tt) {
-                int32_t a, c;
-                Q::partials(wr[r], xt[tt], p, a, c);
+                if constexpr (Q::kFloatParts) {
+                    /* blocks of the super-block in order, then times d8 */
+                    const float t  = Q::part_float(wr[r], xt[tt]);
+                    const int base = (int)(lane & ~7u);
+                    float bsum     = add_rounded(0.0f, __shfl(t, base));
 #pragma unroll
-                for (int o = 1; o < 8; o <<= 1) {
-                    a += __shfl_xor(a, o);
-                    c += __shfl_xor(c, o);
+                    for (int k = 1; k < 8; ++k) bsum = add_rounded(bsum, __shfl(t, base + k));
+                    term[tt][r] = mul_rounded(xt[tt].d8, bsum);
+                } else {
+                    int32_t a, c;
+                    Q::partials(wr[r], xt[tt], p, a, c);
+#pragma unroll
+                    for (int o = 1; o < 8; o <<= 1) {
+                        a += __shfl_xor(a, o);
+                        c += __shfl_xor(c, o);
+                    }
+                    term[tt][r] = Q::term(wr[r], xt[tt].d8, a, c);
                 }
-                term[tt][r] = Q::term(wr[r], xt[tt].d8, a, c);
             }
         /* super-blocks b0 .. b0+7 in order; a block whose d8 is 0 adds nothing */
 #pragma unroll
@@ -352,7 +536,7 @@ int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, 
     if (n_tokens == 0u) return LFM_ATTN_OK;
     const uint32_t nb = n_cols / 256u;
     /* one launch per weight type present, each over its matrices */
-    for (uint32_t type : {12u, 14u}) {
+    for (uint32_t type : {12u, 14u, 13u, 23u, 2u, 8u}) {
         MatSet S{};
         for (uint32_t m = 0; m < n_mats; ++m) {
             if (types[m] != type || rows[m] == 0u) continue;
@@ -362,8 +546,15 @@ int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, 
             ++S.n;
         }
         if (S.n == 0u) continue;
-        const hipError_t e = type == 12u ? launch_type<12>(S, x_q8, nb, n_tokens, stream)
-                                         : launch_type<14>(S, x_q8, nb, n_tokens, stream);
+        hipError_t e;
+        switch (type) {
+        case 12u: e = launch_type<12>(S, x_q8, nb, n_tokens, stream); break;
+        case 14u: e = launch_type<14>(S, x_q8, nb, n_tokens, stream); break;
+        case 13u: e = launch_type<13>(S, x_q8, nb, n_tokens, stream); break;
+        case 23u: e = launch_type<23>(S, x_q8, nb, n_tokens, stream); break;
+        case 2u: e = launch_type<2>(S, x_q8, nb, n_tokens, stream); break;
+        default: e = launch_type<8>(S, x_q8, nb, n_tokens, stream); break;
+        }
         if (e != hipSuccess) return hip_status(e);
     }
     return LFM_ATTN_OK;

@@ -226,6 +226,18 @@ int lfm_hip_fnv1a64(const void *data, size_t n_bytes, uint64_t h_in, uint64_t *h
 /* ---- projections beside the path ------------------------------------------- */
 static inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1u)) == 0u; }
 
+/* Weight types of the projections and the alignment their rows need (0: no
+ * kernel): Q4_K and Q5_K blocks are 16-byte multiples, IQ4_XS 8, Q6_K,
+ * Q4_0 and Q8_0 only 2. */
+static inline uint32_t q_type_alignment(uint32_t type) {
+    switch (type) {
+    case 12u: case 13u: return 16u;
+    case 23u: return 8u;
+    case 14u: case 2u: case 8u: return 2u;
+    default: return 0u;
+    }
+}
+
 int lfm_hip_quantize_q8_K(const float *x, void *y_q8_K, uint32_t n_rows, uint32_t n_cols,
                           lfm_attn_stream_t stream) {
     if (n_rows == 0u || n_cols == 0u) return LFM_ATTN_OK;
@@ -259,15 +271,21 @@ int lfm_hip_gqa_qkv_fused(float *q_out, float *k_out, float *v_out, float *g_out
     for (int m = 0; m < 4; ++m) {
         if (rows[m] == 0u) continue;
         if (!outs[m] || !ws[m] || !aligned(outs[m], 4)) return LFM_ATTN_E_INVALID;
-        if (types[m] == 12u) {
-            if (!aligned(ws[m], 16)) return LFM_ATTN_E_INVALID;
-        } else if (types[m] == 14u) {
-            if (!aligned(ws[m], 2)) return LFM_ATTN_E_INVALID;
-        } else {
-            return LFM_ATTN_E_UNSUPPORTED;
-        }
+        const uint32_t need = q_type_alignment(types[m]);
+        if (!need) return LFM_ATTN_E_UNSUPPORTED;
+        if (!aligned(ws[m], need)) return LFM_ATTN_E_INVALID;
     }
     return lfm::launch_matmul_q(4u, outs, ws, types, rows, n_cols, x_q8_K, n_tokens, to_stream(stream));
+}
+
+int lfm_hip_matmul_prequant(float *out, const void *w, uint32_t w_type, uint32_t n_rows, uint32_t n_cols,
+                            const void *x_q8_K, uint32_t n_tokens, lfm_attn_stream_t stream) {
+    if (n_rows == 0u || n_tokens == 0u) return LFM_ATTN_OK;
+    if (!out || !w || !x_q8_K || n_cols == 0u || !aligned(x_q8_K, 4) || !aligned(out, 4)) return LFM_ATTN_E_INVALID;
+    const uint32_t need = q_type_alignment(w_type);
+    if (!need || n_cols % 256u) return LFM_ATTN_E_UNSUPPORTED;
+    if (!aligned(w, need)) return LFM_ATTN_E_INVALID;
+    return lfm::launch_matmul_q(1u, &out, &w, &w_type, &n_rows, n_cols, x_q8_K, n_tokens, to_stream(stream));
 }
 
 /* ---- attention -------------------------------------------------------------- */

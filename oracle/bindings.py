@@ -265,7 +265,7 @@ def _orc_dot6(self, w_row, x_q8, n_cols):
 
 
 def _orc_matmul_q(self, w, qtype, x_q8, n_cols):
-    """GGML type 12 (Q4_K) or 14 (Q6_K) rows: w uint8 [n_rows, row bytes] -> float32 [B, n_rows]."""
+    """GGML type 2, 8, 12, 13, 14 or 23 rows: w uint8 [n_rows, row bytes] -> float32 [B, n_rows]."""
     w = np.ascontiguousarray(w, np.uint8)
     x_q8 = np.ascontiguousarray(x_q8, np.uint8)
     out = np.zeros((x_q8.shape[0], w.shape[0]), np.float32)
@@ -636,3 +636,52 @@ Oracle.checkpoint_swa_slab = _orc_slab
 Reference.model_fingerprint = _ref_fingerprint
 Reference.checkpoint_swa_save = _ref_slab_save
 Reference.checkpoint_swa_restore = _ref_slab_restore
+
+
+# -- other weight types of the projections (GGML ids 2, 8, 13, 23) ---------------
+Q_BLOCK_BYTES = {2: 144, 8: 272, 12: 144, 13: 176, 14: 210, 23: 136}  # bytes per 256 weights
+
+
+def _orc_types_init(self):
+    L = self.lib
+    for n in ("q4_0", "q8_0", "q5_K", "iq4_xs"):
+        f = getattr(L, f"orc_dot_{n}_q8_K")
+        f.restype = _f32
+        f.argtypes = [_u8p, _u8p, _u32]
+
+
+def _ref_types_init(self):
+    L = self.lib
+    for n in ("q4_0", "q8_0", "q5_K", "iq4_xs"):
+        f = getattr(L, f"ref_dot_{n}_avx2")
+        f.restype = _f32
+        f.argtypes = [_u8p, _u8p, _u32]
+    L.ref_matmul_prequant_type.argtypes = [_f32p, _u8p, _u32, _u32, _u32, _u8p]
+
+
+_DOT_NAMES = {2: "q4_0", 8: "q8_0", 13: "q5_K", 23: "iq4_xs"}
+
+
+def _orc_dot_type(self, w_row, qtype, x_q8, n_cols):
+    f = getattr(self.lib, f"orc_dot_{_DOT_NAMES[qtype]}_q8_K")
+    return float(f(np.ascontiguousarray(w_row, np.uint8), np.ascontiguousarray(x_q8, np.uint8), n_cols))
+
+
+def _ref_dot_type(self, w_row, qtype, x_q8, n_cols):
+    f = getattr(self.lib, f"ref_dot_{_DOT_NAMES[qtype]}_avx2")
+    return float(f(np.ascontiguousarray(w_row, np.uint8), np.ascontiguousarray(x_q8, np.uint8), n_cols))
+
+
+def _ref_matmul_type(self, w, qtype, x_q8, n_cols):
+    """The engine's decode projection (lfm2_matmul_1x4_prequant_mt) for one token."""
+    w = np.ascontiguousarray(w, np.uint8)
+    out = np.zeros((1, w.shape[0]), np.float32)
+    self.lib.ref_matmul_prequant_type(out, w, qtype, w.shape[0], n_cols, np.ascontiguousarray(x_q8, np.uint8))
+    return out
+
+
+_wrap_init(Oracle, _orc_types_init)
+_wrap_init(Reference, _ref_types_init)
+Oracle.dot_type = _orc_dot_type
+Reference.dot_type = _ref_dot_type
+Reference.matmul_prequant_type = _ref_matmul_type

@@ -745,15 +745,183 @@ float orc_dot_q6_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
     return sumf;
 }
 
+/* Q4_0 (fp16 d, qs[16]: element l in the low nibble of qs[l], element l + 16
+ * in the high nibble; w = d * (nibble - 8)) x Q8_K
+ * (lfm2_vec_dot_q4_0_q8_K_scalar, tools/lfm2_cpuid_quants.c:252-281; the
+ * AVX2 and AVX-VNNI variants at :634-672, :1659-1693 round alike): per
+ * super-block, block_sum = sum over its 8 blocks in order of
+ * d * (sum(u4 * q8) - 8 * (bsum[2j] + bsum[2j+1])), then sumf += d8 * block_sum. */
+float orc_dot_q4_0_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    const uint8_t *w  = (const uint8_t *)w_row;
+    const uint8_t *xq = (const uint8_t *)x_q8;
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *xb = xq + (size_t)b * ORC_Q8K_BYTES;
+        float d8;
+        memcpy(&d8, xb, 4);
+        if (d8 == 0.0f) continue;
+        const int8_t *q8 = (const int8_t *)(xb + 4);
+        int16_t bs[16];
+        memcpy(bs, xb + 260, sizeof bs);
+        float block_sum = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            const uint8_t *blk = w + ((size_t)b * 8 + j) * ORC_Q4_0_BYTES;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            int32_t acc = 0;
+            for (int l = 0; l < 16; ++l)
+                acc += (int32_t)(blk[2 + l] & 0x0F) * q8[32 * j + l] + (int32_t)(blk[2 + l] >> 4) * q8[32 * j + 16 + l];
+            const int32_t s8 = (int32_t)bs[2 * j] + bs[2 * j + 1];
+            const float t    = orc_f16_to_f32(dh) * (float)(acc - 8 * s8);
+            block_sum        = block_sum + t;
+        }
+        const float tb = d8 * block_sum;
+        sumf           = sumf + tb;
+    }
+    return sumf;
+}
+
+/* Q8_0 (fp16 d, int8 qs[32]) x Q8_K (lfm2_vec_dot_q8_0_q8_K_avx2,
+ * include/lfm2_simd_avx2.h:639-674; scalar tools/lfm2_cpuid_quants.c:389-410,
+ * AVX-VNNI :1700-1731): the same order as Q4_0 with d * sum(q * q8). */
+float orc_dot_q8_0_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    const uint8_t *w  = (const uint8_t *)w_row;
+    const uint8_t *xq = (const uint8_t *)x_q8;
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *xb = xq + (size_t)b * ORC_Q8K_BYTES;
+        float d8;
+        memcpy(&d8, xb, 4);
+        if (d8 == 0.0f) continue;
+        const int8_t *q8 = (const int8_t *)(xb + 4);
+        float block_sum  = 0.0f;
+        for (int j = 0; j < 8; ++j) {
+            const uint8_t *blk = w + ((size_t)b * 8 + j) * ORC_Q8_0_BYTES;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            int32_t acc = 0;
+            for (int l = 0; l < 32; ++l) acc += (int32_t)(int8_t)blk[2 + l] * q8[32 * j + l];
+            const float t = orc_f16_to_f32(dh) * (float)acc;
+            block_sum     = block_sum + t;
+        }
+        const float tb = d8 * block_sum;
+        sumf           = sumf + tb;
+    }
+    return sumf;
+}
+
+/* Q5_K (fp16 d, fp16 dmin, scales[12] as Q4_K, qh[32], qs[128]; element l of
+ * 64-chunk c: low nibble of qs[32c + l] + 16 * bit 2c of qh[l] (sub-block
+ * 2c), high nibble + 16 * bit 2c+1 (sub-block 2c+1); w = d*sc*q - dmin*m)
+ * x Q8_K (lfm2_vec_dot_q5_K_q8_K_scalar, tools/lfm2_cpuid_quants.c:283-329;
+ * AVX2 :690-740): sumf += (d*d8) * sum(sc*q5*q8) - (dmin*d8) * sum(m*bsum). */
+float orc_dot_q5_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    const uint8_t *w  = (const uint8_t *)w_row;
+    const uint8_t *xq = (const uint8_t *)x_q8;
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *wb = w + (size_t)b * ORC_Q5K_BYTES;
+        const uint8_t *xb = xq + (size_t)b * ORC_Q8K_BYTES;
+        float d8;
+        memcpy(&d8, xb, 4);
+        if (d8 == 0.0f) continue;
+        uint16_t dh, mh;
+        memcpy(&dh, wb, 2);
+        memcpy(&mh, wb + 2, 2);
+        const float d = orc_f16_to_f32(dh) * d8, dmin = orc_f16_to_f32(mh) * d8;
+        const uint8_t *sc = wb + 4, *qh = wb + 16, *qs = wb + 48;
+        const int8_t *q8 = (const int8_t *)(xb + 4);
+        int16_t bs[16];
+        memcpy(bs, xb + 260, sizeof bs);
+        int32_t sum_q = 0, sum_m = 0;
+        for (int c = 0; c < 4; ++c) {
+            int32_t sc1, m1, sc2, m2;
+            q4k_scale_min(2 * c, sc, &sc1, &m1);
+            q4k_scale_min(2 * c + 1, sc, &sc2, &m2);
+            sum_m += m1 * (bs[4 * c] + bs[4 * c + 1]) + m2 * (bs[4 * c + 2] + bs[4 * c + 3]);
+            int32_t s1 = 0, s2 = 0;
+            for (int l = 0; l < 32; ++l) {
+                const int32_t lo = (qs[32 * c + l] & 0x0F) + (((qh[l] >> (2 * c)) & 1) << 4);
+                const int32_t hi = (qs[32 * c + l] >> 4) + (((qh[l] >> (2 * c + 1)) & 1) << 4);
+                s1 += lo * q8[64 * c + l];
+                s2 += hi * q8[64 * c + 32 + l];
+            }
+            sum_q += sc1 * s1 + sc2 * s2;
+        }
+        const float ta = d * (float)sum_q, tm = dmin * (float)sum_m;
+        const float tb = ta - tm;
+        sumf           = sumf + tb;
+    }
+    return sumf;
+}
+
+/* IQ4_XS (fp16 d, scales_h (2 high bits of 8 6-bit scales), scales_l[4] (low
+ * 4 bits), qs[128]; sub-block ib: 16 bytes, element j the low nibble, j + 16
+ * the high nibble, both indices into the fixed IQ4_NL grid; scale
+ * ls = 6-bit - 32) x Q8_K (lfm2_vec_dot_iq4_xs_q8_K_scalar,
+ * tools/lfm2_cpuid_quants.c:336-364; AVX2 :832-880): sumf += (d*d8) * sum(ls * dot). */
+static const int8_t k_iq4nl_grid[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                        1,    13,   25,  38,  53,  69,  89,  113};
+
+float orc_dot_iq4_xs_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    const uint32_t nb = n_cols / 256u;
+    const uint8_t *w  = (const uint8_t *)w_row;
+    const uint8_t *xq = (const uint8_t *)x_q8;
+    float sumf = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const uint8_t *wb = w + (size_t)b * ORC_IQ4XS_BYTES;
+        const uint8_t *xb = xq + (size_t)b * ORC_Q8K_BYTES;
+        float d8;
+        memcpy(&d8, xb, 4);
+        if (d8 == 0.0f) continue;
+        uint16_t dh, sh;
+        memcpy(&dh, wb, 2);
+        memcpy(&sh, wb + 2, 2);
+        const uint8_t *sl = wb + 4, *qs = wb + 8;
+        const int8_t *q8 = (const int8_t *)(xb + 4);
+        int32_t acc = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+            const int32_t ls = (((sl[ib >> 1] >> (4 * (ib & 1))) & 0x0F) | (((sh >> (2 * ib)) & 3) << 4)) - 32;
+            int32_t dot = 0;
+            for (int j = 0; j < 16; ++j)
+                dot += k_iq4nl_grid[qs[16 * ib + j] & 0x0F] * q8[32 * ib + j] +
+                       k_iq4nl_grid[qs[16 * ib + j] >> 4] * q8[32 * ib + 16 + j];
+            acc += ls * dot;
+        }
+        const float d  = orc_f16_to_f32(dh) * d8;
+        const float tb = d * (float)acc;
+        sumf           = sumf + tb;
+    }
+    return sumf;
+}
+
+size_t orc_q_row_bytes(uint32_t type, uint32_t n_cols) {
+    const size_t nb = n_cols / 256u;
+    switch (type) {
+    case 2u: return nb * 8u * ORC_Q4_0_BYTES;
+    case 8u: return nb * 8u * ORC_Q8_0_BYTES;
+    case 12u: return nb * ORC_Q4K_BYTES;
+    case 13u: return nb * ORC_Q5K_BYTES;
+    case 14u: return nb * ORC_Q6K_BYTES;
+    case 23u: return nb * ORC_IQ4XS_BYTES;
+    default: return 0;
+    }
+}
+
 void orc_matmul_q(float *out, const void *w, uint32_t type, uint32_t n_rows, uint32_t n_cols,
                   const void *x_q8, uint32_t n_tokens) {
-    const uint32_t nb   = n_cols / 256u;
-    const size_t rowb   = (size_t)nb * (type == 14u ? ORC_Q6K_BYTES : ORC_Q4K_BYTES);
+    const uint32_t nb = n_cols / 256u;
+    const size_t rowb = orc_q_row_bytes(type, n_cols);
+    float (*dot)(const void *, const void *, uint32_t) =
+        type == 2u ? orc_dot_q4_0_q8_K : type == 8u ? orc_dot_q8_0_q8_K : type == 13u ? orc_dot_q5_K_q8_K
+        : type == 14u ? orc_dot_q6_K_q8_K : type == 23u ? orc_dot_iq4_xs_q8_K : orc_dot_q4_K_q8_K;
     for (uint32_t t = 0; t < n_tokens; ++t)
         for (uint32_t r = 0; r < n_rows; ++r) {
             const void *wr = (const uint8_t *)w + (size_t)r * rowb;
             const void *xt = (const uint8_t *)x_q8 + (size_t)t * nb * ORC_Q8K_BYTES;
-            out[(size_t)t * n_rows + r] = type == 14u ? orc_dot_q6_K_q8_K(wr, xt, n_cols)
-                                                      : orc_dot_q4_K_q8_K(wr, xt, n_cols);
+            out[(size_t)t * n_rows + r] = dot(wr, xt, n_cols);
         }
 }

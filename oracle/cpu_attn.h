@@ -133,9 +133,19 @@ void orc_matmul_q4_K(float *out, const void *w, uint32_t n_rows, uint32_t n_cols
  * (include/lfm2_simd_avx2.h:551-634): exact sum(sc*u*q8) and sum(sc*bsum)
  * per super-block, then sumf += (d*d8) * (float)(sum - 32*offset). */
 #define ORC_Q6K_BYTES 210u
+#define ORC_Q5K_BYTES 176u
+#define ORC_IQ4XS_BYTES 136u
+#define ORC_Q4_0_BYTES 18u /* per 32 weights */
+#define ORC_Q8_0_BYTES 34u
+float orc_dot_q4_0_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
+float orc_dot_q8_0_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
+float orc_dot_q5_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
+float orc_dot_iq4_xs_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
+size_t orc_q_row_bytes(uint32_t type, uint32_t n_cols); /* GGML type id */
 float orc_dot_q6_K_q8_K(const void *w_row, const void *x_q8, uint32_t n_cols);
 
 /* out[t][r] for a matrix of GGML type 12 (Q4_K) or 14 (Q6_K). */
+/* type: GGML id 2 (Q4_0), 8 (Q8_0), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K), 23 (IQ4_XS) */
 void orc_matmul_q(float *out, const void *w, uint32_t type, uint32_t n_rows, uint32_t n_cols,
                   const void *x_q8, uint32_t n_tokens);
 

@@ -478,3 +478,44 @@ int ref_checkpoint_swa_restore(const uint16_t *slab, uint32_t n_layers, const ui
     free(m);
     return ok;
 }
+
+/* ---- other weight types of the decode projection (AVX2 1x1 kernels) ----------- */
+/* lfm2_vec_dot_q4_0_q8_K_avx2 (tools/lfm2_cpuid_quants.c:634-672) */
+float ref_dot_q4_0_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    return lfm2_vec_dot_q4_0_q8_K_avx2(w_row, (const block_q8_K_t *)x_q8, n_cols);
+}
+/* lfm2_vec_dot_q8_0_q8_K_avx2 (include/lfm2_simd_avx2.h:639-674) */
+float ref_dot_q8_0_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    return lfm2_vec_dot_q8_0_q8_K_avx2((const block_q8_0_t *)w_row, (const block_q8_K_t *)x_q8, n_cols);
+}
+/* lfm2_vec_dot_q5_K_q8_K_avx2 (tools/lfm2_cpuid_quants.c:690-740) */
+float ref_dot_q5_K_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    return lfm2_vec_dot_q5_K_q8_K_avx2(w_row, (const block_q8_K_t *)x_q8, n_cols);
+}
+/* lfm2_vec_dot_iq4_xs_q8_K_avx2 (tools/lfm2_cpuid_quants.c:832-880) */
+float ref_dot_iq4_xs_avx2(const void *w_row, const void *x_q8, uint32_t n_cols) {
+    return lfm2_vec_dot_iq4_xs_q8_K_avx2(w_row, (const block_q8_K_t *)x_q8, n_cols);
+}
+/* the engine's decode projection for any weight type: lfm2_matmul_1x4_prequant_mt
+ * (tools/lfm2_decode_1x4.c:795-813) through the CPU kernel table */
+void ref_matmul_prequant_type(float *out, const void *w, uint32_t type, uint32_t n_rows, uint32_t n_cols,
+                              const void *x_q8) {
+    shim_state st;
+    shim_save(&st);
+    GGUFTensor t;
+    memset(&t, 0, sizeof t);
+    t.n_dims = 2;
+    t.ne[0]  = n_cols;
+    t.ne[1]  = n_rows;
+    t.ne[2] = t.ne[3] = 1;
+    t.type   = type;
+    t.data   = w;
+    const size_t per256 = type == GGML_TYPE_Q4_0 ? 8u * sizeof(block_q4_0_t)
+                        : type == GGML_TYPE_Q8_0 ? 8u * sizeof(block_q8_0_t)
+                        : type == GGML_TYPE_Q5_K ? sizeof(block_q5_K_t)
+                        : type == GGML_TYPE_Q6_K ? sizeof(block_q6_K_t)
+                        : type == GGML_TYPE_IQ4_XS ? sizeof(block_iq4_xs_t) : sizeof(block_q4_K_t);
+    t.bytes = (size_t)n_rows * (n_cols / 256u) * per256;
+    lfm2_matmul_1x4_prequant_mt(NULL, out, &t, NULL, (const block_q8_K_t *)x_q8);
+    shim_restore(&st);
+}

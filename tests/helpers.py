@@ -147,3 +147,89 @@ def q6k_dequant(w, n_cols):
                 idx = base + 32 * k + l
                 out[:, idx] = d * sc[:, idx // 16] * (u - 32)
     return out.reshape(n_rows, n_cols)
+
+
+# -- Q4_0 / Q8_0 / Q5_K / IQ4_XS (GGML ids 2, 8, 13, 23) ------------------------
+Q_BYTES_256 = {2: 144, 8: 272, 12: 144, 13: 176, 14: 210, 23: 136}  # bytes per 256 weights
+IQ4NL_GRID = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+                      np.int64)
+
+
+def _fp16_bytes(rng, n, lo, hi):
+    return rng.uniform(lo, hi, size=n).astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+
+def q_random(rng, qtype, n_rows, n_cols):
+    """Random rows of a weight type: every quant bit random, scales fp16 in a
+    range that keeps products in the usual magnitude."""
+    if qtype == 12:
+        return q4k_random(rng, n_rows, n_cols)
+    if qtype == 14:
+        return q6k_random(rng, n_rows, n_cols)
+    nbytes = Q_BYTES_256[qtype] * (n_cols // 256)
+    w = rng.integers(0, 256, size=(n_rows, nbytes), dtype=np.uint8)
+    if qtype in (2, 8):
+        bs = 18 if qtype == 2 else 34
+        blk = w.reshape(-1, bs)
+        blk[:, 0:2] = _fp16_bytes(rng, blk.shape[0], 2.0 ** -9, 2.0 ** -5)
+    elif qtype == 13:
+        blk = w.reshape(-1, 176)
+        blk[:, 0:2] = _fp16_bytes(rng, blk.shape[0], 2.0 ** -10, 2.0 ** -6)
+        blk[:, 2:4] = _fp16_bytes(rng, blk.shape[0], 2.0 ** -10, 2.0 ** -6)
+    elif qtype == 23:
+        blk = w.reshape(-1, 136)
+        blk[:, 0:2] = _fp16_bytes(rng, blk.shape[0], 2.0 ** -12, 2.0 ** -8)
+    return w
+
+
+def q_dequant(w, qtype, n_cols):
+    """float64 [n_rows, n_cols] weights from the format definitions:
+    Q4_0 d*(nibble-8) (element l low nibble of qs[l], l+16 high nibble);
+    Q8_0 d*q; Q5_K d*sc*(q4 + 16*qh bit) - dmin*m (chunk c of 64: low
+    nibbles of qs[32c..] with qh bit 2c, high nibbles with bit 2c+1);
+    IQ4_XS d*(6-bit scale - 32)*grid[nibble]."""
+    if qtype == 12:
+        return q4k_dequant(w, n_cols)
+    if qtype == 14:
+        return q6k_dequant(w, n_cols)
+    n_rows = w.shape[0]
+    f16 = lambda a: a.copy().view(np.float16).astype(np.float64)[:, 0]
+    if qtype in (2, 8):
+        bs = 18 if qtype == 2 else 34
+        blk = w.reshape(-1, bs)
+        d = f16(blk[:, 0:2])
+        if qtype == 2:
+            qs = blk[:, 2:18].astype(np.int64)
+            q = np.concatenate([qs & 0xF, qs >> 4], axis=1) - 8
+        else:
+            q = blk[:, 2:34].copy().view(np.int8).astype(np.int64)
+        return (d[:, None] * q).reshape(n_rows, n_cols)
+    nb = n_cols // 256
+    if qtype == 13:
+        blk = w.reshape(n_rows * nb, 176)
+        d, dm = f16(blk[:, 0:2]), f16(blk[:, 2:4])
+        sc_bytes = blk[:, 4:16].astype(np.int64)
+        qh = blk[:, 16:48].astype(np.int64)
+        qs = blk[:, 48:176].astype(np.int64)
+        out = np.zeros((n_rows * nb, 256))
+        for j in range(8):
+            sc, m = _q4k_scale_min(sc_bytes, j)
+            c = j // 2
+            nib = (qs[:, 32 * c:32 * c + 32] & 0xF) if j % 2 == 0 else (qs[:, 32 * c:32 * c + 32] >> 4)
+            q = nib + 16 * ((qh >> j) & 1)
+            out[:, 32 * j:32 * j + 32] = (d * sc)[:, None] * q - (dm * m)[:, None]
+        return out.reshape(n_rows, n_cols)
+    if qtype == 23:
+        blk = w.reshape(n_rows * nb, 136)
+        d = f16(blk[:, 0:2])
+        sh = blk[:, 2:4].copy().view(np.uint16).astype(np.int64)[:, 0]
+        sl = blk[:, 4:8].astype(np.int64)
+        qs = blk[:, 8:136].astype(np.int64)
+        out = np.zeros((n_rows * nb, 256))
+        for ib in range(8):
+            ls = (((sl[:, ib >> 1] >> (4 * (ib & 1))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4)) - 32
+            sub = qs[:, 16 * ib:16 * ib + 16]
+            vals = np.concatenate([IQ4NL_GRID[sub & 0xF], IQ4NL_GRID[sub >> 4]], axis=1)
+            out[:, 32 * ib:32 * ib + 32] = (d * ls)[:, None] * vals
+        return out.reshape(n_rows, n_cols)
+    raise ValueError(qtype)

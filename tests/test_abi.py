@@ -178,11 +178,24 @@ def test_quant_matmul_validation_before_launch():
     assert mm(FAKE, FAKE, 4, 256, FAKE + 2, 1, None) == E_INVALID  # x_q8 not 4-byte aligned
 
 
+def test_matmul_prequant_validation_before_launch():
+    lib = la.load()
+    f = lib.lfm_hip_matmul_prequant
+    assert f(FAKE, FAKE, 12, 0, 2048, FAKE, 1, None) == 0           # nothing to do
+    assert f(None, FAKE, 12, 8, 2048, FAKE, 1, None) == E_INVALID
+    for t in (3, 6, 9, 10, 11, 15, 16, 20, 30):                       # no kernel for these types
+        assert f(FAKE, FAKE, t, 8, 2048, FAKE, 1, None) == E_UNSUPPORTED
+    assert f(FAKE, FAKE, 2, 8, 2000, FAKE, 1, None) == E_UNSUPPORTED  # n_cols % 256
+    assert f(FAKE, FAKE + 8, 13, 8, 2048, FAKE, 1, None) == E_INVALID  # Q5_K rows 16-byte aligned
+    assert f(FAKE, FAKE + 4, 23, 8, 2048, FAKE, 1, None) == E_INVALID  # IQ4_XS 8-byte aligned
+    assert f(FAKE, FAKE + 1, 8, 8, 2048, FAKE, 1, None) == E_INVALID   # Q8_0 2-byte aligned
+
+
 def test_qkv_fused_validation_before_launch():
     lib = la.load()
     f = lib.lfm_hip_gqa_qkv_fused
     t = (C.c_uint32 * 4)(12, 12, 14, 12)
-    bad = (C.c_uint32 * 4)(12, 12, 8, 12)  # Q8_0: no kernel here
+    bad = (C.c_uint32 * 4)(12, 12, 10, 12)  # Q2_K: no kernel here
     args = lambda types, cols=2048, wv=FAKE: (FAKE, FAKE, FAKE, None, FAKE, FAKE, wv, None, types, 8, 8, 8,
                                               4, cols, FAKE, 1, None)
     assert f(*args(None)) == E_INVALID

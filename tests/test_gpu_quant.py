@@ -8,7 +8,7 @@ the reference's fp32 order."""
 import numpy as np
 import pytest
 
-from helpers import parity, q4k_pattern, q4k_random, q6k_random
+from helpers import parity, q4k_pattern, q4k_random, q6k_random, q_random
 
 pytestmark = pytest.mark.gpu
 
@@ -149,3 +149,63 @@ def test_qkv_fused_lfm2_lfm3_shapes(gpu, orc, B, gate, v_type):
     for o, w, t in zip(outs, ws, types):
         want = orc.matmul_q(w, t, xq, n_cols)
         assert np.array_equal(o.numpy().view(np.uint32), want.view(np.uint32))
+
+
+OTHER_TYPES = {2: "Q4_0", 8: "Q8_0", 13: "Q5_K", 23: "IQ4_XS"}
+
+
+@pytest.mark.parametrize("qtype", sorted(OTHER_TYPES))
+@pytest.mark.parametrize("n_rows,n_cols,B", [(8, 256, 1), (2048, 2048, 1), (130, 2304, 5), (64, 2048, 64)])
+def test_other_types_bit_exact(gpu, orc, qtype, n_rows, n_cols, B):
+    """Q4_0, Q8_0, Q5_K and IQ4_XS rows through lfm_hip_matmul_prequant,
+    bit-exact against the oracle (pinned to the reference's AVX2 1x1 dots),
+    including a zero activation block."""
+    la = gpu
+    rng = np.random.default_rng(qtype * 1000 + n_rows + B)
+    w = q_random(rng, qtype, n_rows, n_cols)
+    x = rng.standard_normal((B, n_cols)).astype(np.float32)
+    if n_cols >= 512:
+        x[0, 256:512] = 0.0
+    xq = orc.quantize_q8_K(x)
+    out = la.DeviceArray.zeros((B, n_rows), np.float32)
+    la.matmul_prequant(out, dev(la, w), qtype, n_rows, n_cols, dev(la, xq), B)
+    want = orc.matmul_q(w, qtype, xq, n_cols)
+    assert np.array_equal(out.numpy().view(np.uint32), want.view(np.uint32)), OTHER_TYPES[qtype]
+
+
+def test_fused_mixed_types(gpu, orc):
+    """One fused call over four matrices of four different types (Q5_K Q,
+    IQ4_XS K, Q8_0 V, Q4_0 gate), three tokens."""
+    la = gpu
+    rng = np.random.default_rng(99)
+    n_cols, rows, types = 2048, [2048, 512, 512, 16], [13, 23, 8, 2]
+    ws = [q_random(rng, t, r, n_cols) for t, r in zip(types, rows)]
+    xq = orc.quantize_q8_K(rng.standard_normal((3, n_cols)).astype(np.float32))
+    outs = [la.DeviceArray.zeros((3, r), np.float32) for r in rows]
+    la.gqa_qkv_fused(outs, [dev(la, w) for w in ws], types, rows, n_cols, dev(la, xq), 3)
+    for o, w, t in zip(outs, ws, types):
+        assert np.array_equal(o.numpy().view(np.uint32), orc.matmul_q(w, t, xq, n_cols).view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [2, 8])
+def test_q4_0_q8_0_reference_patterns(gpu, orc, qtype):
+    """Weight patterns of tests/test_cpuid_quants.c:116-137 (Q4_0) and
+    tests/test_simd_kquants.c:118-121 (Q8_0)."""
+    la = gpu
+    n_cols, n_rows = 2048, 64
+    i = np.arange(n_rows * 64)[:, None]
+    if qtype == 2:
+        blk = np.zeros((n_rows * 64, 18), np.uint8)
+        blk[:, 0:2] = np.array([0x2E00], np.uint16).view(np.uint8)
+        blk[:, 2:] = ((i * 17 + np.arange(16)[None] * 31) & 0xFF).astype(np.uint8)
+        x = np.cos(np.arange(n_cols, dtype=np.float32) * np.float32(0.019)) * np.float32(1.5)
+    else:
+        blk = np.zeros((n_rows * 64, 34), np.uint8)
+        blk[:, 0:2] = np.array([0x3000], np.uint16).view(np.uint8)
+        blk[:, 2:] = (((i * 7 + np.arange(32)[None] * 3) % 127) - 63).astype(np.int8).view(np.uint8)
+        x = np.sin(np.arange(n_cols, dtype=np.float32) * np.float32(0.017)) * np.float32(1.5)
+    w = blk.reshape(n_rows, -1)
+    xq = orc.quantize_q8_K(x[None])
+    out = la.DeviceArray.zeros((1, n_rows), np.float32)
+    la.matmul_prequant(out, dev(la, w), qtype, n_rows, n_cols, dev(la, xq), 1)
+    assert np.array_equal(out.numpy().view(np.uint32), orc.matmul_q(w, qtype, xq, n_cols).view(np.uint32))

@@ -17,7 +17,8 @@ tests/test_cpuid_quants.c:69-112 of the reference."""
 import numpy as np
 import pytest
 
-from helpers import q4k_dequant, q4k_pattern, q4k_random, q6k_dequant, q6k_random, q8k_dequant
+from helpers import (q4k_dequant, q4k_pattern, q4k_random, q6k_dequant, q6k_random, q8k_dequant, q_dequant,
+                     q_random)
 
 
 def test_quantize_matches_reference_test_inputs(orc, ref):
@@ -164,3 +165,76 @@ def test_q6K_closed_form(orc):
     got = orc.matmul_q(w, 14, xq, 1024)
     assert np.all(np.abs(got - xd @ wd.T) <= 1e-5 * (np.abs(xd) @ np.abs(wd).T))
     assert np.array_equal(orc.matmul_q(q4k_random(rng, 8, 1024), 12, xq, 1024).shape, (3, 8))
+
+
+TYPES = {2: "Q4_0", 8: "Q8_0", 13: "Q5_K", 23: "IQ4_XS"}
+
+
+@pytest.mark.parametrize("qtype", sorted(TYPES))
+@pytest.mark.parametrize("seed", [0, 1])
+def test_other_types_dot_matches_reference(orc, ref, qtype, seed):
+    """Q4_0, Q8_0, Q5_K and IQ4_XS rows bit-exact against the reference's AVX2
+    1x1 kernels (lfm2_vec_dot_{q4_0,q8_0,q5_K,iq4_xs}_q8_K_avx2), random blocks
+    and a zero activation block."""
+    rng = np.random.default_rng(seed * 31 + qtype)
+    w = q_random(rng, qtype, 12, 2048)
+    x = rng.standard_normal((1, 2048)).astype(np.float32)
+    if seed == 1:
+        x[0, 512:768] = 0.0
+    xq = orc.quantize_q8_K(x)
+    for r in range(12):
+        got = orc.dot_type(w[r], qtype, xq[0], 2048)
+        want = ref.dot_type(w[r], qtype, xq[0], 2048)
+        assert np.float32(got).tobytes() == np.float32(want).tobytes(), (TYPES[qtype], r, got, want)
+
+
+@pytest.mark.parametrize("qtype", sorted(TYPES))
+def test_other_types_engine_projection(orc, ref, qtype):
+    """The engine's decode projection entry (lfm2_matmul_1x4_prequant_mt
+    through the CPU kernel table).  Its Q4_0 / Q8_0 1x4 kernels are four 1x1
+    calls, so they equal the oracle bit for bit; the Q5_K / IQ4_XS 1x4 kernels
+    fuse the per-block combination into FMAs on AVX-VNNI hosts
+    (tools/lfm2_cpuid_quants.c:1317-1394), so they agree within fp32 rounding."""
+    rng = np.random.default_rng(qtype)
+    w = q_random(rng, qtype, 66, 1536)
+    xq = orc.quantize_q8_K(rng.standard_normal((1, 1536)).astype(np.float32))
+    got = orc.matmul_q(w, qtype, xq, 1536)
+    want = ref.matmul_prequant_type(w, qtype, xq, 1536)
+    if qtype in (2, 8):
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:
+        assert np.abs(got - want).max() <= 2e-6 * np.abs(want).max()
+
+
+@pytest.mark.parametrize("qtype", sorted(TYPES))
+def test_other_types_closed_form(orc, qtype):
+    """float64 dequantized weights x dequantized activations (format
+    definitions in helpers.q_dequant), within fp32 rounding."""
+    rng = np.random.default_rng(100 + qtype)
+    w = q_random(rng, qtype, 20, 1024)
+    xq = orc.quantize_q8_K(rng.standard_normal((2, 1024)).astype(np.float32))
+    xd, _ = q8k_dequant(xq, 1024)
+    wd = q_dequant(w, qtype, 1024)
+    got = orc.matmul_q(w, qtype, xq, 1024)
+    assert np.all(np.abs(got - xd @ wd.T) <= 1e-5 * (np.abs(xd) @ np.abs(wd).T) + 1e-30)
+
+
+def test_reference_test_patterns_q4_0_q8_0(orc, ref):
+    """Weights of tests/test_cpuid_quants.c:116-137 (Q4_0: d 0x2E00, qs
+    (i*17 + j*31) & 0xFF) and tests/test_simd_kquants.c:118-121 (Q8_0: d
+    0x3000, qs (i*7 + j*3) % 127 - 63), activations as there."""
+    n_cols = 2048
+    i = np.arange(16 * 64)[:, None]
+    q40 = np.zeros((16 * 64, 18), np.uint8)
+    q40[:, 0:2] = np.array([0x2E00], np.uint16).view(np.uint8)
+    q40[:, 2:] = ((i * 17 + np.arange(16)[None] * 31) & 0xFF).astype(np.uint8)
+    q80 = np.zeros((16 * 64, 34), np.uint8)
+    q80[:, 0:2] = np.array([0x3000], np.uint16).view(np.uint8)
+    q80[:, 2:] = (((i * 7 + np.arange(32)[None] * 3) % 127) - 63).astype(np.int8).view(np.uint8)
+    xs = {2: np.cos(np.arange(n_cols, dtype=np.float32) * np.float32(0.019)) * np.float32(1.5),
+          8: np.sin(np.arange(n_cols, dtype=np.float32) * np.float32(0.017)) * np.float32(1.5)}
+    for qtype, w in ((2, q40.reshape(16, -1)), (8, q80.reshape(16, -1))):
+        xq = ref.quantize_q8_K(xs[qtype][None])
+        for r in range(16):
+            assert (np.float32(orc.dot_type(w[r], qtype, xq[0], n_cols)).tobytes() ==
+                    np.float32(ref.dot_type(w[r], qtype, xq[0], n_cols)).tobytes())
