@@ -216,18 +216,33 @@ class FusedQkvWorkload:
         self.i = (self.i + 1) % len(self.w)
 
 
-class QuantProjWorkload:
-    """A Q4_K projection beside the attention path: LFM2-1.2B `wo`
-    (2048 x 2048) applied to n_tokens Q8_K tokens.  Each step reads a
-    different copy of the weights, so the weights (not the 256 MB last-level
-    cache) are streamed from HBM as at decode, where a step reads every
-    layer's weights once."""
+# bytes per 256 weights and the offsets of fp16 scale fields within each block
+Q_LAYOUT = {2: (144, 18, (0,)), 8: (272, 34, (0,)), 12: (144, 144, (0, 2)), 13: (176, 176, (0, 2)),
+            14: (210, 210, (208,)), 23: (136, 136, (0,))}
 
-    def __init__(self, la, rng, n_rows=2048, n_cols=2048, n_tokens=1, copies=120):
+
+def random_q_rows(rng, qtype, n_rows, n_cols):
+    """Random weight rows of a GGML type with small finite fp16 scales."""
+    per256, blk, scale_offs = Q_LAYOUT[qtype]
+    w = rng.integers(0, 256, size=(n_rows, n_cols // 256 * per256), dtype=np.uint8)
+    b = w.reshape(-1, blk)
+    for o in scale_offs:
+        b[:, o:o + 2] = np.array([0x2000], np.uint16).view(np.uint8)
+    return w
+
+
+class QuantProjWorkload:
+    """A quantized projection beside the attention path: LFM2-1.2B `wo`
+    (2048 x 2048) applied to n_tokens Q8_K tokens, weights of GGML type qtype
+    (Q4_K by default).  Each step reads a different copy of the weights, so
+    the weights (not the 256 MB last-level cache) are streamed from HBM as at
+    decode, where a step reads every layer's weights once."""
+
+    def __init__(self, la, rng, n_rows=2048, n_cols=2048, n_tokens=1, copies=120, qtype=12):
         self.la, self.n_rows, self.n_cols, self.n_tokens = la, n_rows, n_cols, n_tokens
+        self.qtype = qtype
         nb = n_cols // 256
-        w = rng.integers(0, 256, size=(n_rows, nb * 144), dtype=np.uint8)
-        w.reshape(-1, 144)[:, 0:4] = np.array([0x2400, 0x2000], np.uint16).view(np.uint8)  # d, dmin
+        w = random_q_rows(rng, qtype, n_rows, n_cols)
         self.w = [la.DeviceArray.from_numpy(w) for _ in range(copies)]
         x = rng.standard_normal((n_tokens, n_cols)).astype(np.float32)
         xd = la.DeviceArray.from_numpy(x)
@@ -235,10 +250,11 @@ class QuantProjWorkload:
         la.quantize_q8_K(xd, self.xq, n_tokens, n_cols)
         self.out = la.DeviceArray.zeros((n_tokens, n_rows), np.float32)
         self.i = 0
-        self.bytes = n_rows * nb * 144 + n_tokens * nb * 292 + n_tokens * n_rows * 4
+        self.bytes = w.nbytes + n_tokens * nb * 292 + n_tokens * n_rows * 4
 
     def step(self):
-        self.la.matmul_q4_K(self.out, self.w[self.i], self.n_rows, self.n_cols, self.xq, self.n_tokens)
+        self.la.matmul_prequant(self.out, self.w[self.i], self.qtype, self.n_rows, self.n_cols, self.xq,
+                                self.n_tokens)
         self.i = (self.i + 1) % len(self.w)
 
 
@@ -477,6 +493,16 @@ def main():
                 bytes=qp.bytes, pct_hbm_peak=round(100 * qp.bytes / (qms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
             log(f"wo q4_K tokens {n_tok}: {qms * 1e3:.2f} us/step")
             del qp
+        names = {2: "q4_0", 8: "q8_0", 13: "q5K", 14: "q6K", 23: "iq4xs"}
+        types = {}
+        for qtype in (2, 8, 13, 14, 23):
+            qp = QuantProjWorkload(la, rng, n_tokens=1, qtype=qtype)
+            qms = time_steps(hip, qp, max(20, args.steps), 5)
+            types[names[qtype]] = dict(us_per_step=round(qms * 1e3, 2), bytes=qp.bytes,
+                                       GBps=round(qp.bytes / (qms * 1e-3) / 1e9, 1))
+            del qp
+        secondary["wo_other_types_lfm2_1p2b_2048x2048_tokens1"] = types
+        log("wo other types tokens 1: " + ", ".join(f"{k} {v['us_per_step']} us" for k, v in types.items()))
         fq = FusedQkvWorkload(la, rng)
         fms = time_steps(hip, fq, max(20, args.steps), 5)
         secondary["qkv_fused_q4K_q6K_lfm2_1p2b_tokens1"] = dict(
