@@ -399,12 +399,13 @@ template <> struct QType<8> {
     }
 };
 
-/* Up to four matrices over the same activations (Q, K, V, gate); waves
- * [wave0[m], wave0[m+1]) cover matrix m, RPW rows each. */
+/* Up to four matrices over the same activations (Q, K, V, gate), each of its
+ * own GGML type; waves [wave0[m], wave0[m+1]) cover matrix m, RPW rows each. */
 struct MatSet {
     const uint8_t *w[4];
     float *out[4];
     uint32_t rows[4];
+    uint32_t type[4];
     uint32_t wave0[5];
     uint32_t n;
 };
@@ -416,22 +417,14 @@ struct MatSet {
  * RPW x TCH partials, sums them over its lane group, and adds the
  * super-blocks' terms to the row sums in order. */
 template <int TYPE, int RPW, int TCH>
-__global__ __launch_bounds__(256) void k_matmul_q(const MatSet S, const uint8_t *__restrict__ xq, uint32_t nb,
-                                                  uint32_t n_tokens) {
+__device__ __forceinline__ void matmul_rows(const uint8_t *__restrict__ w, float *__restrict__ out, uint32_t n_rows,
+                                            uint32_t r0, const uint8_t *__restrict__ xq, uint32_t nb,
+                                            uint32_t n_tokens, uint32_t t0) {
     using Q = QType<TYPE>;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wv   = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (wv >= S.wave0[S.n]) return;
-    uint32_t m = 0;
-    while (m + 1u < S.n && wv >= S.wave0[m + 1u]) ++m;
-    const uint32_t n_rows = S.rows[m];
-    const uint32_t r0     = (wv - S.wave0[m]) * RPW;
-    const uint8_t *w      = S.w[m];
-    float *out            = S.out[m];
     const uint32_t p = lane & 7u; /* part within the super-block    */
     const uint32_t g = lane >> 3; /* super-block slot of this step  */
     const size_t row_bytes = (size_t)nb * Q::kBytes;
-    const uint32_t t0      = blockIdx.y * TCH;
 
     float sumf[TCH][RPW];
 #pragma unroll
@@ -500,6 +493,32 @@ __global__ __launch_bounds__(256) void k_matmul_q(const MatSet S, const uint8_t 
                 out[(size_t)(t0 + tt) * n_rows + r0 + r] = sumf[tt][r];
 }
 
+/* one launch over every matrix of the set.  TYPE > 0: all matrices of that
+ * type; TYPE == 0: each wave takes its matrix's type (a wave-uniform branch;
+ * the kernel then needs the registers of the widest type, so sets of one
+ * type take the specialised form) */
+template <int TYPE, int RPW, int TCH>
+__global__ __launch_bounds__(256) void k_matmul_q(const MatSet S, const uint8_t *__restrict__ xq, uint32_t nb,
+                                                  uint32_t n_tokens) {
+    const uint32_t wv = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (wv >= S.wave0[S.n]) return;
+    uint32_t m = 0;
+    while (m + 1u < S.n && wv >= S.wave0[m + 1u]) ++m;
+    const uint32_t r0 = (wv - S.wave0[m]) * RPW, t0 = blockIdx.y * TCH;
+    if constexpr (TYPE != 0) {
+        matmul_rows<TYPE, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0);
+        return;
+    }
+    switch (S.type[m]) {
+    case 12u: matmul_rows<12, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0); break;
+    case 14u: matmul_rows<14, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0); break;
+    case 13u: matmul_rows<13, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0); break;
+    case 23u: matmul_rows<23, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0); break;
+    case 2u: matmul_rows<2, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0); break;
+    default: matmul_rows<8, RPW, TCH>(S.w[m], S.out[m], S.rows[m], r0, xq, nb, n_tokens, t0); break;
+    }
+}
+
 template <int TYPE, int RPW, int TCH>
 hipError_t launch_set(MatSet S, const void *x_q8, uint32_t nb, uint32_t n_tokens, hipStream_t stream) {
     S.wave0[0] = 0;
@@ -513,7 +532,7 @@ hipError_t launch_set(MatSet S, const void *x_q8, uint32_t nb, uint32_t n_tokens
 /* one token: a row per wave (most waves in flight); more: two rows and up to
  * eight tokens per wave share each weight and activation load */
 template <int TYPE>
-hipError_t launch_type(const MatSet &S, const void *x_q8, uint32_t nb, uint32_t n_tokens, hipStream_t stream) {
+hipError_t launch_tokens(const MatSet &S, const void *x_q8, uint32_t nb, uint32_t n_tokens, hipStream_t stream) {
     if (n_tokens == 1u) return launch_set<TYPE, 1, 1>(S, x_q8, nb, n_tokens, stream);
     if (n_tokens == 2u) return launch_set<TYPE, 2, 2>(S, x_q8, nb, n_tokens, stream);
     if (n_tokens <= 4u) return launch_set<TYPE, 2, 4>(S, x_q8, nb, n_tokens, stream);
@@ -535,29 +554,30 @@ int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, 
                     const uint32_t *rows, uint32_t n_cols, const void *x_q8, uint32_t n_tokens, hipStream_t stream) {
     if (n_tokens == 0u) return LFM_ATTN_OK;
     const uint32_t nb = n_cols / 256u;
-    /* one launch per weight type present, each over its matrices */
-    for (uint32_t type : {12u, 14u, 13u, 23u, 2u, 8u}) {
-        MatSet S{};
-        for (uint32_t m = 0; m < n_mats; ++m) {
-            if (types[m] != type || rows[m] == 0u) continue;
-            S.w[S.n]    = static_cast<const uint8_t *>(ws[m]);
-            S.out[S.n]  = outs[m];
-            S.rows[S.n] = rows[m];
-            ++S.n;
-        }
-        if (S.n == 0u) continue;
-        hipError_t e;
-        switch (type) {
-        case 12u: e = launch_type<12>(S, x_q8, nb, n_tokens, stream); break;
-        case 14u: e = launch_type<14>(S, x_q8, nb, n_tokens, stream); break;
-        case 13u: e = launch_type<13>(S, x_q8, nb, n_tokens, stream); break;
-        case 23u: e = launch_type<23>(S, x_q8, nb, n_tokens, stream); break;
-        case 2u: e = launch_type<2>(S, x_q8, nb, n_tokens, stream); break;
-        default: e = launch_type<8>(S, x_q8, nb, n_tokens, stream); break;
-        }
-        if (e != hipSuccess) return hip_status(e);
+    /* one launch over all matrices, whatever their types */
+    MatSet S{};
+    for (uint32_t m = 0; m < n_mats && m < 4u; ++m) {
+        if (rows[m] == 0u) continue;
+        S.w[S.n]    = static_cast<const uint8_t *>(ws[m]);
+        S.out[S.n]  = outs[m];
+        S.rows[S.n] = rows[m];
+        S.type[S.n] = types[m];
+        ++S.n;
     }
-    return LFM_ATTN_OK;
+    if (S.n == 0u) return LFM_ATTN_OK;
+    bool one_type = true;
+    for (uint32_t m = 1; m < S.n; ++m) one_type = one_type && S.type[m] == S.type[0];
+    hipError_t e;
+    switch (one_type ? S.type[0] : 0u) {
+    case 12u: e = launch_tokens<12>(S, x_q8, nb, n_tokens, stream); break;
+    case 14u: e = launch_tokens<14>(S, x_q8, nb, n_tokens, stream); break;
+    case 13u: e = launch_tokens<13>(S, x_q8, nb, n_tokens, stream); break;
+    case 23u: e = launch_tokens<23>(S, x_q8, nb, n_tokens, stream); break;
+    case 2u: e = launch_tokens<2>(S, x_q8, nb, n_tokens, stream); break;
+    case 8u: e = launch_tokens<8>(S, x_q8, nb, n_tokens, stream); break;
+    default: e = launch_tokens<0>(S, x_q8, nb, n_tokens, stream); break;
+    }
+    return hip_status(e);
 }
 
 } // namespace lfm
