@@ -399,6 +399,53 @@ def cpu_prompt_cache(rng, n_tokens=4096, reps=3):
                 cores=1, kind=kind, sample=f"LFM2-1.2B session at {n_tokens} tokens, median of {reps}")
 
 
+def cpu_rows(rng, n_threads):
+    """The reference's CPU path for the other measured rows, on bounded
+    samples (oracle/_ref; skipped when the reference build is absent):
+    config-4 prefill attention rows, LFM2 attention-sink eviction, the Q4_K
+    `wo` projection."""
+    from oracle.bindings import Reference
+
+    if not Reference.available():
+        return {}
+    ref = Reference()
+    rows = {}
+    # prefill: 16 rows of config 4 (32q/8kv, d64) spread over positions 255 .. 4095
+    n_tok, nq, nkv = 4096, 32, 8
+    k16 = (rng.standard_normal((n_tok, nkv * 64)) * 0.5).astype(np.float16).view(np.uint16)
+    v16 = (rng.standard_normal((n_tok, nkv * 64)) * 0.5).astype(np.float16).view(np.uint16)
+    pos = np.arange(255, n_tok, 256, dtype=np.uint32)
+    q = (rng.standard_normal((pos.size, nq * 64)) * 0.5).astype(np.float16).astype(np.float32)
+    dt, used, _ = ref.time_prefill_rows(q, k16, v16, pos, nq, nq // nkv, nkv * 64, n_tok, n_threads, 2)
+    flops = float(sum(4 * 64 * nq * (int(p) + 1) for p in pos))
+    rows["prefill_cfg4_rows"] = dict(TFLOPs=round(flops / dt / 1e12, 4), cores=used, kind="reference",
+                                     sample=f"{pos.size} rows at positions 255..4095 of config 4, "
+                                            f"lfm2_gqa_heads_worker_task per row, {dt * 1e3:.1f} ms")
+    # sink eviction: 6 layers x 8 KV heads x d64, max_seq 8192, position 8184, 64 sinks
+    max_seq, n_layers, pos0, n_sink = 8192, 6, 8184, 64
+    lut = ref.rope_lut_lfm2(max_seq, 64, 1e6)
+    kc = [(rng.standard_normal((max_seq, 512)) * 0.5).astype(np.float16).view(np.uint16) for _ in range(n_layers)]
+    vc = [(rng.standard_normal((max_seq, 512)) * 0.5).astype(np.float16).view(np.uint16) for _ in range(n_layers)]
+    t = time.perf_counter()
+    ref.kv_shift_sinks_lfm2(kc, vc, [8] * n_layers, 64, lut, pos0, n_sink, max_seq // 2)
+    dt = time.perf_counter() - t
+    moved = 4 * n_layers * (pos0 - n_sink - max_seq // 2) * 512 * 2
+    rows["kv_shift_sinks_lfm2"] = dict(GBps=round(moved / dt / 1e9, 2), cores=1, kind="reference",
+                                       sample=f"6 layers, max_seq {max_seq} at position {pos0}, {dt * 1e3:.1f} ms")
+    # `wo`: Q4_K 2048 x 2048, one token, the engine's decode projection without a pool
+    w = rng.integers(0, 256, size=(2048, 8 * 144), dtype=np.uint8)
+    w.reshape(-1, 144)[:, 0:4] = np.array([0x2400, 0x2000], np.uint16).view(np.uint8)
+    xq = ref.quantize_q8_K(rng.standard_normal((1, 2048)).astype(np.float32))
+    ref.matmul_q4_K_prequant(w, xq, 2048)
+    t = time.perf_counter()
+    for _ in range(20):
+        ref.matmul_q4_K_prequant(w, xq, 2048)
+    dt = (time.perf_counter() - t) / 20
+    rows["wo_q4K_q8K_tokens1"] = dict(us=round(dt * 1e6, 1), GBps=round(w.nbytes / dt / 1e9, 2), cores=1,
+                                      kind="reference", sample="2048 x 2048 Q4_K, lfm2_matmul_1x4_prequant_mt")
+    return rows
+
+
 def run_prefill(hip, la, rng, steps):
     pf = PrefillWorkload(la, rng)
     n = max(5, steps // 5)
@@ -523,6 +570,7 @@ def main():
         cpu, cpu_out = cpu_baseline(head, n_thr)
         if not args.quick:
             cpu["rows"] = {"lfmcache_save_load_lfm2_1p2b_n4096": cpu_prompt_cache(rng)}
+            cpu["rows"].update(cpu_rows(rng, n_thr))
         g = gpu_out[:cpu_out.shape[0], 0]
         parity = dict(max_abs=float(np.abs(g - cpu_out).max()),
                       rel_l2=float(np.linalg.norm(g - cpu_out) / np.linalg.norm(cpu_out)),

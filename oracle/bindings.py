@@ -685,3 +685,23 @@ _wrap_init(Reference, _ref_types_init)
 Oracle.dot_type = _orc_dot_type
 Reference.dot_type = _ref_dot_type
 Reference.matmul_prequant_type = _ref_matmul_type
+
+
+def _ref_time_prefill_rows(self, q_rows, k16, v16, pos, n_head_q, kv_mul, kv_dim, max_seq, n_threads, reps=1):
+    """Best-of-reps seconds of the reference's per-row prefill attention
+    dispatch (lfm2_gqa_heads_worker_task over the heads) for the given rows."""
+    q = np.ascontiguousarray(q_rows, np.float32)
+    pos = np.ascontiguousarray(pos, np.uint32)
+    out = np.zeros((pos.size, n_head_q * 64), np.float32)
+    used = _u32(0)
+    L = self.lib
+    L.ref_time_prefill_rows.restype = C.c_double
+    L.ref_time_prefill_rows.argtypes = [_f32p, _u16p, _u16p, _u32p, _f32p, _u32, _u32, _u32, _u32, _u32, _u32,
+                                        _u32, C.POINTER(_u32)]
+    dt = L.ref_time_prefill_rows(q.reshape(-1), np.ascontiguousarray(k16, np.uint16).reshape(-1),
+                                 np.ascontiguousarray(v16, np.uint16).reshape(-1), pos, out, pos.size,
+                                 n_head_q, kv_mul, kv_dim, max_seq, n_threads, reps, C.byref(used))
+    return dt, int(used.value), out
+
+
+Reference.time_prefill_rows = _ref_time_prefill_rows

@@ -519,3 +519,37 @@ void ref_matmul_prequant_type(float *out, const void *w, uint32_t type, uint32_t
     lfm2_matmul_1x4_prequant_mt(NULL, out, &t, NULL, (const block_q8_K_t *)x_q8);
     shim_restore(&st);
 }
+
+/* ---- CPU timing of the batched-prefill attention (baseline only) -------------- */
+/* lfm2_forward_gqa_batch's per-row dispatch (tools/lfm2_prefill_batch.c:1074-1091):
+ * GQAAttnTaskCtx + lfm2_gqa_heads_worker_task over the query heads, fp16
+ * caches, for n_rows rows at positions pos[] with their q rows (fp32); the
+ * pool is created once.  Returns the best of reps passes in seconds. */
+double ref_time_prefill_rows(const float *q, const uint16_t *k16, const uint16_t *v16, const uint32_t *pos,
+                             float *out, uint32_t n_rows, uint32_t n_head_q, uint32_t kv_mul, uint32_t kv_dim,
+                             uint32_t max_seq, uint32_t n_threads, uint32_t reps, uint32_t *threads_out) {
+    shim_state st;
+    shim_save(&st);
+    LFM2ThreadPool pool;
+    lfm2_threadpool_init(&pool, n_threads);
+    if (threads_out) *threads_out = pool.n_threads;
+    float *att  = (float *)calloc((size_t)n_head_q * max_seq, sizeof(float));
+    double best = 1e30;
+    for (uint32_t r = 0; r < reps && att; ++r) {
+        const double t0 = shim_now();
+        for (uint32_t i = 0; i < n_rows; ++i) {
+            GQAAttnTaskCtx ctx = {
+                .pool = &pool, .q = q + (size_t)i * n_head_q * 64u, .k_cache = NULL, .v_cache = NULL,
+                .k_cache_f16 = k16, .v_cache_f16 = v16, .att = att, .xb = out + (size_t)i * n_head_q * 64u,
+                .n_head_q = n_head_q, .kv_mul = kv_mul, .head_dim = 64u, .kv_dim = kv_dim,
+                .max_seq_len = max_seq, .pos = pos[i], .scale = 1.0f / sqrtf(64.0f)};
+            lfm2_parallel_for(&pool, n_head_q, 1, lfm2_gqa_heads_worker_task, &ctx);
+        }
+        const double dt = shim_now() - t0;
+        if (dt < best) best = dt;
+    }
+    free(att);
+    lfm2_threadpool_free(&pool);
+    shim_restore(&st);
+    return best;
+}
