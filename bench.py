@@ -410,19 +410,19 @@ def cpu_rows(rng, n_threads):
         return {}
     ref = Reference()
     rows = {}
-    # prefill: 16 rows of config 4 (32q/8kv, d64) spread over positions 255 .. 4095
+    # prefill: 64 rows of config 4 (32q/8kv, d64) spread over positions 63 .. 4095
     n_tok, nq, nkv = 4096, 32, 8
     k16 = (rng.standard_normal((n_tok, nkv * 64)) * 0.5).astype(np.float16).view(np.uint16)
     v16 = (rng.standard_normal((n_tok, nkv * 64)) * 0.5).astype(np.float16).view(np.uint16)
-    pos = np.arange(255, n_tok, 256, dtype=np.uint32)
+    pos = np.arange(63, n_tok, 64, dtype=np.uint32)
     q = (rng.standard_normal((pos.size, nq * 64)) * 0.5).astype(np.float16).astype(np.float32)
-    dt, used, _ = ref.time_prefill_rows(q, k16, v16, pos, nq, nq // nkv, nkv * 64, n_tok, n_threads, 2)
+    dt, used, _ = ref.time_prefill_rows(q, k16, v16, pos, nq, nq // nkv, nkv * 64, n_tok, n_threads, 3)
     flops = float(sum(4 * 64 * nq * (int(p) + 1) for p in pos))
     rows["prefill_cfg4_rows"] = dict(TFLOPs=round(flops / dt / 1e12, 4), cores=used, kind="reference",
-                                     sample=f"{pos.size} rows at positions 255..4095 of config 4, "
+                                     sample=f"{pos.size} rows at positions 63..4095 of config 4, "
                                             f"lfm2_gqa_heads_worker_task per row, {dt * 1e3:.1f} ms")
-    # sink eviction: 6 layers x 8 KV heads x d64, max_seq 8192, position 8184, 64 sinks
-    max_seq, n_layers, pos0, n_sink = 8192, 6, 8184, 64
+    # sink eviction: 6 layers x 8 KV heads x d64, max_seq 16384, position 16376, 64 sinks
+    max_seq, n_layers, pos0, n_sink = 16384, 6, 16376, 64
     lut = ref.rope_lut_lfm2(max_seq, 64, 1e6)
     kc = [(rng.standard_normal((max_seq, 512)) * 0.5).astype(np.float16).view(np.uint16) for _ in range(n_layers)]
     vc = [(rng.standard_normal((max_seq, 512)) * 0.5).astype(np.float16).view(np.uint16) for _ in range(n_layers)]
