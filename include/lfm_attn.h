@@ -346,6 +346,18 @@ int lfm_attn_ctx_forward(lfm_attn_ctx *ctx, uint32_t layer, uint32_t pos_0, uint
  * cache and host memory (fp16 bits, [slot][n_head_kv][head_dim]) -- the data
  * a checkpoint or .lfmcache file stores (tools/lfm2_moe_checkpoint.c:472-560,
  * tools/lfm2_sys_cache.c:504-799).  Round trips are bit-exact. */
+/* Prompt prefill of one attention layer: n_rows tokens at positions
+ * pos_0 .. pos_0 + n_rows - 1, q/k/v/gate/out as in lfm_attn_ctx_forward
+ * with n_rows rows (any count).  lfm2_forward_batch runs a prompt through
+ * the layer LFM2_MAX_BATCH tokens at a time (tools/lfm2_prefill_batch.c:
+ * 1129-1199, attention :1029-1092); here a full-attention layer of head_dim
+ * 64 without a gate takes the whole prompt in one MFMA prefill (prologue,
+ * then every row attends keys 0 .. its position), and other layers run the
+ * step over chunks of 8 rows.  Synchronous; LFM_ATTN_E_RANGE past max_seq. */
+int lfm_attn_ctx_prefill(lfm_attn_ctx *ctx, uint32_t layer, uint32_t pos_0, uint32_t n_rows,
+                         const float *q, const float *k, const float *v, const float *gate_logits,
+                         float *out);
+
 int lfm_attn_ctx_kv_export(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uint32_t n_slots,
                            uint16_t *k_host, uint16_t *v_host);
 int lfm_attn_ctx_kv_import(lfm_attn_ctx *ctx, uint32_t layer, uint32_t slot, uint32_t n_slots,

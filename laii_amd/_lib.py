@@ -91,6 +91,7 @@ SIGNATURES.update({
     "lfm_attn_ctx_destroy": (None, [_vp]),
     "lfm_attn_ctx_set_norms": (_int, [_vp, _u32, _vp, _vp]),
     "lfm_attn_ctx_forward": (_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _vp]),
+    "lfm_attn_ctx_prefill": (_int, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp, _vp]),
     "lfm_attn_ctx_kv_export": (_int, [_vp, _u32, _u32, _u32, _vp, _vp]),
     "lfm_attn_ctx_kv_import": (_int, [_vp, _u32, _u32, _u32, _vp, _vp]),
     "lfm_attn_ctx_kv_device": (_int, [_vp, _u32, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_u32)]),

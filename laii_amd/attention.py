@@ -361,6 +361,19 @@ class EngineContext:
                                           out.ctypes.data), "lfm_attn_ctx_forward")
         return out
 
+    def prefill(self, layer, pos_0, q, k, v, gate_logits=None):
+        """Prompt rows pos_0 .. pos_0 + n - 1 of one layer (lfm_attn_ctx_prefill)."""
+        q = np.ascontiguousarray(q, np.float32)
+        n = q.size // (self.n_head_q * self.head_dim)
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        g = None if gate_logits is None else np.ascontiguousarray(gate_logits, np.float32)
+        out = np.empty(n * self.n_head_q * self.head_dim, np.float32)
+        check(load().lfm_attn_ctx_prefill(self.h, layer, pos_0, n, q.ctypes.data, k.ctypes.data, v.ctypes.data,
+                                          None if g is None else g.ctypes.data, out.ctypes.data),
+              "lfm_attn_ctx_prefill")
+        return out
+
     def kv_export(self, layer, slot, n_slots):
         row = self.n_head_kv * self.head_dim
         kh = np.empty((n_slots, row), np.uint16)

@@ -34,6 +34,9 @@ struct lfm_attn_ctx {
     unsigned char *stage_host;  /* pinned: q | k | v | gate | pos | out */
     unsigned char *stage_dev;
     size_t off_k, off_v, off_g, off_pos, off_out, stage_in_bytes, out_bytes;
+    unsigned char *pf_host;     /* pinned: prefill q | k | v | pos in, out (grown on demand) */
+    unsigned char *pf_dev;      /* device: the same plus fp16 q */
+    size_t pf_host_bytes, pf_dev_bytes;
     unsigned char *file_host;   /* pinned: a whole .lfmcache file (grown on demand) */
     unsigned char *file_dev;    /* its payload in device memory */
     size_t file_host_bytes, file_dev_bytes;
@@ -65,6 +68,8 @@ void lfm_attn_ctx_destroy(lfm_attn_ctx *c) {
     if (c->stage_host) (void)hipHostFree(c->stage_host);
     (void)hipFree(c->file_dev);
     if (c->file_host) (void)hipHostFree(c->file_host);
+    (void)hipFree(c->pf_dev);
+    if (c->pf_host) (void)hipHostFree(c->pf_host);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     free(c->is_swa);
     free(c->slots);
@@ -242,6 +247,81 @@ int lfm_attn_ctx_forward(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
                               hipMemcpyDeviceToHost, c->stream));
     if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
     if (st == LFM_ATTN_OK) memcpy(out, h + c->off_out, qn * sizeof(float));
+    return st;
+}
+
+/* Prompt prefill of one layer.  Full-attention layers of head_dim 64 with
+ * no gate run the prologue over all rows and the MFMA prefill kernel
+ * (every row attends keys 0 .. its position, causal by write order, as
+ * lfm2_forward_gqa_batch does in chunks of LFM2_MAX_BATCH); other layers
+ * (sliding window, head_dim 128, gated) go through the step in chunks of
+ * LFM_CTX_MAX_ROWS rows, as the reference does. */
+int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32_t n_rows, const float *q,
+                         const float *k, const float *v, const float *gate_logits, float *out) {
+    if (!c || !q || !k || !v || !out || layer >= c->g.n_layers || n_rows == 0u) return LFM_ATTN_E_INVALID;
+    const lfm_attn_geom *g = &c->g;
+    if ((uint64_t)pos_0 + n_rows > g->max_seq) return LFM_ATTN_E_RANGE;
+    const uint32_t kv_mul = g->n_head_q / g->n_head_kv;
+    const size_t qrow = (size_t)g->n_head_q * g->head_dim, krow = (size_t)g->n_head_kv * g->head_dim;
+    const int fast = !c->is_swa[layer] && !gate_logits && g->head_dim == 64u && kv_mul >= 1u &&
+                     kv_mul <= 16u && (256u % kv_mul) == 0u && n_rows > LFM_CTX_MAX_ROWS;
+    if (!fast) {
+        for (uint32_t r = 0; r < n_rows; r += LFM_CTX_MAX_ROWS) {
+            const uint32_t b = n_rows - r < LFM_CTX_MAX_ROWS ? n_rows - r : LFM_CTX_MAX_ROWS;
+            const int st = lfm_attn_ctx_forward(c, layer, pos_0 + r, b, q + r * qrow, k + r * krow, v + r * krow,
+                                                gate_logits ? gate_logits + (size_t)r * g->n_head_q : NULL,
+                                                out + r * qrow);
+            if (st != LFM_ATTN_OK) return st;
+        }
+        return LFM_ATTN_OK;
+    }
+    /* device layout: q f32 | k f32 | v f32 | pos | q f16 | out f32 (256-B aligned parts) */
+    const size_t qb = align256((size_t)n_rows * qrow * sizeof(float));
+    const size_t kb = align256((size_t)n_rows * krow * sizeof(float));
+    const size_t pb = 256u, hb = align256((size_t)n_rows * qrow * sizeof(uint16_t));
+    const size_t in_bytes = qb + 2u * kb + pb, dev_bytes = in_bytes + hb + qb;
+    int st = LFM_ATTN_OK;
+    if (c->pf_host_bytes < in_bytes + qb) {
+        if (c->pf_host) (void)hipHostFree(c->pf_host);
+        c->pf_host = NULL;
+        c->pf_host_bytes = 0;
+        st = st_of(hipHostMalloc((void **)&c->pf_host, in_bytes + qb, hipHostMallocDefault));
+        if (st != LFM_ATTN_OK) return st;
+        c->pf_host_bytes = in_bytes + qb;
+    }
+    if (c->pf_dev_bytes < dev_bytes) {
+        (void)hipFree(c->pf_dev);
+        c->pf_dev = NULL;
+        c->pf_dev_bytes = 0;
+        st = st_of(hipMalloc((void **)&c->pf_dev, dev_bytes));
+        if (st != LFM_ATTN_OK) return st;
+        c->pf_dev_bytes = dev_bytes;
+    }
+    unsigned char *h = c->pf_host, *d = c->pf_dev;
+    memcpy(h, q, (size_t)n_rows * qrow * sizeof(float));
+    memcpy(h + qb, k, (size_t)n_rows * krow * sizeof(float));
+    memcpy(h + qb + kb, v, (size_t)n_rows * krow * sizeof(float));
+    memcpy(h + qb + 2u * kb, &pos_0, sizeof pos_0);
+    st = st_of(hipMemcpyAsync(d, h, in_bytes, hipMemcpyHostToDevice, c->stream));
+    if (st != LFM_ATTN_OK) return st;
+    float *qd        = (float *)d;
+    uint16_t *q16    = (uint16_t *)(d + in_bytes);
+    float *od        = (float *)(d + in_bytes + hb);
+    uint16_t *kcache = c->k_cache[layer], *vcache = c->v_cache[layer];
+    st = lfm_hip_qkv_prologue(qd, (const float *)(d + qb), (const float *)(d + qb + kb), c->tables + 2u * layer,
+                              c->tables + 2u * layer + 1u, (const uint32_t *)(d + qb + 2u * kb), 1u, n_rows,
+                              g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
+                              c->cos_full, c->sin_full, 0u, 0u, c->stream);
+    if (st == LFM_ATTN_OK)
+        st = lfm_hip_store_fp32_to_fp16(q16, qd, (uint32_t)((size_t)n_rows * qrow), c->stream);
+    if (st == LFM_ATTN_OK)
+        st = lfm_hip_prefill_f16(q16, kcache, vcache, od, 1u, n_rows, pos_0, 0u, g->n_head_q, g->n_head_kv,
+                                 g->head_dim, 1.0f / sqrtf((float)g->head_dim), c->stream);
+    if (st == LFM_ATTN_OK)
+        st = st_of(hipMemcpyAsync(h + in_bytes, od, (size_t)n_rows * qrow * sizeof(float), hipMemcpyDeviceToHost,
+                                  c->stream));
+    if (st == LFM_ATTN_OK) st = st_of(hipStreamSynchronize(c->stream));
+    if (st == LFM_ATTN_OK) memcpy(out, h + in_bytes, (size_t)n_rows * qrow * sizeof(float));
     return st;
 }
 

@@ -148,3 +148,77 @@ def test_context_range_errors(gpu):
         ctx.forward(0, 0, z[:8], zk[:8], zk[:8])   # 16 + 8 - 1 > 20 ring slots
     assert e.value.status == -1
     ctx.close()
+
+
+def test_context_prefill_matches_chunked_steps(gpu, orc):
+    """lfm_attn_ctx_prefill of a 600-token prompt after 37 cached tokens (LFM2
+    layer, 32q/8kv d64: the MFMA prefill path) against the same prompt run
+    through the step 8 rows at a time, as lfm2_forward_batch does: caches
+    bit-identical (same prologue), outputs within the attention tolerance;
+    sampled rows also against the oracle engine."""
+    la = gpu
+    rng = np.random.default_rng(21)
+    nq, nkv, hd, max_seq, eps = 32, 8, 64, 1024, 1e-5
+    a = la.EngineContext(1, nq, nkv, hd, max_seq, eps, rope_base=1e6)
+    b = la.EngineContext(1, nq, nkv, hd, max_seq, eps, rope_base=1e6)
+    qn = (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32)
+    for c in (a, b):
+        c.set_norms(0, qn, kn)
+    pre = 37
+    q0 = rng.standard_normal((pre, nq, hd), dtype=np.float32)
+    k0 = rng.standard_normal((pre, nkv, hd), dtype=np.float32)
+    v0 = rng.standard_normal((pre, nkv, hd), dtype=np.float32)
+    for c in (a, b):
+        for p in range(0, pre, 8):
+            c.forward(0, p, q0[p:p + 8], k0[p:p + 8], v0[p:p + 8])
+    n = 600
+    q = rng.standard_normal((n, nq, hd), dtype=np.float32) * 2
+    k = rng.standard_normal((n, nkv, hd), dtype=np.float32) * 2
+    v = rng.standard_normal((n, nkv, hd), dtype=np.float32) * 0.5
+    got = a.prefill(0, pre, q, k, v).reshape(n, nq, hd)
+    want = np.concatenate([b.forward(0, pre + p, q[p:p + 8], k[p:p + 8], v[p:p + 8]).reshape(-1, nq, hd)
+                           for p in range(0, n, 8)])
+    parity(got, want, what="ctx prefill vs chunked steps")
+    ka, va = a.kv_export(0, 0, pre + n)
+    kb, vb = b.kv_export(0, 0, pre + n)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    # sampled rows against the oracle on the exported caches
+    lut = orc.rope_lut_lfm2(max_seq, hd, 1e6)
+    for r in (0, 1, 299, n - 1):
+        p = pre + r
+        qr = orc.qk_norm_rope(q[r], nq, hd, qn, eps, lut[0][p], lut[1][p])
+        ref_o = orc.online_gqa_f16(qr, ka[:p + 1], va[:p + 1], nq, nq // nkv, nkv * hd, p, 1.0 / 8.0)
+        parity(got[r].reshape(-1), ref_o, what=f"ctx prefill row {r} vs oracle")
+    a.close()
+    b.close()
+
+
+def test_context_prefill_chunked_layers(gpu):
+    """Layers the MFMA prefill does not take (a sliding-window layer, a gated
+    d128 layer) run the step in chunks of 8: bit-identical to calling the step
+    that way."""
+    la = gpu
+    rng = np.random.default_rng(22)
+    nq, nkv, hd, max_seq, win, cap = 16, 4, 128, 256, 16, 24
+    rf = np.array([1.0] * 32 + [1e30] * 32, np.float32)
+    mk = lambda: la.EngineContext(2, nq, nkv, hd, max_seq, 1e-5, rope_base=1e6, lfm3=True, sliding_window=win,
+                                  swa_cap=cap, layer_is_swa=[1, 0], rope_base_swa=1e4, rope_dim=hd,
+                                  rope_freqs=rf)
+    a, b = mk(), mk()
+    n = 45
+    for layer in (0, 1):
+        q = rng.standard_normal((n, nq, hd), dtype=np.float32)
+        k = rng.standard_normal((n, nkv, hd), dtype=np.float32)
+        v = rng.standard_normal((n, nkv, hd), dtype=np.float32)
+        g = rng.standard_normal((n, nq)).astype(np.float32)
+        got = a.prefill(layer, 0, q, k, v, g)
+        want = np.concatenate([b.forward(layer, p, q[p:p + 8], k[p:p + 8], v[p:p + 8], g[p:p + 8])
+                               for p in range(0, n, 8)])
+        assert np.array_equal(got, want)
+    with pytest.raises(la.LfmAttnError) as e:
+        a.prefill(1, 250, np.zeros((8, nq, hd), np.float32), np.zeros((8, nkv, hd), np.float32),
+                  np.zeros((8, nkv, hd), np.float32))
+    assert e.value.status == -2
+    a.close()
+    b.close()
