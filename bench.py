@@ -137,12 +137,15 @@ class DecodeWorkload:
 
 class PrefillWorkload:
     """causal prefill, B sequences of N tokens, fp16 Q/K/V
-    (0.5*N(0,1), RoPE assumed applied), fp32 softmax/accumulate, fp32 out."""
+    (0.5*N(0,1), RoPE assumed applied), fp32 softmax/accumulate, fp32 out.
+    The entry point takes Q as float (the reference's rows): the fp16 Q values
+    are passed widened, exactly."""
 
     def __init__(self, la, rng, n_seq=4, n_tok=4096, nq=32, nkv=8, hd=64):
         self.la, self.n_seq, self.n_tok, self.nq, self.nkv, self.hd = la, n_seq, n_tok, nq, nkv, hd
         self.q = la.DeviceArray.from_numpy(
-            f16(rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32) * np.float32(0.5)))
+            f16(rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32) * np.float32(0.5))
+            .view(np.float16).astype(np.float32))
         self.k = la.DeviceArray.from_numpy(
             f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * np.float32(0.5)))
         self.v = la.DeviceArray.from_numpy(

@@ -240,12 +240,13 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
  * runs lfm2_gqa_heads_worker_task once per row (:1029-1092).  Row i of
  * sequence s is position pos_0 + i and attends keys [0, pos_0 + i] of that
  * sequence's cache, which must already hold rows 0 .. pos_0 + n_tok - 1.
- * q:   [n_seq][n_tok][n_head_q][head_dim] fp16 (RoPE applied).
+ * q:   [n_seq][n_tok][n_head_q][head_dim] float (RoPE applied), as the
+ *      reference's rows; q * scale * log2(e) enters the MFMA as fp16.
  * k,v: sequence s at k + s * kv_seq_stride elements, [slot][n_head_kv][head_dim].
  * out: [n_seq][n_tok][n_head_q][head_dim] float.
  * head_dim 64 (MFMA kernel); other head dims return LFM_ATTN_E_UNSUPPORTED.
  * Softmax and accumulation are fp32; P enters the P.V product as fp16. */
-int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, float *out,
                         uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                         lfm_attn_stream_t stream);

@@ -242,7 +242,8 @@ def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0:
                 kv_seq_stride: int, n_head_q: int, n_head_kv: int, head_dim: int,
                 scale: Optional[float] = None, stream=None) -> None:
     """Causal prefill: row i of each sequence (position pos_0 + i) attends
-    keys [0, pos_0 + i] (tools/lfm2_prefill_batch.c:1029-1092)."""
+    keys [0, pos_0 + i] (tools/lfm2_prefill_batch.c:1029-1092).  q is float32
+    [n_seq][n_tok][n_head_q][head_dim]; k/v are the fp16 caches."""
     if scale is None:
         scale = float(1.0 / np.sqrt(np.float32(head_dim)))
     check(load().lfm_hip_prefill_f16(_p(q), _p(k), _p(v), _p(out), n_seq, n_tok, pos_0,

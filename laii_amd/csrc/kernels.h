@@ -48,7 +48,7 @@ int launch_generic(const AttnBatch &b, bool kv_f32, hipStream_t stream);
 
 /* Causal MFMA prefill (fp16 Q/K/V, fp32 out). */
 bool prefill_supports(uint32_t head_dim, uint32_t kv_mul);
-int launch_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+int launch_prefill(const float *q, const uint16_t *k, const uint16_t *v, float *out,
                    uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                    uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                    hipStream_t stream);

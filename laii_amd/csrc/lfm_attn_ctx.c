@@ -275,11 +275,11 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
         }
         return LFM_ATTN_OK;
     }
-    /* device layout: q f32 | k f32 | v f32 | pos | q f16 | out f32 (256-B aligned parts) */
+    /* device layout: q f32 | k f32 | v f32 | pos | out f32 (256-B aligned parts) */
     const size_t qb = align256((size_t)n_rows * qrow * sizeof(float));
     const size_t kb = align256((size_t)n_rows * krow * sizeof(float));
-    const size_t pb = 256u, hb = align256((size_t)n_rows * qrow * sizeof(uint16_t));
-    const size_t in_bytes = qb + 2u * kb + pb, dev_bytes = in_bytes + hb + qb;
+    const size_t pb = 256u;
+    const size_t in_bytes = qb + 2u * kb + pb, dev_bytes = in_bytes + qb;
     int st = LFM_ATTN_OK;
     if (c->pf_host_bytes < in_bytes + qb) {
         if (c->pf_host) (void)hipHostFree(c->pf_host);
@@ -305,17 +305,14 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
     st = st_of(hipMemcpyAsync(d, h, in_bytes, hipMemcpyHostToDevice, c->stream));
     if (st != LFM_ATTN_OK) return st;
     float *qd        = (float *)d;
-    uint16_t *q16    = (uint16_t *)(d + in_bytes);
-    float *od        = (float *)(d + in_bytes + hb);
+    float *od        = (float *)(d + in_bytes);
     uint16_t *kcache = c->k_cache[layer], *vcache = c->v_cache[layer];
     st = lfm_hip_qkv_prologue(qd, (const float *)(d + qb), (const float *)(d + qb + kb), c->tables + 2u * layer,
                               c->tables + 2u * layer + 1u, (const uint32_t *)(d + qb + 2u * kb), 1u, n_rows,
                               g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
                               c->cos_full, c->sin_full, 0u, 0u, c->stream);
     if (st == LFM_ATTN_OK)
-        st = lfm_hip_store_fp32_to_fp16(q16, qd, (uint32_t)((size_t)n_rows * qrow), c->stream);
-    if (st == LFM_ATTN_OK)
-        st = lfm_hip_prefill_f16(q16, kcache, vcache, od, 1u, n_rows, pos_0, 0u, g->n_head_q, g->n_head_kv,
+        st = lfm_hip_prefill_f16(qd, kcache, vcache, od, 1u, n_rows, pos_0, 0u, g->n_head_q, g->n_head_kv,
                                  g->head_dim, 1.0f / sqrtf((float)g->head_dim), c->stream);
     if (st == LFM_ATTN_OK)
         st = st_of(hipMemcpyAsync(h + in_bytes, od, (size_t)n_rows * qrow * sizeof(float), hipMemcpyDeviceToHost,

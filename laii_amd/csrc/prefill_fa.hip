@@ -1,6 +1,6 @@
 /*
- * prefill_fa.hip -- causal prefill attention on gfx950 MFMA (fp16 Q/K/V,
- * fp32 softmax and accumulation, fp32 output).
+ * prefill_fa.hip -- causal prefill attention on gfx950 MFMA (fp32 Q, fp16
+ * K/V cache, fp32 softmax and accumulation, fp32 output).
  *
  * Semantics: lfm2_forward_gqa_batch (tools/lfm2_prefill_batch.c:1029-1092)
  * runs the per-head task once per query row; row i (position pos_0 + i)
@@ -20,13 +20,14 @@
  *
  * Compute runs in 32-key steps, software pipelined so that each step's
  * basic block holds independent MFMA and VALU work:
- *   S^T(k+1) = K . Q^T - m   16x16x32 f16 MFMA on Q*scale (exact in fp16
- *                            for d = 64); the running max enters as the
- *                            accumulator's initial value
- *   p = exp(S^T(k))          exp2(s * log2 e) in fp32.  Lazy max: raised
- *                            only when a step exceeds it by more than
- *                            8 ln 2 (P <= 2^8, fp16 P stays finite), which
- *                            rescales O and l in a rare uniform branch
+ *   S^T(k+1) = K . Q^T - m   16x16x32 f16 MFMA on Q * scale * log2(e),
+ *                            rounded once from fp32 to fp16, so scores come
+ *                            out in log2 units; the running max enters as
+ *                            the accumulator's initial value
+ *   p = exp2(S^T(k))         in fp32.  Lazy max: raised only when a step
+ *                            exceeds it by more than 8 (P <= 2^8, fp16 P
+ *                            stays finite), which rescales O and l in a
+ *                            rare uniform branch
  *   O^T += V^T . P^T(k)      V^T fragments read transposed from row-major V
  *   l += 1 . P^T(k)          one more MFMA with an all-ones A operand: the
  *                            column sums of the same fp16 P, in fp32, on
@@ -59,17 +60,16 @@ constexpr int SB        = 32;          /* keys per compute step                 
 constexpr int NBUF      = 3;           /* LDS ring of K/V blocks                   */
 constexpr int ROWB      = 128;         /* bytes per K/V row of one head (d = 64)   */
 constexpr int BLKB      = KB * ROWB;   /* bytes per K (or V) block                 */
-constexpr float kLn2    = 0.6931471805599453f;
-constexpr float kLazy   = 8.0f * kLn2; /* headroom (natural log units, = 2^8 in P)  */
+constexpr float kLazy   = 8.0f;        /* headroom in log2 units (P <= 2^8)         */
 
 struct PrefillParams {
-    const uint16_t *q;  /* [n_seq][n_tok][n_head_q][HD] fp16 */
+    const float *q;     /* [n_seq][n_tok][n_head_q][HD] fp32 */
     const uint16_t *k;  /* seq s at k + s*kv_seq_stride: [slot][n_head_kv][HD] */
     const uint16_t *v;
     float *out;         /* [n_seq][n_tok][n_head_q][HD] */
     uint64_t kv_seq_stride;
     uint32_t n_seq, n_tok, pos_0, n_head_q, n_head_kv, kv_mul, tq, n_qtiles;
-    float scale;        /* softmax scale, applied to Q before its fp16 rounding */
+    float qmul;         /* softmax scale * log2(e), applied to Q before its fp16 rounding */
 };
 
 __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
@@ -78,11 +78,11 @@ __device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-/* exp of two scores (natural log units, as exp2 of x * log2(e) in fp32),
- * packed to fp16 with round toward zero */
+/* exp2 of two scores (log2 units) in fp32, packed to fp16 with round
+ * toward zero */
 __device__ __forceinline__ half2_t exp_pk(float a, float b) {
-    return __builtin_bit_cast(half2_t, __builtin_amdgcn_cvt_pkrtz(__builtin_amdgcn_exp2f(a * kLog2e),
-                                                                  __builtin_amdgcn_exp2f(b * kLog2e)));
+    return __builtin_bit_cast(half2_t,
+                              __builtin_amdgcn_cvt_pkrtz(__builtin_amdgcn_exp2f(a), __builtin_amdgcn_exp2f(b)));
 }
 
 /* transposing LDS read: within each 16-lane group, lane l receives element
@@ -130,20 +130,24 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
         const uint32_t j = c / P.tq, t = t0 + c % P.tq;
         col_ok[nt]  = t < P.n_tok;
         col_pos[nt] = P.pos_0 + t;
-        const uint16_t *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q +
-                                    kvh * P.kv_mul + j) * HD + 8 * g;
+        const float *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q +
+                                 kvh * P.kv_mul + j) * HD + 8 * g;
 #pragma unroll
         for (int st = 0; st < HD / 32; ++st) {
-            u32x4_t raw = col_ok[nt] ? *reinterpret_cast<const u32x4_t *>(qp + 32 * st) : (u32x4_t)0u;
-            half8_t h   = as_half8(raw);
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (col_ok[nt]) {
+                a = *reinterpret_cast<const float4 *>(qp + 32 * st);
+                b = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
+            }
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            half8_t h;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (_Float16)((float)h[e] * P.scale);
+            for (int e = 0; e < 8; ++e) h[e] = (_Float16)(x[e] * P.qmul);
             qf[nt][st] = h;
         }
     }
-    /* q*scale is exact in fp16 for the power-of-two scale of d = 64 (0.125):
-     * the score accumulator holds q.k in natural log units at fp32 accuracy,
-     * and log2(e) is applied in fp32 inside the exponential */
+    /* one fp16 rounding of q * scale * log2(e): the score accumulator holds
+     * q.k in log2 units, so the exponentials need no multiply */
     const uint32_t lo_pos = P.pos_0 + t0;                               /* smallest query position */
     const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;     /* largest query position  */
     const uint32_t n_keys = hi_pos + 1u;
@@ -232,7 +236,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     };
 
     /* lazy max: raise m (and rescale O, l and the pending scores) when a
-     * column's step maximum exceeds it by more than 2^kLazy; the first step
+     * column's step maximum exceeds it by more than kLazy; the first step
      * sets m to the exact column maximum.  step_max() is the per-lane part,
      * rescale() the rare, wave-uniform branch. */
     auto step_max = [&](auto first_tag, const float4_t (&sc)[2][NT], float (&mx)[NT]) {
@@ -257,7 +261,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 v = fmaxf(v, __shfl_xor(v, 32));
                 const bool raise  = FIRST ? (v > -INFINITY) : (v > kLazy);
                 const float inc   = raise ? v : 0.0f;
-                const float alpha = __builtin_amdgcn_exp2f(-inc * kLog2e);
+                const float alpha = __builtin_amdgcn_exp2f(-inc);
                 negm[nt] -= inc;
                 lacc[nt] *= alpha;
                 sc[0][nt] -= inc;
@@ -365,7 +369,7 @@ bool prefill_supports(uint32_t head_dim, uint32_t kv_mul) {
     return head_dim == 64u && kv_mul >= 1u && kv_mul <= 16u && (256u % kv_mul) == 0u;
 }
 
-int launch_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+int launch_prefill(const float *q, const uint16_t *k, const uint16_t *v, float *out,
                    uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                    uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                    hipStream_t stream) {
@@ -383,7 +387,7 @@ int launch_prefill(const uint16_t *q, const uint16_t *k, const uint16_t *v, floa
     P.kv_mul = n_head_q / n_head_kv;
     P.tq = 256u / P.kv_mul;
     P.n_qtiles = (n_tok + P.tq - 1u) / P.tq;
-    P.scale = scale;
+    P.qmul = scale * kLog2e;
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);

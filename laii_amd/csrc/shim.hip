@@ -407,7 +407,7 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
     return dispatch_f16(b, keys_hint, to_stream(stream));
 }
 
-int lfm_hip_prefill_f16(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *out,
+int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, float *out,
                         uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                         lfm_attn_stream_t stream) {

@@ -14,19 +14,20 @@ def dev(la, arr):
 
 
 def run_prefill(la, rng, n_seq, n_tok, pos_0, nq, nkv, hd=64, scale_qkv=0.5):
+    """fp32 Q (the reference's rows), fp16 K/V caches."""
     slots = pos_0 + n_tok
-    q16 = f16(rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32) * np.float32(scale_qkv))
+    q = rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32) * np.float32(scale_qkv)
     k16 = np.stack([rand_kv(rng, slots, nkv, hd, scale_qkv) for _ in range(n_seq)])
     v16 = np.stack([rand_kv(rng, slots, nkv, hd, scale_qkv) for _ in range(n_seq)])
     out = la.DeviceArray.zeros((n_seq, n_tok, nq, hd), np.float32)
-    la.prefill_f16(dev(la, q16), dev(la, k16), dev(la, v16), out, n_seq, n_tok, pos_0,
+    la.prefill_f16(dev(la, q), dev(la, k16), dev(la, v16), out, n_seq, n_tok, pos_0,
                    slots * nkv * hd, nq, nkv, hd)
-    return q16, k16, v16, out.numpy()
+    return q, k16, v16, out.numpy()
 
 
-def oracle_rows(orc, q16, k16, v16, s, rows, pos_0, nq, nkv, hd=64):
-    """Oracle causal rows for the given row indices of sequence s."""
-    qf = f16_to_f32(q16[s])
+def oracle_rows(orc, q, k16, v16, s, rows, pos_0, nq, nkv, hd=64):
+    """Oracle causal rows for the given row indices of sequence s (fp32 q)."""
+    qf = np.asarray(q[s], dtype=np.float32)
     out = []
     for r in rows:
         out.append(orc.causal_rows_f16(qf[r], k16[s], v16[s], 1, pos_0 + r, nq, nkv, hd))
@@ -43,9 +44,9 @@ def oracle_rows(orc, q16, k16, v16, s, rows, pos_0, nq, nkv, hd=64):
 ])
 def test_prefill_vs_oracle(gpu, orc, n_seq, n_tok, pos_0, nq, nkv):
     rng = np.random.default_rng(n_tok * 7 + pos_0 + nq)
-    q16, k16, v16, got = run_prefill(gpu, rng, n_seq, n_tok, pos_0, nq, nkv)
+    q, k16, v16, got = run_prefill(gpu, rng, n_seq, n_tok, pos_0, nq, nkv)
     for s in range(n_seq):
-        want = oracle_rows(orc, q16, k16, v16, s, range(n_tok), pos_0, nq, nkv)
+        want = oracle_rows(orc, q, k16, v16, s, range(n_tok), pos_0, nq, nkv)
         parity(got[s], want, what=f"prefill s={s} n={n_tok} pos0={pos_0} {nq}q/{nkv}kv")
 
 
@@ -54,10 +55,10 @@ def test_prefill_cfg4_full_size_sampled(gpu, orc):
     against the oracle, and every row's output is a convex combination of V
     rows (|o| <= max |v| per dim), the size-independent property."""
     rng = np.random.default_rng(4096)
-    q16, k16, v16, got = run_prefill(gpu, rng, 4, 4096, 0, 32, 8)
+    q, k16, v16, got = run_prefill(gpu, rng, 4, 4096, 0, 32, 8)
     for s in range(4):
         rows = [0, 1, 63, 64, 1000, 2047, 2048, 4095]
-        want = oracle_rows(orc, q16, k16, v16, s, rows, 0, 32, 8)
+        want = oracle_rows(orc, q, k16, v16, s, rows, 0, 32, 8)
         parity(got[s][rows], want, what=f"prefill cfg4 s={s} sampled")
     vmax = np.abs(f16_to_f32(v16)).max()
     assert np.all(np.isfinite(got)) and np.abs(got).max() <= vmax + 1e-3
@@ -72,9 +73,9 @@ def test_prefill_matches_decode_path(gpu):
     la = gpu
     rng = np.random.default_rng(77)
     n_tok, nq, nkv, hd = 1000, 32, 8, 64
-    q16, k16, v16, got = run_prefill(la, rng, 1, n_tok, 0, nq, nkv)
+    q, k16, v16, got = run_prefill(la, rng, 1, n_tok, 0, nq, nkv)
     out = la.DeviceArray.zeros(nq * hd, np.float32)
-    qf = f16_to_f32(q16[0, n_tok - 1])
+    qf = np.ascontiguousarray(q[0, n_tok - 1])
     la.online_gqa_f16(dev(la, qf), dev(la, k16[0]), dev(la, v16[0]), out, nq, 4, nkv * hd,
                       n_tok - 1, 0.125)
     parity(got[0, n_tok - 1].reshape(-1), out.numpy(), what="prefill last row vs decode")
@@ -85,7 +86,7 @@ def test_prefill_rejects_unsupported(gpu):
     lib = la.load()
     a = la.DeviceArray.zeros(1 << 16, np.uint16)
     o = la.DeviceArray.zeros(1 << 16, np.float32)
-    assert lib.lfm_hip_prefill_f16(a.ptr, a.ptr, a.ptr, o.ptr, 1, 8, 0, 0, 8, 2, 128, 0.088,
+    assert lib.lfm_hip_prefill_f16(o.ptr, a.ptr, a.ptr, o.ptr, 1, 8, 0, 0, 8, 2, 128, 0.088,
                                    None) == -3
 
 
@@ -113,13 +114,12 @@ def test_prefill_lazy_max_raises(gpu, orc, pattern):
     else:
         amp = np.where(t < 64, 40.0, 0.0).astype(np.float32)
     k += amp[None, :, None, None] * u
-    q16 = f16(q)
     k16 = f16(k)
     v16 = f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32))
     out = la.DeviceArray.zeros((n_seq, n_tok, nq, hd), np.float32)
-    la.prefill_f16(dev(la, q16), dev(la, k16), dev(la, v16), out, n_seq, n_tok, 0,
+    la.prefill_f16(dev(la, q), dev(la, k16), dev(la, v16), out, n_seq, n_tok, 0,
                    n_tok * nkv * hd, nq, nkv, hd)
     got = out.numpy()
     assert np.all(np.isfinite(got))
-    want = oracle_rows(orc, q16, k16, v16, 0, range(n_tok), 0, nq, nkv)
+    want = oracle_rows(orc, q, k16, v16, 0, range(n_tok), 0, nq, nkv)
     parity(got[0], want, what=f"prefill lazy max {pattern}")
