@@ -892,13 +892,16 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
  * MI355X, 64 sequences of 512..8192 keys run 23 % faster than on the
  * fixed-chunk grid, which leaves XCDs idle.  A batch that cannot be ragged
  * (one sequence, or one shared host position) takes the grid, which skips the
- * plan's position scan and table (1-9 % faster on equal-length batches).
- * LFM_ATTN_PLAN=grid|balanced overrides (tuning and tests). */
+ * plan's position scan and table (1-9 % faster on equal-length batches).  So
+ * does a sliding-window batch: no row reads more than window keys, which
+ * bounds how ragged it can be (config 5's ring, B32 x 256 keys: 10.7 vs
+ * 11.9 us per call).  LFM_ATTN_PLAN=grid|balanced overrides (tuning and
+ * tests). */
 bool use_grid_plan(const AttnBatch &b) {
     const char *env = getenv("LFM_ATTN_PLAN");
     if (env && env[0] == 'g') return true;
     if (env && env[0] == 'b') return false;
-    return !b.pos0_dev || b.n_seq == 1u;
+    return !b.pos0_dev || b.n_seq == 1u || b.window != 0u;
 }
 
 template <int HD, int NT>
@@ -933,6 +936,7 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool 
 void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, uint32_t *chunk) {
     uint32_t keys = keys_hint;
     if (keys == 0u) keys = b.window ? b.window + b.n_rows - 1u : 4096u;
+    if (b.window && keys > b.window + b.n_rows - 1u) keys = b.window + b.n_rows - 1u;
     const uint64_t pairs  = (uint64_t)b.n_seq * b.n_head_kv;
     const uint64_t ncols  = (uint64_t)b.n_rows * (b.n_head_q / b.n_head_kv);
     const uint64_t target = 4096; /* waves */
