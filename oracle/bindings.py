@@ -306,6 +306,9 @@ class Reference:
         L.ref_time_decode_batch.restype = C.c_double
         L.ref_time_decode_batch.argtypes = [_f32p, C.c_void_p, C.c_void_p, _u32p, _f32p, _u32,
                                             _u32, _u32, _u32, _u32, C.POINTER(_u32)]
+        L.ref_time_decode_batch_fair.restype = C.c_double
+        L.ref_time_decode_batch_fair.argtypes = [_f32p, C.c_void_p, C.c_void_p, _u32p, _f32p, _u32,
+                                                 _u32, _u32, _u32, _u32]
         L.ref_kv_shift_sinks_lfm2.restype = _u32
         L.ref_kv_shift_sinks_lfm2.argtypes = [C.c_void_p, C.c_void_p, _u32, C.c_void_p, _u32,
                                               C.c_void_p, C.c_void_p, _u32, _u32, _u32, _u32]
@@ -408,6 +411,18 @@ class Reference:
                                             vp, np.ascontiguousarray(pos, np.uint32), out, n_seq,
                                             n_head_q, n_head_kv, n_threads, reps, C.byref(used))
         return dt, int(used.value), out
+
+    def time_decode_batch_fair(self, q, k_list, v_list, pos, n_head_q, n_head_kv, n_threads, reps):
+        """The reference's decode worker over every (sequence, 4-head group)
+        item of the batch across n_threads threads; fastest of reps passes."""
+        n_seq = len(k_list)
+        kp = (C.c_void_p * n_seq)(*[k.ctypes.data for k in k_list])
+        vp = (C.c_void_p * n_seq)(*[v.ctypes.data for v in v_list])
+        out = np.zeros(n_seq * n_head_q * 64, np.float32)
+        dt = self.lib.ref_time_decode_batch_fair(np.ascontiguousarray(q, np.float32).reshape(-1), kp,
+                                                 vp, np.ascontiguousarray(pos, np.uint32), out, n_seq,
+                                                 n_head_q, n_head_kv, n_threads, reps)
+        return dt, out
 
 
 def _ref_quant(self, x, y, n_rows, n_cols):

@@ -242,6 +242,68 @@ double ref_time_decode_batch(const float *q, const uint16_t *const *k_seq,
     return best;
 }
 
+/* CPU baseline, fair-batched: the reference's decode worker on every
+ * (sequence, 4-head group) item of the batch, claimed dynamically by
+ * n_threads threads (FTZ/DAZ set as the reference pool sets them,
+ * tools/lfm2_threadpool.c:384-414), so all cores stay busy across sequences.
+ * Each item hands the worker a one-item claim range (the fields that
+ * lfm2_threadpool_claim_chunk reads, tools/lfm2_threadpool.c:506-520), so the
+ * worker computes exactly that group.  head_dim is 64. */
+typedef struct {
+    const float *q;
+    const uint16_t *const *k_seq;
+    const uint16_t *const *v_seq;
+    const uint32_t *pos;
+    float *out;
+    uint32_t n_seq, n_head_q, n_head_kv, n_groups;
+    atomic_uint next;
+} fair_job;
+
+static void *fair_worker(void *arg) {
+    fair_job *j = (fair_job *)arg;
+    _mm_setcsr(_mm_getcsr() | 0x8040u);
+    LFM2ThreadPool one;
+    memset(&one, 0, sizeof one);
+    one.chunk_size = 1u;
+    for (;;) {
+        const uint32_t it = atomic_fetch_add_explicit(&j->next, 1u, memory_order_relaxed);
+        if (it >= j->n_seq * j->n_groups) break;
+        const uint32_t s = it / j->n_groups, g = it % j->n_groups;
+        one.n_items = g + 1u;
+        atomic_store_explicit(&one.next_item, g, memory_order_relaxed);
+        OnlineGQATaskCtx ctx = {
+            .pool = &one, .q = j->q + (size_t)s * j->n_head_q * 64u, .k_cache_f16 = j->k_seq[s],
+            .v_cache_f16 = j->v_seq[s], .xb_out = j->out + (size_t)s * j->n_head_q * 64u,
+            .xb_q8_out = NULL, .n_head_q = j->n_head_q, .kv_mul = j->n_head_q / j->n_head_kv,
+            .kv_dim = j->n_head_kv * 64u, .pos = j->pos[s], .scale = 1.0f / sqrtf(64.0f)};
+        lfm2_online_gqa_f16_worker_simd(&ctx, 0u, 1u);
+    }
+    return NULL;
+}
+
+double ref_time_decode_batch_fair(const float *q, const uint16_t *const *k_seq,
+                                  const uint16_t *const *v_seq, const uint32_t *pos, float *out,
+                                  uint32_t n_seq, uint32_t n_head_q, uint32_t n_head_kv,
+                                  uint32_t n_threads, uint32_t reps) {
+    shim_state st;
+    shim_save(&st);
+    if (n_threads < 1u) n_threads = 1u;
+    if (n_threads > 256u) n_threads = 256u;
+    double best = 1e30;
+    for (uint32_t r = 0; r < reps; ++r) {
+        fair_job job = {q, k_seq, v_seq, pos, out, n_seq, n_head_q, n_head_kv, (n_head_q + 3u) / 4u, 0u};
+        pthread_t th[256];
+        const double t0 = shim_now();
+        for (uint32_t t = 1; t < n_threads; ++t) pthread_create(&th[t], NULL, fair_worker, &job);
+        fair_worker(&job);
+        for (uint32_t t = 1; t < n_threads; ++t) pthread_join(th[t], NULL);
+        const double dt = shim_now() - t0;
+        if (dt < best) best = dt;
+    }
+    shim_restore(&st);
+    return best;
+}
+
 /* ---- attention-sink eviction ------------------------------------------ */
 /* A model description carrying only what the shift functions read:
  * n_layers, head_dim (n_embd / n_head_q for LFM2), n_head_kv, sliding_window

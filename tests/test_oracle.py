@@ -266,6 +266,22 @@ def test_decode_batch_mt_equals_single(orc):
         assert np.array_equal(got[s], orc.online_gqa_f16(q[s], ks[s], vs[s], 32, 4, 512, int(pos[s])))
 
 
+def test_reference_batch_dispatches_agree(orc, ref):
+    """The two CPU-baseline dispatches of the reference's decode worker (per
+    sequence through its pool, and every (sequence, head group) item across
+    threads) give bit-identical rows, equal to the oracle's batch."""
+    rng = np.random.default_rng(12)
+    ks = [f16(rng.standard_normal((n, 8, 64)) * 0.5) for n in (100, 257, 31, 64)]
+    vs = [f16(rng.standard_normal((n, 8, 64)) * 0.5) for n in (100, 257, 31, 64)]
+    pos = np.array([99, 256, 30, 63], np.uint32)
+    q = rng.standard_normal((4, 32 * 64)).astype(np.float32)
+    _, _, per_seq = ref.time_decode_batch(q, ks, vs, pos, 32, 8, 3, 1)
+    _, fair = ref.time_decode_batch_fair(q, ks, vs, pos, 32, 8, 3, 2)
+    assert np.array_equal(per_seq, fair)
+    want = orc.decode_batch_mt(q, ks, vs, pos, 32, 8, 64, 2)
+    assert np.abs(fair - want.reshape(-1)).max() < 1e-6
+
+
 def test_attention_matches_reference_build(orc, ref):
     rng = np.random.default_rng(11)
     nq, nkv, hd, pos = 32, 8, 64, 999
