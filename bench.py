@@ -341,6 +341,39 @@ def time_main_kernel(hip, la, wl, steps):
     return float(np.mean([hip.elapsed_ms(a, b) for a, b in evs]))
 
 
+class _Probe:
+    """One launch of a peak probe as a bench step."""
+
+    def __init__(self, fn):
+        self.step = fn
+
+
+def box_peaks(hip, la, steps=10):
+    """This device's achievable denominators: a 2 GiB streaming read (well
+    past the 256 MB MALL) and a dense fp16 MFMA loop, both hand-written
+    probes of the library (peak_probe.hip)."""
+    from laii_amd._lib import check
+
+    lib = la.load()
+    n_bytes = 2 << 30
+    src = la.DeviceArray.zeros(n_bytes // 4, np.uint32)
+    n_wg = 8192
+    sink = la.DeviceArray.zeros(n_wg, np.uint32)
+    rd = _Probe(lambda: check(lib.lfm_hip_probe_read(src.ptr, n_bytes, sink.ptr, n_wg, None),
+                                 "lfm_hip_probe_read"))
+    read_ms = min(time_steps(hip, rd, steps, 2) for _ in range(2))
+    del src
+    wgs, iters = 4096, 2048
+    out = la.DeviceArray.zeros(wgs * 256, np.float32)
+    mf = _Probe(lambda: check(lib.lfm_hip_probe_mfma(out.ptr, wgs, iters, None), "lfm_hip_probe_mfma"))
+    mfma_ms = min(time_steps(hip, mf, steps, 2) for _ in range(2))
+    flops = wgs * 4 * iters * 8 * 16384
+    return dict(read_GBps=round(n_bytes / (read_ms * 1e-3) / 1e9, 1),
+                mfma_f16_TFLOPs=round(flops / (mfma_ms * 1e-3) / 1e12, 1),
+                read="2 GiB streaming read, 8192 x 256 threads, 16-B nontemporal loads",
+                mfma="4096 x 4 waves, 8 independent 16x16x32 f16 MFMA chains per wave")
+
+
 def cpu_baseline(wl, n_threads, max_seconds=8.0):
     """The reference's AVX2 decode worker (oracle/_ref) on a sample of the
     headline batch, dispatched per sequence as the engine does (the value),
@@ -576,6 +609,14 @@ def main():
         log(f"prompt cache: save {pc['save_ms']} ms, load {pc['load_ms']} ms, "
             f"device FNV-1a {pc['fnv1a64_device_GBps']} GB/s")
 
+    peaks = None
+    if not args.quick:
+        peaks = box_peaks(hip, la)
+        peaks["headline_kernel_frac_of_read"] = round(achieved / peaks["read_GBps"], 3)
+        if prefill:
+            peaks["prefill_kernel_frac_of_mfma"] = round(prefill["kernel_TFLOPs"] / peaks["mfma_f16_TFLOPs"], 3)
+        log(f"box peaks: read {peaks['read_GBps']} GB/s, fp16 MFMA {peaks['mfma_f16_TFLOPs']} TFLOP/s")
+
     cpu = None
     parity = None
     if not args.no_cpu:
@@ -612,6 +653,7 @@ def main():
                      "traffic": HEADLINE_TRAFFIC_BYTES,
                      "kernel": "k_splitkv_bal<64,1,8>", "kernel_us": round(k_ms * 1e3, 2)},
         "prefill": prefill,
+        "box_peaks": peaks,
         "cpu_baseline": cpu,
         "parity_vs_cpu": parity,
         "secondary": secondary,

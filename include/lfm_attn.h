@@ -438,6 +438,18 @@ int lfm_attn_ctx_swa_slab_restore(lfm_attn_ctx *ctx, const void *slab);
 int lfm_attn_ctx_kv_device(lfm_attn_ctx *ctx, uint32_t layer, uint16_t **k_dev, uint16_t **v_dev,
                            uint32_t *n_slots);
 
+/* ---- achievable-peak probes (measurement only) --------------------------------
+ * No counterpart in the reference: they measure this device's achievable
+ * denominators for the roofline figures.  Asynchronous on `stream`.
+ * lfm_hip_probe_read streams n_bytes (>= 16, 16-byte aligned) of device memory
+ * with n_wg workgroups of 256 threads; sink receives n_wg words.
+ * lfm_hip_probe_mfma runs n_wg workgroups of 4 waves, each wave `iters`
+ * rounds of 8 independent 16x16x32 fp16 MFMAs (16,384 FLOPs each); out
+ * receives n_wg * 256 floats. */
+int lfm_hip_probe_read(const void *src, uint64_t n_bytes, uint32_t *sink, uint32_t n_wg,
+                       lfm_attn_stream_t stream);
+int lfm_hip_probe_mfma(float *out, uint32_t n_wg, uint32_t iters, lfm_attn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

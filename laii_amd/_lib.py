@@ -81,6 +81,8 @@ class CacheModelC(C.Structure):
 
 SIGNATURES.update({
     "lfm_hip_fnv1a64": (_int, [_vp, C.c_size_t, C.c_uint64, C.POINTER(C.c_uint64), _vp]),
+    "lfm_hip_probe_read": (_int, [_vp, C.c_uint64, _vp, _u32, _vp]),
+    "lfm_hip_probe_mfma": (_int, [_vp, _u32, _u32, _vp]),
     "lfm_attn_ctx_cache_save": (_int, [_vp, C.c_char_p, C.POINTER(CacheModelC), _vp, _u32, _vp, _vp]),
     "lfm_attn_ctx_cache_load_prefix": (_int, [_vp, C.c_char_p, C.POINTER(CacheModelC), _vp, _u32, _vp,
                                               _vp, C.POINTER(_u32)]),

@@ -96,6 +96,10 @@ size_t fnv1a64_workspace_bytes(uint64_t len);
 int launch_fnv1a64(const void *data, uint64_t len, uint64_t h_in, void *ws, hipStream_t stream);
 uint64_t fnv1a64_finish(uint64_t h_in, uint64_t len, uint64_t acc);
 
+/* Achievable-peak probes (peak_probe.hip). */
+int launch_probe_read(const void *src, uint64_t n_bytes, uint32_t *sink, uint32_t n_wg, hipStream_t stream);
+int launch_probe_mfma(float *out, uint32_t n_wg, uint32_t iters, hipStream_t stream);
+
 } // namespace lfm
 
 #endif

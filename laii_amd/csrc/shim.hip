@@ -223,6 +223,18 @@ int lfm_hip_fnv1a64(const void *data, size_t n_bytes, uint64_t h_in, uint64_t *h
     return LFM_ATTN_OK;
 }
 
+/* ---- achievable-peak probes ------------------------------------------------ */
+int lfm_hip_probe_read(const void *src, uint64_t n_bytes, uint32_t *sink, uint32_t n_wg,
+                       lfm_attn_stream_t stream) {
+    if (!src || !sink || n_wg == 0u || n_bytes < 16u || ((uintptr_t)src & 15u)) return LFM_ATTN_E_INVALID;
+    return lfm::launch_probe_read(src, n_bytes, sink, n_wg, to_stream(stream));
+}
+
+int lfm_hip_probe_mfma(float *out, uint32_t n_wg, uint32_t iters, lfm_attn_stream_t stream) {
+    if (!out || n_wg == 0u || iters == 0u) return LFM_ATTN_E_INVALID;
+    return lfm::launch_probe_mfma(out, n_wg, iters, to_stream(stream));
+}
+
 /* ---- projections beside the path ------------------------------------------- */
 static inline bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p & (a - 1u)) == 0u; }
 

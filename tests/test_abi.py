@@ -104,6 +104,12 @@ def test_rejections_before_launch():
                                     1e-5, FAKE, FAKE, 300, 264, None) == E_INVALID
     out5 = (C.c_uint32 * 5)()
     assert lib.lfm_attn_seg_plan(5, 300, 264, out5) == E_INVALID
+    # peak probes: null, unaligned or empty inputs
+    assert lib.lfm_hip_probe_read(None, 1 << 20, FAKE, 8, None) == E_INVALID
+    assert lib.lfm_hip_probe_read(FAKE + 4, 1 << 20, FAKE, 8, None) == E_INVALID
+    assert lib.lfm_hip_probe_read(FAKE, 8, FAKE, 8, None) == E_INVALID
+    assert lib.lfm_hip_probe_mfma(None, 8, 16, None) == E_INVALID
+    assert lib.lfm_hip_probe_mfma(FAKE, 8, 0, None) == E_INVALID
 
 
 def test_context_rejects_bad_geometry():
