@@ -59,7 +59,11 @@ def test_quantize_ties_round_half_to_even(gpu, orc):
 
 @pytest.mark.parametrize("n_rows,n_cols,B", [(4, 1024, 1), (16, 2048, 1), (2048, 2048, 1),
                                              (5, 2304, 3), (130, 1536, 8), (64, 8192, 2),
-                                             (1, 256, 64), (2048, 2048, 64)])
+                                             (1, 256, 64), (2048, 2048, 64),
+                                             # int8-MFMA path (16-row tiles, >= 8 tokens):
+                                             # super-block rounds of 8 with a remainder,
+                                             # ragged token tiles, one super-block
+                                             (32, 2304, 17), (48, 512, 100), (16, 256, 8)])
 def test_matmul_bit_exact_random(gpu, orc, n_rows, n_cols, B):
     rng = np.random.default_rng(n_rows * 7 + n_cols + B)
     w = q4k_random(rng, n_rows, n_cols)
