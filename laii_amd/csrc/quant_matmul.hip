@@ -30,7 +30,8 @@
  * (2048 columns) per step, reading each weight byte once.  Integer dots use
  * v_dot4_i32_i8; the lane groups' sums meet by shuffles.  The product is
  * HBM-bound on the weights (4.5 bits per weight).  Eight or more tokens on one
- * Q4_K matrix take k_matmul_q4k_mfma instead (int8 MFMA, same arithmetic).
+ * Q4_K or Q5_K matrix take k_matmul_qk_mfma instead (int8 MFMA, same
+ * arithmetic).
  */
 #include <hip/hip_runtime.h>
 
@@ -540,11 +541,12 @@ hipError_t launch_tokens(const MatSet &S, const void *x_q8, uint32_t nb, uint32_
     return launch_set<TYPE, 2, 8>(S, x_q8, nb, n_tokens, stream);
 }
 
-/* ---- Q4_K x Q8_K on int8 MFMA, 16 or more tokens ------------------------------
+/* ---- Q4_K / Q5_K x Q8_K on int8 MFMA, 8 or more tokens -------------------------
  * A workgroup computes a 16-token x 16-row tile with the reference's exact
  * integer sums and its fp32 rounding order.  Per super-block:
  *   per sub-block j   dot_j[t][r] = sum_32 q8[t] * q4[r]  v_mfma_i32_16x16x32_i8
- *                     (A = the tokens' int8 activations, B = the row's nibbles)
+ *                     (A = the tokens' int8 activations, B = the row's 4-bit
+ *                     weights, with Q5_K's fifth bit from qh ORed in)
  *   a[t][r] = sum_j sc_j[r] * dot_j[t][r]                 int32 on the VALU
  *   b[t][r] = sum_j m_j[r] * (bsum[t][2j] + bsum[t][2j+1])  two
  *             v_mfma_f32_16x16x4_f32 on integers below 2^24, hence exact
@@ -569,14 +571,17 @@ __device__ __forceinline__ long ld64_4(const uint8_t *p) { /* 4-byte aligned */
 
 constexpr uint32_t kMfmaChunk = 8u; /* super-blocks per round (two per wave) */
 
-__global__ __launch_bounds__(256) void k_matmul_q4k_mfma(const uint8_t *__restrict__ w, float *__restrict__ out,
-                                                         uint32_t n_rows, const uint8_t *__restrict__ xq,
-                                                         uint32_t nb, uint32_t n_tokens) {
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_matmul_qk_mfma(const uint8_t *__restrict__ w, float *__restrict__ out,
+                                                        uint32_t n_rows, const uint8_t *__restrict__ xq,
+                                                        uint32_t nb, uint32_t n_tokens) {
+    static_assert(TYPE == 12 || TYPE == 13, "Q4_K or Q5_K");
+    constexpr uint32_t kBytes = QType<TYPE>::kBytes, kQs = TYPE == 12 ? 16u : 48u;
     __shared__ float terms[kMfmaChunk][256];   /* [super-block of the round][token * 16 + row] */
     __shared__ uint32_t live[kMfmaChunk][16];  /* d8 != 0 per [super-block][token] */
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, l16 = lane & 15u, g = lane >> 4;
     const uint32_t r0 = blockIdx.x * 16u, t0 = blockIdx.y * 16u;
-    const uint8_t *wr = w + (size_t)(r0 + l16) * nb * kQ4K;
+    const uint8_t *wr = w + (size_t)(r0 + l16) * nb * kBytes;
     const uint8_t *xa = xq + (size_t)min(t0 + l16, n_tokens - 1u) * nb * kQ8K;
     const uint8_t *xd[4];
 #pragma unroll
@@ -587,7 +592,7 @@ __global__ __launch_bounds__(256) void k_matmul_q4k_mfma(const uint8_t *__restri
         for (uint32_t u = 0; u < 2u; ++u) {
             const uint32_t k = 2u * wave + u, b = c0 + k;
             if (b >= nb) break;
-            const uint8_t *blk = wr + (size_t)b * kQ4K;
+            const uint8_t *blk = wr + (size_t)b * kBytes;
             const uint8_t *xb  = xa + (size_t)b * kQ8K;
             const uint4 hdr    = *reinterpret_cast<const uint4 *>(blk);
             int32_t sc[8], mn_unused, m_lo, m_hi, sc_unused;
@@ -597,12 +602,21 @@ __global__ __launch_bounds__(256) void k_matmul_q4k_mfma(const uint8_t *__restri
             scale_min(g, hdr.y, hdr.z, hdr.w, &sc_unused, &m_lo);
             scale_min(g + 4u, hdr.y, hdr.z, hdr.w, &sc_unused, &m_hi);
             i32x4_t a = (i32x4_t)0;
+            uint2 qh = make_uint2(0u, 0u); /* Q5_K: bit j of qh[i] is weight i's fifth bit in sub-block j */
+            if constexpr (TYPE == 13) qh = *reinterpret_cast<const uint2 *>(blk + 16u + 8u * g);
 #pragma unroll
             for (uint32_t jp = 0; jp < 4u; ++jp) {
-                const uint2 wq = *reinterpret_cast<const uint2 *>(blk + 16u + 32u * jp + 8u * g);
-                const long blo = (long)(((uint64_t)(wq.y & 0x0F0F0F0Fu) << 32) | (wq.x & 0x0F0F0F0Fu));
-                const long bhi =
-                    (long)(((uint64_t)((wq.y >> 4) & 0x0F0F0F0Fu) << 32) | ((wq.x >> 4) & 0x0F0F0F0Fu));
+                const uint2 wq = *reinterpret_cast<const uint2 *>(blk + kQs + 32u * jp + 8u * g);
+                uint32_t lx = wq.x & 0x0F0F0F0Fu, ly = wq.y & 0x0F0F0F0Fu;
+                uint32_t hx = (wq.x >> 4) & 0x0F0F0F0Fu, hy = (wq.y >> 4) & 0x0F0F0F0Fu;
+                if constexpr (TYPE == 13) {
+                    lx |= ((qh.x >> (2u * jp)) & 0x01010101u) << 4;
+                    ly |= ((qh.y >> (2u * jp)) & 0x01010101u) << 4;
+                    hx |= ((qh.x >> (2u * jp + 1u)) & 0x01010101u) << 4;
+                    hy |= ((qh.y >> (2u * jp + 1u)) & 0x01010101u) << 4;
+                }
+                const long blo = (long)(((uint64_t)ly << 32) | lx);
+                const long bhi = (long)(((uint64_t)hy << 32) | hx);
                 const long alo = ld64_4(xb + 4u + 32u * (2u * jp) + 8u * g);
                 const long ahi = ld64_4(xb + 4u + 32u * (2u * jp + 1u) + 8u * g);
                 const i32x4_t dlo = __builtin_amdgcn_mfma_i32_16x16x32_i8(alo, blo, (i32x4_t)0, 0, 0, 0);
@@ -662,12 +676,18 @@ int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, 
     bool one_type = true;
     for (uint32_t m = 1; m < S.n; ++m) one_type = one_type && S.type[m] == S.type[0];
     hipError_t e;
-    /* one Q4_K matrix of whole 16-row tiles and >= 8 tokens: int8 MFMA
-     * (measured on MI355X, 2048 x 2048: 8 tokens 8.8 -> 6.3 us, 64 tokens
-     * 36 -> 8.8 us against the dot4 path) */
-    if (S.n == 1u && S.type[0] == 12u && n_tokens >= 8u && S.rows[0] % 16u == 0u) {
-        hipLaunchKernelGGL(k_matmul_q4k_mfma, dim3(S.rows[0] / 16u, (n_tokens + 15u) / 16u), dim3(256), 0, stream,
-                           S.w[0], S.out[0], S.rows[0], static_cast<const uint8_t *>(x_q8), nb, n_tokens);
+    /* one Q4_K or Q5_K matrix of whole 16-row tiles and >= 8 tokens: int8
+     * MFMA (measured on MI355X, Q4_K 2048 x 2048: 8 tokens 8.8 -> 6.3 us,
+     * 64 tokens 36 -> 8.8 us against the dot4 path) */
+    if (S.n == 1u && (S.type[0] == 12u || S.type[0] == 13u) && n_tokens >= 8u && S.rows[0] % 16u == 0u) {
+        const dim3 grid(S.rows[0] / 16u, (n_tokens + 15u) / 16u);
+        const uint8_t *xq = static_cast<const uint8_t *>(x_q8);
+        if (S.type[0] == 12u)
+            hipLaunchKernelGGL(k_matmul_qk_mfma<12>, grid, dim3(256), 0, stream, S.w[0], S.out[0], S.rows[0], xq, nb,
+                               n_tokens);
+        else
+            hipLaunchKernelGGL(k_matmul_qk_mfma<13>, grid, dim3(256), 0, stream, S.w[0], S.out[0], S.rows[0], xq, nb,
+                               n_tokens);
         return hip_status(hipGetLastError());
     }
     switch (one_type ? S.type[0] : 0u) {

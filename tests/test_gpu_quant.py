@@ -159,7 +159,8 @@ OTHER_TYPES = {2: "Q4_0", 8: "Q8_0", 13: "Q5_K", 23: "IQ4_XS"}
 
 
 @pytest.mark.parametrize("qtype", sorted(OTHER_TYPES))
-@pytest.mark.parametrize("n_rows,n_cols,B", [(8, 256, 1), (2048, 2048, 1), (130, 2304, 5), (64, 2048, 64)])
+@pytest.mark.parametrize("n_rows,n_cols,B", [(8, 256, 1), (2048, 2048, 1), (130, 2304, 5), (64, 2048, 64),
+                                             (32, 2304, 17)])
 def test_other_types_bit_exact(gpu, orc, qtype, n_rows, n_cols, B):
     """Q4_0, Q8_0, Q5_K and IQ4_XS rows through lfm_hip_matmul_prequant,
     bit-exact against the oracle (pinned to the reference's AVX2 1x1 dots),
