@@ -676,19 +676,37 @@ int launch_matmul_q(uint32_t n_mats, float *const *outs, const void *const *ws, 
     bool one_type = true;
     for (uint32_t m = 1; m < S.n; ++m) one_type = one_type && S.type[m] == S.type[0];
     hipError_t e;
-    /* one Q4_K or Q5_K matrix of whole 16-row tiles and >= 8 tokens: int8
-     * MFMA (measured on MI355X, Q4_K 2048 x 2048: 8 tokens 8.8 -> 6.3 us,
-     * 64 tokens 36 -> 8.8 us against the dot4 path) */
-    if (S.n == 1u && (S.type[0] == 12u || S.type[0] == 13u) && n_tokens >= 8u && S.rows[0] % 16u == 0u) {
-        const dim3 grid(S.rows[0] / 16u, (n_tokens + 15u) / 16u);
+    /* >= 8 tokens: each Q4_K or Q5_K matrix of whole 16-row tiles goes to the
+     * int8-MFMA kernel (measured on MI355X, Q4_K 2048 x 2048: 8 tokens
+     * 8.8 -> 6.3 us, 64 tokens 36 -> 8.8 us against the dot4 path); the
+     * other matrices of the set stay in one dot4 launch */
+    if (n_tokens >= 8u) {
+        MatSet R{};
         const uint8_t *xq = static_cast<const uint8_t *>(x_q8);
-        if (S.type[0] == 12u)
-            hipLaunchKernelGGL(k_matmul_qk_mfma<12>, grid, dim3(256), 0, stream, S.w[0], S.out[0], S.rows[0], xq, nb,
-                               n_tokens);
-        else
-            hipLaunchKernelGGL(k_matmul_qk_mfma<13>, grid, dim3(256), 0, stream, S.w[0], S.out[0], S.rows[0], xq, nb,
-                               n_tokens);
-        return hip_status(hipGetLastError());
+        for (uint32_t m = 0; m < S.n; ++m) {
+            const bool mfma = (S.type[m] == 12u || S.type[m] == 13u) && S.rows[m] % 16u == 0u;
+            if (!mfma) {
+                R.w[R.n] = S.w[m];
+                R.out[R.n] = S.out[m];
+                R.rows[R.n] = S.rows[m];
+                R.type[R.n] = S.type[m];
+                ++R.n;
+                continue;
+            }
+            const dim3 grid(S.rows[m] / 16u, (n_tokens + 15u) / 16u);
+            if (S.type[m] == 12u)
+                hipLaunchKernelGGL(k_matmul_qk_mfma<12>, grid, dim3(256), 0, stream, S.w[m], S.out[m], S.rows[m], xq,
+                                   nb, n_tokens);
+            else
+                hipLaunchKernelGGL(k_matmul_qk_mfma<13>, grid, dim3(256), 0, stream, S.w[m], S.out[m], S.rows[m], xq,
+                                   nb, n_tokens);
+            const hipError_t le = hipGetLastError();
+            if (le != hipSuccess) return hip_status(le);
+        }
+        if (R.n == 0u) return LFM_ATTN_OK;
+        S = R;
+        one_type = true;
+        for (uint32_t m = 1; m < S.n; ++m) one_type = one_type && S.type[m] == S.type[0];
     }
     switch (one_type ? S.type[0] : 0u) {
     case 12u: e = launch_tokens<12>(S, x_q8, nb, n_tokens, stream); break;

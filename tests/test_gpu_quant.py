@@ -178,16 +178,18 @@ def test_other_types_bit_exact(gpu, orc, qtype, n_rows, n_cols, B):
     assert np.array_equal(out.numpy().view(np.uint32), want.view(np.uint32)), OTHER_TYPES[qtype]
 
 
-def test_fused_mixed_types(gpu, orc):
+@pytest.mark.parametrize("B", [3, 9])
+def test_fused_mixed_types(gpu, orc, B):
     """One fused call over four matrices of four different types (Q5_K Q,
-    IQ4_XS K, Q8_0 V, Q4_0 gate), three tokens."""
+    IQ4_XS K, Q8_0 V, Q4_0 gate); at 9 tokens the Q5_K matrix takes the
+    int8-MFMA kernel and the rest one dot4 launch."""
     la = gpu
-    rng = np.random.default_rng(99)
+    rng = np.random.default_rng(99 + B)
     n_cols, rows, types = 2048, [2048, 512, 512, 16], [13, 23, 8, 2]
     ws = [q_random(rng, t, r, n_cols) for t, r in zip(types, rows)]
-    xq = orc.quantize_q8_K(rng.standard_normal((3, n_cols)).astype(np.float32))
-    outs = [la.DeviceArray.zeros((3, r), np.float32) for r in rows]
-    la.gqa_qkv_fused(outs, [dev(la, w) for w in ws], types, rows, n_cols, dev(la, xq), 3)
+    xq = orc.quantize_q8_K(rng.standard_normal((B, n_cols)).astype(np.float32))
+    outs = [la.DeviceArray.zeros((B, r), np.float32) for r in rows]
+    la.gqa_qkv_fused(outs, [dev(la, w) for w in ws], types, rows, n_cols, dev(la, xq), B)
     for o, w, t in zip(outs, ws, types):
         assert np.array_equal(o.numpy().view(np.uint32), orc.matmul_q(w, t, xq, n_cols).view(np.uint32))
 
