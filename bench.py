@@ -410,7 +410,31 @@ def cpu_baseline(wl, n_threads, max_seconds=8.0):
                       f"{dt * 1e3:.1f} ms per pass")
     if fair:
         res["fair_batched"] = fair
+    res["host"] = host_cpu()
     return res, out.reshape(n, wl.nq, wl.hd)
+
+
+def host_cpu():
+    """CPU model, logical CPUs and physical cores of the timing host."""
+    model, cores = None, set()
+    try:
+        phys = core = None
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model is None:
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    return dict(model=model, logical_cpus=os.cpu_count(), physical_cores=len(cores) or None,
+                affinity_cpus=len(os.sched_getaffinity(0)))
 
 
 def cpu_prompt_cache(rng, n_tokens=4096, reps=3):
