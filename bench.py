@@ -540,8 +540,9 @@ def main():
                     help="only the config-4 prefill workload (for kernel profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU's share only; --gpus {args.gpus} is not supported "
-              "(the sharding plan is described in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU's share only; --gpus {args.gpus} is not supported: "
+              "this build runs on one GPU (sequences or KV heads would shard across GPUs "
+              "with no exchange, each GPU running this same single-GPU path)", file=sys.stderr)
         sys.exit(2)
 
     import laii_amd as la
