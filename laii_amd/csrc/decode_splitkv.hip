@@ -411,6 +411,63 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
     run_segment<HD, NT>(P, vt_all[wave], s, k.pos0, kvh, kb, ke, P.n_splits == 1u, part);
 }
 
+/* Small batches (few (sequence, KV head) pairs): one workgroup per pair, its
+ * WW waves taking the key splits, and the log-sum-exp merge done by the same
+ * workgroup after a barrier, so no second kernel is launched.  The partials
+ * go through the workspace as on the grid (they stay in the CU's caches). */
+template <int HD, int NT, int WW>
+__global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
+    constexpr uint32_t D4 = HD / 4;
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[WW][HD * kVtStride];
+    const int lane       = threadIdx.x & 63;
+    const uint32_t split = threadIdx.x >> 6, kvh = blockIdx.x, s = blockIdx.y;
+    const SeqKeys k      = seq_keys(P, s);
+    const uint32_t total = k.last - k.lo + 1u;
+    uint32_t chunk       = P.chunk;
+    if ((uint64_t)chunk * P.n_splits < total) chunk = (((total + P.n_splits - 1u) / P.n_splits) + 31u) & ~31u;
+    const size_t base = (size_t)(s * P.n_head_kv + kvh) * P.n_splits * P.ncols;
+    if (split < P.n_splits) {
+        const uint32_t kb = k.lo + split * chunk;
+        const uint32_t ke = min(kb + chunk, k.last + 1u);
+        const size_t part = base + (size_t)split * P.ncols;
+        if (kb > k.last) {
+            for (uint32_t n = (uint32_t)lane; n < P.ncols; n += 64u) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
+        } else {
+            run_segment<HD, NT>(P, vt_all[split], s, k.pos0, kvh, kb, ke, false, part);
+        }
+    }
+    __syncthreads();
+    for (uint32_t it = threadIdx.x; it < P.ncols * D4; it += 64u * WW) {
+        const uint32_t n = it / D4, d4 = it - n * D4;
+        float M = kNegBig, L = 0.0f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (uint32_t sp = 0; sp < P.n_splits; ++sp) {
+            const size_t idx = base + (size_t)sp * P.ncols + n;
+            const float2 ml  = P.part_ml[idx];
+            const float4 o   = *reinterpret_cast<const float4 *>(P.part_o + idx * HD + 4 * d4);
+            if (ml.y > 0.0f) {
+                const float Mn = fmaxf(M, ml.x);
+                const float a  = __builtin_amdgcn_exp2f(M - Mn);
+                const float b  = __builtin_amdgcn_exp2f(ml.x - Mn);
+                L   = L * a + ml.y * b;
+                O.x = O.x * a + o.x * b;
+                O.y = O.y * a + o.y * b;
+                O.z = O.z * a + o.z * b;
+                O.w = O.w * a + o.w * b;
+                M   = Mn;
+            }
+        }
+        const uint32_t r  = n / P.kv_mul;
+        const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
+        const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+        const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+        const float inv   = (L > 0.0f) ? gv / L : 0.0f;
+        const uint32_t d  = 4 * d4;
+        if (d < P.out_dims)
+            *reinterpret_cast<float4 *>(P.out + orow * HD + d) = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+    }
+}
+
 /* ---- balanced plan -----------------------------------------------------------------
  * The batch's keys are cut into 32-key tiles and laid out as one sequence:
  * sequence major, then KV-head group, then tile (so the groups of a cache row
@@ -910,17 +967,55 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
  * plan's position scan and table (1-9 % faster on equal-length batches).  So
  * does a sliding-window batch: no row reads more than window keys, which
  * bounds how ragged it can be (config 5's ring, B32 x 256 keys: 10.7 vs
- * 11.9 us per call).  LFM_ATTN_PLAN=grid|balanced overrides (tuning and
+ * 11.9 us per call).  LFM_ATTN_PLAN=grid|balanced|wg overrides (tuning and
  * tests). */
 bool use_grid_plan(const AttnBatch &b) {
     const char *env = getenv("LFM_ATTN_PLAN");
-    if (env && env[0] == 'g') return true;
+    if (env && (env[0] == 'g' || env[0] == 'w')) return true; /* wg: a form of the grid */
     if (env && env[0] == 'b') return false;
     return !b.pos0_dev || b.n_seq == 1u || b.window != 0u;
 }
 
+/* One workgroup per (sequence, KV head), the key splits as its waves and the
+ * merge inside it (k_splitkv_wg): taken by grid-plan batches of at most a
+ * quarter as many pairs as compute units whose planned splits fit the
+ * workgroup's waves (short contexts), where a second (merge) launch would
+ * cost about as much as the attention itself.  LFM_ATTN_PLAN=grid keeps such a
+ * batch on the two-kernel grid, =wg forces this form. */
+bool use_wg_plan(const SplitParams &p, uint32_t n_seq, uint32_t ww) {
+    const char *env = getenv("LFM_ATTN_PLAN");
+    if (env && env[0] == 'w') return p.n_splits >= 2u;
+    if (env && env[0] == 'g') return false;
+    if (getenv("LFM_ATTN_WAVES") || getenv("LFM_ATTN_CHUNK")) return false;
+    /* only when the planned splits fit the workgroup's waves as they are:
+     * lengthening them measured slower than the second launch (B1 ctx 1024,
+     * 16 splits on 8 waves: 10.3 vs 8.5 us) */
+    return p.n_splits >= 2u && p.n_splits <= ww && (uint64_t)n_seq * p.n_head_kv * 4u <= device_cus();
+}
+
+template <int HD, int NT>
+constexpr uint32_t wg_waves() {
+    /* 8 waves (4 at head_dim 128 or 64 query columns, whose waves need more
+     * than the 256 registers an 8-wave workgroup leaves them) */
+    return (HD == 64 && NT <= 2) ? 8u : 4u;
+}
+
+template <int HD, int NT>
+int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
+    constexpr int WW = (int)wg_waves<HD, NT>();
+    if (p.n_splits > (uint32_t)WW) p.n_splits = WW; /* forced: the kernel lengthens the chunks */
+    hipEvent_t ev0, ev1;
+    profile_events(&ev0, &ev1);
+    if (ev0) (void)hipEventRecord(ev0, stream);
+    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW>), dim3(p.n_head_kv, n_seq), dim3(64 * WW), 0, stream, p);
+    const hipError_t e = hipGetLastError();
+    if (ev1) (void)hipEventRecord(ev1, stream);
+    return hip_status(e);
+}
+
 template <int HD, int NT>
 int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream) {
+    if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) return launch_wg<HD, NT>(p, n_seq, stream);
     uint32_t w = choose_waves(p.n_head_kv, HD);
     /* a grid of fewer workgroups than compute units (one short sequence)
      * spreads its KV heads over more, smaller workgroups: measured on MI355X

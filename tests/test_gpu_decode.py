@@ -274,3 +274,31 @@ def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
         outs.append(got)
     for o in outs[1:]:
         assert np.abs(outs[0] - o).max() < 1e-5
+
+
+@pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq,max_ctx", [
+    (64, 16, 8, 1, 1, 300),    # config-1 heads, short context: the default small-batch form
+    (64, 32, 8, 8, 2, 400),    # verify rows (32 query columns)
+    (64, 32, 4, 8, 1, 200),    # 64 query columns (four-wave workgroups)
+    (128, 16, 4, 1, 3, 500),   # LFM3 head_dim 128
+    (64, 32, 8, 1, 2, 3000),   # forced: more planned splits than waves, chunks lengthened
+])
+def test_workgroup_merge_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq, max_ctx):
+    """Small batches take one workgroup per (sequence, KV head) whose waves
+    split the keys and merge in place (k_splitkv_wg, LFM_ATTN_PLAN=wg forces
+    it); it matches the oracle and the two-kernel grid."""
+    la = gpu
+    rng = np.random.default_rng(max_ctx + n_seq + hd)
+    ctx = [int(c) for c in rng.integers(1, max_ctx, size=n_seq)]
+    ctx[0] = max_ctx - 1
+    outs = []
+    for env in ({"LFM_ATTN_PLAN": "wg"}, {"LFM_ATTN_PLAN": "grid"}):
+        os.environ.update(env)
+        try:
+            got, want = _varlen_case(la, orc, np.random.default_rng(9), n_seq, n_rows, nq, nkv, hd, ctx)
+        finally:
+            for k in env:
+                os.environ.pop(k, None)
+        parity(got, want, what=f"{env}")
+        outs.append(got)
+    assert np.abs(outs[0] - outs[1]).max() < 1e-5
