@@ -35,6 +35,7 @@
 
 #include "attn_index.h"
 #include "kernels.h"
+#include "splitkv_plan.h"
 #include "lfm_attn.h"
 
 namespace lfm {
@@ -63,10 +64,10 @@ struct SplitParams {
     float2 *part_ml; /* [seq][kvh][split][col] (running max, sum) in log2 units */
     uint32_t pos0_host, n_rows, n_head_q, n_head_kv, kv_mul, ncols;
     uint32_t window, cap, n_splits, chunk, out_dims;
-    /* balanced plan (k_splitkv_bal): n_wg workgroups share the batch's 32-key
-     * tiles evenly; each takes at least min_tiles */
-    uint32_t n_seq, n_groups, n_wg, min_tiles, wpg; /* n_wg: workgroups launched; wpg: KV heads per group */
-    uint32_t n_res, target_waves; /* resident workgroups; waves per uniform batch */
+    /* balanced plan (k_splitkv_bal): plan.n_wg workgroups share the batch's
+     * 32-key tiles evenly (splitkv_plan.h); wpg: KV heads per group */
+    lfm_bal_cfg plan;
+    uint32_t wpg;
     uint32_t *tile_prefix; /* [n_seq + 2] tiles before each sequence, then G (device positions) */
     int gate_is_logit;
     float qscale; /* scale * log2(e) */
@@ -480,17 +481,9 @@ __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
  * short sequences leave XCDs idle.)  G is the resident workgroup count, or
  * fewer so that each takes >= min_tiles; when every sequence has the same
  * length, G is a multiple of the (sequence, group) count so that segments
- * never straddle two sequences.
- * Segment (g, unit v = s * n_groups + group) writes partial slot g + v: the
- * workgroups meeting unit v are owner(first tile) .. owner(last tile), a run
- * that no other unit's slots overlap, so slots are unique and number
- * < G + n_seq * n_groups.  A unit that one workgroup covers whole is written
- * directly. */
-__device__ __forceinline__ uint32_t tiles_at(const SplitParams &P, uint32_t pos0) {
-    const uint32_t lo = lfm_plan_row(pos0, P.window, P.cap).t_start;
-    return (pos0 + P.n_rows - 1u - lo + 32u) >> 5;
-}
-
+ * never straddle two sequences.  The index math (shares, segments, partial
+ * slots, the merge's slot range) is splitkv_plan.h, which the tests run on
+ * the CPU over random ragged batches. */
 __device__ __forceinline__ uint32_t wave_sum(uint32_t x) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
@@ -513,54 +506,32 @@ struct TilePlan {
     bool uniform;      /* every sequence has the same number of tiles         */
 };
 
-/* Workgroups for the batch's totals. */
-__device__ __forceinline__ uint32_t plan_wgs(const SplitParams &P, uint32_t T, bool uniform) {
-    const uint64_t N     = (uint64_t)T * P.n_groups;
-    const uint32_t units = P.n_seq * P.n_groups;
-    uint64_t G;
-    if (uniform) {
-        /* equal sequences: every (sequence, group) unit gets n equal
-         * workgroups, about target_waves waves over the batch (several
-         * residency rounds absorb slow workgroups) */
-        const uint32_t tiles = T / P.n_seq;
-        uint64_t ct = ((uint64_t)tiles * P.n_seq * P.n_head_kv + P.target_waves - 1u) / P.target_waves;
-        if (ct < P.min_tiles) ct = P.min_tiles;
-        G = (uint64_t)units * ((tiles + ct - 1u) / ct);
-    } else {
-        /* ragged: one residency round of equal shares */
-        G = N / P.min_tiles;
-        if (G > P.n_res) G = P.n_res;
-    }
-    if (G > P.n_wg) G = P.n_wg;
-    if (uniform && G >= units) G -= G % units;
-    return (uint32_t)(G ? G : 1u);
-}
-
 /* All lanes of the wave take part (wave-wide reductions). */
 __device__ __forceinline__ TilePlan tile_plan(const SplitParams &P, int lane) {
     TilePlan p;
+    const lfm_bal_cfg &c = P.plan;
     if (!P.pos0_dev) {
         p.lane_pos = P.pos0_host;
-        p.T        = P.n_seq * tiles_at(P, P.pos0_host);
+        p.T        = c.n_seq * lfm_bal_seq_tiles(&c, P.pos0_host);
         p.uniform  = true;
     } else {
         uint32_t sum = 0, odd = 0, t0 = 0;
-        for (uint32_t b = 0; b < P.n_seq; b += 64u) {
+        for (uint32_t b = 0; b < c.n_seq; b += 64u) {
             const uint32_t s   = b + (uint32_t)lane;
-            const uint32_t pos = s < P.n_seq ? P.pos0_dev[s] : 0u;
-            uint32_t x         = s < P.n_seq ? tiles_at(P, pos) : 0u;
+            const uint32_t pos = s < c.n_seq ? P.pos0_dev[s] : 0u;
+            uint32_t x         = s < c.n_seq ? lfm_bal_seq_tiles(&c, pos) : 0u;
             if (b == 0u) {
                 p.lane_pos = pos;
                 t0         = __shfl(x, 0);
             }
             sum += wave_sum(x);
-            if (s >= P.n_seq) x = t0;
+            if (s >= c.n_seq) x = t0;
             odd |= (uint32_t)(__ballot(x != t0) != 0);
         }
         p.T       = sum;
         p.uniform = odd == 0u;
     }
-    p.G = plan_wgs(P, p.T, p.uniform);
+    p.G = lfm_bal_plan_wgs(&c, p.T, p.uniform);
     return p;
 }
 
@@ -570,16 +541,17 @@ __device__ __forceinline__ uint32_t pos_of(const SplitParams &P, const TilePlan 
 }
 
 /* Ragged batches: the sequence holding tile t (0 <= t < N) and its first
- * tile (prefix over sequences of n_groups * tiles). */
+ * tile -- the wave-parallel form of a prefix walk over n_groups * tiles(s). */
 __device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int lane, uint32_t *s_out,
                                          uint64_t *first_out) {
+    const lfm_bal_cfg &c = P.plan;
     uint64_t base = 0;
     for (uint32_t b = 0;; b += 64u) {
         const uint32_t s    = b + (uint32_t)lane;
-        const uint32_t x    = s < P.n_seq ? tiles_at(P, P.pos0_dev[s]) * P.n_groups : 0u;
+        const uint32_t x    = s < c.n_seq ? lfm_bal_seq_tiles(&c, P.pos0_dev[s]) * c.n_groups : 0u;
         const uint32_t incl = wave_incl_scan(x, lane);
         const uint32_t tot  = __shfl(incl, 63);
-        if (t < base + tot || b + 64u >= P.n_seq) {
+        if (t < base + tot || b + 64u >= c.n_seq) {
             const uint64_t m = __ballot(base + incl > t);
             const int l      = m ? (int)__builtin_ctzll(m) : 0;
             *s_out           = b + (uint32_t)l;
@@ -590,76 +562,62 @@ __device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int l
     }
 }
 
-__device__ __forceinline__ uint32_t tile_owner(uint64_t t, uint64_t n_tiles, uint32_t G) {
-    return (uint32_t)(((t + 1u) * G - 1u) / n_tiles);
-}
-
 template <int HD, int NT, int W>
 __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
+    const lfm_bal_cfg &c = P.plan;
     const int lane       = threadIdx.x & 63;
     const uint32_t wave  = threadIdx.x >> 6;
     const uint32_t wg    = blockIdx.x;
-    const uint32_t units = P.n_seq * P.n_groups;
     const TilePlan pl    = tile_plan(P, lane);
     if (wg == 0u && wave == 0u && P.pos0_dev) {
         /* tiles before each sequence and the plan, for the merge */
         uint32_t base = 0;
-        for (uint32_t b = 0; b < P.n_seq; b += 64u) {
+        for (uint32_t b = 0; b < c.n_seq; b += 64u) {
             const uint32_t s    = b + (uint32_t)lane;
-            const uint32_t x    = s < P.n_seq ? tiles_at(P, pos_of(P, pl, s)) : 0u;
+            const uint32_t x    = s < c.n_seq ? lfm_bal_seq_tiles(&c, pos_of(P, pl, s)) : 0u;
             const uint32_t incl = wave_incl_scan(x, lane);
-            if (s < P.n_seq) P.tile_prefix[s] = base + incl - x;
+            if (s < c.n_seq) P.tile_prefix[s] = base + incl - x;
             base += __shfl(incl, 63);
         }
         if (lane == 0) {
-            P.tile_prefix[P.n_seq]      = base;
-            P.tile_prefix[P.n_seq + 1u] = pl.G;
+            P.tile_prefix[c.n_seq]      = base;
+            P.tile_prefix[c.n_seq + 1u] = pl.G;
         }
     }
     if (wg >= pl.G) return;
     if (pl.uniform) {
         /* unit = (sequence, group), n workgroups per unit, equal shares */
-        const uint32_t tiles = pl.T / P.n_seq;
-        const uint32_t n     = pl.G / units;
-        const uint32_t unit  = wg / n, sp = wg - unit * n;
-        const uint32_t s = unit / P.n_groups, grp = unit - s * P.n_groups;
-        const uint32_t kvh = grp * W + wave;
+        const lfm_bal_useg u = lfm_bal_uniform_segment(&c, wg, pl.G, pl.T / c.n_seq);
+        const uint32_t kvh   = u.grp * W + wave;
         if (kvh >= P.n_head_kv) return;
-        const uint32_t a    = (uint32_t)((uint64_t)sp * tiles / n);
-        const uint32_t b    = (uint32_t)((uint64_t)(sp + 1u) * tiles / n);
-        const uint32_t pos0 = pos_of(P, pl, s);
-        const uint32_t lo   = lfm_plan_row(pos0, P.window, P.cap).t_start;
-        const uint32_t kb   = lo + 32u * a;
-        const uint32_t ke   = min(lo + 32u * b, pos0 + P.n_rows);
-        const size_t slot   = (size_t)wg + unit;
-        run_segment<HD, NT>(P, vt_all[wave], s, pos0, kvh, kb, ke, n == 1u, (slot * P.n_head_kv + kvh) * P.ncols);
+        const uint32_t pos0 = pos_of(P, pl, u.s);
+        uint32_t kb, ke;
+        lfm_bal_seg_keys(&c, pos0, u.a, u.b, &kb, &ke);
+        run_segment<HD, NT>(P, vt_all[wave], u.s, pos0, kvh, kb, ke, u.n == 1u,
+                            ((size_t)u.slot * P.n_head_kv + kvh) * P.ncols);
         return;
     }
-    const uint64_t N  = (uint64_t)pl.T * P.n_groups;
-    uint64_t t        = (uint64_t)wg * N / pl.G;
-    const uint64_t t1 = (uint64_t)(wg + 1u) * N / pl.G;
+    const uint64_t N = (uint64_t)pl.T * c.n_groups;
+    uint64_t t, t1;
+    lfm_bal_wg_tiles(wg, N, pl.G, &t, &t1);
     uint32_t s;
     uint64_t first;
     find_seq(P, t, lane, &s, &first);
     while (t < t1) {
         const uint32_t pos0  = pos_of(P, pl, s);
-        const uint32_t lo    = lfm_plan_row(pos0, P.window, P.cap).t_start;
-        const uint32_t tiles = (pos0 + P.n_rows - 1u - lo + 32u) >> 5;
-        const uint32_t grp   = (uint32_t)((t - first) / tiles);
-        const uint64_t u0    = first + (uint64_t)grp * tiles; /* the unit's tile 0 */
-        const uint64_t e     = min(t1, u0 + tiles);
-        const uint32_t a = (uint32_t)(t - u0), b = (uint32_t)(e - u0);
-        const uint32_t kvh = grp * W + wave;
+        const uint32_t tiles = lfm_bal_seq_tiles(&c, pos0);
+        const lfm_bal_seg sg = lfm_bal_segment(t, t1, first, tiles);
+        const uint32_t kvh   = sg.grp * W + wave;
         if (kvh < P.n_head_kv) {
-            const uint32_t kb = lo + 32u * a;
-            const uint32_t ke = min(lo + 32u * b, pos0 + P.n_rows);
-            const size_t slot = (size_t)wg + (size_t)s * P.n_groups + grp;
-            run_segment<HD, NT>(P, vt_all[wave], s, pos0, kvh, kb, ke, a == 0u && b == tiles,
-                                (slot * P.n_head_kv + kvh) * P.ncols);
+            uint32_t kb, ke;
+            lfm_bal_seg_keys(&c, pos0, sg.a, sg.b, &kb, &ke);
+            const uint64_t slot = lfm_bal_slot(wg, s, c.n_groups, sg.grp);
+            run_segment<HD, NT>(P, vt_all[wave], s, pos0, kvh, kb, ke, sg.whole != 0,
+                                ((size_t)slot * P.n_head_kv + kvh) * P.ncols);
         }
-        t = e;
-        if (t == first + (uint64_t)tiles * P.n_groups) {
+        t = sg.end;
+        if (t == first + (uint64_t)tiles * c.n_groups) {
             first = t;
             ++s;
         }
@@ -674,12 +632,13 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
     constexpr uint32_t D4 = HD / 4;
     constexpr uint32_t SG = 4;
+    const lfm_bal_cfg &c  = P.plan;
     const uint32_t t      = blockIdx.x * 256u + threadIdx.x;
     const uint32_t q      = t % SG;
     const uint32_t per    = P.ncols * D4; /* items per (sequence, KV head) */
     const uint32_t item   = t / SG;
     const uint32_t w      = item / per;   /* s * n_head_kv + kvh */
-    const bool live       = w < P.n_seq * P.n_head_kv;
+    const bool live       = w < c.n_seq * P.n_head_kv;
     const uint32_t wl     = live ? w : 0u;
     const uint32_t s = wl / P.n_head_kv, kvh = wl - s * P.n_head_kv;
     const uint32_t grp = kvh / P.wpg;
@@ -687,20 +646,18 @@ __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
     const uint32_t n = rem / D4, d4 = rem - n * D4;
     uint32_t T, G, tiles, before;
     if (!P.pos0_dev) {
-        tiles  = tiles_at(P, P.pos0_host);
-        T      = P.n_seq * tiles;
+        tiles  = lfm_bal_seq_tiles(&c, P.pos0_host);
+        T      = c.n_seq * tiles;
         before = s * tiles;
-        G      = plan_wgs(P, T, true);
+        G      = lfm_bal_plan_wgs(&c, T, 1);
     } else { /* the attention kernel's plan */
         before = P.tile_prefix[s];
         tiles  = P.tile_prefix[s + 1u] - before;
-        T      = P.tile_prefix[P.n_seq];
-        G      = P.tile_prefix[P.n_seq + 1u];
+        T      = P.tile_prefix[c.n_seq];
+        G      = P.tile_prefix[c.n_seq + 1u];
     }
-    const uint64_t N  = (uint64_t)T * P.n_groups;
-    const uint64_t u0 = (uint64_t)before * P.n_groups + (uint64_t)grp * tiles;
-    const uint32_t g0 = tile_owner(u0, N, G), g1 = tile_owner(u0 + tiles - 1u, N, G);
-    const size_t v    = (size_t)s * P.n_groups + grp;
+    uint32_t g0, g1;
+    lfm_bal_merge_range(before, tiles, grp, T, c.n_groups, G, &g0, &g1);
     float M = kNegBig, L = 0.0f;
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live && g0 != g1) {
@@ -713,9 +670,10 @@ __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
                 ml[j] = make_float2(kNegBig, 0.0f);
                 o[j]  = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (g + j * SG <= g1) {
-                    const size_t idx = (((size_t)(g + j * SG) + v) * P.n_head_kv + kvh) * P.ncols + n;
-                    ml[j]            = P.part_ml[idx];
-                    o[j]             = *reinterpret_cast<const float4 *>(P.part_o + idx * HD + 4 * d4);
+                    const size_t slot = (size_t)lfm_bal_slot(g + j * SG, s, c.n_groups, grp);
+                    const size_t idx  = (slot * P.n_head_kv + kvh) * P.ncols + n;
+                    ml[j]             = P.part_ml[idx];
+                    o[j]              = *reinterpret_cast<const float4 *>(P.part_o + idx * HD + 4 * d4);
                 }
             }
 #pragma unroll
@@ -886,63 +844,40 @@ uint32_t resident_wgs() {
 template <int HD, int NT, int W>
 int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
     const uint32_t cus = device_cus();
-    p.wpg          = W;
-    p.n_groups     = (p.n_head_kv + W - 1u) / W;
-    p.n_res        = resident_wgs<HD, NT, W>();
+    lfm_bal_cfg &c     = p.plan;
+    p.wpg              = W;
+    c.n_groups         = (p.n_head_kv + W - 1u) / W;
+    c.n_res            = resident_wgs<HD, NT, W>();
     /* 16 waves per CU over a batch of equal sequences: two residency rounds of
      * 8-wave workgroups at head_dim 64 (measured best on MI355X) */
-    p.target_waves = 16u * cus;
+    c.target_waves = 16u * cus;
     /* each workgroup's partials cost about one 32-key tile per 32 query
      * columns: keep >= 12 tiles per workgroup per 32 columns (measured on
      * MI355X for 8 rows x 4 heads), and >= 2 tiles */
-    p.min_tiles = (12u * p.ncols + 31u) / 32u;
-    if (p.min_tiles < 2u) p.min_tiles = 2u;
-    /* launch: enough workgroups for either plan.  With at most `tiles`
-     * tiles per sequence, a uniform batch needs units * n, n <=
-     * ceil(target_waves / (n_seq * n_head_kv)) and n <= ceil(tiles /
-     * min_tiles); a ragged one min(n_res, N / min_tiles).  keys_hint bounds the
-     * tiles; without it (or if it is wrong) the device plan is capped by the
-     * launch, which only makes the shares longer. */
-    const uint64_t units = (uint64_t)p.n_groups * p.n_seq;
-    uint64_t n_launch;
-    {
-        uint32_t keys = p.pos0_dev ? keys_hint : 0u;
-        if (!p.pos0_dev) {
-            const uint32_t lo = lfm_plan_row(p.pos0_host, p.window, p.cap).t_start;
-            keys              = p.pos0_host + p.n_rows - lo;
-        }
-        const uint64_t pairs  = (uint64_t)p.n_seq * p.n_head_kv;
-        uint64_t per_unit     = (p.target_waves + pairs - 1u) / pairs; /* uniform n bound */
-        uint64_t ragged       = p.n_res;
-        if (keys) {
-            const uint64_t most = (((uint64_t)keys + 31u) / 32u + p.min_tiles - 1u) / p.min_tiles;
-            if (per_unit > most) per_unit = most;
-            if (ragged > units * most) ragged = units * most;
-        }
-        n_launch = units * per_unit;
-        if (n_launch < ragged) n_launch = ragged;
-        if (n_launch < units) n_launch = units;
-    }
+    c.min_tiles = (12u * p.ncols + 31u) / 32u;
+    if (c.min_tiles < 2u) c.min_tiles = 2u;
+    /* keys_hint bounds the keys a row attends */
+    uint32_t keys = keys_hint;
+    if (!p.pos0_dev) keys = p.pos0_host + p.n_rows - lfm_plan_row(p.pos0_host, p.window, p.cap).t_start;
     if (const char *env = getenv("LFM_ATTN_CHUNK")) {
         /* about c keys per workgroup (tests, tuning): enough workgroups for
          * the longest sequences keys_hint allows; longer ones get more keys */
-        const int c = atoi(env);
-        if (c > 0) {
-            p.min_tiles   = (uint32_t)(c + 31) / 32u;
-            p.n_res       = 0x7fffffffu;
-            p.target_waves = 0x7fffffffu;
-            uint32_t keys = p.pos0_dev ? keys_hint : p.pos0_host + p.n_rows;
+        const int ck = atoi(env);
+        if (ck > 0) {
+            c.min_tiles    = (uint32_t)(ck + 31) / 32u;
+            c.n_res        = 0x7fffffffu;
+            c.target_waves = 0x7fffffffu;
+            keys           = p.pos0_dev ? keys_hint : p.pos0_host + p.n_rows;
             if (keys == 0u) keys = p.window ? p.window + p.n_rows - 1u : 4096u;
-            n_launch = units * (((keys + 31u) / 32u + p.min_tiles - 1u) / p.min_tiles);
         }
     }
-    if (n_launch > 0x1000000u) n_launch = 0x1000000u;
-    p.n_wg = (uint32_t)n_launch;
-    const size_t n_part  = ((size_t)n_launch + (size_t)p.n_groups * p.n_seq) * p.n_head_kv * p.ncols;
+    c.n_wg                  = lfm_bal_launch_wgs(&c, keys);
+    const uint64_t n_launch = c.n_wg;
+    const size_t n_part  = (size_t)lfm_bal_n_slots(c.n_wg, c.n_groups, c.n_seq) * p.n_head_kv * p.ncols;
     const size_t o_bytes = (n_part * HD * sizeof(float) + 255) & ~(size_t)255;
     const size_t m_bytes = (n_part * sizeof(float2) + 255) & ~(size_t)255;
     int st   = LFM_ATTN_OK;
-    char *ws = static_cast<char *>(workspace(o_bytes + m_bytes + ((size_t)p.n_seq + 2u) * sizeof(uint32_t), stream, &st));
+    char *ws = static_cast<char *>(workspace(o_bytes + m_bytes + ((size_t)c.n_seq + 2u) * sizeof(uint32_t), stream, &st));
     if (!ws) return st;
     p.part_o      = reinterpret_cast<float *>(ws);
     p.part_ml     = reinterpret_cast<float2 *>(ws + o_bytes);
@@ -954,7 +889,7 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     if (e != hipSuccess) return hip_status(e);
-    const uint64_t mt = (uint64_t)p.n_seq * p.n_head_kv * p.ncols * (HD / 4) * 4u;
+    const uint64_t mt = (uint64_t)c.n_seq * p.n_head_kv * p.ncols * (HD / 4) * 4u;
     hipLaunchKernelGGL((k_merge_bal<HD>), dim3((uint32_t)((mt + 255u) / 256u)), dim3(256), 0, stream, p);
     return hip_status(hipGetLastError());
 }
@@ -1098,7 +1033,11 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
     p.cap           = b.cap;
     p.out_dims      = b.out_dims;
     p.qscale        = b.scale * kLog2e;
-    p.n_seq         = b.n_seq;
+    p.plan.n_seq    = b.n_seq;
+    p.plan.n_rows   = b.n_rows;
+    p.plan.n_head_kv = b.n_head_kv;
+    p.plan.window   = b.window;
+    p.plan.cap      = b.cap;
     const uint32_t nt = (p.ncols + 15u) / 16u;
     const bool grid   = use_grid_plan(b);
     if (!grid) {
