@@ -41,6 +41,7 @@ extern "C" {
 #define LFM_ATTN_E_DEVICE     -4 /* HIP runtime error (see lfm_attn_last_error)    */
 #define LFM_ATTN_E_NOMEM      -5 /* device allocation failed                       */
 #define LFM_ATTN_E_IO         -6 /* a file could not be written                     */
+#define LFM_ATTN_E_SCRATCH    -7 /* more split partials than the no-alloc scratch holds */
 
 typedef void *lfm_attn_stream_t; /* hipStream_t */
 
@@ -234,6 +235,25 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
                            uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
                            uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
                            lfm_attn_stream_t stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): lfm_hip_gqa_f16_varlen with the same arguments, kernels
+ * and results, whose split partials go to a fixed device array of the
+ * library (LFM_ATTN_NOALLOC_SCRATCH_BYTES per device, held until the process
+ * ends) instead of the growing workspace, so the call allocates nothing.  A
+ * batch whose partials need more returns LFM_ATTN_E_SCRATCH before anything
+ * is launched.  Every call on a device shares that device's array: calls that
+ * overlap on one device (any streams) race.  Nothing in the array needs to
+ * start at zero: every partial the merge reads is written earlier by the
+ * same call. */
+#define LFM_ATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int lfm_hip_gqa_f16_varlen_noalloc(const float *q, const float *gate, int gate_is_logit,
+                                   const uint16_t *const *k_seq, const uint16_t *const *v_seq,
+                                   const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
+                                   uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                                   uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                                   lfm_attn_stream_t stream);
 
 /* Causal prefill on MFMA -- the prompt path of lfm2_prefill_prompt /
  * lfm2_forward_batch (tools/lfm2_prefill_batch.c:1129-1199), whose attention

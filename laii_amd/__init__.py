@@ -18,6 +18,7 @@ from .attention import (  # noqa: F401
     device_count,
     fnv1a64,
     gqa_f16_varlen,
+    gqa_f16_varlen_noalloc,
     gqa_heads,
     gqa_qkv_fused,
     kv_cache_shift_sinks,

@@ -238,6 +238,20 @@ def gqa_f16_varlen(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Pt
                                         cap, scale, stream), "lfm_hip_gqa_f16_varlen")
 
 
+def gqa_f16_varlen_noalloc(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr,
+                           out: Ptr, n_seq: int, n_rows: int, keys_hint: int, n_head_q: int,
+                           n_head_kv: int, head_dim: int, window_len: int = 0, cap: int = 0,
+                           scale: Optional[float] = None, stream=None) -> None:
+    """gqa_f16_varlen whose split partials go to the library's fixed device
+    array instead of its workspace (the call allocates nothing)."""
+    if scale is None:
+        scale = float(1.0 / np.sqrt(np.float32(head_dim)))
+    check(load().lfm_hip_gqa_f16_varlen_noalloc(_p(q), _p(gate), int(bool(gate_is_logit)), _p(k_seq),
+                                                _p(v_seq), _p(pos_0), _p(out), n_seq, n_rows,
+                                                keys_hint, n_head_q, n_head_kv, head_dim, window_len,
+                                                cap, scale, stream), "lfm_hip_gqa_f16_varlen_noalloc")
+
+
 def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0: int,
                 kv_seq_stride: int, n_head_q: int, n_head_kv: int, head_dim: int,
                 scale: Optional[float] = None, stream=None) -> None:

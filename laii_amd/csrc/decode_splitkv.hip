@@ -811,6 +811,17 @@ uint32_t device_cus() {
     return cus;
 }
 
+/* Split partials: the caller's scratch (the allocation-free entry point) or
+ * the library workspace (grown on demand). */
+void *split_ws(size_t bytes, hipStream_t stream, const Scratch *sc, int *st) {
+    if (!sc) return workspace(bytes, stream, st);
+    if (bytes > sc->bytes) {
+        *st = LFM_ATTN_E_SCRATCH;
+        return nullptr;
+    }
+    return sc->ptr;
+}
+
 /* Waves per workgroup: W adjacent KV heads over one key chunk.  Measured on
  * MI355X: all KV heads of a row together (W = n_head_kv, up to 8) for
  * head_dim 64; W = 2 for head_dim 128, whose waves are register-heavy.
@@ -842,7 +853,7 @@ uint32_t resident_wgs() {
 /* Balanced plan: launch sized for the plan the device will pick, partial
  * slots and the tile prefix table in the workspace, then the merge. */
 template <int HD, int NT, int W>
-int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
+int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scratch *sc) {
     const uint32_t cus = device_cus();
     lfm_bal_cfg &c     = p.plan;
     p.wpg              = W;
@@ -877,7 +888,7 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream) {
     const size_t o_bytes = (n_part * HD * sizeof(float) + 255) & ~(size_t)255;
     const size_t m_bytes = (n_part * sizeof(float2) + 255) & ~(size_t)255;
     int st   = LFM_ATTN_OK;
-    char *ws = static_cast<char *>(workspace(o_bytes + m_bytes + ((size_t)c.n_seq + 2u) * sizeof(uint32_t), stream, &st));
+    char *ws = static_cast<char *>(split_ws(o_bytes + m_bytes + ((size_t)c.n_seq + 2u) * sizeof(uint32_t), stream, sc, &st));
     if (!ws) return st;
     p.part_o      = reinterpret_cast<float *>(ws);
     p.part_ml     = reinterpret_cast<float2 *>(ws + o_bytes);
@@ -949,7 +960,8 @@ int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
 }
 
 template <int HD, int NT>
-int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream) {
+int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream,
+                 const Scratch *sc) {
     if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) return launch_wg<HD, NT>(p, n_seq, stream);
     uint32_t w = choose_waves(p.n_head_kv, HD);
     /* a grid of fewer workgroups than compute units (one short sequence)
@@ -959,10 +971,10 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool 
     if (grid && !getenv("LFM_ATTN_WAVES"))
         while (w > 1u && (uint64_t)p.n_splits * ((p.n_head_kv + w - 1u) / w) * n_seq < device_cus()) w >>= 1;
     if (!grid) {
-        if (w == 8u) return launch_bal<HD, NT, 8>(p, keys_hint, stream);
-        if (w == 4u) return launch_bal<HD, NT, 4>(p, keys_hint, stream);
-        if (w == 2u) return launch_bal<HD, NT, 2>(p, keys_hint, stream);
-        return launch_bal<HD, NT, 1>(p, keys_hint, stream);
+        if (w == 8u) return launch_bal<HD, NT, 8>(p, keys_hint, stream, sc);
+        if (w == 4u) return launch_bal<HD, NT, 4>(p, keys_hint, stream, sc);
+        if (w == 2u) return launch_bal<HD, NT, 2>(p, keys_hint, stream, sc);
+        return launch_bal<HD, NT, 1>(p, keys_hint, stream, sc);
     }
     hipError_t e;
     if (w == 8u) e = launch_hd_nt_w<HD, NT, 8>(p, n_seq, stream);
@@ -1010,7 +1022,7 @@ bool splitkv_supports(const AttnBatch &b) {
     return ncols <= 32u;
 }
 
-int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
+int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, const Scratch *sc) {
     if (!splitkv_supports(b)) return LFM_ATTN_E_UNSUPPORTED;
     SplitParams p{};
     p.q             = b.q;
@@ -1042,30 +1054,30 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
     const bool grid   = use_grid_plan(b);
     if (!grid) {
         if (b.head_dim == 64u) {
-            if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream);
-            if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream);
-            return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream);
+            if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
+            if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
+            return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream, sc);
         }
-        if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream);
-        return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream);
+        if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
+        return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
     }
     choose_split(b, keys_hint, &p.n_splits, &p.chunk);
     if (p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
         const size_t bytes  = n_part * b.head_dim * sizeof(float) + n_part * sizeof(float2) + 256;
         int st              = LFM_ATTN_OK;
-        char *ws            = static_cast<char *>(workspace(bytes, stream, &st));
+        char *ws            = static_cast<char *>(split_ws(bytes, stream, sc, &st));
         if (!ws) return st;
         p.part_o  = reinterpret_cast<float *>(ws);
         p.part_ml = reinterpret_cast<float2 *>(ws + ((n_part * b.head_dim * sizeof(float) + 255) & ~(size_t)255));
     }
     if (b.head_dim == 64u) {
-        if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream);
-        if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream);
-        return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream);
+        if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
+        if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
+        return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream, sc);
     }
-    if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream);
-    return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream);
+    if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
+    return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
 }
 
 } // namespace lfm

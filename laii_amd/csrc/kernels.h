@@ -36,10 +36,19 @@ struct AttnBatch {
 /* Device workspace owned by the shim (grown on demand). */
 void *workspace(size_t bytes, hipStream_t stream, int *status);
 
+/* Device memory handed to a launch for its split partials in place of the
+ * library workspace (the allocation-free entry point). */
+struct Scratch {
+    void *ptr;
+    size_t bytes;
+};
+
 /* Split-KV MFMA kernel for fp16 caches, head_dim 64 or 128, up to 64 query
  * columns (n_rows * kv_mul) per KV head.  Returns LFM_ATTN_E_UNSUPPORTED for
- * other shapes (the caller then uses the generic kernel). */
-int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream);
+ * other shapes (the caller then uses the generic kernel).  Split partials go
+ * to `sc` when non-null (LFM_ATTN_E_SCRATCH, nothing launched, when they do
+ * not fit), else to the library workspace. */
+int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, const Scratch *sc = nullptr);
 bool splitkv_supports(const AttnBatch &b);
 
 /* Generic one-wave-per-head kernel (any head_dim % 8 == 0, <= 256), fp16 or

@@ -64,6 +64,35 @@ void *workspace(size_t bytes, hipStream_t stream, int *status) {
     return w.ptr;
 }
 
+/* Split partials of lfm_hip_gqa_f16_varlen_noalloc: one fixed array per
+ * device, resolved to its device address once per device (the array's name
+ * is a host-side stand-in: only the address from hipGetSymbolAddress may be
+ * handed to kernels). */
+static __device__ __align__(256) unsigned char scratch[LFM_ATTN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mutex;
+std::vector<void *> g_scratch_ptr;
+} // namespace
+
+static int noalloc_scratch(Scratch *out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if ((size_t)dev >= g_scratch_ptr.size()) g_scratch_ptr.resize((size_t)dev + 1, nullptr);
+    if (!g_scratch_ptr[(size_t)dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (!ptr) return LFM_ATTN_E_DEVICE;
+        g_scratch_ptr[(size_t)dev] = ptr;
+    }
+    out->ptr   = g_scratch_ptr[(size_t)dev];
+    out->bytes = LFM_ATTN_NOALLOC_SCRATCH_BYTES;
+    return LFM_ATTN_OK;
+}
+
 } // namespace lfm
 
 using lfm::AttnBatch;
@@ -71,10 +100,11 @@ using lfm::AttnBatch;
 static inline hipStream_t to_stream(lfm_attn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0u; }
 
-static int dispatch_f16(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream) {
+static int dispatch_f16(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream,
+                        const lfm::Scratch *sc = nullptr) {
     const bool fast = lfm::splitkv_supports(b) && aligned16(b.q) && aligned16(b.out) &&
                       (b.k_seq || (aligned16(b.k_base) && aligned16(b.v_base)));
-    if (fast) return lfm::launch_splitkv(b, keys_hint, stream);
+    if (fast) return lfm::launch_splitkv(b, keys_hint, stream, sc);
     return lfm::launch_generic(b, false, stream);
 }
 
@@ -89,6 +119,7 @@ const char *lfm_attn_status_string(int status) {
     case LFM_ATTN_E_DEVICE: return "device error";
     case LFM_ATTN_E_NOMEM: return "out of device memory";
     case LFM_ATTN_E_IO: return "file could not be written";
+    case LFM_ATTN_E_SCRATCH: return "split partials exceed the no-alloc scratch";
     default: return "unknown status";
     }
 }
@@ -386,12 +417,11 @@ int lfm_hip_lfm3_online_gqa_f16_dispatch(const float *q_batch, const float *gate
     return dispatch_f16(b, max_keys, to_stream(stream));
 }
 
-int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
-                           const uint16_t *const *k_seq, const uint16_t *const *v_seq,
-                           const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
-                           uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
-                           uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
-                           lfm_attn_stream_t stream) {
+static int varlen_call(const float *q, const float *gate, int gate_is_logit, const uint16_t *const *k_seq,
+                       const uint16_t *const *v_seq, const uint32_t *pos_0, float *out, uint32_t n_seq,
+                       uint32_t n_rows, uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                       uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                       lfm_attn_stream_t stream, bool noalloc) {
     if (!q || !k_seq || !v_seq || !pos_0 || !out) return LFM_ATTN_E_INVALID;
     if (n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u ||
         n_head_q % n_head_kv != 0u)
@@ -416,7 +446,31 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
     b.window = window_len;
     b.cap = cap;
     b.scale = scale;
-    return dispatch_f16(b, keys_hint, to_stream(stream));
+    if (!noalloc) return dispatch_f16(b, keys_hint, to_stream(stream));
+    lfm::Scratch sc;
+    const int st = lfm::noalloc_scratch(&sc);
+    if (st != LFM_ATTN_OK) return st;
+    return dispatch_f16(b, keys_hint, to_stream(stream), &sc);
+}
+
+int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
+                           const uint16_t *const *k_seq, const uint16_t *const *v_seq,
+                           const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
+                           uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                           uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                           lfm_attn_stream_t stream) {
+    return varlen_call(q, gate, gate_is_logit, k_seq, v_seq, pos_0, out, n_seq, n_rows, keys_hint, n_head_q,
+                       n_head_kv, head_dim, window_len, cap, scale, stream, false);
+}
+
+int lfm_hip_gqa_f16_varlen_noalloc(const float *q, const float *gate, int gate_is_logit,
+                                   const uint16_t *const *k_seq, const uint16_t *const *v_seq,
+                                   const uint32_t *pos_0, float *out, uint32_t n_seq, uint32_t n_rows,
+                                   uint32_t keys_hint, uint32_t n_head_q, uint32_t n_head_kv,
+                                   uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                                   lfm_attn_stream_t stream) {
+    return varlen_call(q, gate, gate_is_logit, k_seq, v_seq, pos_0, out, n_seq, n_rows, keys_hint, n_head_q,
+                       n_head_kv, head_dim, window_len, cap, scale, stream, true);
 }
 
 int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, float *out,
