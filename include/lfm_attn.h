@@ -236,6 +236,31 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
                            uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
                            lfm_attn_stream_t stream);
 
+/* One attention step of the forward stacks with the prologue fused into the
+ * attention kernel: per row, QK-RMSNorm + NeoX RoPE of the raw query and of
+ * the raw new-token key, the RNE fp16 store of that key and value at the
+ * position's slot, then attention over the row's keys (times the gate).
+ * Replaces steps 3-4 of lfm2_forward_gqa_fast (tools/lfm2_kernels_fast.c:
+ * 1046-1066: lfm2_qk_norm_rope_simd, the fp16 stores, then the
+ * OnlineGQATaskCtx dispatch), the per-token prologue + attention of
+ * lfm2_forward_gqa_batch (tools/lfm2_prefill_batch.c:1029-1092) and the
+ * attention block of lfm3_forward_token_internal / lfm3_forward_batch_core
+ * (tools/lfm3_engine.c:1885-1896, 2006-2022), over many sequences.
+ * q: raw queries [n_seq][n_rows][n_head_q][head_dim] (left unchanged);
+ * k, v: raw new-token rows [n_seq][n_rows][n_head_kv][head_dim];
+ * q_norm_w, k_norm_w: [head_dim] or NULL (no norm); cos_lut/sin_lut: the RoPE
+ * table [> last position][head_dim / 2]; the rest as lfm_hip_gqa_f16_varlen.
+ * With a sliding window, window_len + n_rows - 1 <= cap (each row's window
+ * survives the later rows' ring writes).  Head dims 64 and 128 run one
+ * attention launch (plus the split merge where the keys are split); other
+ * head dims run the prologue on a copy of q and the generic kernel. */
+int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const float *gate, int gate_is_logit,
+                         uint16_t *const *k_seq, uint16_t *const *v_seq, const uint32_t *pos_0, float *out,
+                         uint32_t n_seq, uint32_t n_rows, uint32_t keys_hint, uint32_t n_head_q,
+                         uint32_t n_head_kv, uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                         const float *q_norm_w, const float *k_norm_w, float eps, const float *cos_lut,
+                         const float *sin_lut, lfm_attn_stream_t stream);
+
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): lfm_hip_gqa_f16_varlen with the same arguments, kernels

@@ -17,6 +17,7 @@ from .attention import (  # noqa: F401
     EngineContext,
     device_count,
     fnv1a64,
+    gqa_f16_step,
     gqa_f16_varlen,
     gqa_f16_varlen_noalloc,
     gqa_heads,

@@ -238,6 +238,22 @@ def gqa_f16_varlen(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Pt
                                         cap, scale, stream), "lfm_hip_gqa_f16_varlen")
 
 
+def gqa_f16_step(q: Ptr, k: Ptr, v: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Ptr,
+                 pos_0: Ptr, out: Ptr, n_seq: int, n_rows: int, keys_hint: int, n_head_q: int,
+                 n_head_kv: int, head_dim: int, q_norm_w: Ptr, k_norm_w: Ptr, eps: float,
+                 cos_lut: Ptr, sin_lut: Ptr, window_len: int = 0, cap: int = 0,
+                 scale: Optional[float] = None, stream=None) -> None:
+    """One attention step with the prologue fused: raw q/k/v rows in, the new
+    rows stored in the caches, attention out (lfm_hip_gqa_f16_step)."""
+    if scale is None:
+        scale = float(1.0 / np.sqrt(np.float32(head_dim)))
+    check(load().lfm_hip_gqa_f16_step(_p(q), _p(k), _p(v), _p(gate), int(bool(gate_is_logit)), _p(k_seq),
+                                      _p(v_seq), _p(pos_0), _p(out), n_seq, n_rows, keys_hint, n_head_q,
+                                      n_head_kv, head_dim, window_len, cap, scale, _p(q_norm_w),
+                                      _p(k_norm_w), eps, _p(cos_lut), _p(sin_lut), stream),
+          "lfm_hip_gqa_f16_step")
+
+
 def gqa_f16_varlen_noalloc(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr,
                            out: Ptr, n_seq: int, n_rows: int, keys_hint: int, n_head_q: int,
                            n_head_kv: int, head_dim: int, window_len: int = 0, cap: int = 0,

@@ -71,6 +71,10 @@ struct SplitParams {
     uint32_t *tile_prefix; /* [n_seq + 2] tiles before each sequence, then G (device positions) */
     int gate_is_logit;
     float qscale; /* scale * log2(e) */
+    /* fused prologue (FUSE kernels): raw new-token K/V rows, norm weights,
+     * RoPE tables (AttnBatch) */
+    const float *k_new, *v_new, *q_norm_w, *k_norm_w, *cos_lut, *sin_lut;
+    float eps;
 };
 
 __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
@@ -103,6 +107,129 @@ __device__ __forceinline__ float gate_value(const float *gate, size_t idx, int i
     return is_logit ? 1.0f / (1.0f + expf(-g)) : g;
 }
 
+/* Sum of squares of one head held in MFMA fragment order (lane (l16, g)
+ * holds dims 32*st + 8*g + j), added in the order of the reference's AVX2
+ * kernels so the normalised rows are bit-identical to theirs; the result is
+ * returned on every lane of the l16 group.
+ *   HD 64 (lfm2_qk_norm_rope_avx2, tools/lfm2_kernels_fast.c:443-449): per
+ *   8-lane column j, ss0 = x[j]^2 + x[32+j]^2, ss1 = x[8+j]^2 + x[40+j]^2,
+ *   ss0 = fma(x[16+j], ., fma(x[48+j], ., ss0)), ss1 likewise with 24/56,
+ *   t[j] = ss0 + ss1, then ((t0+t4) + (t2+t6)) + ((t1+t5) + (t3+t7)).
+ *   HD 128 (lfm3_qk_norm_rope_128_avx2, tools/lfm3_engine.c:480-494): per
+ *   column j, fma chains ss0 over dims 16k + j and ss1 over 16k + 8 + j,
+ *   k = 0..7, s[j] = ss0 + ss1, then ((s0+s4) + (s1+s5)) + ((s2+s6) + (s3+s7)).
+ * Dims 16k + j alternate between lanes g and g + 2, so the chains hop
+ * between the two halves of the wave. */
+template <int HD>
+__device__ __forceinline__ float sumsq_ref_order(const float (&x)[HD / 32][8], int g) {
+#pragma clang fp contract(off)
+    float t[8];
+    if constexpr (HD == 64) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float a = x[0][j], b = x[1][j];
+            const float v = a * a + b * b;                    /* g 0: ss0, g 1: ss1 (first terms) */
+            const float w = __shfl_xor(v, 32);                /* to g 2 / g 3                     */
+            const float u = __builtin_fmaf(a, a, __builtin_fmaf(b, b, w)); /* g 2: ss0, g 3: ss1 */
+            t[j]          = u + __shfl_xor(u, 16);            /* g 2, 3: ss0 + ss1                */
+        }
+        const float T = ((t[0] + t[4]) + (t[2] + t[6])) + ((t[1] + t[5]) + (t[3] + t[7]));
+        const float o = __shfl_xor(T, 32);
+        return g >= 2 ? T : o;
+    } else {
+        static_assert(HD == 128, "reference summation order is defined for head_dim 64 and 128");
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const float xx = x[st][j];
+                if (g < 2) acc = __builtin_fmaf(xx, xx, acc); /* dims 32 st + j (+8)        */
+                acc = __shfl_xor(acc, 32);
+                if (g >= 2) acc = __builtin_fmaf(xx, xx, acc); /* dims 32 st + 16 + j (+8)  */
+                acc = __shfl_xor(acc, 32);
+            }
+            t[j] = acc + __shfl_xor(acc, 16); /* g 0, 1: ss0 + ss1 */
+        }
+        const float T = ((t[0] + t[4]) + (t[1] + t[5])) + ((t[2] + t[6]) + (t[3] + t[7]));
+        const float o = __shfl_xor(T, 32);
+        return g < 2 ? T : o;
+    }
+}
+
+/* QK-RMSNorm + NeoX RoPE of one head held in MFMA fragment order: lane
+ * (l16, g) holds dims 32*st + 8*g + j (st < HD/32, j < 8) of the head of
+ * its column, and the four lanes g = 0..3 of an l16 hold the whole head.
+ * x <- (x * irms) * w with irms = 1/sqrtf(sum(x^2)/HD + eps) (skipped when
+ * norm_w is null), then pairs (d, d + HD/2) -- which sit in fragments st and
+ * st + HD/64 of the same lane -- rotate by the table row of position `pos`:
+ * lo' = fma(lo, c, -(hi*s)), hi' = fma(hi, c, lo*s).  The arithmetic of the
+ * prologue kernel and of the reference's AVX2 kernels
+ * (tools/lfm2_kernels_fast.c:403-497, tools/lfm3_engine.c:463-525), sum of
+ * squares included.  Every lane of the wave must call it (cross-lane sums). */
+template <int HD>
+__device__ __forceinline__ void norm_rope_frag(float (&x)[HD / 32][8], uint32_t pos, const float *norm_w, float eps,
+                                               const float *cos_lut, const float *sin_lut, int g) {
+    constexpr int NS = HD / 32, HALF = HD / 2;
+    if (norm_w) {
+        const float ss   = sumsq_ref_order<HD>(x, g);
+        const float irms = 1.0f / sqrtf(ss / (float)HD + eps);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            const float4 w0 = *reinterpret_cast<const float4 *>(norm_w + 32 * st + 8 * g);
+            const float4 w1 = *reinterpret_cast<const float4 *>(norm_w + 32 * st + 8 * g + 4);
+            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[st][j] = (x[st][j] * irms) * w[j];
+        }
+    }
+    const float *cr = cos_lut + (size_t)pos * HALF;
+    const float *sr = sin_lut + (size_t)pos * HALF;
+#pragma unroll
+    for (int st = 0; st < NS / 2; ++st) {
+        const float4 c0 = *reinterpret_cast<const float4 *>(cr + 32 * st + 8 * g);
+        const float4 c1 = *reinterpret_cast<const float4 *>(cr + 32 * st + 8 * g + 4);
+        const float4 s0 = *reinterpret_cast<const float4 *>(sr + 32 * st + 8 * g);
+        const float4 s1 = *reinterpret_cast<const float4 *>(sr + 32 * st + 8 * g + 4);
+        const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float lo = x[st][j], hi = x[st + NS / 2][j];
+            x[st][j]          = __builtin_fmaf(lo, c[j], -(hi * sn[j]));
+            x[st + NS / 2][j] = __builtin_fmaf(hi, c[j], lo * sn[j]);
+        }
+    }
+}
+
+/* Two fp32 values stored as RNE fp16 (packed).  Each value is first
+ * materialised in fp32 (the reference stores fp32 results with
+ * _mm256_cvtps_ph): the barrier keeps the compiler from fusing a producing
+ * fma with the conversion into v_fma_mixlo_f16, whose single rounding
+ * differs on ties. */
+__device__ __forceinline__ uint32_t pack_rne(float a, float b) {
+    asm volatile("" : "+v"(a));
+    asm volatile("" : "+v"(b));
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
+__device__ __forceinline__ u32x4_t pack8_rne(const float (&x)[8]) {
+    u32x4_t w;
+    w[0] = pack_rne(x[0], x[1]);
+    w[1] = pack_rne(x[2], x[3]);
+    w[2] = pack_rne(x[4], x[5]);
+    w[3] = pack_rne(x[6], x[7]);
+    return w;
+}
+
+__device__ __forceinline__ void load8(const float *p, float (&x)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
 /* Keys [lo, last] that the rows of sequence s attend (their union). */
 struct SeqKeys {
     uint32_t pos0, lo, last;
@@ -119,7 +246,7 @@ __device__ __forceinline__ SeqKeys seq_keys(const SplitParams &P, uint32_t s) {
  * direct: the range is the sequence's whole key set, so the normalised,
  * gated output is written; otherwise the unnormalised O^T and (max, sum)
  * go to the partial slots part + column. */
-template <int HD, int NT>
+template <int HD, int NT, bool FUSE>
 __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, uint32_t s, uint32_t pos0, uint32_t kvh,
                                             uint32_t kb, uint32_t ke, bool direct, size_t part) {
     constexpr int NS  = HD / 32; /* MFMA k-steps of Q.K^T (32 dims each)          */
@@ -146,33 +273,36 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         const uint32_t n = (uint32_t)(l16 + 16 * nt);
         col_lo[nt] = 0xFFFFFFFFu; /* padding column: every key masked */
         col_hi[nt] = 0u;
-        if (n < P.ncols) {
-            const uint32_t r   = n / P.kv_mul;
-            const uint32_t h   = kvh * P.kv_mul + (n - r * P.kv_mul);
-            const uint32_t abs = pos0 + r;
-            col_lo[nt]         = lfm_plan_row(abs, P.window, P.cap).t_start;
-            col_hi[nt]         = abs;
-            const float *qp    = P.q + (((size_t)s * P.n_rows + r) * P.n_head_q + h) * HD + 8 * g;
+        float x[NS][8];
+        const bool live = n < P.ncols;
+        uint32_t abs    = pos0;
+        if (live) {
+            const uint32_t r = n / P.kv_mul;
+            const uint32_t h = kvh * P.kv_mul + (n - r * P.kv_mul);
+            abs              = pos0 + r;
+            col_lo[nt]       = lfm_plan_row(abs, P.window, P.cap).t_start;
+            col_hi[nt]       = abs;
+            const float *qp  = P.q + (((size_t)s * P.n_rows + r) * P.n_head_q + h) * HD + 8 * g;
 #pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                const float4 a = *reinterpret_cast<const float4 *>(qp + 32 * st);
-                const float4 b = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
-                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float xs      = x[j] * P.qscale;
-                    const _Float16 hi   = (_Float16)xs;
-                    qh[nt][st][j]       = hi;
-                    ql[nt][st][j]       = (_Float16)(xs - (float)hi);
-                }
-            }
+            for (int st = 0; st < NS; ++st) load8(qp + 32 * st, x[st]);
         } else {
 #pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                qh[nt][st] = (half8_t)(_Float16)0.0f;
-                ql[nt][st] = (half8_t)(_Float16)0.0f;
-            }
+            for (int st = 0; st < NS; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[st][j] = 0.0f;
         }
+        /* fused prologue: the raw query is normalised and rotated here, by
+         * every wave that reads it (all lanes take part in the sums) */
+        if constexpr (FUSE) norm_rope_frag<HD>(x, abs, P.q_norm_w, P.eps, P.cos_lut, P.sin_lut, g);
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float xs    = x[st][j] * P.qscale;
+                const _Float16 hi = (_Float16)xs;
+                qh[nt][st][j]     = hi;
+                ql[nt][st][j]     = (_Float16)(xs - (float)hi);
+            }
     }
     /* keys every real column may see without a per-key test */
     const uint32_t free_lo = lfm_plan_row(last, P.window, P.cap).t_start;
@@ -202,6 +332,67 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                 uint32_t slot = base + off;
                 if (P.window) { while (slot >= P.cap) slot -= P.cap; }
                 vd[ps * 4 + i] = load16(vc + (size_t)slot * row + 8 * (lane % CH));
+            }
+        }
+    };
+
+    /* ---- fused prologue: the rows of this call's positions -------------------
+     * Keys >= pos0 are the new tokens.  The sub-tile that holds one gets its
+     * row from the raw k/v (normalised, rotated, RNE fp16) instead of from
+     * the cache it was loaded from, and the lane that owns the row's 16 bytes
+     * stores them at the row's slot.  Lanes clamped to the last key (past ke)
+     * take that key's new row too, so no stale slot content enters the
+     * product.  Each new key lies in exactly one segment of the plan, so each
+     * row is stored once; no other wave reads those bytes in this launch. */
+    uint16_t *kw = nullptr, *vw = nullptr;
+    if constexpr (FUSE) {
+        kw = const_cast<uint16_t *>(P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride) + (size_t)kvh * HD;
+        vw = const_cast<uint16_t *>(P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride) + (size_t)kvh * HD;
+    }
+    auto patch_new_rows = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            uint32_t key    = p0 + (uint32_t)(16 * kt + l16);
+            const bool real = key < ke;
+            if (!real) key = ke - 1u;
+            const bool fresh = key >= pos0;
+            float x[NS][8];
+            if (fresh) {
+                const float *kp = P.k_new + (((size_t)s * P.n_rows + (key - pos0)) * P.n_head_kv + kvh) * HD + 8 * g;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) load8(kp + 32 * st, x[st]);
+            } else {
+#pragma unroll
+                for (int st = 0; st < NS; ++st)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) x[st][j] = 0.0f;
+            }
+            norm_rope_frag<HD>(x, fresh ? key : pos0, P.k_norm_w, P.eps, P.cos_lut, P.sin_lut, g);
+            if (fresh) {
+                const size_t off = (size_t)lfm_slot_of(key, P.window, P.cap) * row + 8 * g;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    const u32x4_t w = pack8_rne(x[st]);
+                    kd[kt][st]      = w;
+                    if (real) *reinterpret_cast<u32x4_t *>(kw + off + 32 * st) = w;
+                }
+            }
+        }
+#pragma unroll
+        for (int ps = 0; ps < HD / 64; ++ps) {
+            const int quad = ps * QPP + lane / CH;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t key    = p0 + (uint32_t)(4 * quad + i);
+                const bool real = key < ke;
+                if (!real) key = ke - 1u;
+                if (key < pos0) continue;
+                float x[8];
+                load8(P.v_new + (((size_t)s * P.n_rows + (key - pos0)) * P.n_head_kv + kvh) * HD + 8 * (lane % CH), x);
+                const u32x4_t w  = pack8_rne(x);
+                vd[ps * 4 + i]   = w;
+                if (real)
+                    *reinterpret_cast<u32x4_t *>(vw + (size_t)lfm_slot_of(key, P.window, P.cap) * row + 8 * (lane % CH)) = w;
             }
         }
     };
@@ -330,23 +521,30 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
      * 41.7 -> 39.7 us, LFM3 SWA 10.6 -> 10.3 us, outputs bit-identical. */
     const uint32_t nsub = (ke - kb + 31u) / 32u;
     u32x4_t kA[2][NS], vA[NVL], kB[2][NS], vB[NVL];
+    /* sub-tile at p0 with its new rows substituted (FUSE), then consumed */
+    auto consume = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
+        if constexpr (FUSE) {
+            if (p0 + 31u >= pos0) patch_new_rows(p0, kd, vd);
+        }
+        process(p0, kd, vd);
+    };
     load_tile(kb, kA, vA);
     uint32_t it = 0;
     for (; it + 2u < nsub; it += 2u) {
         const uint32_t p0 = kb + 32u * it;
         load_tile(p0 + 32u, kB, vB);
-        process(p0, kA, vA);
+        consume(p0, kA, vA);
         load_tile(p0 + 64u, kA, vA);
-        process(p0 + 32u, kB, vB);
+        consume(p0 + 32u, kB, vB);
     }
     {
         const uint32_t p0 = kb + 32u * it;
         if (it + 1u < nsub) {
             load_tile(p0 + 32u, kB, vB);
-            process(p0, kA, vA);
-            process(p0 + 32u, kB, vB);
+            consume(p0, kA, vA);
+            consume(p0 + 32u, kB, vB);
         } else {
-            process(p0, kA, vA);
+            consume(p0, kA, vA);
         }
     }
 
@@ -391,7 +589,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
  * contiguous runs of the cache rows.  Fixed-length chunks; a sequence longer
  * than n_splits chunks gets longer chunks; splits past a short sequence's end
  * mark their partials empty. */
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool FUSE>
 __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
     const int lane       = threadIdx.x & 63;
@@ -409,14 +607,14 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
         for (uint32_t n = lane; n < P.ncols; n += 64) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
         return;
     }
-    run_segment<HD, NT>(P, vt_all[wave], s, k.pos0, kvh, kb, ke, P.n_splits == 1u, part);
+    run_segment<HD, NT, FUSE>(P, vt_all[wave], s, k.pos0, kvh, kb, ke, P.n_splits == 1u, part);
 }
 
 /* Small batches (few (sequence, KV head) pairs): one workgroup per pair, its
  * WW waves taking the key splits, and the log-sum-exp merge done by the same
  * workgroup after a barrier, so no second kernel is launched.  The partials
  * go through the workspace as on the grid (they stay in the CU's caches). */
-template <int HD, int NT, int WW>
+template <int HD, int NT, int WW, bool FUSE>
 __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
     constexpr uint32_t D4 = HD / 4;
     __shared__ __attribute__((aligned(16))) uint16_t vt_all[WW][HD * kVtStride];
@@ -434,7 +632,7 @@ __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
         if (kb > k.last) {
             for (uint32_t n = (uint32_t)lane; n < P.ncols; n += 64u) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
         } else {
-            run_segment<HD, NT>(P, vt_all[split], s, k.pos0, kvh, kb, ke, false, part);
+            run_segment<HD, NT, FUSE>(P, vt_all[split], s, k.pos0, kvh, kb, ke, false, part);
         }
     }
     __syncthreads();
@@ -562,7 +760,7 @@ __device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int l
     }
 }
 
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool FUSE>
 __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
     const lfm_bal_cfg &c = P.plan;
@@ -594,7 +792,7 @@ __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
         const uint32_t pos0 = pos_of(P, pl, u.s);
         uint32_t kb, ke;
         lfm_bal_seg_keys(&c, pos0, u.a, u.b, &kb, &ke);
-        run_segment<HD, NT>(P, vt_all[wave], u.s, pos0, kvh, kb, ke, u.n == 1u,
+        run_segment<HD, NT, FUSE>(P, vt_all[wave], u.s, pos0, kvh, kb, ke, u.n == 1u,
                             ((size_t)u.slot * P.n_head_kv + kvh) * P.ncols);
         return;
     }
@@ -613,7 +811,7 @@ __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
             uint32_t kb, ke;
             lfm_bal_seg_keys(&c, pos0, sg.a, sg.b, &kb, &ke);
             const uint64_t slot = lfm_bal_slot(wg, s, c.n_groups, sg.grp);
-            run_segment<HD, NT>(P, vt_all[wave], s, pos0, kvh, kb, ke, sg.whole != 0,
+            run_segment<HD, NT, FUSE>(P, vt_all[wave], s, pos0, kvh, kb, ke, sg.whole != 0,
                                 ((size_t)slot * P.n_head_kv + kvh) * P.ncols);
         }
         t = sg.end;
@@ -777,13 +975,13 @@ __global__ __launch_bounds__(256) void k_merge(const SplitParams P, uint32_t n_i
         *reinterpret_cast<float4 *>(P.out + orow * HD + d) = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
 }
 
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool FUSE>
 hipError_t launch_hd_nt_w(const SplitParams &p, uint32_t n_seq, hipStream_t stream) {
     dim3 grid(p.n_splits, (p.n_head_kv + W - 1) / W, n_seq);
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv<HD, NT, W>), grid, dim3(64 * W), 0, stream, p);
+    hipLaunchKernelGGL((k_splitkv<HD, NT, W, FUSE>), grid, dim3(64 * W), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     if (e != hipSuccess || p.n_splits == 1u) return e;
@@ -836,14 +1034,14 @@ uint32_t choose_waves(uint32_t n_head_kv, uint32_t head_dim) {
 
 /* Workgroups of k_splitkv_bal<HD, NT, W> resident on the whole device at
  * once (queried once per instantiation). */
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool FUSE>
 uint32_t resident_wgs() {
     static uint32_t cached = 0;
     if (cached) return cached;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W>, 64 * W, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE>, 64 * W, 0) !=
             hipSuccess)
         return 256u;
     cached = (uint32_t)((cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1));
@@ -852,13 +1050,13 @@ uint32_t resident_wgs() {
 
 /* Balanced plan: launch sized for the plan the device will pick, partial
  * slots and the tile prefix table in the workspace, then the merge. */
-template <int HD, int NT, int W>
+template <int HD, int NT, int W, bool FUSE>
 int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scratch *sc) {
     const uint32_t cus = device_cus();
     lfm_bal_cfg &c     = p.plan;
     p.wpg              = W;
     c.n_groups         = (p.n_head_kv + W - 1u) / W;
-    c.n_res            = resident_wgs<HD, NT, W>();
+    c.n_res            = resident_wgs<HD, NT, W, FUSE>();
     /* 16 waves per CU over a batch of equal sequences: two residency rounds of
      * 8-wave workgroups at head_dim 64 (measured best on MI355X) */
     c.target_waves = 16u * cus;
@@ -896,7 +1094,7 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W>), dim3((uint32_t)n_launch), dim3(64 * W), 0, stream, p);
+    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W, FUSE>), dim3((uint32_t)n_launch), dim3(64 * W), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     if (e != hipSuccess) return hip_status(e);
@@ -946,24 +1144,27 @@ constexpr uint32_t wg_waves() {
     return (HD == 64 && NT <= 2) ? 8u : 4u;
 }
 
-template <int HD, int NT>
+template <int HD, int NT, bool FUSE>
 int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
     constexpr int WW = (int)wg_waves<HD, NT>();
     if (p.n_splits > (uint32_t)WW) p.n_splits = WW; /* forced: the kernel lengthens the chunks */
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW>), dim3(p.n_head_kv, n_seq), dim3(64 * WW), 0, stream, p);
+    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW, FUSE>), dim3(p.n_head_kv, n_seq), dim3(64 * WW), 0, stream, p);
     const hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     return hip_status(e);
 }
 
-template <int HD, int NT>
+template <int HD, int NT, bool FUSE>
 int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream,
                  const Scratch *sc) {
-    if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) return launch_wg<HD, NT>(p, n_seq, stream);
+    if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
     uint32_t w = choose_waves(p.n_head_kv, HD);
+    /* fused prologue at 32+ query columns: 8-wave workgroups would spill the
+     * new-row registers (256 VGPRs per wave at two waves per SIMD) */
+    if (FUSE && NT >= 2 && w > 4u) w = 4u;
     /* a grid of fewer workgroups than compute units (one short sequence)
      * spreads its KV heads over more, smaller workgroups: measured on MI355X
      * at B1, 8 KV heads, ctx 256-4096, 9.6-12.0 us -> 8.2-10.5 us per call
@@ -971,16 +1172,16 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool 
     if (grid && !getenv("LFM_ATTN_WAVES"))
         while (w > 1u && (uint64_t)p.n_splits * ((p.n_head_kv + w - 1u) / w) * n_seq < device_cus()) w >>= 1;
     if (!grid) {
-        if (w == 8u) return launch_bal<HD, NT, 8>(p, keys_hint, stream, sc);
-        if (w == 4u) return launch_bal<HD, NT, 4>(p, keys_hint, stream, sc);
-        if (w == 2u) return launch_bal<HD, NT, 2>(p, keys_hint, stream, sc);
-        return launch_bal<HD, NT, 1>(p, keys_hint, stream, sc);
+        if (w == 8u) return launch_bal<HD, NT, 8, FUSE>(p, keys_hint, stream, sc);
+        if (w == 4u) return launch_bal<HD, NT, 4, FUSE>(p, keys_hint, stream, sc);
+        if (w == 2u) return launch_bal<HD, NT, 2, FUSE>(p, keys_hint, stream, sc);
+        return launch_bal<HD, NT, 1, FUSE>(p, keys_hint, stream, sc);
     }
     hipError_t e;
-    if (w == 8u) e = launch_hd_nt_w<HD, NT, 8>(p, n_seq, stream);
-    else if (w == 4u) e = launch_hd_nt_w<HD, NT, 4>(p, n_seq, stream);
-    else if (w == 2u) e = launch_hd_nt_w<HD, NT, 2>(p, n_seq, stream);
-    else e = launch_hd_nt_w<HD, NT, 1>(p, n_seq, stream);
+    if (w == 8u) e = launch_hd_nt_w<HD, NT, 8, FUSE>(p, n_seq, stream);
+    else if (w == 4u) e = launch_hd_nt_w<HD, NT, 4, FUSE>(p, n_seq, stream);
+    else if (w == 2u) e = launch_hd_nt_w<HD, NT, 2, FUSE>(p, n_seq, stream);
+    else e = launch_hd_nt_w<HD, NT, 1, FUSE>(p, n_seq, stream);
     return hip_status(e);
 }
 
@@ -1010,6 +1211,20 @@ void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, ui
     if (n > 1024) { n = 1024; c = (((keys + n - 1) / n) + 31) & ~(uint64_t)31; }
     *n_splits = (uint32_t)(n ? n : 1);
     *chunk    = (uint32_t)c;
+}
+
+/* Head dim and 16-column tiles of the batch -> kernel instantiation. */
+template <bool FUSE>
+int dispatch_nt(const SplitParams &p, const AttnBatch &b, uint32_t keys_hint, bool grid, hipStream_t stream,
+                const Scratch *sc) {
+    const uint32_t nt = (p.ncols + 15u) / 16u;
+    if (b.head_dim == 64u) {
+        if (nt == 1u) return launch_hd_nt<64, 1, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
+        if (nt == 2u) return launch_hd_nt<64, 2, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
+        return launch_hd_nt<64, 4, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
+    }
+    if (nt == 1u) return launch_hd_nt<128, 1, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
+    return launch_hd_nt<128, 2, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
 }
 
 } // namespace
@@ -1050,17 +1265,16 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, c
     p.plan.n_head_kv = b.n_head_kv;
     p.plan.window   = b.window;
     p.plan.cap      = b.cap;
-    const uint32_t nt = (p.ncols + 15u) / 16u;
-    const bool grid   = use_grid_plan(b);
-    if (!grid) {
-        if (b.head_dim == 64u) {
-            if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
-            if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
-            return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream, sc);
-        }
-        if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
-        return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
-    }
+    p.k_new         = b.k_new;
+    p.v_new         = b.v_new;
+    p.q_norm_w      = b.q_norm_w;
+    p.k_norm_w      = b.k_norm_w;
+    p.cos_lut       = b.cos_lut;
+    p.sin_lut       = b.sin_lut;
+    p.eps           = b.eps;
+    const bool grid = use_grid_plan(b);
+    if (!grid) return b.k_new ? dispatch_nt<true>(p, b, keys_hint, grid, stream, sc)
+                              : dispatch_nt<false>(p, b, keys_hint, grid, stream, sc);
     choose_split(b, keys_hint, &p.n_splits, &p.chunk);
     if (p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
@@ -1071,13 +1285,8 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, c
         p.part_o  = reinterpret_cast<float *>(ws);
         p.part_ml = reinterpret_cast<float2 *>(ws + ((n_part * b.head_dim * sizeof(float) + 255) & ~(size_t)255));
     }
-    if (b.head_dim == 64u) {
-        if (nt == 1u) return launch_hd_nt<64, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
-        if (nt == 2u) return launch_hd_nt<64, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
-        return launch_hd_nt<64, 4>(p, b.n_seq, keys_hint, grid, stream, sc);
-    }
-    if (nt == 1u) return launch_hd_nt<128, 1>(p, b.n_seq, keys_hint, grid, stream, sc);
-    return launch_hd_nt<128, 2>(p, b.n_seq, keys_hint, grid, stream, sc);
+    return b.k_new ? dispatch_nt<true>(p, b, keys_hint, grid, stream, sc)
+                   : dispatch_nt<false>(p, b, keys_hint, grid, stream, sc);
 }
 
 } // namespace lfm

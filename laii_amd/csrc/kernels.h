@@ -31,6 +31,15 @@ struct AttnBatch {
     uint32_t n_seq = 1, n_rows = 1, n_head_q = 0, n_head_kv = 0, head_dim = 0;
     uint32_t window = 0, cap = 0;
     float scale = 0.0f;
+    /* Fused prologue (the step entry): q holds the raw query rows, and the
+     * kernel applies QK-RMSNorm + RoPE to q and to the raw new-token rows
+     * k_new / v_new ([n_seq][n_rows][n_head_kv][head_dim]), which it also
+     * stores as RNE fp16 at their slots.  k_new == nullptr: q is final and
+     * the caches already hold every attended row. */
+    const float *k_new = nullptr, *v_new = nullptr;
+    const float *q_norm_w = nullptr, *k_norm_w = nullptr; /* [head_dim] or null (no norm) */
+    const float *cos_lut = nullptr, *sin_lut = nullptr;   /* [position][head_dim / 2]     */
+    float eps = 0.0f;
 };
 
 /* Device workspace owned by the shim (grown on demand). */

@@ -4,10 +4,10 @@
  * attention step the forward stacks call (include/lfm_attn.h).
  *
  * Each step stages q | k | v | gate | position in one pinned host buffer,
- * moves it with a single host-to-device copy, runs the batched prologue
- * (QK-RMSNorm + RoPE, RNE fp16 K/V store at the position's slot) and the
- * attention kernel, and returns the output with a single device-to-host copy,
- * all on the context's stream.
+ * moves it with a single host-to-device copy, runs the attention kernel with
+ * the prologue fused (QK-RMSNorm + RoPE, RNE fp16 K/V store at the
+ * position's slot, lfm_hip_gqa_f16_step), and returns the output with a
+ * single device-to-host copy, all on the context's stream.
  */
 #define _POSIX_C_SOURCE 200809L /* getpid, fsync, fileno */
 #include <hip/hip_runtime_api.h>
@@ -227,21 +227,20 @@ int lfm_attn_ctx_forward(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
     if (st != LFM_ATTN_OK) return st;
 
     unsigned char *d     = c->stage_dev;
-    float *qd            = (float *)d;
+    const float *qd      = (const float *)d;
     const uint32_t *posd = (const uint32_t *)(d + c->off_pos);
     uint16_t *const *kt  = c->tables + 2u * layer;
     uint16_t *const *vt  = c->tables + 2u * layer + 1u;
     const float *cosd    = swa ? c->cos_swa : c->cos_full;
     const float *sind    = swa ? c->sin_swa : c->sin_full;
-    st = lfm_hip_qkv_prologue(qd, (const float *)(d + c->off_k), (const float *)(d + c->off_v), kt, vt,
-                              posd, 1u, B, g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer],
-                              c->k_norm[layer], g->eps, cosd, sind, window, cap, c->stream);
-    if (st != LFM_ATTN_OK) return st;
+    /* one launch: QK-norm + RoPE, the fp16 K/V store and the attention
+     * (plus the split merge when the keys are split) */
     const uint32_t keys = window ? window + B - 1u : pos_0 + B;
-    st = lfm_hip_gqa_f16_varlen(qd, gate_logits ? (const float *)(d + c->off_g) : NULL, 1,
-                                (const uint16_t *const *)kt, (const uint16_t *const *)vt, posd,
-                                (float *)(d + c->off_out), 1u, B, keys, g->n_head_q, g->n_head_kv,
-                                g->head_dim, window, cap, 1.0f / sqrtf((float)g->head_dim), c->stream);
+    st = lfm_hip_gqa_f16_step(qd, (const float *)(d + c->off_k), (const float *)(d + c->off_v),
+                              gate_logits ? (const float *)(d + c->off_g) : NULL, 1, kt, vt, posd,
+                              (float *)(d + c->off_out), 1u, B, keys, g->n_head_q, g->n_head_kv, g->head_dim,
+                              window, cap, 1.0f / sqrtf((float)g->head_dim), c->q_norm[layer], c->k_norm[layer],
+                              g->eps, cosd, sind, c->stream);
     if (st != LFM_ATTN_OK) return st;
     st = st_of(hipMemcpyAsync(h + c->off_out, d + c->off_out, qn * sizeof(float),
                               hipMemcpyDeviceToHost, c->stream));

@@ -8,7 +8,8 @@
  *   batched per-token prologue         tools/lfm2_prefill_batch.c:1029-1072,
  *                                      tools/lfm3_engine.c:2006-2016
  *
- * Per head: irms = 1/sqrtf(sum(x^2)/head_dim + eps); x <- (x*irms)*w (skipped
+ * Per head: irms = 1/sqrtf(sum(x^2)/head_dim + eps), the sum added in the
+ * AVX2 kernels' order at head_dim 64 and 128; x <- (x*irms)*w (skipped
  * when w is NULL); pairs (i, i+head_dim/2) rotate by the LUT row of the
  * position: lo' = lo*c - hi*s, hi' = hi*c + lo*s (fused multiply-add, as the
  * AVX2 kernels do).  fp16 stores round to nearest even.  One wave64 per head;
@@ -38,6 +39,44 @@ __device__ __forceinline__ float wave_sum_uniform(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }
 
+/* Sum of squares of the head at `in` for head_dim 64 or 128, added in the
+ * order of the reference's AVX2 kernels (lanes 0..7 play its eight vector
+ * columns), so normalised rows are bit-identical to theirs:
+ *   64  lfm2_qk_norm_rope_avx2 (tools/lfm2_kernels_fast.c:443-449):
+ *       ss0 = x[j]^2 + x[32+j]^2, ss1 = x[8+j]^2 + x[40+j]^2,
+ *       ss0 = fma(x[16+j], ., fma(x[48+j], ., ss0)), ss1 likewise (24, 56),
+ *       t = ss0 + ss1, total ((t0+t4) + (t2+t6)) + ((t1+t5) + (t3+t7));
+ *   128 lfm3_qk_norm_rope_128_avx2 (tools/lfm3_engine.c:480-494):
+ *       fma chains over dims 16k + j and 16k + 8 + j, s = ss0 + ss1,
+ *       total ((s0+s4) + (s1+s5)) + ((s2+s6) + (s3+s7)).
+ * Returned on every lane. */
+__device__ __forceinline__ float sumsq_ref_order(const float *in, uint32_t hd) {
+#pragma clang fp contract(off)
+    const uint32_t j = threadIdx.x & 7u;
+    float t;
+    if (hd == 64u) {
+        float ss0 = in[j] * in[j] + in[32u + j] * in[32u + j];
+        float ss1 = in[8u + j] * in[8u + j] + in[40u + j] * in[40u + j];
+        ss0 = __builtin_fmaf(in[16u + j], in[16u + j], __builtin_fmaf(in[48u + j], in[48u + j], ss0));
+        ss1 = __builtin_fmaf(in[24u + j], in[24u + j], __builtin_fmaf(in[56u + j], in[56u + j], ss1));
+        t = ss0 + ss1;
+        t = t + __shfl_xor(t, 4); /* j < 4: t_j + t_(j+4)        */
+        t = t + __shfl_xor(t, 2); /* (t0+t4) + (t2+t6), ...      */
+        t = t + __shfl_xor(t, 1);
+    } else {
+        float ss0 = 0.0f, ss1 = 0.0f;
+        for (uint32_t i = 0; i < 128u; i += 16u) {
+            ss0 = __builtin_fmaf(in[i + j], in[i + j], ss0);
+            ss1 = __builtin_fmaf(in[i + 8u + j], in[i + 8u + j], ss1);
+        }
+        t = ss0 + ss1;
+        t = t + __shfl_xor(t, 4); /* j < 4: s_j + s_(j+4)        */
+        t = t + __shfl_xor(t, 1); /* (s0+s4) + (s1+s5), ...      */
+        t = t + __shfl_xor(t, 2);
+    }
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, t)));
+}
+
 /* Normalise + rotate one head held as pairs; writes fp32 (vec_out) or fp16. */
 __device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, uint16_t *dst_f16,
                                                uint32_t hd, const float *norm_w, float eps,
@@ -54,7 +93,8 @@ __device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, 
         ss += x0[j] * x0[j] + x1[j] * x1[j];
     }
     if (norm_w) {
-        const float irms = 1.0f / sqrtf(wave_sum_uniform(ss) / (float)hd + eps);
+        const float sum  = (hd == 64u || hd == 128u) ? sumsq_ref_order(in, hd) : wave_sum_uniform(ss);
+        const float irms = 1.0f / sqrtf(sum / (float)hd + eps);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const uint32_t i = lane + 64u * j;

@@ -473,6 +473,66 @@ int lfm_hip_gqa_f16_varlen_noalloc(const float *q, const float *gate, int gate_i
                        n_head_kv, head_dim, window_len, cap, scale, stream, true);
 }
 
+int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const float *gate, int gate_is_logit,
+                         uint16_t *const *k_seq, uint16_t *const *v_seq, const uint32_t *pos_0, float *out,
+                         uint32_t n_seq, uint32_t n_rows, uint32_t keys_hint, uint32_t n_head_q,
+                         uint32_t n_head_kv, uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
+                         const float *q_norm_w, const float *k_norm_w, float eps, const float *cos_lut,
+                         const float *sin_lut, lfm_attn_stream_t stream) {
+    if (!q || !k || !v || !k_seq || !v_seq || !pos_0 || !out || !cos_lut || !sin_lut) return LFM_ATTN_E_INVALID;
+    if (n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u || n_head_q % n_head_kv != 0u)
+        return LFM_ATTN_E_INVALID;
+    if (n_seq > 65535u || n_head_kv > 65535u) return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || head_dim % 8u != 0u || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (window_len > 0u && (cap == 0u || window_len > cap)) return LFM_ATTN_E_INVALID;
+    /* every row's window must survive the later rows' ring writes */
+    if (window_len > 0u && (uint64_t)window_len + n_rows - 1u > cap) return LFM_ATTN_E_INVALID;
+    AttnBatch b;
+    b.q = q;
+    b.gate = gate;
+    b.gate_is_logit = gate_is_logit;
+    b.k_seq = reinterpret_cast<const void *const *>(k_seq);
+    b.v_seq = reinterpret_cast<const void *const *>(v_seq);
+    b.pos0_dev = pos_0;
+    b.out = out;
+    b.out_dims = head_dim;
+    b.n_seq = n_seq;
+    b.n_rows = n_rows;
+    b.n_head_q = n_head_q;
+    b.n_head_kv = n_head_kv;
+    b.head_dim = head_dim;
+    b.window = window_len;
+    b.cap = cap;
+    b.scale = scale;
+    const hipStream_t st = to_stream(stream);
+    const bool fused = lfm::splitkv_supports(b) && aligned16(q) && aligned16(out) && aligned16(k) && aligned16(v) &&
+                       aligned16(cos_lut) && aligned16(sin_lut) && (!q_norm_w || aligned16(q_norm_w)) &&
+                       (!k_norm_w || aligned16(k_norm_w));
+    if (fused) {
+        b.k_new = k;
+        b.v_new = v;
+        b.q_norm_w = q_norm_w;
+        b.k_norm_w = k_norm_w;
+        b.cos_lut = cos_lut;
+        b.sin_lut = sin_lut;
+        b.eps = eps;
+        return lfm::launch_splitkv(b, keys_hint, st);
+    }
+    /* shapes the split-KV kernel does not take: the prologue on a copy of q
+     * (q stays as passed), then the generic kernel */
+    const size_t q_bytes = (size_t)n_seq * n_rows * n_head_q * head_dim * sizeof(float);
+    int ws_st = LFM_ATTN_OK;
+    float *qw = static_cast<float *>(lfm::workspace(q_bytes, st, &ws_st));
+    if (!qw) return ws_st;
+    int r = lfm::hip_status(hipMemcpyAsync(qw, q, q_bytes, hipMemcpyDeviceToDevice, st));
+    if (r != LFM_ATTN_OK) return r;
+    r = lfm::launch_qkv_prologue(qw, k, v, k_seq, v_seq, pos_0, n_seq, n_rows, n_head_q, n_head_kv, head_dim,
+                                 q_norm_w, k_norm_w, eps, cos_lut, sin_lut, window_len, cap, st);
+    if (r != LFM_ATTN_OK) return r;
+    b.q = qw;
+    return lfm::launch_generic(b, false, st);
+}
+
 int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, float *out,
                         uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,

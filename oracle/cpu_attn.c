@@ -150,6 +150,41 @@ void orc_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq,
  * x <- (x * irms) * w with irms = 1/sqrtf(mean(x^2) + eps); NeoX rotation of
  * pairs (i, i + head_dim/2); with dst_f16 the rotated head is stored as RNE
  * fp16 and vec is left untouched, otherwise vec is overwritten. */
+/* Sum of squares of one head in the order of the reference's AVX2 kernels
+ * (eight vector columns j, then a horizontal sum), which the engine runs:
+ *   64  lfm2_qk_norm_rope_avx2, tools/lfm2_kernels_fast.c:443-449, hsum of
+ *       include/lfm2_simd_avx2.h:286-293;
+ *   128 lfm3_qk_norm_rope_128_avx2, tools/lfm3_engine.c:480-494.
+ * Other head dims: the scalar kernels' double sum
+ * (tools/lfm2_kernels_fast.c:527-529). */
+static float sumsq_ref(const float *x, uint32_t head_dim) {
+    float t[8];
+    if (head_dim == 64u) {
+        for (int j = 0; j < 8; ++j) {
+            float ss0 = x[j] * x[j] + x[32 + j] * x[32 + j];
+            float ss1 = x[8 + j] * x[8 + j] + x[40 + j] * x[40 + j];
+            ss0 = fmaf(x[16 + j], x[16 + j], fmaf(x[48 + j], x[48 + j], ss0));
+            ss1 = fmaf(x[24 + j], x[24 + j], fmaf(x[56 + j], x[56 + j], ss1));
+            t[j] = ss0 + ss1;
+        }
+        return ((t[0] + t[4]) + (t[2] + t[6])) + ((t[1] + t[5]) + (t[3] + t[7]));
+    }
+    if (head_dim == 128u) {
+        for (int j = 0; j < 8; ++j) {
+            float ss0 = 0.0f, ss1 = 0.0f;
+            for (int i = 0; i < 128; i += 16) {
+                ss0 = fmaf(x[i + j], x[i + j], ss0);
+                ss1 = fmaf(x[i + 8 + j], x[i + 8 + j], ss1);
+            }
+            t[j] = ss0 + ss1;
+        }
+        return ((t[0] + t[4]) + (t[1] + t[5])) + ((t[2] + t[6]) + (t[3] + t[7]));
+    }
+    double ss = 0.0;
+    for (uint32_t i = 0; i < head_dim; ++i) ss += (double)x[i] * (double)x[i];
+    return (float)ss;
+}
+
 void orc_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads,
                       uint32_t head_dim, const float *norm_w, float eps,
                       const float *cos_row, const float *sin_row) {
@@ -159,16 +194,18 @@ void orc_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads,
         const float *hp = vec + (size_t)h * head_dim;
         for (uint32_t i = 0; i < head_dim; ++i) tmp[i] = hp[i];
         if (norm_w != NULL) {
-            double ss = 0.0;
-            for (uint32_t i = 0; i < head_dim; ++i) ss += (double)tmp[i] * (double)tmp[i];
-            const float irms = 1.0f / sqrtf((float)(ss / (double)head_dim) + eps);
+            const float ss   = sumsq_ref(tmp, head_dim);
+            const float irms = 1.0f / sqrtf(ss / (float)head_dim + eps);
             for (uint32_t i = 0; i < head_dim; ++i) tmp[i] = (tmp[i] * irms) * norm_w[i];
         }
+        /* the AVX2 kernels (head_dim 64, 128) rotate with fmsub / fmadd,
+         * the scalar kernels with separately rounded products */
+        const int fused = head_dim == 64u || head_dim == 128u;
         for (uint32_t i = 0; i < half; ++i) {
             const float x0 = tmp[i], x1 = tmp[i + half];
             const float c = cos_row[i], s = sin_row[i];
-            const float r0 = x0 * c - x1 * s;
-            const float r1 = x1 * c + x0 * s;
+            const float r0 = fused ? fmaf(x0, c, -(x1 * s)) : x0 * c - x1 * s;
+            const float r1 = fused ? fmaf(x1, c, x0 * s) : x1 * c + x0 * s;
             if (dst_f16 != NULL) {
                 dst_f16[(size_t)h * head_dim + i]        = orc_f32_to_f16(r0);
                 dst_f16[(size_t)h * head_dim + i + half] = orc_f32_to_f16(r1);

@@ -81,6 +81,20 @@ class _Decode:
                           self.n_seq, 1, int(self.ctx.max()), self.nq, self.nkv, self.hd)
         return out.numpy()
 
+    def run_fused(self):
+        """lfm_hip_gqa_f16_step: the prologue inside the attention kernel."""
+        la = self.la
+        out = la.DeviceArray.zeros(self.q_raw.shape, np.float32)
+        qd = dev(la, self.q_raw)
+        la.gqa_f16_step(qd, dev(la, self.k_raw), dev(la, self.v_raw), None if self.g is None else dev(la, self.g),
+                        True, self.kt, self.vt, dev(la, self.pos), out, self.n_seq, 1, int(self.ctx.max()), self.nq,
+                        self.nkv, self.hd, dev(la, self.qw), dev(la, self.kw), EPS, self.cd, self.sd)
+        assert np.array_equal(qd.numpy(), self.q_raw)
+        return out.numpy()
+
+    def run(self, mode):
+        return self.run_fused() if mode == "fused" else self.run_two_launch()
+
     def caches_after(self, s):
         """The device caches of sequence s (with the prologue's new row)."""
         return self.kd[s].numpy(), self.vd[s].numpy()
@@ -90,8 +104,7 @@ class _Decode:
         q = orc.qk_norm_rope(self.q_raw[s], self.nq, self.hd, self.qw, EPS, self.cos[p], self.sin[p])
         want_k = orc.qk_norm_rope(self.k_raw[s], self.nkv, self.hd, self.kw, EPS, self.cos[p], self.sin[p],
                                   store_f16=True)
-        ulp = np.abs(k16[p].reshape(-1).astype(np.int32) - want_k.astype(np.int32))
-        assert ulp.max() <= 1, f"seq {s}: new K row differs by {ulp.max()} ulp"
+        assert np.array_equal(k16[p].reshape(-1), want_k), f"seq {s}: new K row"
         assert np.array_equal(v16[p].reshape(-1), f16(self.v_raw[s]).reshape(-1)), f"seq {s}: new V row"
         g = None if self.g is None else (1.0 / (1.0 + np.exp(-self.g[s]))).astype(np.float32)
         return orc.lfm3_online_gqa_f16(q, g, k16, v16, 1, p, 0, p + 1, self.nq, self.nkv, self.hd)
@@ -115,11 +128,14 @@ class _Decode:
                 parity(got[s], self.oracle(orc, s, k16, v16), what=f"{what} seq {s} ctx {p + 1}")
 
 
+@pytest.mark.parametrize("mode", ["two_launch", "fused"])
 @pytest.mark.parametrize("kind", ["ragged", "northstar"])
-def test_cfg2_fullsize_prologue_then_decode(gpu, orc, kind):
+def test_cfg2_fullsize_prologue_then_decode(gpu, orc, kind, mode):
     """Config 2: 64 sequences, 32q/8kv d64, ctx ~ U[512, 8192] (and all 8192),
     QK-RMSNorm (w = 1 + 0.05 N, eps 1e-5) + RoPE theta 1e6 of the new token,
-    then batched decode.  Every sequence against the oracle and by bounds."""
+    then batched decode -- as two launches (lfm_hip_qkv_prologue, then
+    lfm_hip_gqa_f16_varlen) and fused (lfm_hip_gqa_f16_step).  Every sequence
+    against the oracle and by bounds."""
     la = gpu
     rng = np.random.default_rng(2 if kind == "ragged" else 8192)
     ctx = rng.integers(512, 8193, size=64) if kind == "ragged" else np.full(64, 8192)
@@ -127,8 +143,8 @@ def test_cfg2_fullsize_prologue_then_decode(gpu, orc, kind):
         ctx[0], ctx[1] = 512, 8192
     cos, sin = la.rope_lut_lfm2(8192, 64, 1e6)
     d = _Decode(la, rng, ctx, 32, 8, 64, cos, sin, orc.rope_lut_lfm2(8192, 64, 1e6))
-    got = d.run_two_launch()
-    d.check(orc, got, set(range(64)), f"cfg2 {kind}")
+    got = d.run(mode)
+    d.check(orc, got, set(range(64)), f"cfg2 {kind} {mode}")
 
 
 def test_cfg3_fullsize_verify(gpu, orc):
@@ -156,7 +172,8 @@ def test_cfg3_fullsize_verify(gpu, orc):
                 check_convex(got[s, r, h], vlo[h // 4], vhi[h // 4], f"cfg3 seq {s} row {r} head {h}")
 
 
-def test_cfg5_fullsize_lfm3_full_layer(gpu, orc):
+@pytest.mark.parametrize("mode", ["two_launch", "fused"])
+def test_cfg5_fullsize_lfm3_full_layer(gpu, orc, mode):
     """Config 5, full-attention layer: 32 sequences x ctx 32768, 16q/4kv
     d128, partial-RoPE prologue (theta 1e6; pairs i < 32 rotate, the rest are
     identity) and the sigmoid gate from logits.  8 sequences against the
@@ -167,5 +184,5 @@ def test_cfg5_fullsize_lfm3_full_layer(gpu, orc):
     cos, sin = la.rope_lut_lfm3(32768, 128, 128, 1e6, rf)
     d = _Decode(la, rng, np.full(32, 32768), 16, 4, 128, cos, sin, orc.rope_lut_lfm3(32768, 128, 128, 1e6, rf),
                 gate=True)
-    got = d.run_two_launch()
-    d.check(orc, got, {0, 5, 9, 14, 18, 23, 27, 31}, "cfg5 full")
+    got = d.run(mode)
+    d.check(orc, got, {0, 5, 9, 14, 18, 23, 27, 31}, f"cfg5 full {mode}")

@@ -34,7 +34,8 @@ def test_store_fp32_to_fp16_bit_exact(gpu):
 @pytest.mark.parametrize("hd,base,rope_dim,partial", [(64, 1e6, 64, False), (128, 1e4, 128, False),
                                                        (128, 1e6, 128, True)])
 def test_qk_norm_rope(gpu, orc, hd, base, rope_dim, partial):
-    """A4/A5 for Q (fp32 in place) and K (RNE fp16 store)."""
+    """A4/A5 for Q (fp32 in place) and K (RNE fp16 store), bit for bit: the
+    oracle follows the reference's AVX2 kernels exactly at d64 and d128."""
     la = gpu
     rng = np.random.default_rng(hd)
     n_heads, max_seq, pos, eps = 16, 2048, 1337, 1e-5
@@ -49,15 +50,14 @@ def test_qk_norm_rope(gpu, orc, hd, base, rope_dim, partial):
     xq = dev(la, x)
     la.qk_norm_rope(xq, None, n_heads, hd, wd, eps, cd, sd, pos)
     want_q = orc.qk_norm_rope(x, n_heads, hd, w, eps, cos[pos], sin[pos])
-    parity(xq.numpy(), want_q, max_abs=2e-6, rel_l2=1e-6, what=f"Q norm+rope hd={hd}")
+    # the oracle is bit-identical to the reference's AVX2 kernels at d64 / d128
+    assert np.array_equal(xq.numpy().view(np.uint32), want_q.view(np.uint32)), f"Q norm+rope hd={hd}"
     k16 = la.DeviceArray.zeros(n_heads * hd, np.uint16)
     xk = dev(la, x)
     la.qk_norm_rope(xk, k16, n_heads, hd, wd, eps, cd, sd, pos)
     assert np.array_equal(xk.numpy(), x), "fp16-store mode must leave the source untouched"
     want_k = orc.qk_norm_rope(x, n_heads, hd, w, eps, cos[pos], sin[pos], store_f16=True)
-    got_k = k16.numpy()
-    ulp = np.abs(got_k.astype(np.int32) - want_k.astype(np.int32))
-    assert ulp.max() <= 1 and np.count_nonzero(ulp) <= max(2, got_k.size // 500), ulp.max()
+    assert np.array_equal(k16.numpy(), want_k), f"K fp16 store hd={hd}"
     if partial:  # dims of identity pairs are the normalised input, unrotated
         keep = np.r_[hd // 4:hd // 2, 3 * hd // 4:hd]
         normed = orc.qk_norm_rope(x, n_heads, hd, w, eps, np.ones(hd // 2, np.float32),
@@ -92,8 +92,7 @@ def test_qkv_prologue_batched(gpu, orc):
             slot = p % cap
             assert la.slot_of(p, win, cap) == slot
             wq = orc.qk_norm_rope(q[s, r], nq, hd, qw, eps, cos[p], sin[p])
-            parity(gq[s, r], wq, max_abs=2e-6, rel_l2=1e-6, what=f"q s={s} r={r}")
+            assert np.array_equal(gq[s, r].reshape(-1).view(np.uint32), wq.view(np.uint32)), f"q s={s} r={r}"
             wk = orc.qk_norm_rope(k[s, r], nkv, hd, kw, eps, cos[p], sin[p], store_f16=True)
-            d = np.abs(ks[slot].reshape(-1).astype(np.int32) - wk.astype(np.int32))
-            assert d.max() <= 1
+            assert np.array_equal(ks[slot].reshape(-1), wk), f"k s={s} r={r}"
             assert np.array_equal(vs[slot].reshape(-1), f16(v[s, r]).reshape(-1))

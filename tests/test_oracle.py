@@ -109,12 +109,12 @@ def test_qk_norm_rope_closed_form(orc):
 
 def test_qk_norm_rope_reference_inputs(orc, gold):
     """tests/test_kernels_fast.c:121-173 (16 heads, d64, pos 42): within 1e-4 of
-    the powf/cosf/sinf formula there, and equal to the reference kernel's
-    golden output to fp32 rounding."""
+    the powf/cosf/sinf formula there, and bit-identical to the reference
+    kernel's golden output (Q fp32 and the fp16 K store)."""
     q, w = gold["qk_lfm2_in"], gold["qk_lfm2_w"]
     c, s = orc.rope_lut_lfm2(128, 64, 1e6)
     got = orc.qk_norm_rope(q, 16, 64, w, 1e-5, c[42], s[42])
-    assert np.abs(got - gold["qk_lfm2_out"]).max() < 1e-6
+    assert np.array_equal(got.view(np.uint32), gold["qk_lfm2_out"].view(np.uint32))
     want = q.reshape(16, 64).astype(np.float64)
     want = want / np.sqrt((want ** 2).mean(1, keepdims=True) + 1e-5) * w
     i = np.arange(32)
@@ -123,28 +123,63 @@ def test_qk_norm_rope_reference_inputs(orc, gold):
     want = np.concatenate([want[:, :32] * cc - want[:, 32:] * ss, want[:, 32:] * cc + want[:, :32] * ss], 1)
     assert np.abs(got - want.reshape(-1)).max() < 1e-4
     k16 = orc.qk_norm_rope(q, 16, 64, w, 1e-5, c[42], s[42], store_f16=True)
-    assert np.abs(k16.astype(np.int32) - gold["qk_lfm2_k16"].astype(np.int32)).max() <= 1
+    assert np.array_equal(k16, gold["qk_lfm2_k16"])
 
 
 def test_qk_norm_rope_partial_reference(orc, gold):
-    """tests/test_lfm3.c:104-168: d128 partial RoPE, pos 17, 4 heads."""
+    """tests/test_lfm3.c:104-168: d128 partial RoPE, pos 17, 4 heads;
+    bit-identical to the reference kernel's golden output."""
     c, s = orc.rope_lut_lfm3(64, 128, 128, 1e6, gold["qk_lfm3_rf"])
     got = orc.qk_norm_rope(gold["qk_lfm3_in"], 4, 128, gold["qk_lfm3_w"], 1e-5, c[17], s[17])
-    assert np.abs(got - gold["qk_lfm3_out"]).max() < 1e-5
+    assert np.array_equal(got.view(np.uint32), gold["qk_lfm3_out"].view(np.uint32))
     k16 = orc.qk_norm_rope(gold["qk_lfm3_in"], 4, 128, gold["qk_lfm3_w"], 1e-5, c[17], s[17],
                            store_f16=True)
-    assert np.abs(f16_to_f32(k16) - f16_to_f32(gold["qk_lfm3_k16"])).max() <= 1e-3
+    assert np.array_equal(k16, gold["qk_lfm3_k16"])
 
 
-def test_qk_norm_rope_matches_reference_kernels(orc, ref):
+@pytest.mark.parametrize("hd", [64, 128])
+def test_qk_norm_rope_matches_reference_kernels(orc, ref, hd):
+    """Bit for bit against the engine's AVX2 kernels (lfm2_qk_norm_rope_avx2
+    at d64, lfm3_qk_norm_rope_128_avx2 at d128): the sum of squares in their
+    column order and horizontal-sum tree, fmsub/fmadd rotation, RNE store;
+    the scalar kernels (double or float sums, separately rounded rotation)
+    within 2e-6."""
     rng = np.random.default_rng(4)
-    c, s = orc.rope_lut_lfm2(512, 64, 1e6)
-    x = rng.standard_normal(32 * 64).astype(np.float32) * 3
-    w = (1 + 0.05 * rng.standard_normal(64)).astype(np.float32)
-    mine = orc.qk_norm_rope(x, 32, 64, w, 1e-5, c[300], s[300])
-    for scalar in (False, True):
-        theirs = ref.qk_norm_rope(x, 32, 64, w, 1e-5, c, s, 300, scalar=scalar)
+    if hd == 64:
+        c, s = orc.rope_lut_lfm2(512, 64, 1e6)
+    else:
+        c, s = orc.rope_lut_lfm3(512, 128, 128, 1e6, np.array([1.0] * 32 + [1e30] * 32, np.float32))
+    for trial in range(20):
+        x = rng.standard_normal(32 * hd).astype(np.float32) * np.float32(3 if trial % 2 else 0.01)
+        w = (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32)
+        mine = orc.qk_norm_rope(x, 32, hd, w, 1e-5, c[300], s[300])
+        assert np.array_equal(mine.view(np.uint32), ref.qk_norm_rope(x, 32, hd, w, 1e-5, c, s, 300).view(np.uint32))
+        k_mine = orc.qk_norm_rope(x, 32, hd, w, 1e-5, c[300], s[300], store_f16=True)
+        assert np.array_equal(k_mine, ref.qk_norm_rope(x, 32, hd, w, 1e-5, c, s, 300, store_f16=True))
+        theirs = ref.qk_norm_rope(x, 32, hd, w, 1e-5, c, s, 300, scalar=True)
         assert np.abs(mine - theirs).max() < 2e-6
+
+
+def test_qk_norm_rope_order_pins_a_planted_mistake(orc, ref):
+    """A sum of squares added in plain sequential order (a plausible
+    restatement) is not bit-identical to the AVX2 kernels on these inputs,
+    so the bit-exact check above has teeth."""
+    rng = np.random.default_rng(9)
+    c, s = orc.rope_lut_lfm2(64, 64, 1e6)
+    diffs = 0
+    for _ in range(20):
+        x = rng.standard_normal(16 * 64).astype(np.float32) * 3
+        w = (1 + 0.05 * rng.standard_normal(64)).astype(np.float32)
+        theirs = ref.qk_norm_rope(x, 16, 64, w, 1e-5, c, s, 33)
+        xs = x.reshape(16, 64)
+        ss = np.zeros(16, np.float32)
+        for i in range(64):
+            ss = (ss + xs[:, i] * xs[:, i]).astype(np.float32)
+        irms = (np.float32(1.0) / np.sqrt(ss / np.float32(64) + np.float32(1e-5))).astype(np.float32)
+        normed = ((xs * irms[:, None]).astype(np.float32) * w).astype(np.float32)
+        mine = orc.qk_norm_rope(normed.reshape(-1), 16, 64, None, 1e-5, c[33], s[33])
+        diffs += int(np.count_nonzero(mine.view(np.uint32) != theirs.view(np.uint32)))
+    assert diffs > 0
 
 
 # ---- A1/A2/A3/A7 attention ----------------------------------------------------------------------
