@@ -20,8 +20,11 @@
  *     shapes and positions are rejected on the host before any launch; no
  *     partial work is enqueued for a rejected call.
  *   - Entry points that split the key range across workgroups use a
- *     library-owned device workspace (grown on demand, one per device);
- *     calls that overlap on one device from several host threads race on it.
+ *     library-owned device workspace (grown on demand, one per device):
+ *     work on one device must run on one stream at a time, since two calls
+ *     on different streams with no synchronization between them can overlap
+ *     on the GPU and race on it (whether one host thread enqueued them or
+ *     several).
  */
 #ifndef LFM_ATTN_H
 #define LFM_ATTN_H
@@ -84,6 +87,13 @@ int lfm_attn_rope_lut_lfm2(float *cos_lut, float *sin_lut, uint32_t max_seq, uin
 int lfm_attn_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq, uint32_t head_dim,
                            uint32_t rope_dim, float freq_base, const float *rope_freqs,
                            uint32_t n_rope_freqs);
+
+/* Gen-1 RoPE row (host): cos_row[i], sin_row[i] of (float)pos * (1 /
+ * powf(theta, 2i / head_dim)), i < head_dim / 2, computed in float with
+ * powf/cosf/sinf on every call as lfm_rope_neox does (src/lfm_forward.c:97-111;
+ * the Gen-1 engine has no table).  Upload the row for the position of a
+ * lfm_hip_gen1_gqa_step call. */
+int lfm_attn_rope_row_gen1(float *cos_row, float *sin_row, uint32_t head_dim, uint32_t pos, float theta);
 
 /* ---- prologue: per-head QK-RMSNorm + NeoX RoPE (+ RNE fp16 KV store) -------- */
 /* Replaces lfm2_qk_norm_rope_simd (tools/lfm2_kernels_fast.c:403-497, :511-547)
@@ -201,6 +211,22 @@ int lfm_hip_gqa_heads(const float *q, const float *k_cache, const float *v_cache
                       const uint16_t *k_cache_f16, const uint16_t *v_cache_f16, float *xb,
                       uint32_t n_head_q, uint32_t kv_mul, uint32_t head_dim, uint32_t kv_dim,
                       uint32_t max_seq_len, uint32_t pos, float scale, lfm_attn_stream_t stream);
+
+/* A6 -- replaces steps 2-4 of the Gen-1 lfm_gqa_step (src/lfm_forward.c:
+ * 184-244, include/lfm_forward.h:64-72): per head RMSNorm
+ * (lfm_vec_rmsnorm_f32, src/lfm_simd.c:125-174) and NeoX RoPE of q and k,
+ * the FP32 append of k and v at cache row pos, then softmax(q.k / sqrt(hd)).v
+ * over rows 0..pos of every query head (kv head = h / (n_heads_q /
+ * n_heads_kv)).  q, k, v: the projections ([n_heads][head_dim] float, device);
+ * q is normalised and rotated in place (the reference's arena scratch).
+ * q_norm, k_norm: [head_dim] or NULL (no weight).  k_cache, v_cache:
+ * [max_seq][n_heads_kv * head_dim] float.  cos_row, sin_row: the row of
+ * lfm_attn_rope_row_gen1 for pos (device).  attn_out: [n_heads_q][head_dim];
+ * the wo projection stays with the caller.  head_dim % 8 == 0, <= 256. */
+int lfm_hip_gen1_gqa_step(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                          float *k_cache, float *v_cache, float *attn_out, uint32_t pos, uint32_t max_seq,
+                          uint32_t n_heads_q, uint32_t n_heads_kv, uint32_t head_dim, float eps,
+                          const float *cos_row, const float *sin_row, lfm_attn_stream_t stream);
 
 /* A3 -- replaces lfm3_online_gqa_f16_dispatch, tools/lfm3_engine.c:1155-1204
  * (workers :851-946, :1057-1153).  Row b is position pos_0 + b and attends

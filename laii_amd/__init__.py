@@ -17,6 +17,7 @@ from .attention import (  # noqa: F401
     EngineContext,
     device_count,
     fnv1a64,
+    gen1_gqa_step,
     gqa_f16_step,
     gqa_f16_varlen,
     gqa_f16_varlen_noalloc,
@@ -36,6 +37,7 @@ from .attention import (  # noqa: F401
     require_gpu,
     rope_lut_lfm2,
     rope_lut_lfm3,
+    rope_row_gen1,
     seg_plan,
     slot_of,
     store_fp32_to_fp16,

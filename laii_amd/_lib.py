@@ -54,6 +54,9 @@ SIGNATURES = {
                                    _u32, _f32, _vp]),
     "lfm_hip_gqa_f16_varlen": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _u32, _u32, _u32, _f32, _vp]),
+    "lfm_attn_rope_row_gen1": (_int, [_vp, _vp, _u32, _u32, _f32]),
+    "lfm_hip_gen1_gqa_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32,
+                                     _vp, _vp, _vp]),
     "lfm_hip_gqa_f16_step": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                     _u32, _u32, _u32, _u32, _f32, _vp, _vp, _f32, _vp, _vp, _vp]),
     "lfm_hip_gqa_f16_varlen_noalloc": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,

@@ -238,6 +238,25 @@ def gqa_f16_varlen(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Pt
                                         cap, scale, stream), "lfm_hip_gqa_f16_varlen")
 
 
+def rope_row_gen1(head_dim: int, pos: int, theta: float):
+    """Gen-1 per-call rotation row (lfm_rope_neox, src/lfm_forward.c:97-111)."""
+    c = np.empty(head_dim // 2, np.float32)
+    s = np.empty_like(c)
+    check(load().lfm_attn_rope_row_gen1(c.ctypes.data, s.ctypes.data, head_dim, pos, theta),
+          "lfm_attn_rope_row_gen1")
+    return c, s
+
+
+def gen1_gqa_step(q: Ptr, k: Ptr, v: Ptr, q_norm: Ptr, k_norm: Ptr, k_cache: Ptr, v_cache: Ptr,
+                  attn_out: Ptr, pos: int, max_seq: int, n_heads_q: int, n_heads_kv: int, head_dim: int,
+                  eps: float, cos_row: Ptr, sin_row: Ptr, stream=None) -> None:
+    """Steps 2-4 of the Gen-1 lfm_gqa_step (src/lfm_forward.c:184-244) on
+    device buffers: QK-RMSNorm + RoPE, FP32 KV append at pos, attention."""
+    check(load().lfm_hip_gen1_gqa_step(_p(q), _p(k), _p(v), _p(q_norm), _p(k_norm), _p(k_cache), _p(v_cache),
+                                       _p(attn_out), pos, max_seq, n_heads_q, n_heads_kv, head_dim, eps,
+                                       _p(cos_row), _p(sin_row), stream), "lfm_hip_gen1_gqa_step")
+
+
 def gqa_f16_step(q: Ptr, k: Ptr, v: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v_seq: Ptr,
                  pos_0: Ptr, out: Ptr, n_seq: int, n_rows: int, keys_hint: int, n_head_q: int,
                  n_head_kv: int, head_dim: int, q_norm_w: Ptr, k_norm_w: Ptr, eps: float,

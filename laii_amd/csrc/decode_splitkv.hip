@@ -167,6 +167,13 @@ __device__ __forceinline__ float sumsq_ref_order(const float (&x)[HD / 32][8], i
  * prologue kernel and of the reference's AVX2 kernels
  * (tools/lfm2_kernels_fast.c:403-497, tools/lfm3_engine.c:463-525), sum of
  * squares included.  Every lane of the wave must call it (cross-lane sums). */
+__device__ __forceinline__ void load8(const float *p, float (&x)[8]) {
+    const float4 a = *reinterpret_cast<const float4 *>(p);
+    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+}
+
 template <int HD>
 __device__ __forceinline__ void norm_rope_frag(float (&x)[HD / 32][8], uint32_t pos, const float *norm_w, float eps,
                                                const float *cos_lut, const float *sin_lut, int g) {
@@ -176,9 +183,8 @@ __device__ __forceinline__ void norm_rope_frag(float (&x)[HD / 32][8], uint32_t 
         const float irms = 1.0f / sqrtf(ss / (float)HD + eps);
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
-            const float4 w0 = *reinterpret_cast<const float4 *>(norm_w + 32 * st + 8 * g);
-            const float4 w1 = *reinterpret_cast<const float4 *>(norm_w + 32 * st + 8 * g + 4);
-            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            float w[8];
+            load8(norm_w + 32 * st + 8 * g, w);
 #pragma unroll
             for (int j = 0; j < 8; ++j) x[st][j] = (x[st][j] * irms) * w[j];
         }
@@ -187,12 +193,9 @@ __device__ __forceinline__ void norm_rope_frag(float (&x)[HD / 32][8], uint32_t 
     const float *sr = sin_lut + (size_t)pos * HALF;
 #pragma unroll
     for (int st = 0; st < NS / 2; ++st) {
-        const float4 c0 = *reinterpret_cast<const float4 *>(cr + 32 * st + 8 * g);
-        const float4 c1 = *reinterpret_cast<const float4 *>(cr + 32 * st + 8 * g + 4);
-        const float4 s0 = *reinterpret_cast<const float4 *>(sr + 32 * st + 8 * g);
-        const float4 s1 = *reinterpret_cast<const float4 *>(sr + 32 * st + 8 * g + 4);
-        const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        float c[8], sn[8];
+        load8(cr + 32 * st + 8 * g, c);
+        load8(sr + 32 * st + 8 * g, sn);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float lo = x[st][j], hi = x[st + NS / 2][j];
@@ -223,13 +226,6 @@ __device__ __forceinline__ u32x4_t pack8_rne(const float (&x)[8]) {
     return w;
 }
 
-__device__ __forceinline__ void load8(const float *p, float (&x)[8]) {
-    const float4 a = *reinterpret_cast<const float4 *>(p);
-    const float4 b = *reinterpret_cast<const float4 *>(p + 4);
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-}
-
 /* Keys [lo, last] that the rows of sequence s attend (their union). */
 struct SeqKeys {
     uint32_t pos0, lo, last;
@@ -247,8 +243,9 @@ __device__ __forceinline__ SeqKeys seq_keys(const SplitParams &P, uint32_t s) {
  * gated output is written; otherwise the unnormalised O^T and (max, sum)
  * go to the partial slots part + column. */
 template <int HD, int NT, bool FUSE>
-__device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, uint32_t s, uint32_t pos0, uint32_t kvh,
-                                            uint32_t kb, uint32_t ke, bool direct, size_t part) {
+__device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, uint16_t *fresh, uint32_t s,
+                                            uint32_t pos0, uint32_t kvh, uint32_t kb, uint32_t ke, bool direct,
+                                            size_t part) {
     constexpr int NS  = HD / 32; /* MFMA k-steps of Q.K^T (32 dims each)          */
     constexpr int NM  = HD / 16; /* 16-dim tiles of O^T                            */
     constexpr int NVL = HD / 16; /* 16-byte V pieces per lane per 32-key sub-tile  */
@@ -264,6 +261,39 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     const size_t row   = (size_t)P.n_head_kv * HD; /* elements per cache slot */
     kc += (size_t)kvh * HD;
     vc += (size_t)kvh * HD;
+
+    /* ---- sub-tile loader ------------------------------------------------------ */
+    auto load_tile = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
+        const uint32_t base = P.window ? (p0 % P.cap) : p0;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            uint32_t off = (uint32_t)(16 * kt + l16);
+            if (p0 + off >= ke) off = ke - 1u - p0; /* clamp: masked later */
+            uint32_t slot = base + off;
+            if (P.window) { while (slot >= P.cap) slot -= P.cap; }
+            gu16_ptr kp = kc + (size_t)slot * row + 8 * g;
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+                kd[kt][st] = load16(kp + 32 * st);
+        }
+#pragma unroll
+        for (int ps = 0; ps < HD / 64; ++ps) {
+            const int quad = ps * QPP + lane / CH;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t off = (uint32_t)(4 * quad + i);
+                if (p0 + off >= ke) off = ke - 1u - p0;
+                uint32_t slot = base + off;
+                if (P.window) { while (slot >= P.cap) slot -= P.cap; }
+                vd[ps * 4 + i] = load16(vc + (size_t)slot * row + 8 * (lane % CH));
+            }
+        }
+    };
+
+    /* the first sub-tile is in flight while the query fragments are built */
+    const uint32_t nsub = (ke - kb + 31u) / 32u;
+    u32x4_t kA[2][NS], vA[NVL], kB[2][NS], vB[NVL];
+    load_tile(kb, kA, vA);
 
     /* ---- per-column row bounds and Q fragments ------------------------------ */
     uint32_t col_lo[NT], col_hi[NT];
@@ -308,74 +338,73 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     const uint32_t free_lo = lfm_plan_row(last, P.window, P.cap).t_start;
     const uint32_t free_hi = min(pos0, ke - 1u);
 
-    /* ---- sub-tile loader ------------------------------------------------------ */
-    auto load_tile = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
-        const uint32_t base = P.window ? (p0 % P.cap) : p0;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            uint32_t off = (uint32_t)(16 * kt + l16);
-            if (p0 + off >= ke) off = ke - 1u - p0; /* clamp: masked later */
-            uint32_t slot = base + off;
-            if (P.window) { while (slot >= P.cap) slot -= P.cap; }
-            gu16_ptr kp = kc + (size_t)slot * row + 8 * g;
-#pragma unroll
-            for (int st = 0; st < NS; ++st)
-                kd[kt][st] = load16(kp + 32 * st);
-        }
-#pragma unroll
-        for (int ps = 0; ps < HD / 64; ++ps) {
-            const int quad = ps * QPP + lane / CH;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t off = (uint32_t)(4 * quad + i);
-                if (p0 + off >= ke) off = ke - 1u - p0;
-                uint32_t slot = base + off;
-                if (P.window) { while (slot >= P.cap) slot -= P.cap; }
-                vd[ps * 4 + i] = load16(vc + (size_t)slot * row + 8 * (lane % CH));
-            }
-        }
-    };
 
     /* ---- fused prologue: the rows of this call's positions -------------------
-     * Keys >= pos0 are the new tokens.  The sub-tile that holds one gets its
-     * row from the raw k/v (normalised, rotated, RNE fp16) instead of from
-     * the cache it was loaded from, and the lane that owns the row's 16 bytes
-     * stores them at the row's slot.  Lanes clamped to the last key (past ke)
-     * take that key's new row too, so no stale slot content enters the
-     * product.  Each new key lies in exactly one segment of the plan, so each
-     * row is stored once; no other wave reads those bytes in this launch. */
-    uint16_t *kw = nullptr, *vw = nullptr;
+     * Keys >= pos0 are the new tokens.  Before the key loop, the wave whose
+     * range [kb, ke) holds new keys builds those rows from the raw k/v
+     * (normalised, rotated, RNE fp16), stores them at their cache slots and
+     * stages them in its LDS area `fresh` ([n_rows][HD] K, then V).  Each new
+     * key lies in exactly one segment of the plan, so each row is stored once,
+     * and no other wave reads those bytes in this launch.  In the loop, the
+     * sub-tiles that reach pos0 take those rows from LDS in place of what was
+     * loaded from the slots (lanes clamped past ke take the last key's row
+     * too, so no stale slot content enters the product); the loop itself
+     * issues no extra global memory operations. */
+    const bool has_fresh = FUSE && ke > pos0;
     if constexpr (FUSE) {
-        kw = const_cast<uint16_t *>(P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride) + (size_t)kvh * HD;
-        vw = const_cast<uint16_t *>(P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride) + (size_t)kvh * HD;
+        if (has_fresh) {
+            uint16_t *kw = const_cast<uint16_t *>(P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride) +
+                           (size_t)kvh * HD;
+            uint16_t *vw = const_cast<uint16_t *>(P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride) +
+                           (size_t)kvh * HD;
+            const uint32_t r0 = max(kb, pos0) - pos0, r1 = ke - pos0; /* rows of this segment */
+            for (uint32_t rb = r0; rb < r1; rb += 16u) {
+                const uint32_t r  = rb + (uint32_t)l16;
+                const bool real   = r < r1;
+                float x[NS][8];
+                if (real) {
+                    const float *kp = P.k_new + (((size_t)s * P.n_rows + r) * P.n_head_kv + kvh) * HD + 8 * g;
+#pragma unroll
+                    for (int st = 0; st < NS; ++st) load8(kp + 32 * st, x[st]);
+                } else {
+#pragma unroll
+                    for (int st = 0; st < NS; ++st)
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) x[st][j] = 0.0f;
+                }
+                norm_rope_frag<HD>(x, real ? pos0 + r : pos0, P.k_norm_w, P.eps, P.cos_lut, P.sin_lut, g);
+                if (real) {
+                    const size_t off = (size_t)lfm_slot_of(pos0 + r, P.window, P.cap) * row + 8 * g;
+#pragma unroll
+                    for (int st = 0; st < NS; ++st) {
+                        const u32x4_t w = pack8_rne(x[st]);
+                        *reinterpret_cast<u32x4_t *>(kw + off + 32 * st)                        = w;
+                        *reinterpret_cast<u32x4_t *>(fresh + (size_t)r * HD + 8 * g + 32 * st) = w;
+                    }
+                }
+            }
+            for (uint32_t e = r0 * CH + (uint32_t)lane; e < r1 * CH; e += 64u) {
+                const uint32_t r = e / CH, c = e % CH;
+                float x[8];
+                load8(P.v_new + (((size_t)s * P.n_rows + r) * P.n_head_kv + kvh) * HD + 8 * c, x);
+                const u32x4_t w = pack8_rne(x);
+                *reinterpret_cast<u32x4_t *>(vw + (size_t)lfm_slot_of(pos0 + r, P.window, P.cap) * row + 8 * c) = w;
+                *reinterpret_cast<u32x4_t *>(fresh + (size_t)(P.n_rows + r) * HD + 8 * c)                     = w;
+            }
+            wave_lds_sync();
+        }
     }
+    /* the staged rows in place of the slots' contents, for the lanes whose
+     * (clamped) key is >= pos0 */
     auto patch_new_rows = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            uint32_t key    = p0 + (uint32_t)(16 * kt + l16);
-            const bool real = key < ke;
-            if (!real) key = ke - 1u;
-            const bool fresh = key >= pos0;
-            float x[NS][8];
-            if (fresh) {
-                const float *kp = P.k_new + (((size_t)s * P.n_rows + (key - pos0)) * P.n_head_kv + kvh) * HD + 8 * g;
-#pragma unroll
-                for (int st = 0; st < NS; ++st) load8(kp + 32 * st, x[st]);
-            } else {
+            uint32_t key = p0 + (uint32_t)(16 * kt + l16);
+            if (key >= ke) key = ke - 1u;
+            if (key >= pos0) {
 #pragma unroll
                 for (int st = 0; st < NS; ++st)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) x[st][j] = 0.0f;
-            }
-            norm_rope_frag<HD>(x, fresh ? key : pos0, P.k_norm_w, P.eps, P.cos_lut, P.sin_lut, g);
-            if (fresh) {
-                const size_t off = (size_t)lfm_slot_of(key, P.window, P.cap) * row + 8 * g;
-#pragma unroll
-                for (int st = 0; st < NS; ++st) {
-                    const u32x4_t w = pack8_rne(x[st]);
-                    kd[kt][st]      = w;
-                    if (real) *reinterpret_cast<u32x4_t *>(kw + off + 32 * st) = w;
-                }
+                    kd[kt][st] = *reinterpret_cast<const u32x4_t *>(fresh + (size_t)(key - pos0) * HD + 8 * g + 32 * st);
             }
         }
 #pragma unroll
@@ -383,16 +412,11 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
             const int quad = ps * QPP + lane / CH;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                uint32_t key    = p0 + (uint32_t)(4 * quad + i);
-                const bool real = key < ke;
-                if (!real) key = ke - 1u;
-                if (key < pos0) continue;
-                float x[8];
-                load8(P.v_new + (((size_t)s * P.n_rows + (key - pos0)) * P.n_head_kv + kvh) * HD + 8 * (lane % CH), x);
-                const u32x4_t w  = pack8_rne(x);
-                vd[ps * 4 + i]   = w;
-                if (real)
-                    *reinterpret_cast<u32x4_t *>(vw + (size_t)lfm_slot_of(key, P.window, P.cap) * row + 8 * (lane % CH)) = w;
+                uint32_t key = p0 + (uint32_t)(4 * quad + i);
+                if (key >= ke) key = ke - 1u;
+                if (key >= pos0)
+                    vd[ps * 4 + i] = *reinterpret_cast<const u32x4_t *>(
+                        fresh + (size_t)(P.n_rows + key - pos0) * HD + 8 * (lane % CH));
             }
         }
     };
@@ -519,16 +543,13 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
      * skipped it, so each sub-tile waited for the next one's loads as well
      * (vmcnt(0)).  Measured on MI355X: headline 192.4 -> 190.0 us, verify
      * 41.7 -> 39.7 us, LFM3 SWA 10.6 -> 10.3 us, outputs bit-identical. */
-    const uint32_t nsub = (ke - kb + 31u) / 32u;
-    u32x4_t kA[2][NS], vA[NVL], kB[2][NS], vB[NVL];
     /* sub-tile at p0 with its new rows substituted (FUSE), then consumed */
     auto consume = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
         if constexpr (FUSE) {
-            if (p0 + 31u >= pos0) patch_new_rows(p0, kd, vd);
+            if (has_fresh && p0 + 31u >= pos0) patch_new_rows(p0, kd, vd);
         }
         process(p0, kd, vd);
     };
-    load_tile(kb, kA, vA);
     uint32_t it = 0;
     for (; it + 2u < nsub; it += 2u) {
         const uint32_t p0 = kb + 32u * it;
@@ -584,6 +605,21 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     }
 }
 
+/* Dynamic LDS of the fused kernels: per wave, the staged new rows
+ * ([n_rows][HD] K, then V, fp16). */
+extern __shared__ __attribute__((aligned(16))) uint16_t fresh_lds[];
+
+template <int HD, bool FUSE>
+__device__ __forceinline__ uint16_t *fresh_area(const SplitParams &P, uint32_t wave) {
+    return FUSE ? fresh_lds + (size_t)wave * 2u * P.n_rows * HD : nullptr;
+}
+
+/* Dynamic LDS bytes of a fused launch of W waves. */
+template <int HD, bool FUSE>
+constexpr size_t fresh_bytes(uint32_t W, uint32_t n_rows) {
+    return FUSE ? (size_t)W * 2u * n_rows * HD * sizeof(uint16_t) : 0u;
+}
+
 /* Grid form: workgroup (split, head group, sequence); the W waves take W
  * adjacent KV heads over the same key chunk, so each workgroup streams
  * contiguous runs of the cache rows.  Fixed-length chunks; a sequence longer
@@ -607,7 +643,8 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
         for (uint32_t n = lane; n < P.ncols; n += 64) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
         return;
     }
-    run_segment<HD, NT, FUSE>(P, vt_all[wave], s, k.pos0, kvh, kb, ke, P.n_splits == 1u, part);
+    run_segment<HD, NT, FUSE>(P, vt_all[wave], fresh_area<HD, FUSE>(P, wave), s, k.pos0, kvh, kb, ke,
+                              P.n_splits == 1u, part);
 }
 
 /* Small batches (few (sequence, KV head) pairs): one workgroup per pair, its
@@ -632,7 +669,8 @@ __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
         if (kb > k.last) {
             for (uint32_t n = (uint32_t)lane; n < P.ncols; n += 64u) P.part_ml[part + n] = make_float2(kNegBig, 0.0f);
         } else {
-            run_segment<HD, NT, FUSE>(P, vt_all[split], s, k.pos0, kvh, kb, ke, false, part);
+            run_segment<HD, NT, FUSE>(P, vt_all[split], fresh_area<HD, FUSE>(P, split), s, k.pos0, kvh, kb, ke,
+                                      false, part);
         }
     }
     __syncthreads();
@@ -784,40 +822,46 @@ __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
         }
     }
     if (wg >= pl.G) return;
+    /* One walk for both plans, so the kernel holds one copy of the segment
+     * code: a uniform batch has one segment per workgroup (unit = (sequence,
+     * group), n workgroups per unit, equal shares), a ragged one cuts its
+     * tile share at unit boundaries. */
+    lfm_bal_useg u{};
+    uint64_t t = 0, t1 = 1, first = 0;
+    uint32_t s = 0;
     if (pl.uniform) {
-        /* unit = (sequence, group), n workgroups per unit, equal shares */
-        const lfm_bal_useg u = lfm_bal_uniform_segment(&c, wg, pl.G, pl.T / c.n_seq);
-        const uint32_t kvh   = u.grp * W + wave;
-        if (kvh >= P.n_head_kv) return;
-        const uint32_t pos0 = pos_of(P, pl, u.s);
-        uint32_t kb, ke;
-        lfm_bal_seg_keys(&c, pos0, u.a, u.b, &kb, &ke);
-        run_segment<HD, NT, FUSE>(P, vt_all[wave], u.s, pos0, kvh, kb, ke, u.n == 1u,
-                            ((size_t)u.slot * P.n_head_kv + kvh) * P.ncols);
-        return;
+        u = lfm_bal_uniform_segment(&c, wg, pl.G, pl.T / c.n_seq);
+    } else {
+        lfm_bal_wg_tiles(wg, (uint64_t)pl.T * c.n_groups, pl.G, &t, &t1);
+        find_seq(P, t, lane, &s, &first);
     }
-    const uint64_t N = (uint64_t)pl.T * c.n_groups;
-    uint64_t t, t1;
-    lfm_bal_wg_tiles(wg, N, pl.G, &t, &t1);
-    uint32_t s;
-    uint64_t first;
-    find_seq(P, t, lane, &s, &first);
     while (t < t1) {
-        const uint32_t pos0  = pos_of(P, pl, s);
-        const uint32_t tiles = lfm_bal_seq_tiles(&c, pos0);
-        const lfm_bal_seg sg = lfm_bal_segment(t, t1, first, tiles);
-        const uint32_t kvh   = sg.grp * W + wave;
+        uint32_t seq, grp, a, b, pos0;
+        uint64_t slot;
+        bool direct;
+        if (pl.uniform) {
+            seq = u.s, grp = u.grp, a = u.a, b = u.b, slot = u.slot, direct = u.n == 1u;
+            pos0 = pos_of(P, pl, seq);
+            t    = t1;
+        } else {
+            seq                  = s;
+            pos0                 = pos_of(P, pl, s);
+            const uint32_t tiles = lfm_bal_seq_tiles(&c, pos0);
+            const lfm_bal_seg sg = lfm_bal_segment(t, t1, first, tiles);
+            grp = sg.grp, a = sg.a, b = sg.b, direct = sg.whole != 0;
+            slot = lfm_bal_slot(wg, s, c.n_groups, sg.grp);
+            t    = sg.end;
+            if (t == first + (uint64_t)tiles * c.n_groups) {
+                first = t;
+                ++s;
+            }
+        }
+        const uint32_t kvh = grp * W + wave;
         if (kvh < P.n_head_kv) {
             uint32_t kb, ke;
-            lfm_bal_seg_keys(&c, pos0, sg.a, sg.b, &kb, &ke);
-            const uint64_t slot = lfm_bal_slot(wg, s, c.n_groups, sg.grp);
-            run_segment<HD, NT, FUSE>(P, vt_all[wave], s, pos0, kvh, kb, ke, sg.whole != 0,
-                                ((size_t)slot * P.n_head_kv + kvh) * P.ncols);
-        }
-        t = sg.end;
-        if (t == first + (uint64_t)tiles * c.n_groups) {
-            first = t;
-            ++s;
+            lfm_bal_seg_keys(&c, pos0, a, b, &kb, &ke);
+            run_segment<HD, NT, FUSE>(P, vt_all[wave], fresh_area<HD, FUSE>(P, wave), seq, pos0, kvh, kb, ke, direct,
+                                      ((size_t)slot * P.n_head_kv + kvh) * P.ncols);
         }
     }
 }
@@ -981,7 +1025,8 @@ hipError_t launch_hd_nt_w(const SplitParams &p, uint32_t n_seq, hipStream_t stre
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv<HD, NT, W, FUSE>), grid, dim3(64 * W), 0, stream, p);
+    hipLaunchKernelGGL((k_splitkv<HD, NT, W, FUSE>), grid, dim3(64 * W), (fresh_bytes<HD, FUSE>(W, p.n_rows)), stream,
+                       p);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     if (e != hipSuccess || p.n_splits == 1u) return e;
@@ -1032,19 +1077,22 @@ uint32_t choose_waves(uint32_t n_head_kv, uint32_t head_dim) {
     return w >= 8u ? 8u : (w >= 4u ? 4u : (w >= 2u ? 2u : 1u));
 }
 
-/* Workgroups of k_splitkv_bal<HD, NT, W> resident on the whole device at
- * once (queried once per instantiation). */
+/* Workgroups of k_splitkv_bal<HD, NT, W, FUSE> resident on the whole
+ * device at once, with `dyn` bytes of dynamic LDS each (queried once per
+ * instantiation and LDS size). */
 template <int HD, int NT, int W, bool FUSE>
-uint32_t resident_wgs() {
+uint32_t resident_wgs(size_t dyn) {
     static uint32_t cached = 0;
-    if (cached) return cached;
+    static size_t cached_dyn = 0;
+    if (cached && cached_dyn == dyn) return cached;
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE>, 64 * W, 0) !=
-            hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE>, 64 * W,
+                                                     dyn) != hipSuccess)
         return 256u;
-    cached = (uint32_t)((cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1));
+    cached     = (uint32_t)((cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1));
+    cached_dyn = dyn;
     return cached;
 }
 
@@ -1056,7 +1104,7 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
     lfm_bal_cfg &c     = p.plan;
     p.wpg              = W;
     c.n_groups         = (p.n_head_kv + W - 1u) / W;
-    c.n_res            = resident_wgs<HD, NT, W, FUSE>();
+    c.n_res            = resident_wgs<HD, NT, W, FUSE>(fresh_bytes<HD, FUSE>(W, p.n_rows));
     /* 16 waves per CU over a batch of equal sequences: two residency rounds of
      * 8-wave workgroups at head_dim 64 (measured best on MI355X) */
     c.target_waves = 16u * cus;
@@ -1094,7 +1142,8 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W, FUSE>), dim3((uint32_t)n_launch), dim3(64 * W), 0, stream, p);
+    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W, FUSE>), dim3((uint32_t)n_launch), dim3(64 * W),
+                       (fresh_bytes<HD, FUSE>(W, p.n_rows)), stream, p);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     if (e != hipSuccess) return hip_status(e);
@@ -1151,7 +1200,8 @@ int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW, FUSE>), dim3(p.n_head_kv, n_seq), dim3(64 * WW), 0, stream, p);
+    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW, FUSE>), dim3(p.n_head_kv, n_seq), dim3(64 * WW),
+                       (fresh_bytes<HD, FUSE>(WW, p.n_rows)), stream, p);
     const hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     return hip_status(e);
@@ -1162,9 +1212,11 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool 
                  const Scratch *sc) {
     if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
     uint32_t w = choose_waves(p.n_head_kv, HD);
-    /* fused prologue at 32+ query columns: 8-wave workgroups would spill the
-     * new-row registers (256 VGPRs per wave at two waves per SIMD) */
-    if (FUSE && NT >= 2 && w > 4u) w = 4u;
+    /* fused prologue: the staged new rows and the V^T tiles stay within
+     * 64 KB of LDS per workgroup */
+    if (FUSE)
+        while (w > 1u && (size_t)w * HD * kVtStride * sizeof(uint16_t) + fresh_bytes<HD, FUSE>(w, p.n_rows) > 65536u)
+            w >>= 1;
     /* a grid of fewer workgroups than compute units (one short sequence)
      * spreads its KV heads over more, smaller workgroups: measured on MI355X
      * at B1, 8 KV heads, ctx 256-4096, 9.6-12.0 us -> 8.2-10.5 us per call

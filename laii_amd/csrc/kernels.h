@@ -83,6 +83,13 @@ int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *cons
                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
                         uint32_t cap, hipStream_t stream);
 
+/* Gen-1 prologue (FP32 caches): Q normalised and rotated in place, K to
+ * k_cache row pos, V copied to v_cache row pos. */
+int launch_gen1_prologue(float *q, const float *k, const float *v, float *k_cache, float *v_cache,
+                         const float *q_norm_w, const float *k_norm_w, float eps, const float *cos_row,
+                         const float *sin_row, uint32_t pos, uint32_t n_head_q, uint32_t n_head_kv,
+                         uint32_t head_dim, hipStream_t stream);
+
 /* Projections beside the attention path (quant_matmul.hip).  y/x_q8:
  * packed block_q8_K rows; w: packed block_q4_K rows; n_cols % 256 == 0. */
 int launch_quantize_q8_K(const float *x, void *y, uint32_t n_rows, uint32_t n_cols, hipStream_t stream);

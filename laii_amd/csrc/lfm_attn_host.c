@@ -7,6 +7,9 @@
  *   lfm2_rope_lut_init  tools/lfm2_kernels_fast.c:370-388
  *   lfm3_rope_lut_init  tools/lfm3_engine.c:403-450
  * Layout [pos][head_dim/2], entry i rotating the pair (i, i + head_dim/2).
+ * The Gen-1 engine has no table: lfm_rope_neox (src/lfm_forward.c:97-111)
+ * recomputes one position's angles in float on every call, which
+ * lfm_attn_rope_row_gen1 repeats with the same libm calls.
  */
 #include <math.h>
 #include <stddef.h>
@@ -55,6 +58,18 @@ int lfm_attn_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq, uin
             cos_lut[(size_t)p * half + i] = c;
             sin_lut[(size_t)p * half + i] = s;
         }
+    }
+    return LFM_ATTN_OK;
+}
+
+int lfm_attn_rope_row_gen1(float *cos_row, float *sin_row, uint32_t head_dim, uint32_t pos, float theta) {
+    if (!cos_row || !sin_row || head_dim == 0u || (head_dim & 1u)) return LFM_ATTN_E_INVALID;
+    const uint32_t half = head_dim / 2u;
+    for (uint32_t i = 0; i < half; ++i) {
+        const float freq = 1.0f / powf(theta, (float)(2u * i) / (float)head_dim);
+        const float phi  = (float)pos * freq;
+        cos_row[i]       = cosf(phi);
+        sin_row[i]       = sinf(phi);
     }
     return LFM_ATTN_OK;
 }

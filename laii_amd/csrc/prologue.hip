@@ -173,7 +173,85 @@ __global__ __launch_bounds__(64) void k_qkv_prologue(const PrologueParams P) {
     for (uint32_t i = threadIdx.x; i < hd; i += 64u) vd[i] = f16_rne(P.v[src + i]);
 }
 
+/* Gen-1 (src/lfm_forward.c:184-202): per head lfm_vec_rmsnorm_f32
+ * (src/lfm_simd.c:125-174) then lfm_rope_neox (:97-111).  The sum of
+ * squares follows the AVX2 kernel: eight vector columns j accumulate
+ * fma(x, x, .) over dims 32b + j, 32b + 8 + j, 32b + 16 + j, 32b + 24 + j of
+ * each full 32-block b; hsum256_ps adds columns k and k + 4, then the four
+ * results in sequence; dims past the last full block are added one at a time
+ * (product, then sum).  x <- (x * r) * w, r = 1/sqrtf(sum/n + eps); the
+ * rotation uses separately rounded products (lo*c - hi*s, hi*c + lo*s) with
+ * the row of lfm_attn_rope_row_gen1.  Q is rotated in place; K goes to the
+ * FP32 cache row at pos, V is copied there unchanged. */
+__device__ __forceinline__ void gen1_norm_rope(const float *in, float *dst, uint32_t hd, const float *norm_w,
+                                               float eps, const float *cos_row, const float *sin_row) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x;
+    float col = 0.0f;
+    const uint32_t full = hd & ~31u;
+    if (lane < 8u)
+        for (uint32_t b = 0; b < full; b += 32u)
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) col = __builtin_fmaf(in[b + 8u * q + lane], in[b + 8u * q + lane], col);
+    const float pair = col + __shfl_xor(col, 4); /* columns k + k + 4 on lanes 0..3 */
+    const float c1 = __shfl(pair, 1), c2 = __shfl(pair, 2), c3 = __shfl(pair, 3);
+    float sum = ((pair + c1) + c2) + c3;         /* lane 0 */
+    if (lane == 0u)
+        for (uint32_t i = full; i < hd; ++i) sum = sum + in[i] * in[i];
+    sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, sum)));
+    const float r    = 1.0f / sqrtf(sum / (float)hd + eps);
+    const uint32_t half = hd / 2u;
+    for (uint32_t i = lane; i < half; i += 64u) {
+        float x0 = in[i] * r, x1 = in[i + half] * r;
+        if (norm_w) {
+            x0 = x0 * norm_w[i];
+            x1 = x1 * norm_w[i + half];
+        }
+        const float c = cos_row[i], s = sin_row[i];
+        dst[i]        = x0 * c - x1 * s;
+        dst[i + half] = x1 * c + x0 * s;
+    }
+}
+
+struct Gen1Params {
+    float *q;
+    const float *k;
+    const float *v;
+    float *k_cache;
+    float *v_cache;
+    const float *q_norm_w;
+    const float *k_norm_w;
+    const float *cos_row;
+    const float *sin_row;
+    uint32_t n_head_q, n_head_kv, head_dim, pos;
+    float eps;
+};
+
+/* blockIdx.x < n_head_q: query head (in place); otherwise KV head. */
+__global__ __launch_bounds__(64) void k_gen1_prologue(const Gen1Params P) {
+    const uint32_t b = blockIdx.x, hd = P.head_dim;
+    if (b < P.n_head_q) {
+        float *qh = P.q + (size_t)b * hd;
+        gen1_norm_rope(qh, qh, hd, P.q_norm_w, P.eps, P.cos_row, P.sin_row);
+        return;
+    }
+    const uint32_t j   = b - P.n_head_q;
+    const size_t dst   = (size_t)P.pos * P.n_head_kv * hd + (size_t)j * hd;
+    gen1_norm_rope(P.k + (size_t)j * hd, P.k_cache + dst, hd, P.k_norm_w, P.eps, P.cos_row, P.sin_row);
+    for (uint32_t i = threadIdx.x; i < hd; i += 64u) P.v_cache[dst + i] = P.v[(size_t)j * hd + i];
+}
+
 } // namespace
+
+int launch_gen1_prologue(float *q, const float *k, const float *v, float *k_cache, float *v_cache,
+                         const float *q_norm_w, const float *k_norm_w, float eps, const float *cos_row,
+                         const float *sin_row, uint32_t pos, uint32_t n_head_q, uint32_t n_head_kv,
+                         uint32_t head_dim, hipStream_t stream) {
+    Gen1Params P{q, k, v, k_cache, v_cache, q_norm_w, k_norm_w, cos_row, sin_row, n_head_q, n_head_kv, head_dim,
+                 pos, eps};
+    hipLaunchKernelGGL(k_gen1_prologue, dim3(n_head_q + n_head_kv), dim3(64), 0, stream, P);
+    return hip_status(hipGetLastError());
+}
 
 int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
                         const float *norm_w, float eps, const float *cos_lut,

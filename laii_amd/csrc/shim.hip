@@ -473,6 +473,32 @@ int lfm_hip_gqa_f16_varlen_noalloc(const float *q, const float *gate, int gate_i
                        n_head_kv, head_dim, window_len, cap, scale, stream, true);
 }
 
+int lfm_hip_gen1_gqa_step(float *q, const float *k, const float *v, const float *q_norm, const float *k_norm,
+                          float *k_cache, float *v_cache, float *attn_out, uint32_t pos, uint32_t max_seq,
+                          uint32_t n_heads_q, uint32_t n_heads_kv, uint32_t head_dim, float eps,
+                          const float *cos_row, const float *sin_row, lfm_attn_stream_t stream) {
+    if (!q || !k || !v || !k_cache || !v_cache || !attn_out || !cos_row || !sin_row) return LFM_ATTN_E_INVALID;
+    if (n_heads_q == 0u || n_heads_kv == 0u || n_heads_q % n_heads_kv != 0u) return LFM_ATTN_E_INVALID;
+    if (head_dim == 0u || head_dim % 8u != 0u || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (pos >= max_seq || pos >= 0x7FFFFFFFu) return LFM_ATTN_E_RANGE;
+    const hipStream_t st = to_stream(stream);
+    const int r = lfm::launch_gen1_prologue(q, k, v, k_cache, v_cache, q_norm, k_norm, eps, cos_row, sin_row, pos,
+                                            n_heads_q, n_heads_kv, head_dim, st);
+    if (r != LFM_ATTN_OK) return r;
+    AttnBatch b;
+    b.q = q;
+    b.k_base = k_cache;
+    b.v_base = v_cache;
+    b.pos0_host = pos;
+    b.out = attn_out;
+    b.out_dims = head_dim;
+    b.n_head_q = n_heads_q;
+    b.n_head_kv = n_heads_kv;
+    b.head_dim = head_dim;
+    b.scale = 1.0f / sqrtf((float)head_dim);
+    return lfm::launch_generic(b, true, st);
+}
+
 int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const float *gate, int gate_is_logit,
                          uint16_t *const *k_seq, uint16_t *const *v_seq, const uint32_t *pos_0, float *out,
                          uint32_t n_seq, uint32_t n_rows, uint32_t keys_hint, uint32_t n_head_q,
@@ -614,18 +640,30 @@ int lfm_hip_lfm3_kv_cache_shift_sinks(uint16_t *const *k_caches, uint16_t *const
     const uint32_t cap     = swa_cap > 0u ? swa_cap : swa_win + 8u;
     if (cap < swa_win) return LFM_ATTN_E_INVALID;
     const hipStream_t st = to_stream(stream);
+    /* :1101-1135: an SWA layer re-slots the window [new_pos - window,
+     * new_pos) through a staging area.  Every layer is checked, and the
+     * largest stage reserved, before any layer is touched: a failure leaves
+     * every cache as it was. */
+    const uint32_t t0      = new_pos > swa_win ? new_pos - swa_win : 0u;
+    const uint32_t n_valid = new_pos - t0;
+    size_t stage_elems     = 0;
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        if (layer_kind[l] == 0u || !k_caches[l] || !v_caches[l] || n_head_kv[l] == 0u) continue;
+        if ((uint64_t)n_head_kv[l] * head_dim > 0xFFFFFFFFull) return LFM_ATTN_E_INVALID;
+        const size_t e = (size_t)2u * n_valid * n_head_kv[l] * head_dim;
+        if (layer_kind[l] == 2u && e > stage_elems) stage_elems = e;
+    }
+    uint16_t *stage = nullptr;
+    if (stage_elems) {
+        int ws_st = LFM_ATTN_OK;
+        stage = (uint16_t *)lfm::workspace(stage_elems * sizeof(uint16_t), st, &ws_st);
+        if (!stage) return ws_st;
+    }
     for (uint32_t l = 0; l < n_layers; ++l) {
         if (layer_kind[l] == 0u || !k_caches[l] || !v_caches[l] || n_head_kv[l] == 0u) continue;
         const uint32_t kv_dim = n_head_kv[l] * head_dim;
         int r;
         if (layer_kind[l] == 2u) {
-            /* :1101-1135: re-slot the window [new_pos - window, new_pos) */
-            const uint32_t t0      = new_pos > swa_win ? new_pos - swa_win : 0u;
-            const uint32_t n_valid = new_pos - t0;
-            int ws_st = LFM_ATTN_OK;
-            uint16_t *stage = (uint16_t *)lfm::workspace((size_t)2u * n_valid * kv_dim * sizeof(uint16_t),
-                                                         st, &ws_st);
-            if (!stage) return ws_st;
             r = lfm::launch_kv_swa_repack(k_caches[l], v_caches[l], kv_dim, head_dim, cap, t0, n_valid,
                                           n_sink, n_discard, cos_swa + (size_t)n_discard * half,
                                           sin_swa + (size_t)n_discard * half, stage,

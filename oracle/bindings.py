@@ -1,6 +1,6 @@
-"""ctypes bindings for the oracle (liboracle.so) and the reference build
-(_ref/libref_attn.so).  TEST INFRASTRUCTURE ONLY -- the checker, never the
-thing measured or shipped.
+"""ctypes bindings for the oracle (liboracle.so) and the reference builds
+(_ref/libref_attn.so, _ref/libref_gen1.so).  TEST INFRASTRUCTURE ONLY -- the
+checker, never the thing measured or shipped.
 """
 from __future__ import annotations
 
@@ -13,6 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libref_attn.so")
+REF_GEN1_SO = os.path.join(HERE, "_ref", "libref_gen1.so")
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
@@ -277,6 +278,49 @@ Oracle.dot_q4_K = _orc_dot
 Oracle.matmul_q4_K = _orc_matmul
 Oracle.dot_q6_K = _orc_dot6
 Oracle.matmul_q = _orc_matmul_q
+
+
+class RefGen1:
+    """The reference's Gen-1 FP32 step (src/lfm_forward.c, ref_gen1_shim.c)."""
+
+    @staticmethod
+    def available(path: str = REF_GEN1_SO) -> bool:
+        return os.path.exists(path)
+
+    def __init__(self, path: str = REF_GEN1_SO):
+        L = self.lib = C.CDLL(path)
+        L.ref_gen1_rope_neox.argtypes = [_f32p, _u32, _u32, _f32]
+        L.ref_gen1_rmsnorm.argtypes = [_f32p, _f32p, C.c_void_p, _u32, _f32]
+        L.ref_gen1_gqa_step.restype = C.c_int
+        L.ref_gen1_gqa_step.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, C.c_void_p, C.c_void_p,
+                                        _f32p, _f32p, _u32, _u32, _u32, _u32, _u32, _u32, _f32, _f32]
+
+    def rope_row(self, head_dim, pos, theta):
+        """cos, sin of lfm_rope_neox's angles: the rotation of (1, 0) pairs."""
+        v = np.zeros(head_dim, np.float32)
+        v[:head_dim // 2] = 1.0
+        self.lib.ref_gen1_rope_neox(v, head_dim, pos, theta)
+        return v[:head_dim // 2].copy(), v[head_dim // 2:].copy()
+
+    def rmsnorm(self, x, weight, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        w = None if weight is None else np.ascontiguousarray(weight, np.float32)
+        self.lib.ref_gen1_rmsnorm(out, x, _opt(w, C.c_void_p), x.size, eps)
+        return out
+
+    def gqa_step(self, x_norm, wq, wk, wv, wo, q_norm, k_norm, k_cache, v_cache, pos, nq, nkv, hd, eps, theta):
+        """lfm_gqa_step with F32 weights; k_cache/v_cache are updated in place."""
+        D = x_norm.size
+        out = np.zeros(D, np.float32)
+        qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+        kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+        rc = self.lib.ref_gen1_gqa_step(out, np.ascontiguousarray(x_norm, np.float32),
+                                        *[np.ascontiguousarray(w, np.float32).reshape(-1) for w in (wq, wk, wv, wo)],
+                                        _opt(qn, C.c_void_p), _opt(kn, C.c_void_p), k_cache.reshape(-1),
+                                        v_cache.reshape(-1), pos, k_cache.shape[0], D, nq, nkv, hd, eps, theta)
+        assert rc == 0
+        return out
 
 
 class Reference:

@@ -398,10 +398,49 @@ void orc_lfm3_online_gqa_f16(const float *q_batch, const float *gate_sig,
 }
 
 /* ------------------------------------------------------------------------ */
+/* Gen-1 AVX2 helpers in their exact summation order.
+ * hsum256_ps (src/lfm_simd.c:51-58): columns k and k + 4 added, then the four
+ * sums one after another. */
+static float gen1_hsum8(const float *c) {
+    const float b0 = c[0] + c[4], b1 = c[1] + c[5], b2 = c[2] + c[6], b3 = c[3] + c[7];
+    return ((b0 + b1) + b2) + b3;
+}
+
+/* Sum of squares of lfm_vec_rmsnorm_f32 (src/lfm_simd.c:125-145): eight
+ * columns j accumulate fma over dims 32b + j, +8, +16, +24 of each full
+ * 32-block, then hsum256_ps, then the remaining dims one at a time. */
+static float gen1_sumsq(const float *x, uint32_t n) {
+    float col[8] = {0};
+    uint32_t i = 0;
+    for (; i + 32u <= n; i += 32u)
+        for (uint32_t q = 0; q < 4u; ++q)
+            for (uint32_t j = 0; j < 8u; ++j) col[j] = fmaf(x[i + 8u * q + j], x[i + 8u * q + j], col[j]);
+    float s = gen1_hsum8(col);
+    for (; i < n; ++i) s += x[i] * x[i];
+    return s;
+}
+
+/* lfm_vec_dot_f32 (src/lfm_simd.c:61-83): four 8-column accumulators over the
+ * dims 32b + j, +8, +16, +24, combined (acc0 + acc1) + (acc2 + acc3), hsum,
+ * then the remaining dims one at a time. */
+static float gen1_dot(const float *a, const float *b, uint32_t n) {
+    float acc[4][8] = {{0}};
+    uint32_t i = 0;
+    for (; i + 32u <= n; i += 32u)
+        for (uint32_t q = 0; q < 4u; ++q)
+            for (uint32_t j = 0; j < 8u; ++j) acc[q][j] = fmaf(a[i + 8u * q + j], b[i + 8u * q + j], acc[q][j]);
+    float t[8];
+    for (uint32_t j = 0; j < 8u; ++j) t[j] = (acc[0][j] + acc[1][j]) + (acc[2][j] + acc[3][j]);
+    float s = gen1_hsum8(t);
+    for (; i < n; ++i) s += a[i] * b[i];
+    return s;
+}
+
 /* A6: src/lfm_forward.c:181-244 after the projections.  RMSNorm per
- * src/lfm_simd.c:125-170 (float sum of squares, x * r * w), RoPE per
- * src/lfm_forward.c:97-111 (float powf/cosf/sinf per call), FP32 append at
- * pos (:198-202), two-pass softmax attention (:204-244). */
+ * src/lfm_simd.c:125-170 (the AVX2 sum of squares above, x * r * w), RoPE
+ * per src/lfm_forward.c:97-111 (float powf/cosf/sinf per call, separately
+ * rounded products), FP32 append at pos (:198-202), two-pass softmax
+ * attention with lfm_vec_dot_f32 scores (:204-244). */
 void orc_gen1_gqa_attend(float *attn_out, float *q, float *k, const float *v,
                          const float *q_norm, const float *k_norm,
                          float *k_cache, float *v_cache, uint32_t pos,
@@ -415,9 +454,8 @@ void orc_gen1_gqa_attend(float *attn_out, float *q, float *k, const float *v,
         const uint32_t nh   = pass == 0u ? n_heads_q : n_heads_kv;
         for (uint32_t h = 0; h < nh; ++h) {
             float *x = vec + (size_t)h * head_dim;
-            float ss = 0.0f;
-            for (uint32_t i = 0; i < head_dim; ++i) ss += x[i] * x[i];
-            const float r = 1.0f / sqrtf((ss / (float)head_dim) + eps);
+            const float ss = gen1_sumsq(x, head_dim);
+            const float r  = 1.0f / sqrtf((ss / (float)head_dim) + eps);
             for (uint32_t i = 0; i < head_dim; ++i) x[i] = w ? x[i] * r * w[i] : x[i] * r;
             for (uint32_t i = 0; i < half; ++i) {
                 const float freq = 1.0f / powf(theta, (float)(2u * i) / (float)head_dim);
@@ -442,9 +480,7 @@ void orc_gen1_gqa_attend(float *attn_out, float *q, float *k, const float *v,
         float max_score = -1e30f;
         for (uint32_t t = 0; t <= pos; ++t) {
             const float *kt = k_cache + (size_t)t * kv_dim + (size_t)hkv * head_dim;
-            float dot = 0.0f;
-            for (uint32_t i = 0; i < head_dim; ++i) dot += qh[i] * kt[i];
-            scores[t] = dot * scale;
+            scores[t] = gen1_dot(qh, kt, head_dim) * scale;
             if (scores[t] > max_score) max_score = scores[t];
         }
         float sum_exp = 0.0f;

@@ -29,6 +29,15 @@ def ref():
 
 
 @pytest.fixture(scope="session")
+def ref_gen1():
+    from oracle.bindings import RefGen1
+
+    if not RefGen1.available():
+        pytest.skip("oracle/_ref/libref_gen1.so not built (reference sources absent)")
+    return RefGen1()
+
+
+@pytest.fixture(scope="session")
 def gpu():
     """The native library on a visible device.  Fails (does not skip) when the
     library or the device is missing: GPU tests must exercise the HIP path."""

@@ -73,6 +73,19 @@ def test_rope_lut_lfm3_bit_exact(orc, ref):
         assert np.array_equal(c, oc) and np.array_equal(s, os_)
 
 
+def test_rope_row_gen1_bit_exact(ref_gen1):
+    """The Gen-1 rotation row equals the angles the reference's lfm_rope_neox
+    computes per call (src/lfm_forward.c:97-111): its rotation of (1, 0)
+    pairs, bit for bit, over head dims and positions past 2^16."""
+    for hd in (16, 64, 96, 128):
+        for pos in (0, 1, 5, 777, 8191, 32767, 100003):
+            c, s = la.rope_row_gen1(hd, pos, 1e6)
+            rc, rs = ref_gen1.rope_row(hd, pos, 1e6)
+            assert np.array_equal(c, rc) and np.array_equal(s, rs), (hd, pos)
+    c, s = la.rope_row_gen1(64, 0, 1e4)
+    assert np.all(c == 1.0) and np.all(s == 0.0)
+
+
 def test_rejections_before_launch():
     lib = la.load()
     # A1: null pointer, kv_dim inconsistent with n_head_q / kv_mul, kv_mul not dividing
@@ -98,6 +111,14 @@ def test_rejections_before_launch():
                                       0, 0.125, None) == E_INVALID
     assert lib.lfm_hip_gqa_f16_varlen(FAKE, None, 0, FAKE, FAKE, FAKE, FAKE, 4, 1, 0, 32, 8, 60, 0,
                                       0, 0.125, None) == E_INVALID
+    # Gen-1 step: position past the cache, odd head grouping; fused step: a
+    # window whose later rows would overwrite earlier rows' keys
+    assert lib.lfm_hip_gen1_gqa_step(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, 10, 10, 4, 2, 16, 1e-5,
+                                     FAKE, FAKE, None) == E_RANGE
+    assert lib.lfm_hip_gen1_gqa_step(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, 1, 10, 6, 4, 16, 1e-5,
+                                     FAKE, FAKE, None) == E_INVALID
+    assert lib.lfm_hip_gqa_f16_step(FAKE, FAKE, FAKE, None, 1, FAKE, FAKE, FAKE, FAKE, 1, 8, 0, 16, 4, 128, 256,
+                                    260, 0.088, None, None, 1e-5, FAKE, FAKE, None) == E_INVALID
     # prologue
     assert lib.lfm_hip_qk_norm_rope(FAKE, None, 4, 63, None, 1e-5, FAKE, FAKE, 0, None) == E_INVALID
     assert lib.lfm_hip_qkv_prologue(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 16, 4, 128, None, None,

@@ -371,6 +371,41 @@ def test_gen1_fixture(orc):
     assert np.abs(out - expected).max() < 1e-4
 
 
+def _gen1_one_hot_case(rng, nq, nkv, hd, pos):
+    """Inputs for lfm_gqa_step whose projections and wo are exact: x is the
+    one-hot e_0 (each projected value is one weight) and wo the identity, so
+    the step's output is its attention output bit for bit."""
+    D = nq * hd
+    x = np.zeros(D, np.float32)
+    x[0] = 1.0
+    wq = rng.standard_normal((nq * hd, D)).astype(np.float32)
+    wk = rng.standard_normal((nkv * hd, D)).astype(np.float32)
+    wv = rng.standard_normal((nkv * hd, D)).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kc = rng.standard_normal((pos + 3, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((pos + 3, nkv * hd)).astype(np.float32)
+    return x, wq, wk, wv, np.eye(D, dtype=np.float32), qn, kn, kc, vc
+
+
+@pytest.mark.parametrize("nq,nkv,hd,pos", [(4, 2, 16, 5), (32, 8, 64, 300), (16, 4, 128, 77), (8, 8, 40, 0),
+                                            (12, 4, 96, 1000)])
+def test_gen1_bit_exact_vs_reference_step(orc, ref_gen1, nq, nkv, hd, pos):
+    """The oracle's Gen-1 step against the reference's own lfm_gqa_step
+    (src/lfm_forward.c:162-248, compiled from its sources): attention output
+    and the appended cache rows bit for bit -- the AVX2 sums of squares and
+    dot products in their column order, powf/cosf/sinf angles, two-pass
+    softmax."""
+    rng = np.random.default_rng(pos + hd)
+    x, wq, wk, wv, wo, qn, kn, kc, vc = _gen1_one_hot_case(rng, nq, nkv, hd, pos)
+    kc2, vc2 = kc.copy(), vc.copy()
+    out = ref_gen1.gqa_step(x, wq, wk, wv, wo, qn, kn, kc, vc, pos, nq, nkv, hd, 1e-5, 1e6)
+    att = orc.gen1_gqa_attend(wq[:, 0].copy(), wk[:, 0].copy(), wv[:, 0].copy(), qn, kn, kc2, vc2, pos, nq, nkv,
+                              hd, 1e-5, 1e6)
+    assert np.array_equal(out.view(np.uint32), att.view(np.uint32))
+    assert np.array_equal(kc, kc2) and np.array_equal(vc, vc2)
+
+
 # ---- planted mistakes: the checks above are sensitive ------------------------------------------
 
 def test_planted_mistakes_are_caught(orc):
