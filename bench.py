@@ -135,6 +135,62 @@ class DecodeWorkload:
         return self.sets[copy]["out"].numpy()
 
 
+class FusedStepWorkload(DecodeWorkload):
+    """A decode step through lfm_hip_gqa_f16_step: the raw new-token q/k/v go
+    through QK-RMSNorm (w = 1 + 0.05 N, eps 1e-5) + RoPE (theta 1e6) inside
+    the attention kernel, which also stores the new K/V rows (config 2 as
+    BASELINE defines it, prologue included).  Each step rewrites the same
+    rows, so the bytes per step stay those of DecodeWorkload."""
+
+    def __init__(self, la, rng, *a, **kw):
+        super().__init__(la, rng, *a, **kw)
+        hd = self.hd
+        shape = (self.n_seq, self.n_rows, self.nkv, hd)
+        self.k_raw = la.DeviceArray.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+        self.v_raw = la.DeviceArray.from_numpy(rng.standard_normal(shape, dtype=np.float32))
+        self.qw = la.DeviceArray.from_numpy((1 + 0.05 * rng.standard_normal(hd)).astype(np.float32))
+        self.kw = la.DeviceArray.from_numpy((1 + 0.05 * rng.standard_normal(hd)).astype(np.float32))
+        c, s = la.rope_lut_lfm2(int(self.pos0.max()) + self.n_rows, hd, 1e6)
+        self.cos, self.sin = la.DeviceArray.from_numpy(c), la.DeviceArray.from_numpy(s)
+
+    def step(self):
+        st = self.sets[self._i % len(self.sets)]
+        self._i += 1
+        self.la.gqa_f16_step(st["q"], self.k_raw, self.v_raw, st["g"], True, st["kt"], st["vt"], st["pos"],
+                             st["out"], self.n_seq, self.n_rows, self.keys_hint, self.nq, self.nkv, self.hd,
+                             self.qw, self.kw, 1e-5, self.cos, self.sin, self.window, self.cap)
+
+
+def bench_engine_step(la, rng, nq=16, nkv=8, hd=64, pos=1023, calls=500):
+    """lfm_attn_ctx_forward end to end, as the engine calls it per attention
+    layer (host q/k/v in, host output out, synchronous): one host-to-device
+    copy, the fused attention launch (+ split merge), one device-to-host
+    copy.  Config 1's shape (16q/8kv d64, position 1023).  Wall clock per
+    call, median of 5 batches of `calls`."""
+    ctx = la.EngineContext(1, nq, nkv, hd, pos + 1, 1e-5, rope_base=1e6)
+    try:
+        ctx.set_norms(0, (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32),
+                      (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32))
+        kv = (pos, nkv * hd)
+        ctx.kv_import(0, 0, f16(rng.standard_normal(kv) * 0.5), f16(rng.standard_normal(kv) * 0.5))
+        q = rng.standard_normal((1, nq, hd), dtype=np.float32)
+        k = rng.standard_normal((1, nkv, hd), dtype=np.float32)
+        v = rng.standard_normal((1, nkv, hd), dtype=np.float32)
+        for _ in range(50):
+            ctx.forward(0, pos, q, k, v)
+        per = []
+        for _ in range(5):
+            t = time.perf_counter()
+            for _ in range(calls):
+                ctx.forward(0, pos, q, k, v)
+            per.append((time.perf_counter() - t) / calls)
+    finally:
+        ctx.close()
+    us = float(np.median(per)) * 1e6
+    return dict(us_per_call=round(us, 2), shape=f"{nq}q/{nkv}kv d{hd}, position {pos}, one layer",
+                includes="host->device copy, fused QK-norm+RoPE+K/V store+attention, merge, device->host copy, sync")
+
+
 class PrefillWorkload:
     """causal prefill, B sequences of N tokens, fp16 Q/K/V
     (0.5*N(0,1), RoPE assumed applied), fp32 softmax/accumulate, fp32 out.
@@ -538,6 +594,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-4 prefill workload (for kernel profiling)")
+    ap.add_argument("--engine-only", action="store_true",
+                    help="only the engine step, lfm_attn_ctx_forward (for kernel tracing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share only; --gpus {args.gpus} is not supported: "
@@ -551,6 +609,11 @@ def main():
     hip = Hip()
     rng = np.random.default_rng(20261201)
     t_setup = time.perf_counter()
+    if args.engine_only:
+        es = bench_engine_step(la, rng, calls=max(10, args.steps))
+        print(json.dumps({"metric": "engine attention step, host in/out", "value": es["us_per_call"],
+                          "unit": "us", "n_gpus": 1, "higher_is_better": False, "engine_step": es}), flush=True)
+        return
     if args.prefill_only:
         prefill = run_prefill(hip, la, rng, args.steps)
         print(json.dumps({"metric": "prefill attn TFLOP/s, config 4", "value": prefill["TFLOPs"],
@@ -580,8 +643,10 @@ def main():
                                                       gate=True, copies=36)),
             ("cfg5_lfm3_full_b32_ctx32768", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
                                                  ctx=[32768] * 32, gate=True)),
+            # 2 MB per call: 160 rotated copies (320 MB) keep it out of the 256 MB
+            # MALL; the row is latency-bound, so us_per_step is its figure
             ("cfg1_decode_b1_16q8kv_ctx1024", dict(n_seq=1, n_rows=1, nq=16, nkv=8, hd=64,
-                                                   ctx=[1024], copies=1)),
+                                                   ctx=[1024], copies=160)),
         ]
         for name, kw in cases:
             wl = DecodeWorkload(la, rng, name, **kw)
@@ -593,6 +658,24 @@ def main():
                                    us_per_step=round(sms * 1e3, 2), bytes=wl.bytes,
                                    pct_hbm_peak=round(100 * wl.bytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
             del wl
+
+    if not args.quick:
+        # config 2 as BASELINE defines it: the QK-norm + RoPE prologue of the
+        # new token inside the attention kernel, which also stores its K/V
+        for name, ctx in (("cfg2_fused_step_b64_ctx8192", [8192] * 64),
+                          ("cfg2_fused_step_b64_ctxU512_8192", rng.integers(512, 8193, size=64))):
+            wl = FusedStepWorkload(la, rng, name, 64, 1, 32, 8, 64, ctx)
+            sms = time_steps(hip, wl, args.steps, args.warmup)
+            kms = time_main_kernel(hip, la, wl, args.steps)
+            log(f"{name}: {sms * 1e3:.1f} us/step")
+            secondary[name] = dict(GBps=round(wl.bytes / (sms * 1e-3) / 1e9, 1),
+                                   kernel_GBps=round(wl.bytes / (kms * 1e-3) / 1e9, 1),
+                                   us_per_step=round(sms * 1e3, 2), bytes=wl.bytes,
+                                   pct_hbm_peak=round(100 * wl.bytes / (sms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1))
+            del wl
+        es = bench_engine_step(la, rng)
+        secondary["engine_step_cfg1_host_in_out"] = es
+        log(f"engine step (host in/out): {es['us_per_call']} us per call")
 
     prefill = run_prefill(hip, la, rng, args.steps)
 
@@ -676,7 +759,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "kernel": "k_splitkv_bal<64,1,8>", "kernel_us": round(k_ms * 1e3, 2)},
+                     "traffic_source": "constant from the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of "
+                                       "profiles/k_splitkv_decode_b64_ctx8192_pmc.md, not measured in this run",
+                     "kernel": "k_splitkv_bal<64,1,8,false>", "kernel_us": round(k_ms * 1e3, 2)},
         "prefill": prefill,
         "box_peaks": peaks,
         "cpu_baseline": cpu,
