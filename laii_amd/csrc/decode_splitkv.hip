@@ -254,6 +254,19 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     const int lane = threadIdx.x & 63;
     const int l16  = lane & 15;
     const int g    = lane >> 4;
+    /* The segment is the same for every lane, but in k_splitkv_wg and
+     * k_splitkv_bal it derives from threadIdx and lane shuffles, so the
+     * compiler held it in VGPRs and lowered the key loop and the fused
+     * prologue's branches as divergent (EXEC-masked) code.  The head_dim-128,
+     * 32-column fused instantiations of those two kernels then returned wrong
+     * outputs on MI355X (up to 1.5 absolute, every plan but the grid, whose
+     * segment comes from blockIdx); with the values made explicitly uniform
+     * the control flow is scalar and every plan matches the oracle. */
+    kb   = __builtin_amdgcn_readfirstlane(kb);
+    ke   = __builtin_amdgcn_readfirstlane(ke);
+    pos0 = __builtin_amdgcn_readfirstlane(pos0);
+    kvh  = __builtin_amdgcn_readfirstlane(kvh);
+    s    = __builtin_amdgcn_readfirstlane(s);
     const uint32_t last = pos0 + P.n_rows - 1u;
 
     gu16_ptr kc = (gu16_ptr)(P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride);

@@ -116,6 +116,18 @@ def test_step_lfm3_swa_ring_gate(gpu, orc, env):
                env=env)
 
 
+@pytest.mark.parametrize("env", PLANS)
+@pytest.mark.parametrize("n_rows,nq,nkv,pos0", [(8, 16, 4, [600]), (8, 16, 4, [380, 1000, 5]), (1, 32, 1, [600, 77]),
+                                                 (3, 32, 4, [999])])
+def test_step_lfm3_full_32_columns(gpu, orc, env, n_rows, nq, nkv, pos0):
+    """head_dim 128 with 17..32 query columns per KV head (two 16-column
+    tiles): an LFM3 full layer's 8-row chunk, 32 heads on one KV head, under
+    every plan.  These instantiations of the workgroup-merge and balanced
+    kernels returned wrong outputs while the segment bounds were held in
+    VGPRs; the key loop now runs on wave-uniform bounds."""
+    _step_case(gpu, orc, 18, len(pos0), n_rows, nq, nkv, 128, pos0, gate=True, lut_kind="partial", env=env)
+
+
 def test_step_lfm3_full_partial_rope(gpu, orc):
     """LFM3 full layer: partial RoPE (pairs i < 32 rotate), gate, B = 1."""
     _step_case(gpu, orc, 14, 3, 1, 16, 4, 128, [2000, 0, 77], gate=True, lut_kind="partial")
