@@ -215,6 +215,34 @@ class PrefillWorkload:
                             self.n_tok * self.nkv * self.hd, self.nq, self.nkv, self.hd)
 
 
+class Lfm3PrefillWorkload:
+    """LFM3 attention-layer prefill (lfm_hip_lfm3_prefill_f16): B sequences
+    of N tokens, 16q/4kv, head_dim 128, gate logits N(0,1); a full layer
+    (window 0) or a sliding-window layer (every row attends its last `window`
+    positions).  Q/K/V as for config 4 (0.5*N(0,1), fp16 values)."""
+
+    def __init__(self, la, rng, n_seq=4, n_tok=4096, nq=16, nkv=4, hd=128, window=0):
+        self.la, self.n_seq, self.n_tok, self.nq, self.nkv, self.hd = la, n_seq, n_tok, nq, nkv, hd
+        self.window = window
+        self.q = la.DeviceArray.from_numpy(
+            f16(rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32) * np.float32(0.5))
+            .view(np.float16).astype(np.float32))
+        self.k = la.DeviceArray.from_numpy(
+            f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * np.float32(0.5)))
+        self.v = la.DeviceArray.from_numpy(
+            f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * np.float32(0.5)))
+        self.gate = la.DeviceArray.from_numpy(rng.standard_normal((n_seq, n_tok, nq)).astype(np.float32))
+        self.out = la.DeviceArray.zeros((n_seq, n_tok, nq, hd), np.float32)
+        p = np.arange(n_tok, dtype=np.int64)
+        keys = np.minimum(p + 1, window) if window else p + 1
+        # 2 GEMMs x 2 flop x d per (row, attended key) per head
+        self.flops = int(4 * hd * nq * n_seq * keys.sum())
+
+    def step(self):
+        self.la.lfm3_prefill_f16(self.q, self.k, self.v, self.gate, True, self.out, self.n_seq, self.n_tok, 0, 0,
+                                 self.n_tok * self.nkv * self.hd, self.window, self.nq, self.nkv, self.hd)
+
+
 class KvShiftWorkload:
     """Attention-sink eviction at the engine trigger (src/lfm2_api.c:871-891)
     for the LFM2-1.2B attention layers: 6 layers x 8 KV heads x d64 caches of
@@ -585,6 +613,21 @@ def run_prefill(hip, la, rng, steps):
     return prefill
 
 
+def run_prefill_lfm3(hip, la, rng, steps, window):
+    pf = Lfm3PrefillWorkload(la, rng, window=window)
+    n = max(5, steps // 5)
+    pms = time_steps(hip, pf, n, 3)
+    pkms = time_main_kernel(hip, la, pf, n)
+    kind = f"swa{window}" if window else "full"
+    row = dict(workload=f"lfm3_{kind}_prefill_b4_n4096_16q4kv_d128_gate", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
+               kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4), flops=pf.flops,
+               pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1),
+               kernel="k_prefill128")
+    log(f"lfm3 {kind} prefill: {pms:.3f} ms/step, {row['TFLOPs']} TFLOP/s")
+    del pf
+    return row
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -594,6 +637,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config-4 prefill workload (for kernel profiling)")
+    ap.add_argument("--prefill128-only", action="store_true",
+                    help="only the LFM3 head_dim-128 prefill workloads (for kernel profiling)")
     ap.add_argument("--engine-only", action="store_true",
                     help="only the engine step, lfm_attn_ctx_forward (for kernel tracing)")
     args = ap.parse_args()
@@ -613,6 +658,12 @@ def main():
         es = bench_engine_step(la, rng, calls=max(10, args.steps))
         print(json.dumps({"metric": "engine attention step, host in/out", "value": es["us_per_call"],
                           "unit": "us", "n_gpus": 1, "higher_is_better": False, "engine_step": es}), flush=True)
+        return
+    if args.prefill128_only:
+        rows = [run_prefill_lfm3(hip, la, rng, args.steps, w) for w in (0, 256)]
+        print(json.dumps({"metric": "LFM3 prefill attn TFLOP/s, B4 x 4096, 16q/4kv d128", "value": rows[0]["TFLOPs"],
+                          "unit": "TFLOP/s", "n_gpus": 1, "steps": max(5, args.steps // 5),
+                          "higher_is_better": True, "prefill_lfm3": rows}), flush=True)
         return
     if args.prefill_only:
         prefill = run_prefill(hip, la, rng, args.steps)
@@ -678,6 +729,9 @@ def main():
         log(f"engine step (host in/out): {es['us_per_call']} us per call")
 
     prefill = run_prefill(hip, la, rng, args.steps)
+    for w in (0, 256):
+        row = run_prefill_lfm3(hip, la, rng, args.steps, w)
+        secondary[row["workload"]] = row
 
     if not args.quick:
         ks = KvShiftWorkload(la, rng)

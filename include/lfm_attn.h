@@ -315,12 +315,37 @@ int lfm_hip_gqa_f16_varlen_noalloc(const float *q, const float *gate, int gate_i
  *      reference's rows; q * scale * log2(e) enters the MFMA as fp16.
  * k,v: sequence s at k + s * kv_seq_stride elements, [slot][n_head_kv][head_dim].
  * out: [n_seq][n_tok][n_head_q][head_dim] float.
- * head_dim 64 (MFMA kernel); other head dims return LFM_ATTN_E_UNSUPPORTED.
- * Softmax and accumulation are fp32; P enters the P.V product as fp16. */
+ * head_dim 64 (MFMA kernel); other head dims return LFM_ATTN_E_UNSUPPORTED
+ * (the reference's fp16 LFM2 heads worker writes at most 64 output dims per
+ * head, tools/lfm2_threadpool.c:778-828; LFM3 layers of head_dim 128 use
+ * lfm_hip_lfm3_prefill_f16).  Softmax and accumulation are fp32; P enters
+ * the P.V product as fp16. */
 int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, float *out,
                         uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint64_t kv_seq_stride,
                         uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                         lfm_attn_stream_t stream);
+
+/* Causal prefill of an LFM3 attention layer (full or sliding-window, with the
+ * output gate) on MFMA: the attention of lfm3_forward_batch_core
+ * (tools/lfm3_engine.c:1918-2055; per-row window :862-873, gate scaling
+ * :902-911), whose batches hold at most LFM2_MAX_BATCH rows, for a whole
+ * prompt in one launch.  Row i of sequence s is position p = pos_0 + i and
+ * attends keys [t_start(p), p], t_start(p) = p + 1 - window_len when
+ * window_len > 0 and p + 1 > window_len, else 0; with gate non-NULL
+ * ([n_seq][n_tok][n_head_q]) its output is scaled by sigmoid(gate) when
+ * gate_is_logit, else by gate.
+ * K/V row r of sequence s (at k + s * kv_seq_stride elements,
+ * [row][n_head_kv][head_dim]) holds position kv_pos0 + r, for positions
+ * kv_pos0 .. pos_0 + n_tok - 1: a full layer passes its cache (kv_pos0 = 0);
+ * a sliding-window layer passes a linear copy of the window before the
+ * prompt plus the prompt's rows (a ring of window + 8 slots cannot hold a
+ * whole prompt).  kv_pos0 must not exceed t_start(pos_0)
+ * (LFM_ATTN_E_INVALID).  q, out as for lfm_hip_prefill_f16.  head_dim 128
+ * with n_head_q / n_head_kv dividing 128, else LFM_ATTN_E_UNSUPPORTED. */
+int lfm_hip_lfm3_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, const float *gate,
+                             int gate_is_logit, float *out, uint32_t n_seq, uint32_t n_tok, uint32_t pos_0,
+                             uint32_t kv_pos0, uint64_t kv_seq_stride, uint32_t window_len, uint32_t n_head_q,
+                             uint32_t n_head_kv, uint32_t head_dim, float scale, lfm_attn_stream_t stream);
 
 /* ---- attention-sink eviction on device caches ------------------------------ */
 /* When the position nears max_seq the engine keeps the first n_sink rows,

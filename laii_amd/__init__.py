@@ -26,6 +26,7 @@ from .attention import (  # noqa: F401
     kv_cache_shift_sinks,
     lfm3_kv_cache_shift_sinks,
     lfm3_online_gqa_f16_dispatch,
+    lfm3_prefill_f16,
     matmul_prequant,
     matmul_q4_K,
     online_gqa_f16,

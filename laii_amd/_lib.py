@@ -52,6 +52,8 @@ SIGNATURES = {
                                                     _u32, _u32, _u32, _u32, _vp]),
     "lfm_hip_prefill_f16": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, C.c_uint64, _u32, _u32,
                                    _u32, _f32, _vp]),
+    "lfm_hip_lfm3_prefill_f16": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _u32, _u32, _u32, _u32, C.c_uint64,
+                                        _u32, _u32, _u32, _u32, _f32, _vp]),
     "lfm_hip_gqa_f16_varlen": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                       _u32, _u32, _u32, _u32, _f32, _vp]),
     "lfm_attn_rope_row_gen1": (_int, [_vp, _vp, _u32, _u32, _f32]),

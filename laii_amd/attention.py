@@ -300,6 +300,20 @@ def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0:
           "lfm_hip_prefill_f16")
 
 
+def lfm3_prefill_f16(q: Ptr, k: Ptr, v: Ptr, gate: Optional[Ptr], gate_is_logit: bool, out: Ptr, n_seq: int,
+                     n_tok: int, pos_0: int, kv_pos0: int, kv_seq_stride: int, window_len: int, n_head_q: int,
+                     n_head_kv: int, head_dim: int, scale: Optional[float] = None, stream=None) -> None:
+    """Causal prefill of an LFM3 layer (tools/lfm3_engine.c:1918-2055): row
+    i (position p = pos_0 + i) attends keys [t_start(p), p] (the last
+    window_len positions when window_len > 0), scaled by sigmoid(gate)
+    (gate_is_logit) or gate.  K/V row r holds position kv_pos0 + r."""
+    if scale is None:
+        scale = float(1.0 / np.sqrt(np.float32(head_dim)))
+    check(load().lfm_hip_lfm3_prefill_f16(_p(q), _p(k), _p(v), _p(gate), int(bool(gate_is_logit)), _p(out), n_seq,
+                                          n_tok, pos_0, kv_pos0, kv_seq_stride, window_len, n_head_q, n_head_kv,
+                                          head_dim, scale, stream), "lfm_hip_lfm3_prefill_f16")
+
+
 def _host_ptrs(arrays) -> "C.Array":
     return (C.c_void_p * len(arrays))(*[None if a is None else int(a) for a in arrays])
 

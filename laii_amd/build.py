@@ -23,7 +23,7 @@ HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["shim.hip", "decode_splitkv.hip", "generic.hip", "prologue.hip", "prefill_fa.hip",
-               "kv_shift.hip", "quant_matmul.hip", "fnv_hash.hip", "peak_probe.hip"]
+               "prefill_ext.hip", "kv_shift.hip", "quant_matmul.hip", "fnv_hash.hip", "peak_probe.hip"]
 C_SOURCES = ["lfm_attn_host.c", "lfm_attn_ctx.c"]
 
 HIP_FLAGS = [
@@ -33,7 +33,7 @@ HIP_FLAGS = [
     f"-I{CSRC}", f"-I{INCLUDE}",
 ]
 # per-file additions:
-# - the prefill kernel takes maxima of MFMA results, which are never NaN
+# - the prefill kernels take maxima of MFMA results, which are never NaN
 #   there; without the no-NaN assumption every fmaxf operand is canonicalised
 #   first (one extra VALU op per score);
 # - MFMA accumulators in ordinary VGPRs: for workgroups of <= 4 waves the
@@ -43,7 +43,8 @@ HIP_FLAGS = [
 #   e.g. k_splitkv_bal<64,2,4> 272 -> 245 VGPRs (two waves per SIMD), B1 LFM3
 #   decode 44.2 -> 39.8 us, ragged B64 decode 104 -> 102.4 us on MI355X.
 VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-HIP_FILE_FLAGS = {"prefill_fa.hip": ["-fno-honor-nans"], "decode_splitkv.hip": VGPR_MFMA,
+HIP_FILE_FLAGS = {"prefill_fa.hip": ["-fno-honor-nans"], "prefill_ext.hip": ["-fno-honor-nans"],
+                  "decode_splitkv.hip": VGPR_MFMA,
                   "peak_probe.hip": VGPR_MFMA}
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
            f"-I{ROCM}/include", f"-I{CSRC}", f"-I{INCLUDE}"]

@@ -71,6 +71,14 @@ int launch_prefill(const float *q, const uint16_t *k, const uint16_t *v, float *
                    uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, float scale,
                    hipStream_t stream);
 
+/* Causal MFMA prefill for head_dim 128 with an optional sliding window and
+ * output gate; K/V row r of a sequence's buffer holds position kv_pos0 + r. */
+bool prefill_ext_supports(uint32_t head_dim, uint32_t kv_mul);
+int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, const float *gate, int gate_is_logit,
+                       float *out, uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t kv_pos0,
+                       uint64_t kv_seq_stride, uint32_t window, uint32_t n_head_q, uint32_t n_head_kv,
+                       uint32_t head_dim, float scale, hipStream_t stream);
+
 /* Prologue kernels. */
 int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
                         const float *norm_w, float eps, const float *cos_lut,

@@ -249,12 +249,54 @@ int lfm_attn_ctx_forward(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
     return st;
 }
 
-/* Prompt prefill of one layer.  Full-attention layers of head_dim 64 with
- * no gate run the prologue over all rows and the MFMA prefill kernel
- * (every row attends keys 0 .. its position, causal by write order, as
- * lfm2_forward_gqa_batch does in chunks of LFM2_MAX_BATCH); other layers
- * (sliding window, head_dim 128, gated) go through the step in chunks of
- * LFM_CTX_MAX_ROWS rows, as the reference does. */
+/* Prompt prefill of one layer in one attention launch (after one prologue
+ * launch), where lfm2_forward_batch / lfm3_forward_batch_core run the layer
+ * LFM2_MAX_BATCH rows at a time (tools/lfm2_prefill_batch.c:1129-1199,
+ * tools/lfm3_engine.c:1918-2055):
+ *  - full-attention layers: the prologue writes every row's K/V into the
+ *    cache, then every row attends keys 0 .. its position (head_dim 64
+ *    without a gate: lfm_hip_prefill_f16; head_dim 128, gated or not:
+ *    lfm_hip_lfm3_prefill_f16);
+ *  - sliding-window layers (head_dim 128): the ring of window + 8 slots
+ *    cannot hold a whole prompt, so the window before the prompt (positions
+ *    kv_pos0 .. pos_0 - 1, at most window - 1 of them) is copied from the
+ *    ring into a linear buffer, the prologue appends the prompt's rows, the
+ *    prefill reads the buffer (row r = position kv_pos0 + r), and the last
+ *    min(n_rows, cap) rows are copied back to their ring slots -- the ring
+ *    then holds what the chunked steps leave in it.
+ * The prologue addresses the buffer with positions relative to kv_pos0 and
+ * RoPE tables offset by kv_pos0 rows, so every row is rotated with its
+ * absolute position.  Other shapes, and prompts of at most 8 rows, run the
+ * step over chunks of LFM_CTX_MAX_ROWS rows. */
+static int ring_copy(uint16_t *dst, size_t dst_row, const uint16_t *src, size_t src_row, uint32_t n, size_t row_elems,
+                     hipStream_t stream) {
+    return st_of(hipMemcpyAsync(dst + dst_row * row_elems, src + src_row * row_elems,
+                                (size_t)n * row_elems * sizeof(uint16_t), hipMemcpyDeviceToDevice, stream));
+}
+
+/* positions p0 .. p0 + n - 1: ring slots p % cap <-> linear rows p - base */
+static int ring_move(lfm_attn_ctx *c, uint32_t layer, uint16_t *lin_k, uint16_t *lin_v, uint32_t base, uint32_t p0,
+                     uint32_t n, int to_ring) {
+    const uint32_t cap = c->slots[layer];
+    const size_t row   = (size_t)c->g.n_head_kv * c->g.head_dim;
+    uint32_t done = 0;
+    int st = LFM_ATTN_OK;
+    while (st == LFM_ATTN_OK && done < n) {
+        const uint32_t slot = (p0 + done) % cap;
+        const uint32_t run  = (n - done < cap - slot) ? n - done : cap - slot;
+        const uint32_t lrow = p0 + done - base;
+        if (to_ring) {
+            st = ring_copy(c->k_cache[layer], slot, lin_k, lrow, run, row, c->stream);
+            if (st == LFM_ATTN_OK) st = ring_copy(c->v_cache[layer], slot, lin_v, lrow, run, row, c->stream);
+        } else {
+            st = ring_copy(lin_k, lrow, c->k_cache[layer], slot, run, row, c->stream);
+            if (st == LFM_ATTN_OK) st = ring_copy(lin_v, lrow, c->v_cache[layer], slot, run, row, c->stream);
+        }
+        done += run;
+    }
+    return st;
+}
+
 int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32_t n_rows, const float *q,
                          const float *k, const float *v, const float *gate_logits, float *out) {
     if (!c || !q || !k || !v || !out || layer >= c->g.n_layers || n_rows == 0u) return LFM_ATTN_E_INVALID;
@@ -262,9 +304,10 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
     if ((uint64_t)pos_0 + n_rows > g->max_seq) return LFM_ATTN_E_RANGE;
     const uint32_t kv_mul = g->n_head_q / g->n_head_kv;
     const size_t qrow = (size_t)g->n_head_q * g->head_dim, krow = (size_t)g->n_head_kv * g->head_dim;
-    const int fast = !c->is_swa[layer] && !gate_logits && g->head_dim == 64u && kv_mul >= 1u &&
-                     kv_mul <= 16u && (256u % kv_mul) == 0u && n_rows > LFM_CTX_MAX_ROWS;
-    if (!fast) {
+    const int swa = c->is_swa[layer];
+    const int mfma64 = !swa && !gate_logits && g->head_dim == 64u && kv_mul <= 16u && (256u % kv_mul) == 0u;
+    const int mfma128 = g->head_dim == 128u && kv_mul <= 32u && (128u % kv_mul) == 0u;
+    if (n_rows <= LFM_CTX_MAX_ROWS || !(mfma64 || mfma128)) {
         for (uint32_t r = 0; r < n_rows; r += LFM_CTX_MAX_ROWS) {
             const uint32_t b = n_rows - r < LFM_CTX_MAX_ROWS ? n_rows - r : LFM_CTX_MAX_ROWS;
             const int st = lfm_attn_ctx_forward(c, layer, pos_0 + r, b, q + r * qrow, k + r * krow, v + r * krow,
@@ -274,11 +317,19 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
         }
         return LFM_ATTN_OK;
     }
-    /* device layout: q f32 | k f32 | v f32 | pos | out f32 (256-B aligned parts) */
+    const uint32_t window = swa ? g->sliding_window : 0u;
+    const uint32_t n_old  = swa ? (pos_0 < window - 1u ? pos_0 : window - 1u) : 0u;
+    const uint32_t kv_pos0 = pos_0 - n_old; /* position of linear row 0 (sliding window) */
+    const uint32_t rel_pos = swa ? n_old : pos_0;
+    /* device layout: q f32 | k f32 | v f32 | gate f32 | pos + pointer pair,
+     * out f32, then (sliding window) the linear K and V buffers */
     const size_t qb = align256((size_t)n_rows * qrow * sizeof(float));
     const size_t kb = align256((size_t)n_rows * krow * sizeof(float));
+    const size_t gb = gate_logits ? align256((size_t)n_rows * g->n_head_q * sizeof(float)) : 0u;
     const size_t pb = 256u;
-    const size_t in_bytes = qb + 2u * kb + pb, dev_bytes = in_bytes + qb;
+    const size_t in_bytes = qb + 2u * kb + gb + pb;
+    const size_t lin_bytes = swa ? align256((size_t)(n_old + n_rows) * krow * sizeof(uint16_t)) : 0u;
+    const size_t dev_bytes = in_bytes + qb + 2u * lin_bytes;
     int st = LFM_ATTN_OK;
     if (c->pf_host_bytes < in_bytes + qb) {
         if (c->pf_host) (void)hipHostFree(c->pf_host);
@@ -289,6 +340,7 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
         c->pf_host_bytes = in_bytes + qb;
     }
     if (c->pf_dev_bytes < dev_bytes) {
+        (void)hipStreamSynchronize(c->stream);
         (void)hipFree(c->pf_dev);
         c->pf_dev = NULL;
         c->pf_dev_bytes = 0;
@@ -297,22 +349,50 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
         c->pf_dev_bytes = dev_bytes;
     }
     unsigned char *h = c->pf_host, *d = c->pf_dev;
+    const size_t off_k = qb, off_v = qb + kb, off_g = qb + 2u * kb, off_p = off_g + gb;
+    uint16_t *lin_k = swa ? (uint16_t *)(d + in_bytes + qb) : NULL;
+    uint16_t *lin_v = swa ? (uint16_t *)(d + in_bytes + qb + lin_bytes) : NULL;
     memcpy(h, q, (size_t)n_rows * qrow * sizeof(float));
-    memcpy(h + qb, k, (size_t)n_rows * krow * sizeof(float));
-    memcpy(h + qb + kb, v, (size_t)n_rows * krow * sizeof(float));
-    memcpy(h + qb + 2u * kb, &pos_0, sizeof pos_0);
+    memcpy(h + off_k, k, (size_t)n_rows * krow * sizeof(float));
+    memcpy(h + off_v, v, (size_t)n_rows * krow * sizeof(float));
+    if (gate_logits) memcpy(h + off_g, gate_logits, (size_t)n_rows * g->n_head_q * sizeof(float));
+    memcpy(h + off_p, &rel_pos, sizeof rel_pos);
+    uint16_t *pair[2] = {lin_k, lin_v};
+    memcpy(h + off_p + 16u, pair, sizeof pair);
     st = st_of(hipMemcpyAsync(d, h, in_bytes, hipMemcpyHostToDevice, c->stream));
     if (st != LFM_ATTN_OK) return st;
-    float *qd        = (float *)d;
-    float *od        = (float *)(d + in_bytes);
-    uint16_t *kcache = c->k_cache[layer], *vcache = c->v_cache[layer];
-    st = lfm_hip_qkv_prologue(qd, (const float *)(d + qb), (const float *)(d + qb + kb), c->tables + 2u * layer,
-                              c->tables + 2u * layer + 1u, (const uint32_t *)(d + qb + 2u * kb), 1u, n_rows,
-                              g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
-                              c->cos_full, c->sin_full, 0u, 0u, c->stream);
-    if (st == LFM_ATTN_OK)
-        st = lfm_hip_prefill_f16(qd, kcache, vcache, od, 1u, n_rows, pos_0, 0u, g->n_head_q, g->n_head_kv,
-                                 g->head_dim, 1.0f / sqrtf((float)g->head_dim), c->stream);
+    float *qd = (float *)d;
+    float *od = (float *)(d + in_bytes);
+    const float *gd = gate_logits ? (const float *)(d + off_g) : NULL;
+    const float scale = 1.0f / sqrtf((float)g->head_dim);
+    const size_t half = g->head_dim / 2u;
+    if (swa) {
+        uint16_t *const *lin_t = (uint16_t *const *)(d + off_p + 16u);
+        st = ring_move(c, layer, lin_k, lin_v, kv_pos0, kv_pos0, n_old, 0);
+        if (st == LFM_ATTN_OK)
+            st = lfm_hip_qkv_prologue(qd, (const float *)(d + off_k), (const float *)(d + off_v), lin_t, lin_t + 1,
+                                      (const uint32_t *)(d + off_p), 1u, n_rows, g->n_head_q, g->n_head_kv,
+                                      g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
+                                      c->cos_swa + (size_t)kv_pos0 * half, c->sin_swa + (size_t)kv_pos0 * half, 0u,
+                                      0u, c->stream);
+        if (st == LFM_ATTN_OK)
+            st = lfm_hip_lfm3_prefill_f16(qd, lin_k, lin_v, gd, 1, od, 1u, n_rows, pos_0, kv_pos0, 0u, window,
+                                          g->n_head_q, g->n_head_kv, g->head_dim, scale, c->stream);
+        const uint32_t cap = c->slots[layer];
+        const uint32_t n_back = n_rows < cap ? n_rows : cap;
+        if (st == LFM_ATTN_OK) st = ring_move(c, layer, lin_k, lin_v, kv_pos0, pos_0 + n_rows - n_back, n_back, 1);
+    } else {
+        st = lfm_hip_qkv_prologue(qd, (const float *)(d + off_k), (const float *)(d + off_v), c->tables + 2u * layer,
+                                  c->tables + 2u * layer + 1u, (const uint32_t *)(d + off_p), 1u, n_rows,
+                                  g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
+                                  c->cos_full, c->sin_full, 0u, 0u, c->stream);
+        if (st == LFM_ATTN_OK && mfma128)
+            st = lfm_hip_lfm3_prefill_f16(qd, c->k_cache[layer], c->v_cache[layer], gd, 1, od, 1u, n_rows, pos_0, 0u,
+                                          0u, 0u, g->n_head_q, g->n_head_kv, g->head_dim, scale, c->stream);
+        else if (st == LFM_ATTN_OK)
+            st = lfm_hip_prefill_f16(qd, c->k_cache[layer], c->v_cache[layer], od, 1u, n_rows, pos_0, 0u,
+                                     g->n_head_q, g->n_head_kv, g->head_dim, scale, c->stream);
+    }
     if (st == LFM_ATTN_OK)
         st = st_of(hipMemcpyAsync(h + in_bytes, od, (size_t)n_rows * qrow * sizeof(float), hipMemcpyDeviceToHost,
                                   c->stream));

@@ -1,0 +1,417 @@
+/*
+ * prefill_ext.hip -- causal prefill on gfx950 MFMA for head_dim 128 (the LFM3
+ * full and sliding-window layers), with an optional sliding window and the
+ * sigmoid output gate (fp32 Q, fp16 K/V, fp32 softmax and accumulation, fp32
+ * output).
+ *
+ * Semantics: lfm3_forward_batch_core (tools/lfm3_engine.c:1918-2055) runs
+ * the attention of every prompt row over [t_start(pos), pos] of its layer's
+ * cache -- t_start = pos + 1 - window for a sliding window, 0 otherwise
+ * (:862-873) -- and scales the result by sigmoid(gate) (:1983-2004,
+ * :902-911).  Here every row of a prompt runs in one launch.  K/V row r of
+ * the buffer holds position kv_pos0 + r, so a full layer passes its cache
+ * (kv_pos0 = 0) and a sliding-window layer a linear staging copy of the
+ * window before the prompt plus the prompt's rows.
+ *
+ * Workgroup = 4 waves = 128 query columns: TQ = 128 / kv_mul positions x
+ * kv_mul query heads of one KV head, so each K/V block staged in LDS serves
+ * every query head that reads it; 32 columns per wave.
+ *
+ * Each 32-key block of K (and of V) is kept in LDS as two 64-dim halves of
+ * [32 keys][128 B], with the 16-B chunks of row r XOR-swizzled by
+ * 2 * ((r >> 2) & 3): the layout of the head_dim-64 prefill kernel
+ * (prefill_fa.hip), whose K fragment reads (ds_read_b128) and transposing V
+ * reads (ds_read_b64_tr_b16) it serves without bank conflicts.  Blocks move
+ * global -> registers -> a ring of 3 LDS blocks: block b + 2 is fetched
+ * while block b is computed, one barrier per block.
+ *
+ * Per 32-key block (software pipelined as in the head_dim-64 kernel: P(k)
+ * and PV(k), then S^T(k + 1) into the same registers):
+ *   S^T = K . Q^T - m        16x16x32 f16 MFMA on q * scale * log2(e)
+ *                            rounded once to fp16 (scores in log2 units);
+ *                            the running max is the accumulator's initial
+ *                            value
+ *   p = exp2(S^T)            lazy max: raised only when a block exceeds it
+ *                            by more than 8 (P <= 2^8)
+ *   O^T += V^T . P^T, l += 1 . P^T   (row sums of the same fp16 P on the
+ *                            matrix pipe)
+ * Blocks below the lowest row's window and above the highest row are
+ * skipped; only blocks crossing the diagonal or the window's lower edge are
+ * masked.  Workgroups run heaviest-first.
+ */
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "kernels.h"
+#include "lfm_attn.h"
+
+namespace lfm {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int HD       = 128;
+constexpr int KB       = 32;            /* keys per block (one compute step)       */
+constexpr int NBUF     = 3;             /* LDS ring of blocks                      */
+constexpr int HALFB    = KB * 128;      /* bytes of one 64-dim half of a block     */
+constexpr int BLKB     = 4 * HALFB;     /* K half 0, K half 1, V half 0, V half 1  */
+constexpr int NT       = 2;             /* 16-column tiles per wave                */
+constexpr int NS       = HD / 32;       /* k-steps of Q.K^T                        */
+constexpr int NM       = HD / 16;       /* 16-dim tiles of O^T                     */
+constexpr float kLazy  = 8.0f;          /* headroom in log2 units (P <= 2^8)        */
+
+struct PrefillExtParams {
+    const float *q;     /* [n_seq][n_tok][n_head_q][HD] fp32                        */
+    const uint16_t *k;  /* seq s at k + s*kv_seq_stride: [row][n_head_kv][HD]       */
+    const uint16_t *v;
+    const float *gate;  /* [n_seq][n_tok][n_head_q] or null                          */
+    float *out;         /* [n_seq][n_tok][n_head_q][HD]                             */
+    uint64_t kv_seq_stride;
+    uint32_t n_seq, n_tok, pos_0, kv_pos0, window, n_head_q, n_head_kv, kv_mul, tq, n_qtiles;
+    int gate_is_logit;
+    float qmul;         /* softmax scale * log2(e), applied to Q before its fp16 rounding */
+};
+
+__device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
+
+__device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half2_t exp_pk(float a, float b) {
+    return __builtin_bit_cast(half2_t,
+                              __builtin_amdgcn_cvt_pkrtz(__builtin_amdgcn_exp2f(a), __builtin_amdgcn_exp2f(b)));
+}
+
+/* transposing LDS read: within each 16-lane group, lane l receives element
+ * l % 4 of the 8-byte chunks addressed by lanes l/4, l/4 + 4, l/4 + 8 and
+ * l/4 + 12 */
+__device__ __forceinline__ half4_t lds_read_tr(const uint8_t *p) {
+    return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4 *)p));
+}
+
+__device__ __forceinline__ float max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+__global__ __launch_bounds__(256, 2) void k_prefill128(const PrefillExtParams P) {
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[NBUF * BLKB];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    /* 1-D grid, heaviest query tiles first; consecutive workgroups take
+     * consecutive (sequence, KV head) pairs */
+    const uint32_t pairs = P.n_head_kv * P.n_seq;
+    const uint32_t qt    = P.n_qtiles - 1u - blockIdx.x / pairs;
+    const uint32_t pair  = blockIdx.x % pairs;
+    const uint32_t kvh = pair % P.n_head_kv, s = pair / P.n_head_kv;
+    const uint32_t t0  = qt * P.tq;
+
+    const uint16_t *kc = P.k + (size_t)s * P.kv_seq_stride + (size_t)kvh * HD;
+    const uint16_t *vc = P.v + (size_t)s * P.kv_seq_stride + (size_t)kvh * HD;
+    const size_t row   = (size_t)P.n_head_kv * HD;
+
+    /* ---- columns of this lane: (head j, row t) per N-tile -------------- */
+    uint32_t col_pos[NT], col_lo[NT];
+    bool col_ok[NT];
+    half8_t qf[NT][NS];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t c = (uint32_t)(wave * 32 + nt * 16 + l16);
+        const uint32_t j = c / P.tq, t = t0 + c % P.tq;
+        col_ok[nt]  = t < P.n_tok;
+        col_pos[nt] = P.pos_0 + t;
+        col_lo[nt]  = (P.window && col_pos[nt] + 1u > P.window) ? col_pos[nt] + 1u - P.window : 0u;
+        const float *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q + kvh * P.kv_mul + j) * HD + 8 * g;
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (col_ok[nt]) {
+                a = *reinterpret_cast<const float4 *>(qp + 32 * st);
+                b = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
+            }
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            half8_t h;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = (_Float16)(x[e] * P.qmul);
+            qf[nt][st] = h;
+        }
+    }
+    /* key rows [r_lo, r_hi) of the buffer, in 32-key blocks */
+    const uint32_t lo_pos = P.pos_0 + t0;
+    const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;
+    const uint32_t r_hi   = hi_pos + 1u - P.kv_pos0;
+    uint32_t first_key    = P.window && lo_pos + 1u > P.window ? lo_pos + 1u - P.window : 0u;
+    first_key             = max(first_key, P.kv_pos0);
+    const uint32_t b_lo   = (first_key - P.kv_pos0) / KB;    /* first block       */
+    const uint32_t b_hi   = (r_hi + KB - 1u) / KB;           /* past the last     */
+    /* blocks needing no per-key test: every key >= the highest row's window
+     * start and <= the lowest row, i.e. blocks [u0, u1) */
+    const uint32_t free_key_lo = P.window && hi_pos + 1u > P.window ? hi_pos + 1u - P.window : 0u;
+    const uint32_t b_free = free_key_lo > P.kv_pos0 ? (free_key_lo - P.kv_pos0 + KB - 1u) / KB : 0u;
+    const uint32_t b_diag = (lo_pos - P.kv_pos0 + 1u) / KB;
+    const uint32_t u0     = min(max(b_lo, b_free), b_hi);
+    const uint32_t u1     = max(u0, min(b_hi, b_diag));
+    auto block_masked = [&](uint32_t b) { return b < u0 || b >= u1; };
+
+    /* ---- staging: thread tid moves 16-B chunks tid and tid + 256 of the K
+     * block and of the V block; chunk p is row p / 16, global chunk p % 16
+     * of that row, stored in half (p % 16) / 8 at slot ((p % 8) ^ swz(row)) */
+    uint32_t st_row[2], st_dst[2], st_col[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t p = (uint32_t)tid + 256u * e, r = p >> 4, c = p & 15u;
+        st_row[e] = r;
+        st_col[e] = 8u * c; /* halfs within the head's row */
+        st_dst[e] = (c >> 3) * HALFB + r * 128u + 16u * ((c & 7u) ^ (2u * ((r >> 2) & 3u)));
+    }
+    u32x4_t stage[4];
+    auto load_regs = [&](uint32_t b) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            uint32_t r = b * KB + st_row[e];
+            r = r < r_hi ? r : r_hi - 1u; /* rows past the keys: masked */
+            const size_t off = (size_t)r * row + st_col[e];
+            stage[e]     = *reinterpret_cast<const u32x4_t *>(kc + off);
+            stage[2 + e] = *reinterpret_cast<const u32x4_t *>(vc + off);
+        }
+    };
+    auto store_regs = [&](uint32_t b) {
+        uint8_t *dst = ring + (b % NBUF) * BLKB;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            *reinterpret_cast<u32x4_t *>(dst + st_dst[e])             = stage[e];
+            *reinterpret_cast<u32x4_t *>(dst + 2 * HALFB + st_dst[e]) = stage[2 + e];
+        }
+    };
+
+    /* fragment offsets within a 64-dim half (bytes).  K: row 16*mt + l16,
+     * chunk 4*(st % 2) + g.  V (transposing read): lane l16 of group g
+     * addresses row 4g + l16/4 of a 16-key half, dims 16*mt + 4*(l16 % 4) */
+    const uint32_t kswz  = (uint32_t)(g ^ (2 * ((l16 >> 2) & 3)));
+    const uint32_t koff0 = (uint32_t)l16 * 128u + 16u * kswz;
+    const uint32_t koff1 = (uint32_t)l16 * 128u + 16u * (kswz ^ 4u);
+    uint32_t voff[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+        voff[mt] = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)(mt ^ g) + 16u * ((l16 >> 1) & 1) +
+                   8u * (l16 & 1);
+
+    float4_t oacc[NM][NT];
+    float4_t negm[NT];
+    float4_t lacc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        negm[nt] = (float4_t)0.0f;
+        lacc[nt] = (float4_t)0.0f;
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
+    }
+    const half8_t ones8 = (half8_t)(_Float16)1.0f;
+
+    /* S^T of block b: two 16-key tiles x NT column tiles */
+    auto scores = [&](auto mask_tag, uint32_t b, float4_t (&sc)[2][NT]) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const uint8_t *kb = ring + (b % NBUF) * BLKB;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            half8_t kf[NS];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                kf[2 * h]     = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff0));
+                kf[2 * h + 1] = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff1));
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float4_t a = mfma(kf[0], qf[nt][0], negm[nt]);
+#pragma unroll
+                for (int st = 1; st < NS; ++st) a = mfma(kf[st], qf[nt][st], a);
+                sc[mt][nt] = a;
+            }
+        }
+        if constexpr (MASK) {
+            /* element (mt, i) is key key0 + 16 mt + i of the column */
+            const int key0 = (int)(P.kv_pos0 + b * KB) + 4 * g;
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int hi = (int)col_pos[nt] - key0, lo = (int)col_lo[nt] - key0;
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (16 * mt + i > hi || 16 * mt + i < lo) sc[mt][nt][i] = -INFINITY;
+            }
+        }
+    };
+
+    /* lazy max per column: m is set by the first block holding one of the
+     * column's keys (its exact maximum there) and raised later only when a
+     * block exceeds it by more than kLazy, rescaling O, l and the pending
+     * scores (a rare, wave-uniform branch).  With a window, a column's first
+     * keys may lie in a later block than the workgroup's first; until then
+     * its scores are all masked, p = 0 and O = l = 0, so setting m needs no
+     * rescale (and exp2(-m) could overflow). */
+    bool mset[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) mset[nt] = false;
+    auto update_max = [&](float4_t (&sc)[2][NT]) {
+        float mx[NT];
+        bool any_raise = false;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            float v = max3(max3(sc[0][nt][0], sc[0][nt][1], sc[0][nt][2]), sc[0][nt][3], sc[1][nt][0]);
+            v = max3(max3(v, sc[1][nt][1], sc[1][nt][2]), sc[1][nt][3], -INFINITY);
+            mx[nt] = v;
+            any_raise |= v > kLazy || (!mset[nt] && v > -INFINITY);
+        }
+        if (__builtin_amdgcn_ballot_w64(any_raise) != 0ull) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float v = mx[nt]; /* column max over the 4 lanes holding it */
+                v = fmaxf(v, __shfl_xor(v, 16));
+                v = fmaxf(v, __shfl_xor(v, 32));
+                const bool raise  = v > kLazy || (!mset[nt] && v > -INFINITY);
+                const float inc   = raise ? v : 0.0f;
+                const float alpha = mset[nt] ? __builtin_amdgcn_exp2f(-inc) : 1.0f;
+                mset[nt] = mset[nt] || raise;
+                negm[nt] -= inc;
+                lacc[nt] *= alpha;
+                sc[0][nt] -= inc;
+                sc[1][nt] -= inc;
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
+            }
+        }
+    };
+
+    auto accumulate = [&](uint32_t b, const float4_t (&sc)[2][NT]) {
+        u32x4_t pf[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const float4_t a = sc[0][nt], c = sc[1][nt];
+            const half2_t h0 = exp_pk(a[0], a[1]);
+            const half2_t h1 = exp_pk(a[2], a[3]);
+            const half2_t h2 = exp_pk(c[0], c[1]);
+            const half2_t h3 = exp_pk(c[2], c[3]);
+            u32x4_t w;
+            w[0] = __builtin_bit_cast(uint32_t, h0);
+            w[1] = __builtin_bit_cast(uint32_t, h1);
+            w[2] = __builtin_bit_cast(uint32_t, h2);
+            w[3] = __builtin_bit_cast(uint32_t, h3);
+            pf[nt] = w;
+        }
+        const uint8_t *vb = ring + (b % NBUF) * BLKB + 2 * HALFB;
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) {
+            const uint8_t *vh = vb + (mt >> 2) * HALFB;
+            const half4_t lo  = lds_read_tr(vh + voff[mt & 3]);
+            const half4_t hi  = lds_read_tr(vh + 16 * 128 + voff[mt & 3]);
+            const half8_t av  = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
+    };
+
+    /* entering block b: block b (stored at the previous entry) becomes
+     * visible to every wave; the slot of block b + 1 is free (its previous
+     * block, b - 2, was last read before this barrier), so block b + 1 moves
+     * from the staging registers into it and block b + 2 is fetched */
+    auto enter_block = [&](uint32_t b) {
+        __syncthreads();
+        if (b + 1u < b_hi) store_regs(b + 1u);
+        if (b + 2u < b_hi) load_regs(b + 2u);
+    };
+
+    load_regs(b_lo);
+    store_regs(b_lo);
+    if (b_lo + 1u < b_hi) load_regs(b_lo + 1u);
+    enter_block(b_lo);
+    float4_t scur[2][NT];
+    if (block_masked(b_lo)) scores(std::true_type{}, b_lo, scur);
+    else scores(std::false_type{}, b_lo, scur);
+    update_max(scur);
+    auto step = [&](auto mask_tag, uint32_t b) {
+        accumulate(b, scur);
+        enter_block(b + 1u);
+        scores(mask_tag, b + 1u, scur);
+        update_max(scur);
+    };
+    /* blocks [u0, u1) need no mask; masked ones sit below (window edge)
+     * and above (diagonal) */
+    uint32_t b = b_lo;
+    for (; b + 1u < u0; ++b) step(std::true_type{}, b);
+    for (; b + 1u < u1; ++b) step(std::false_type{}, b);
+    for (; b + 1u < b_hi; ++b) step(std::true_type{}, b);
+    accumulate(b, scur);
+
+    /* ---- epilogue: O * gate / l ------------------------------------------ */
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const float lt = lacc[nt][0];
+        if (!col_ok[nt]) continue;
+        const uint32_t c    = (uint32_t)(wave * 32 + nt * 16 + l16);
+        const uint32_t j    = c / P.tq, t = t0 + c % P.tq;
+        const size_t orow   = ((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j;
+        float gv            = 1.0f;
+        if (P.gate) {
+            const float gl = P.gate[orow];
+            gv             = P.gate_is_logit ? 1.0f / (1.0f + expf(-gl)) : gl;
+        }
+        const float inv = lt > 0.0f ? gv / lt : 0.0f;
+        float *op       = P.out + orow * HD;
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt)
+            *reinterpret_cast<float4 *>(op + 16 * mt + 4 * g) =
+                make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv, oacc[mt][nt][2] * inv,
+                            oacc[mt][nt][3] * inv);
+    }
+}
+
+} // namespace
+
+bool prefill_ext_supports(uint32_t head_dim, uint32_t kv_mul) {
+    return head_dim == 128u && kv_mul >= 1u && kv_mul <= 32u && (128u % kv_mul) == 0u;
+}
+
+int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, const float *gate, int gate_is_logit,
+                       float *out, uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t kv_pos0,
+                       uint64_t kv_seq_stride, uint32_t window, uint32_t n_head_q, uint32_t n_head_kv,
+                       uint32_t head_dim, float scale, hipStream_t stream) {
+    PrefillExtParams P{};
+    P.q             = q;
+    P.k             = k;
+    P.v             = v;
+    P.gate          = gate;
+    P.gate_is_logit = gate_is_logit;
+    P.out           = out;
+    P.kv_seq_stride = kv_seq_stride;
+    P.n_seq         = n_seq;
+    P.n_tok         = n_tok;
+    P.pos_0         = pos_0;
+    P.kv_pos0       = kv_pos0;
+    P.window        = window;
+    P.n_head_q      = n_head_q;
+    P.n_head_kv     = n_head_kv;
+    P.kv_mul        = n_head_q / n_head_kv;
+    P.tq            = 128u / P.kv_mul;
+    P.n_qtiles      = (n_tok + P.tq - 1u) / P.tq;
+    P.qmul          = scale * kLog2e;
+    hipEvent_t ev0, ev1;
+    profile_events(&ev0, &ev1);
+    if (ev0) (void)hipEventRecord(ev0, stream);
+    hipLaunchKernelGGL(k_prefill128, dim3(P.n_qtiles * n_head_kv * n_seq), dim3(256), 0, stream, P);
+    hipError_t e = hipGetLastError();
+    if (ev1) (void)hipEventRecord(ev1, stream);
+    (void)head_dim;
+    return hip_status(e);
+}
+
+} // namespace lfm

@@ -263,7 +263,10 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
                 v = fmaxf(v, __shfl_xor(v, 32));
                 const bool raise  = FIRST ? (v > -INFINITY) : (v > kLazy);
                 const float inc   = raise ? v : 0.0f;
-                const float alpha = __builtin_amdgcn_exp2f(-inc);
+                /* O and l are still zero at the first step: no rescale
+                 * (exp2(-m) overflows to inf for m < -128, and 0 * inf is
+                 * NaN) */
+                const float alpha = FIRST ? 1.0f : __builtin_amdgcn_exp2f(-inc);
                 negm[nt] -= inc;
                 lacc[nt] *= alpha;
                 sc[0][nt] -= inc;

@@ -578,6 +578,29 @@ int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, fl
                                n_head_kv, head_dim, scale, to_stream(stream));
 }
 
+int lfm_hip_lfm3_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, const float *gate,
+                             int gate_is_logit, float *out, uint32_t n_seq, uint32_t n_tok, uint32_t pos_0,
+                             uint32_t kv_pos0, uint64_t kv_seq_stride, uint32_t window_len, uint32_t n_head_q,
+                             uint32_t n_head_kv, uint32_t head_dim, float scale, lfm_attn_stream_t stream) {
+    if (!q || !k || !v || !out) return LFM_ATTN_E_INVALID;
+    if (n_seq == 0u || n_tok == 0u || n_head_q == 0u || n_head_kv == 0u || n_head_q % n_head_kv != 0u)
+        return LFM_ATTN_E_INVALID;
+    if (n_seq > 65535u || n_head_kv > 65535u) return LFM_ATTN_E_INVALID;
+    if ((uint64_t)pos_0 + n_tok > 0x7FFFFFFFull) return LFM_ATTN_E_RANGE;
+    /* every key a row attends must be in the buffer: kv_pos0 <= t_start(pos_0) */
+    const uint32_t t_first = (window_len > 0u && pos_0 + 1u > window_len) ? pos_0 + 1u - window_len : 0u;
+    if (kv_pos0 > t_first) return LFM_ATTN_E_INVALID;
+    const uint64_t rows = (uint64_t)pos_0 + n_tok - kv_pos0;
+    if (n_seq > 1u && kv_seq_stride < rows * n_head_kv * head_dim)
+        return LFM_ATTN_E_INVALID; /* sequences would overlap */
+    if (!lfm::prefill_ext_supports(head_dim, n_head_q / n_head_kv)) return LFM_ATTN_E_UNSUPPORTED;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) || (kv_seq_stride % 8u))
+        return LFM_ATTN_E_INVALID;
+    return lfm::launch_prefill_ext(q, k, v, gate, gate_is_logit, out, n_seq, n_tok, pos_0, kv_pos0,
+                                   kv_seq_stride, window_len, n_head_q, n_head_kv, head_dim, scale,
+                                   to_stream(stream));
+}
+
 /* ---- attention-sink eviction ------------------------------------------- */
 
 static inline int shift_caches_ok(uint16_t *const *k_caches, uint16_t *const *v_caches,

@@ -194,31 +194,80 @@ def test_context_prefill_matches_chunked_steps(gpu, orc):
     b.close()
 
 
-def test_context_prefill_chunked_layers(gpu):
-    """Layers the MFMA prefill does not take (a sliding-window layer, a gated
-    d128 layer) run the step in chunks of 8: bit-identical to calling the step
-    that way."""
+@pytest.mark.parametrize("win,cap,pre,n", [(16, 24, 0, 45), (16, 24, 21, 45), (256, 264, 300, 700)])
+def test_context_prefill_lfm3_layers(gpu, orc, win, cap, pre, n):
+    """LFM3 prompt prefill through the head_dim-128 MFMA kernel: a
+    sliding-window layer (the window before the prompt copied out of the
+    ring into a linear buffer, the ring refilled afterwards) and a gated full
+    layer with partial RoPE, after `pre` cached tokens.  Against the same
+    prompt run through the step 8 rows at a time (lfm3_forward_batch_core's
+    batches): every cache slot bit-identical (same prologue, same ring state),
+    outputs within the attention tolerance; and against the oracle engine."""
     la = gpu
-    rng = np.random.default_rng(22)
-    nq, nkv, hd, max_seq, win, cap = 16, 4, 128, 256, 16, 24
+    rng = np.random.default_rng(22 + pre + win)
+    nq, nkv, hd, max_seq, eps = 16, 4, 128, 1024, 1e-5
     rf = np.array([1.0] * 32 + [1e30] * 32, np.float32)
-    mk = lambda: la.EngineContext(2, nq, nkv, hd, max_seq, 1e-5, rope_base=1e6, lfm3=True, sliding_window=win,
+    mk = lambda: la.EngineContext(2, nq, nkv, hd, max_seq, eps, rope_base=1e6, lfm3=True, sliding_window=win,
                                   swa_cap=cap, layer_is_swa=[1, 0], rope_base_swa=1e4, rope_dim=hd,
                                   rope_freqs=rf)
     a, b = mk(), mk()
-    n = 45
-    for layer in (0, 1):
+    norms = []
+    for layer in range(2):
+        qn = (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32)
+        kn = (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32)
+        norms.append((qn, kn))
+        for c in (a, b):
+            c.set_norms(layer, qn, kn)
+    luts = [orc.rope_lut_lfm3(max_seq, hd, hd, 1e4, None), orc.rope_lut_lfm3(max_seq, hd, hd, 1e6, rf)]
+    ref = RefEngine(orc, nq, nkv, hd, max_seq, eps, luts, norms, swa=[1, 0], cap=cap)
+    mk_rows = lambda m: (rng.standard_normal((m, nq, hd), dtype=np.float32) * 2,
+                         rng.standard_normal((m, nkv, hd), dtype=np.float32) * 2,
+                         rng.standard_normal((m, nkv, hd), dtype=np.float32) * 0.5,
+                         rng.standard_normal((m, nq)).astype(np.float32))
+    for layer in range(2):
+        window = win if layer == 0 else 0
+        q, k, v, g = mk_rows(pre)
+        for p in range(0, pre, 8):
+            sl = slice(p, p + 8)
+            for c in (a, b):
+                c.forward(layer, p, q[sl], k[sl], v[sl], g[sl])
+            ref.step(layer, p, q[sl], k[sl], v[sl], g[sl], window)
+        q, k, v, g = mk_rows(n)
+        got = a.prefill(layer, pre, q, k, v, g).reshape(n, nq, hd)
+        want = np.concatenate([b.forward(layer, pre + p, q[p:p + 8], k[p:p + 8], v[p:p + 8], g[p:p + 8])
+                               .reshape(-1, nq, hd) for p in range(0, n, 8)])
+        parity(got, want, what=f"ctx prefill layer {layer} vs chunked steps")
+        oracle = np.concatenate([ref.step(layer, pre + p, q[p:p + 8], k[p:p + 8], v[p:p + 8], g[p:p + 8], window)
+                                 .reshape(-1, nq, hd) for p in range(0, n, 8)])
+        parity(got, oracle, what=f"ctx prefill layer {layer} vs oracle engine")
+        slots = cap if layer == 0 else pre + n
+        ka, va = a.kv_export(layer, 0, slots)
+        kb, vb = b.kv_export(layer, 0, slots)
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"layer {layer}: caches differ"
+    a.close()
+    b.close()
+
+
+def test_context_prefill_chunked_layers(gpu):
+    """Shapes the MFMA prefill kernels do not take (a gated head_dim-64
+    layer) and prompts of at most 8 rows run the step in chunks of 8:
+    bit-identical to calling the step that way."""
+    la = gpu
+    rng = np.random.default_rng(23)
+    for nq, nkv, hd, n, gated in ((16, 4, 64, 45, True), (16, 4, 128, 8, True)):
+        a = la.EngineContext(1, nq, nkv, hd, 256, 1e-5, rope_base=1e6)
+        b = la.EngineContext(1, nq, nkv, hd, 256, 1e-5, rope_base=1e6)
         q = rng.standard_normal((n, nq, hd), dtype=np.float32)
         k = rng.standard_normal((n, nkv, hd), dtype=np.float32)
         v = rng.standard_normal((n, nkv, hd), dtype=np.float32)
-        g = rng.standard_normal((n, nq)).astype(np.float32)
-        got = a.prefill(layer, 0, q, k, v, g)
-        want = np.concatenate([b.forward(layer, p, q[p:p + 8], k[p:p + 8], v[p:p + 8], g[p:p + 8])
-                               for p in range(0, n, 8)])
+        g = rng.standard_normal((n, nq)).astype(np.float32) if gated else None
+        got = a.prefill(0, 0, q, k, v, g)
+        want = np.concatenate([b.forward(0, p, q[p:p + 8], k[p:p + 8], v[p:p + 8],
+                                         None if g is None else g[p:p + 8]) for p in range(0, n, 8)])
         assert np.array_equal(got, want)
-    with pytest.raises(la.LfmAttnError) as e:
-        a.prefill(1, 250, np.zeros((8, nq, hd), np.float32), np.zeros((8, nkv, hd), np.float32),
-                  np.zeros((8, nkv, hd), np.float32))
-    assert e.value.status == -2
-    a.close()
-    b.close()
+        with pytest.raises(la.LfmAttnError) as e:
+            a.prefill(0, 250, np.zeros((8, nq, hd), np.float32), np.zeros((8, nkv, hd), np.float32),
+                      np.zeros((8, nkv, hd), np.float32))
+        assert e.value.status == -2
+        a.close()
+        b.close()

@@ -90,15 +90,17 @@ def test_prefill_rejects_unsupported(gpu):
                                    None) == -3
 
 
-@pytest.mark.parametrize("pattern", ["rising", "spike", "falling"])
+@pytest.mark.parametrize("pattern", ["rising", "spike", "falling", "sunk"])
 def test_prefill_lazy_max_raises(gpu, orc, pattern):
     """Score patterns that force the lazy running max to be raised after the
     first step (and in masked diagonal steps): keys whose scores climb by tens
     of log2 units along the sequence ("rising"), isolated huge scores
-    ("spike"), and a large first block followed by tiny ones ("falling").
+    ("spike"), a large first block followed by tiny ones ("falling"), and a
+    first step whose scores all lie below -128 log2 units, where exp2(-m)
+    overflows and must not scale the (zero) accumulators ("sunk").
     Against the oracle's causal rows."""
     la = gpu
-    rng = np.random.default_rng({"rising": 1, "spike": 2, "falling": 3}[pattern])
+    rng = np.random.default_rng({"rising": 1, "spike": 2, "falling": 3, "sunk": 4}[pattern])
     n_seq, n_tok, nq, nkv, hd = 1, 300, 16, 4, 64
     q = rng.standard_normal((n_seq, n_tok, nq, hd), dtype=np.float32)
     k = rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32) * 0.5
@@ -111,8 +113,10 @@ def test_prefill_lazy_max_raises(gpu, orc, pattern):
         amp = 0.25 * t          # scores grow ~ 0.125 * 3 * 0.25 t: +28 log2 units by the end
     elif pattern == "spike":
         amp = np.where(t % 97 == 40, 60.0, 0.0).astype(np.float32)
-    else:
+    elif pattern == "falling":
         amp = np.where(t < 64, 40.0, 0.0).astype(np.float32)
+    else:
+        amp = np.where(t < 32, -400.0, 0.0).astype(np.float32)
     k += amp[None, :, None, None] * u
     k16 = f16(k)
     v16 = f16(rng.standard_normal((n_seq, n_tok, nkv, hd), dtype=np.float32))
