@@ -51,6 +51,11 @@ typedef void *lfm_attn_stream_t; /* hipStream_t */
 const char *lfm_attn_status_string(int status);
 /* Text of the last HIP error seen by this thread ("" if none). */
 const char *lfm_attn_last_error(void);
+/* Diagnostic, no reference counterpart: the form of this thread's last
+ * decode / step attention launch -- "wg" (one workgroup per sequence and KV
+ * head, in-workgroup merge), "grid" (fixed key chunks + merge kernel),
+ * "balanced" (tile shares + merge kernel) or "generic" ("" before any). */
+const char *lfm_attn_last_plan(void);
 const char *lfm_attn_version(void);
 
 /* ---- device plumbing (so C11 callers need no HIP headers) ------------------ */

@@ -24,6 +24,7 @@ from .attention import (  # noqa: F401
     gqa_heads,
     gqa_qkv_fused,
     kv_cache_shift_sinks,
+    last_plan,
     lfm3_kv_cache_shift_sinks,
     lfm3_online_gqa_f16_dispatch,
     lfm3_prefill_f16,

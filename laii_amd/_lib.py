@@ -21,6 +21,7 @@ _sz = C.c_size_t
 SIGNATURES = {
     "lfm_attn_status_string": (C.c_char_p, [_int]),
     "lfm_attn_last_error": (C.c_char_p, []),
+    "lfm_attn_last_plan": (C.c_char_p, []),
     "lfm_attn_version": (C.c_char_p, []),
     "lfm_attn_device_count": (_int, [C.POINTER(_int)]),
     "lfm_attn_set_device": (_int, [_int]),

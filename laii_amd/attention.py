@@ -287,6 +287,12 @@ def gqa_f16_varlen_noalloc(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v
                                                 cap, scale, stream), "lfm_hip_gqa_f16_varlen_noalloc")
 
 
+def last_plan() -> str:
+    """Form of this thread's last decode / step attention launch: "wg",
+    "grid", "balanced" or "generic" (lfm_attn_last_plan)."""
+    return load().lfm_attn_last_plan().decode()
+
+
 def prefill_f16(q: Ptr, k: Ptr, v: Ptr, out: Ptr, n_seq: int, n_tok: int, pos_0: int,
                 kv_seq_stride: int, n_head_q: int, n_head_kv: int, head_dim: int,
                 scale: Optional[float] = None, stream=None) -> None:

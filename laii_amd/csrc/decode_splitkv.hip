@@ -1223,7 +1223,11 @@ int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
 template <int HD, int NT, bool FUSE>
 int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream,
                  const Scratch *sc) {
-    if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
+    if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) {
+        note_plan("wg");
+        return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
+    }
+    note_plan(grid ? "grid" : "balanced");
     uint32_t w = choose_waves(p.n_head_kv, HD);
     /* fused prologue: the staged new rows and the V^T tiles stay within
      * 64 KB of LDS per workgroup */

@@ -120,6 +120,7 @@ __global__ __launch_bounds__(64) void k_generic(const GenericParams G) {
 } // namespace
 
 int launch_generic(const AttnBatch &b, bool kv_f32, hipStream_t stream) {
+    note_plan("generic");
     GenericParams G{};
     G.q             = b.q;
     G.gate          = b.gate;

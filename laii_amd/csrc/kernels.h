@@ -124,6 +124,10 @@ void profile_events(hipEvent_t *before, hipEvent_t *after);
 /* Record a HIP error for lfm_attn_last_error and map it to a status. */
 int hip_status(hipError_t e);
 
+/* Record the plan of this thread's last attention launch (a string literal)
+ * for lfm_attn_last_plan. */
+void note_plan(const char *name);
+
 /* FNV-1a 64 of a device buffer (fnv_hash.hip). */
 size_t fnv1a64_workspace_bytes(uint64_t len);
 int launch_fnv1a64(const void *data, uint64_t len, uint64_t h_in, void *ws, hipStream_t stream);

@@ -19,6 +19,9 @@ namespace lfm {
 static thread_local char g_last_error[256] = "";
 static thread_local hipEvent_t g_prof_before = nullptr;
 static thread_local hipEvent_t g_prof_after  = nullptr;
+static thread_local const char *g_last_plan = "";
+
+void note_plan(const char *name) { g_last_plan = name; }
 
 void profile_events(hipEvent_t *before, hipEvent_t *after) {
     *before = g_prof_before;
@@ -125,6 +128,8 @@ const char *lfm_attn_status_string(int status) {
 }
 
 const char *lfm_attn_last_error(void) { return lfm::g_last_error; }
+
+const char *lfm_attn_last_plan(void) { return lfm::g_last_plan; }
 
 const char *lfm_attn_version(void) { return "lfm_attn 0.1 gfx950"; }
 

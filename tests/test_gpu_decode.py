@@ -276,29 +276,34 @@ def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
         assert np.abs(outs[0] - o).max() < 1e-5
 
 
-@pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq,max_ctx", [
-    (64, 16, 8, 1, 1, 300),    # config-1 heads, short context: the default small-batch form
-    (64, 32, 8, 8, 2, 400),    # verify rows (32 query columns)
-    (64, 32, 4, 8, 1, 200),    # 64 query columns (four-wave workgroups)
-    (128, 16, 4, 1, 3, 500),   # LFM3 head_dim 128
-    (64, 32, 8, 1, 2, 3000),   # forced: more planned splits than waves, chunks lengthened
+@pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq,max_ctx,win,cap,gate,default", [
+    (64, 16, 8, 1, 1, 300, 0, 0, False, "wg"),       # config-1 heads, short context: the default small-batch form
+    (64, 32, 8, 8, 2, 400, 0, 0, False, "balanced"),  # verify rows (32 query columns; two sequences: balanced)
+    (64, 32, 4, 8, 1, 1000, 0, 0, False, "wg"),      # 64 query columns (four-wave workgroups, 2 splits)
+    (128, 16, 4, 1, 3, 500, 0, 0, False, "balanced"),  # LFM3 head_dim 128 (ragged: balanced by default)
+    (128, 16, 4, 1, 1, 900, 200, 208, True, "wg"),   # SWA ring (window 200, 208 slots) + gate: 4 splits
+    (64, 32, 8, 1, 2, 3000, 0, 0, False, "balanced"),  # forced: more planned splits than waves, chunks lengthened
 ])
-def test_workgroup_merge_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq, max_ctx):
+def test_workgroup_merge_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq, max_ctx, win, cap, gate, default):
     """Small batches take one workgroup per (sequence, KV head) whose waves
     split the keys and merge in place (k_splitkv_wg, LFM_ATTN_PLAN=wg forces
-    it); it matches the oracle and the two-kernel grid."""
+    it); it matches the oracle and the two-kernel grid, and with no override
+    the automatic rule picks the expected form (lfm_attn_last_plan)."""
     la = gpu
     rng = np.random.default_rng(max_ctx + n_seq + hd)
     ctx = [int(c) for c in rng.integers(1, max_ctx, size=n_seq)]
     ctx[0] = max_ctx - 1
     outs = []
-    for env in ({"LFM_ATTN_PLAN": "wg"}, {"LFM_ATTN_PLAN": "grid"}):
+    for env in ({}, {"LFM_ATTN_PLAN": "wg"}, {"LFM_ATTN_PLAN": "grid"}):
         os.environ.update(env)
         try:
-            got, want = _varlen_case(la, orc, np.random.default_rng(9), n_seq, n_rows, nq, nkv, hd, ctx)
+            got, want = _varlen_case(la, orc, np.random.default_rng(9), n_seq, n_rows, nq, nkv, hd, ctx, win=win,
+                                     cap=cap, gate=gate, slots=cap or None)
+            plan = la.last_plan()
         finally:
             for k in env:
                 os.environ.pop(k, None)
         parity(got, want, what=f"{env}")
+        assert plan == (default if not env else env["LFM_ATTN_PLAN"]), f"{env}: plan {plan}"
         outs.append(got)
-    assert np.abs(outs[0] - outs[1]).max() < 1e-5
+    assert np.abs(outs[1] - outs[2]).max() < 1e-5
