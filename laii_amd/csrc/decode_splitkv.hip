@@ -85,7 +85,18 @@ __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_ca
  * loop wait for the next sub-tile's loads as well. */
 typedef const __attribute__((address_space(1))) uint16_t *gu16_ptr;
 typedef const __attribute__((address_space(1))) u32x4_t *gu32x4_ptr;
-__device__ __forceinline__ u32x4_t load16(gu16_ptr p) { return *reinterpret_cast<gu32x4_ptr>(p); }
+/* STREAM: non-temporal loads (the "nt" cache policy), for cache rows read
+ * once.  Measured on MI355X with rotated copies larger than the 256 MB MALL:
+ * single-row decode kernels (one 16-column tile) run faster with them --
+ * B64 x 8192 (32q/8kv d64) 186.9 -> 170 us, ragged B64 100.2 -> 92.3 us,
+ * LFM3 full B32 x 32768 374.8 -> 346.5 us, SWA ring 11.0 -> 10.6 us -- while
+ * the 8-row verify kernel (two tiles) runs slower, 37.0 -> 40.7 us at
+ * B16 x 4104, so it keeps the default policy. */
+template <bool STREAM>
+__device__ __forceinline__ u32x4_t load16(gu16_ptr p) {
+    if constexpr (STREAM) return __builtin_nontemporal_load(reinterpret_cast<gu32x4_ptr>(p));
+    else return *reinterpret_cast<gu32x4_ptr>(p);
+}
 
 __device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -287,7 +298,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
             gu16_ptr kp = kc + (size_t)slot * row + 8 * g;
 #pragma unroll
             for (int st = 0; st < NS; ++st)
-                kd[kt][st] = load16(kp + 32 * st);
+                kd[kt][st] = load16<NT == 1>(kp + 32 * st);
         }
 #pragma unroll
         for (int ps = 0; ps < HD / 64; ++ps) {
@@ -298,7 +309,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                 if (p0 + off >= ke) off = ke - 1u - p0;
                 uint32_t slot = base + off;
                 if (P.window) { while (slot >= P.cap) slot -= P.cap; }
-                vd[ps * 4 + i] = load16(vc + (size_t)slot * row + 8 * (lane % CH));
+                vd[ps * 4 + i] = load16<NT == 1>(vc + (size_t)slot * row + 8 * (lane % CH));
             }
         }
     };
