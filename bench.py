@@ -632,7 +632,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # warm-up long enough for the clocks to settle: on MI355X the first 50
+    # timed headline steps ran 183 us after 10 warm-up steps and 171-172 us
+    # after 100-300 (steady state 170.5 us)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
