@@ -601,6 +601,26 @@ def cpu_rows(rng, n_threads):
     return rows
 
 
+def decode_cases(rng):
+    """The secondary decode / verify / LFM3 workloads (name, DecodeWorkload
+    arguments)."""
+    return [
+        ("cfg2_varlen_b64_ctxU512_8192", dict(n_seq=64, n_rows=1, nq=32, nkv=8, hd=64,
+                                              ctx=rng.integers(512, 8193, size=64))),
+        ("cfg3_verify_b16_rows8_ctx4096", dict(n_seq=16, n_rows=8, nq=32, nkv=8, hd=64,
+                                               ctx=[4096] * 16, copies=4)),
+        ("cfg5_lfm3_swa_b32_cap256_pos1000", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
+                                                  ctx=[1001] * 32, window=256, cap=256,
+                                                  gate=True, copies=36)),
+        ("cfg5_lfm3_full_b32_ctx32768", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
+                                             ctx=[32768] * 32, gate=True)),
+        # 2 MB per call: 160 rotated copies (320 MB) keep it out of the 256 MB
+        # MALL; the row is latency-bound, so us_per_step is its figure
+        ("cfg1_decode_b1_16q8kv_ctx1024", dict(n_seq=1, n_rows=1, nq=16, nkv=8, hd=64,
+                                               ctx=[1024], copies=160)),
+    ]
+
+
 def run_prefill(hip, la, rng, steps):
     pf = PrefillWorkload(la, rng)
     n = max(5, steps // 5)
@@ -642,6 +662,9 @@ def main():
                     help="only the config-4 prefill workload (for kernel profiling)")
     ap.add_argument("--prefill128-only", action="store_true",
                     help="only the LFM3 head_dim-128 prefill workloads (for kernel profiling)")
+    ap.add_argument("--only", default=None,
+                    help="only the named decode / verify / LFM3 workload of the secondary rows "
+                         "(for kernel profiling), e.g. cfg3_verify_b16_rows8_ctx4096")
     ap.add_argument("--engine-only", action="store_true",
                     help="only the engine step, lfm_attn_ctx_forward (for kernel tracing)")
     args = ap.parse_args()
@@ -657,6 +680,16 @@ def main():
     hip = Hip()
     rng = np.random.default_rng(20261201)
     t_setup = time.perf_counter()
+    if args.only:
+        kw = dict(decode_cases(rng))[args.only]
+        wl = DecodeWorkload(la, rng, args.only, **kw)
+        sms = time_steps(hip, wl, args.steps, args.warmup)
+        kms = time_main_kernel(hip, la, wl, args.steps)
+        print(json.dumps({"metric": f"{args.only} GB/s", "value": round(wl.bytes / (sms * 1e-3) / 1e9, 1),
+                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "higher_is_better": True,
+                          "us_per_step": round(sms * 1e3, 2), "kernel_us": round(kms * 1e3, 2),
+                          "plan": la.last_plan(), "bytes": wl.bytes}), flush=True)
+        return
     if args.engine_only:
         es = bench_engine_step(la, rng, calls=max(10, args.steps))
         print(json.dumps({"metric": "engine attention step, host in/out", "value": es["us_per_call"],
@@ -687,21 +720,7 @@ def main():
 
     secondary = {}
     if not args.quick:
-        cases = [
-            ("cfg2_varlen_b64_ctxU512_8192", dict(n_seq=64, n_rows=1, nq=32, nkv=8, hd=64,
-                                                  ctx=rng.integers(512, 8193, size=64))),
-            ("cfg3_verify_b16_rows8_ctx4096", dict(n_seq=16, n_rows=8, nq=32, nkv=8, hd=64,
-                                                   ctx=[4096] * 16, copies=4)),
-            ("cfg5_lfm3_swa_b32_cap256_pos1000", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
-                                                      ctx=[1001] * 32, window=256, cap=256,
-                                                      gate=True, copies=36)),
-            ("cfg5_lfm3_full_b32_ctx32768", dict(n_seq=32, n_rows=1, nq=16, nkv=4, hd=128,
-                                                 ctx=[32768] * 32, gate=True)),
-            # 2 MB per call: 160 rotated copies (320 MB) keep it out of the 256 MB
-            # MALL; the row is latency-bound, so us_per_step is its figure
-            ("cfg1_decode_b1_16q8kv_ctx1024", dict(n_seq=1, n_rows=1, nq=16, nkv=8, hd=64,
-                                                   ctx=[1024], copies=160)),
-        ]
+        cases = decode_cases(rng)
         for name, kw in cases:
             wl = DecodeWorkload(la, rng, name, **kw)
             sms = time_steps(hip, wl, args.steps, args.warmup)

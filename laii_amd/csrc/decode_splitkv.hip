@@ -48,6 +48,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e     = 1.4426950408889634f;
 constexpr float kNegBig    = -1e30f; /* running-max sentinel (finite)          */
+constexpr float kLazyMax   = 8.0f;   /* running max raised only past m + 8 (log2 units) */
 constexpr int kVtStride    = 36;     /* halfs per d-row of the LDS V^T tile    */
 
 struct SplitParams {
@@ -85,6 +86,17 @@ __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_ca
  * loop wait for the next sub-tile's loads as well. */
 typedef const __attribute__((address_space(1))) uint16_t *gu16_ptr;
 typedef const __attribute__((address_space(1))) u32x4_t *gu32x4_ptr;
+typedef const __attribute__((address_space(1))) uint8_t *gu8_ptr;
+
+/* A pointer every lane holds the same value of, moved to scalar registers so
+ * that loads from it plus a per-lane 32-bit offset use the SGPR-base
+ * addressing form (no 64-bit address arithmetic per load). */
+__device__ __forceinline__ gu8_ptr uniform_ptr(gu8_ptr p) {
+    const uint64_t a  = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    return (gu8_ptr)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
 /* STREAM: non-temporal loads (the "nt" cache policy), for cache rows read
  * once.  Measured on MI355X with rotated copies larger than the 256 MB MALL:
  * single-row decode kernels (one 16-column tile) run faster with them --
@@ -262,6 +274,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     constexpr int NVL = HD / 16; /* 16-byte V pieces per lane per 32-key sub-tile  */
     constexpr int CH  = HD / 8;  /* 16-byte chunks per V row                       */
     constexpr int QPP = 64 / CH; /* 4-key quads covered by one pass of 64 lanes    */
+    constexpr bool PSPLIT = NT == 1; /* P split hi + lo (one 16-column tile)       */
     const int lane = threadIdx.x & 63;
     const int l16  = lane & 15;
     const int g    = lane >> 4;
@@ -286,9 +299,27 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     kc += (size_t)kvh * HD;
     vc += (size_t)kvh * HD;
 
-    /* ---- sub-tile loader ------------------------------------------------------ */
-    auto load_tile = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL]) {
+    /* ---- sub-tile loader ------------------------------------------------------
+     * A sub-tile whose 32 slots are contiguous and inside [kb, ke) (every one
+     * but a segment's last, or one that wraps the ring) loads from a
+     * wave-uniform base pointer plus per-lane 32-bit byte offsets fixed for
+     * the segment, so no per-load address arithmetic runs on the VALU; the
+     * others clamp and wrap per lane. */
+    uint32_t koffb[2], voffb[NVL]; /* set after the first sub-tile's loads are issued */
+    auto load_tile = [&](uint32_t p0, u32x4_t (&kd)[2][NS], u32x4_t (&vd)[NVL], bool may_fast) {
         const uint32_t base = P.window ? (p0 % P.cap) : p0;
+        if (may_fast && p0 + 32u <= ke && (!P.window || base + 32u <= P.cap)) {
+            gu8_ptr k0 = uniform_ptr((gu8_ptr)(kc + (size_t)base * row));
+            gu8_ptr v0 = uniform_ptr((gu8_ptr)(vc + (size_t)base * row));
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int st = 0; st < NS; ++st)
+                    kd[kt][st] = load16<NT == 1>((gu16_ptr)(k0 + koffb[kt] + 64u * st));
+#pragma unroll
+            for (int j = 0; j < NVL; ++j) vd[j] = load16<NT == 1>((gu16_ptr)(v0 + voffb[j]));
+            return;
+        }
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
             uint32_t off = (uint32_t)(16 * kt + l16);
@@ -317,7 +348,15 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     /* the first sub-tile is in flight while the query fragments are built */
     const uint32_t nsub = (ke - kb + 31u) / 32u;
     u32x4_t kA[2][NS], vA[NVL], kB[2][NS], vB[NVL];
-    load_tile(kb, kA, vA);
+    load_tile(kb, kA, vA, false);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) koffb[kt] = (uint32_t)(((16 * kt + l16) * row + 8 * g) * sizeof(uint16_t));
+#pragma unroll
+    for (int ps = 0; ps < HD / 64; ++ps)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            voffb[ps * 4 + i] =
+                (uint32_t)(((4 * (ps * QPP + lane / CH) + i) * row + 8 * (lane % CH)) * sizeof(uint16_t));
 
     /* ---- per-column row bounds and Q fragments ------------------------------ */
     uint32_t col_lo[NT], col_hi[NT];
@@ -506,8 +545,13 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                     }
         }
 
-        /* online softmax; P^T fragments (hi, lo).  O is rescaled only when
-         * some column's running max rose (alpha == 1 exactly otherwise) */
+        /* online softmax; P^T fragments.  Lazy running max: m is raised only
+         * when a sub-tile's column max exceeds it by more than kLazyMax (so
+         * p <= 2^kLazyMax), and O is rescaled only then; the first sub-tile
+         * with an unmasked key sets m (from the kNegBig sentinel).  With one
+         * 16-column tile P is split hi + lo like Q (the MFMAs are free in
+         * this HBM-bound kernel); with more, P enters as one fp16 value
+         * (relative rounding 2^-11 per weight). */
         half8_t ph[NT], pl[NT];
         float alpha_nt[NT];
         bool rose = false;
@@ -517,9 +561,10 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                              fmaxf(fmaxf(sacc[1][nt][0], sacc[1][nt][1]), fmaxf(sacc[1][nt][2], sacc[1][nt][3])));
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float mnew  = fmaxf(mrun[nt], mx);
-            const float alpha = __builtin_amdgcn_exp2f(mrun[nt] - mnew);
-            rose             |= mnew > mrun[nt];
+            const bool raise  = mx > mrun[nt] + kLazyMax;
+            const float mnew  = raise ? mx : mrun[nt];
+            const float alpha = raise ? __builtin_amdgcn_exp2f(mrun[nt] - mnew) : 1.0f;
+            rose             |= raise;
             alpha_nt[nt]      = alpha;
             mrun[nt]          = mnew;
             float psum        = 0.0f;
@@ -531,7 +576,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                     psum              += p;
                     const _Float16 hi  = (_Float16)p;
                     ph[nt][4 * kt + i] = hi;
-                    pl[nt][4 * kt + i] = (_Float16)(p - (float)hi);
+                    if constexpr (PSPLIT) pl[nt][4 * kt + i] = (_Float16)(p - (float)hi);
                 }
             lrun[nt] = lrun[nt] * alpha + psum;
         }
@@ -555,7 +600,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 oacc[mt][nt] = mfma(av, ph[nt], oacc[mt][nt]);
-                oacc[mt][nt] = mfma(av, pl[nt], oacc[mt][nt]);
+                if constexpr (PSPLIT) oacc[mt][nt] = mfma(av, pl[nt], oacc[mt][nt]);
             }
         }
     };
@@ -577,15 +622,15 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     uint32_t it = 0;
     for (; it + 2u < nsub; it += 2u) {
         const uint32_t p0 = kb + 32u * it;
-        load_tile(p0 + 32u, kB, vB);
+        load_tile(p0 + 32u, kB, vB, true);
         consume(p0, kA, vA);
-        load_tile(p0 + 64u, kA, vA);
+        load_tile(p0 + 64u, kA, vA, true);
         consume(p0 + 32u, kB, vB);
     }
     {
         const uint32_t p0 = kb + 32u * it;
         if (it + 1u < nsub) {
-            load_tile(p0 + 32u, kB, vB);
+            load_tile(p0 + 32u, kB, vB, true);
             consume(p0, kA, vA);
             consume(p0 + 32u, kB, vB);
         } else {

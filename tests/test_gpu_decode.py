@@ -248,6 +248,14 @@ def test_repeated_calls_shared_workspace(gpu, orc):
         parity(got, want, what=f"repeat {i}")
 
 
+def plan_tol(n_rows, nq, nkv):
+    """Agreement expected between two plans of the same batch: fp32 rounding
+    with one 16-column tile (P enters P.V split hi + lo, ~exact); with more
+    query columns P enters as one fp16 value, and plans that cut the keys at
+    other points (so with other running maxima) round it differently."""
+    return 1e-5 if n_rows * (nq // nkv) <= 16 else 2e-4
+
+
 @pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq", [(64, 32, 8, 1, 130), (128, 16, 4, 1, 9),
                                                     (64, 32, 8, 8, 5), (64, 16, 8, 1, 1)])
 def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
@@ -273,7 +281,7 @@ def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
         parity(got, want, what=f"{env}")
         outs.append(got)
     for o in outs[1:]:
-        assert np.abs(outs[0] - o).max() < 1e-5
+        assert np.abs(outs[0] - o).max() < plan_tol(n_rows, nq, nkv)
 
 
 @pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq,max_ctx,win,cap,gate,default", [
@@ -306,4 +314,4 @@ def test_workgroup_merge_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq, max_ctx, win
         parity(got, want, what=f"{env}")
         assert plan == (default if not env else env["LFM_ATTN_PLAN"]), f"{env}: plan {plan}"
         outs.append(got)
-    assert np.abs(outs[1] - outs[2]).max() < 1e-5
+    assert np.abs(outs[1] - outs[2]).max() < plan_tol(n_rows, nq, nkv)
