@@ -1239,10 +1239,14 @@ bool use_grid_plan(const AttnBatch &b) {
 }
 
 /* One workgroup per (sequence, KV head), the key splits as its waves and the
- * merge inside it (k_splitkv_wg): taken by grid-plan batches of at most a
- * quarter as many pairs as compute units whose planned splits fit the
- * workgroup's waves (short contexts), where a second (merge) launch would
- * cost about as much as the attention itself.  LFM_ATTN_PLAN=grid keeps such a
+ * merge inside it (k_splitkv_wg): taken by grid-plan batches of at most as
+ * many pairs as compute units whose planned splits fit the workgroup's waves
+ * (short contexts, sliding windows), where a second (merge) launch would
+ * cost about as much as the attention itself.  Measured on MI355X (us per
+ * call, grid + merge kernel -> this form): SWA window 256, d128 16q/4kv, B16
+ * 11.2 -> 10.8, B32 12.3 -> 11.2, B64 15.2 -> 12.5; d64 32q/8kv, B32 11.3 ->
+ * 8.5; with more planned splits than waves (window 512: 8 splits, 4 waves)
+ * the grid stays faster (15.6 vs 17.4).  LFM_ATTN_PLAN=grid keeps such a
  * batch on the two-kernel grid, =wg forces this form. */
 bool use_wg_plan(const SplitParams &p, uint32_t n_seq, uint32_t ww) {
     const char *env = getenv("LFM_ATTN_PLAN");
@@ -1252,7 +1256,7 @@ bool use_wg_plan(const SplitParams &p, uint32_t n_seq, uint32_t ww) {
     /* only when the planned splits fit the workgroup's waves as they are:
      * lengthening them measured slower than the second launch (B1 ctx 1024,
      * 16 splits on 8 waves: 10.3 vs 8.5 us) */
-    return p.n_splits >= 2u && p.n_splits <= ww && (uint64_t)n_seq * p.n_head_kv * 4u <= device_cus();
+    return p.n_splits >= 2u && p.n_splits <= ww && (uint64_t)n_seq * p.n_head_kv <= device_cus();
 }
 
 template <int HD, int NT>
