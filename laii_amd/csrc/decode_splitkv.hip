@@ -1181,10 +1181,20 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
      * columns: keep >= 12 tiles per workgroup per 32 columns (measured on
      * MI355X for 8 rows x 4 heads), and >= 2 tiles */
     c.min_tiles = (12u * p.ncols + 31u) / 32u;
-    if (c.min_tiles < 2u) c.min_tiles = 2u;
     /* keys_hint bounds the keys a row attends */
     uint32_t keys = keys_hint;
     if (!p.pos0_dev) keys = p.pos0_host + p.n_rows - lfm_plan_row(p.pos0_host, p.window, p.cap).t_start;
+    /* ...but a batch too small for that many workgroups per tile share
+     * takes shorter shares, down to about two thirds of the resident
+     * workgroups (a full residency round measured no faster, and any
+     * workgroup past it doubles the time): verify 8 rows x 4 heads at B8 x
+     * 4104 keys 31.9 -> 24.6 us (86 -> 172 workgroups); B16, B32 unchanged */
+    const uint64_t t_max = (uint64_t)c.n_seq * c.n_groups * ((keys + 31u) / 32u + 1u);
+    const uint64_t fill  = t_max * 3u / (2u * (uint64_t)(c.n_res ? c.n_res : 1u));
+    if (fill < c.min_tiles) c.min_tiles = (uint32_t)fill;
+    if (c.min_tiles < 2u) c.min_tiles = 2u;
+    if (const char *env = getenv("LFM_ATTN_MINTILES")) /* tuning */
+        if (atoi(env) > 0) c.min_tiles = (uint32_t)atoi(env);
     if (const char *env = getenv("LFM_ATTN_CHUNK")) {
         /* about c keys per workgroup (tests, tuning): enough workgroups for
          * the longest sequences keys_hint allows; longer ones get more keys */
