@@ -642,7 +642,7 @@ def run_prefill_lfm3(hip, la, rng, steps, window):
     row = dict(workload=f"lfm3_{kind}_prefill_b4_n4096_16q4kv_d128_gate", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
                kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4), flops=pf.flops,
                pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1),
-               kernel="k_prefill128")
+               kernel="k_prefill_ext<128>")
     log(f"lfm3 {kind} prefill: {pms:.3f} ms/step, {row['TFLOPs']} TFLOP/s")
     del pf
     return row

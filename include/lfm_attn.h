@@ -346,7 +346,8 @@ int lfm_hip_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, fl
  * prompt plus the prompt's rows (a ring of window + 8 slots cannot hold a
  * whole prompt).  kv_pos0 must not exceed t_start(pos_0)
  * (LFM_ATTN_E_INVALID).  q, out as for lfm_hip_prefill_f16.  head_dim 128
- * with n_head_q / n_head_kv dividing 128, else LFM_ATTN_E_UNSUPPORTED. */
+ * (LFM3) or 64, with n_head_q / n_head_kv dividing 128, else
+ * LFM_ATTN_E_UNSUPPORTED. */
 int lfm_hip_lfm3_prefill_f16(const float *q, const uint16_t *k, const uint16_t *v, const float *gate,
                              int gate_is_logit, float *out, uint32_t n_seq, uint32_t n_tok, uint32_t pos_0,
                              uint32_t kv_pos0, uint64_t kv_seq_stride, uint32_t window_len, uint32_t n_head_q,

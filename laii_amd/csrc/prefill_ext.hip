@@ -58,14 +58,10 @@ typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int HD       = 128;
 constexpr int KB       = 32;            /* keys per block (one compute step)       */
 constexpr int NBUF     = 3;             /* LDS ring of blocks                      */
 constexpr int HALFB    = KB * 128;      /* bytes of one 64-dim half of a block     */
-constexpr int BLKB     = 4 * HALFB;     /* K half 0, K half 1, V half 0, V half 1  */
 constexpr int NT       = 2;             /* 16-column tiles per wave                */
-constexpr int NS       = HD / 32;       /* k-steps of Q.K^T                        */
-constexpr int NM       = HD / 16;       /* 16-dim tiles of O^T                     */
 constexpr float kLazy  = 8.0f;          /* headroom in log2 units (P <= 2^8)        */
 
 struct PrefillExtParams {
@@ -100,7 +96,14 @@ __device__ __forceinline__ half4_t lds_read_tr(const uint8_t *p) {
 
 __device__ __forceinline__ float max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 
-__global__ __launch_bounds__(256, 2) void k_prefill128(const PrefillExtParams P) {
+/* HD 128 (LFM3 layers) or 64: blocks of NH = HD / 64 halves for K, then V */
+template <int HD>
+__global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const PrefillExtParams P) {
+    constexpr int NH   = HD / 64;            /* 64-dim halves per row              */
+    constexpr int BLKB = 2 * NH * HALFB;     /* K halves, then V halves            */
+    constexpr int NS   = HD / 32;            /* k-steps of Q.K^T                   */
+    constexpr int NM   = HD / 16;            /* 16-dim tiles of O^T                */
+    constexpr int CPR  = HD / 8;             /* 16-byte chunks per row             */
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NBUF * BLKB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -160,34 +163,35 @@ __global__ __launch_bounds__(256, 2) void k_prefill128(const PrefillExtParams P)
     const uint32_t u1     = max(u0, min(b_hi, b_diag));
     auto block_masked = [&](uint32_t b) { return b < u0 || b >= u1; };
 
-    /* ---- staging: thread tid moves 16-B chunks tid and tid + 256 of the K
-     * block and of the V block; chunk p is row p / 16, global chunk p % 16
-     * of that row, stored in half (p % 16) / 8 at slot ((p % 8) ^ swz(row)) */
-    uint32_t st_row[2], st_dst[2], st_col[2];
+    /* ---- staging: thread tid moves 16-B chunks tid + 256 e (e < NH) of the
+     * K block and of the V block; chunk p is row p / CPR, global chunk
+     * c = p % CPR of that row, stored in half c / 8 at slot
+     * ((c % 8) ^ swz(row)) */
+    uint32_t st_row[NH], st_dst[NH], st_col[NH];
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const uint32_t p = (uint32_t)tid + 256u * e, r = p >> 4, c = p & 15u;
+    for (int e = 0; e < NH; ++e) {
+        const uint32_t p = (uint32_t)tid + 256u * e, r = p / CPR, c = p % CPR;
         st_row[e] = r;
         st_col[e] = 8u * c; /* halfs within the head's row */
         st_dst[e] = (c >> 3) * HALFB + r * 128u + 16u * ((c & 7u) ^ (2u * ((r >> 2) & 3u)));
     }
-    u32x4_t stage[4];
+    u32x4_t stage[2 * NH];
     auto load_regs = [&](uint32_t b) {
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
+        for (int e = 0; e < NH; ++e) {
             uint32_t r = b * KB + st_row[e];
             r = r < r_hi ? r : r_hi - 1u; /* rows past the keys: masked */
             const size_t off = (size_t)r * row + st_col[e];
-            stage[e]     = *reinterpret_cast<const u32x4_t *>(kc + off);
-            stage[2 + e] = *reinterpret_cast<const u32x4_t *>(vc + off);
+            stage[e]      = *reinterpret_cast<const u32x4_t *>(kc + off);
+            stage[NH + e] = *reinterpret_cast<const u32x4_t *>(vc + off);
         }
     };
     auto store_regs = [&](uint32_t b) {
         uint8_t *dst = ring + (b % NBUF) * BLKB;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            *reinterpret_cast<u32x4_t *>(dst + st_dst[e])             = stage[e];
-            *reinterpret_cast<u32x4_t *>(dst + 2 * HALFB + st_dst[e]) = stage[2 + e];
+        for (int e = 0; e < NH; ++e) {
+            *reinterpret_cast<u32x4_t *>(dst + st_dst[e])                  = stage[e];
+            *reinterpret_cast<u32x4_t *>(dst + NH * HALFB + st_dst[e]) = stage[NH + e];
         }
     };
 
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill128(const PrefillExtParams P)
         for (int mt = 0; mt < 2; ++mt) {
             half8_t kf[NS];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
+            for (int h = 0; h < NH; ++h) {
                 kf[2 * h]     = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff0));
                 kf[2 * h + 1] = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff1));
             }
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill128(const PrefillExtParams P)
             w[3] = __builtin_bit_cast(uint32_t, h3);
             pf[nt] = w;
         }
-        const uint8_t *vb = ring + (b % NBUF) * BLKB + 2 * HALFB;
+        const uint8_t *vb = ring + (b % NBUF) * BLKB + NH * HALFB;
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) {
             const uint8_t *vh = vb + (mt >> 2) * HALFB;
@@ -378,7 +382,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill128(const PrefillExtParams P)
 } // namespace
 
 bool prefill_ext_supports(uint32_t head_dim, uint32_t kv_mul) {
-    return head_dim == 128u && kv_mul >= 1u && kv_mul <= 32u && (128u % kv_mul) == 0u;
+    return (head_dim == 128u || head_dim == 64u) && kv_mul >= 1u && kv_mul <= 32u && (128u % kv_mul) == 0u;
 }
 
 int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, const float *gate, int gate_is_logit,
@@ -407,10 +411,12 @@ int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, con
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL(k_prefill128, dim3(P.n_qtiles * n_head_kv * n_seq), dim3(256), 0, stream, P);
+    if (head_dim == 128u)
+        hipLaunchKernelGGL(k_prefill_ext<128>, dim3(P.n_qtiles * n_head_kv * n_seq), dim3(256), 0, stream, P);
+    else
+        hipLaunchKernelGGL(k_prefill_ext<64>, dim3(P.n_qtiles * n_head_kv * n_seq), dim3(256), 0, stream, P);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
-    (void)head_dim;
     return hip_status(e);
 }
 

@@ -121,11 +121,11 @@ def test_rejections_before_launch():
                                     260, 0.088, None, None, 1e-5, FAKE, FAKE, None) == E_INVALID
     # LFM3 prefill: K/V buffer starting after the first row's window start
     # (row 0 at 1000 with window 256 needs position 745), with no window a
-    # buffer not starting at 0, head_dim 64, heads not grouped evenly
+    # buffer not starting at 0, head_dim 96, heads not grouped evenly
     f = lib.lfm_hip_lfm3_prefill_f16
     assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 1, 64, 1000, 746, 0, 256, 16, 4, 128, 0.088, None) == E_INVALID
     assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 1, 64, 1000, 1, 0, 0, 16, 4, 128, 0.088, None) == E_INVALID
-    assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 1, 64, 1000, 745, 0, 256, 32, 8, 64, 0.125, None) == E_UNSUPPORTED
+    assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 1, 64, 1000, 745, 0, 256, 32, 8, 96, 0.102, None) == E_UNSUPPORTED
     assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 1, 64, 0, 0, 0, 0, 12, 8, 128, 0.088, None) == E_INVALID
     # sequences whose buffers would overlap (stride below the rows x kv_dim)
     assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 2, 64, 0, 0, 64 * 512 - 8, 0, 16, 4, 128, 0.088, None) == E_INVALID

@@ -25,8 +25,9 @@ def sigmoid(g):
     return (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
 
 
-def run(la, rng, n_seq, n_tok, pos_0, nq, nkv, window=0, kv_pos0=0, gate=True, q=None, k16=None, v16=None):
+def run(la, rng, n_seq, n_tok, pos_0, nq, nkv, window=0, kv_pos0=0, gate=True, q=None, k16=None, v16=None, hd=HD):
     """fp32 Q rows, fp16 K/V buffers whose row r is position kv_pos0 + r."""
+    HD = hd
     rows = pos_0 + n_tok - kv_pos0
     if q is None:
         q = rng.standard_normal((n_seq, n_tok, nq, HD), dtype=np.float32) * np.float32(0.5)
@@ -44,7 +45,7 @@ def run(la, rng, n_seq, n_tok, pos_0, nq, nkv, window=0, kv_pos0=0, gate=True, q
 def oracle(orc, q, k16, v16, g, s, pos_0, kv_pos0, window, nq, nkv, rows=None):
     """The oracle on a cache of absolute positions: rows below kv_pos0 hold
     fp16 NaN, so reading one would poison the result."""
-    n_tok = q.shape[1]
+    n_tok, HD = q.shape[1], q.shape[-1]
     cap = max(pos_0 + n_tok, window)
     kf = np.full((cap, nkv, HD), 0x7E00, np.uint16)
     vf = np.full((cap, nkv, HD), 0x7E00, np.uint16)
@@ -153,3 +154,16 @@ def test_prefill128_lazy_max(gpu, orc, pattern):
     _, _, _, g, got = run(la, rng, 1, n_tok, 0, nq, nkv, window=window, q=q, k16=k16, v16=v16)
     want = oracle(orc, q, k16, v16, g, 0, 0, 0, window, nq, nkv)
     parity(got[0], want, what=f"prefill128 lazy max {pattern}")
+
+
+@pytest.mark.parametrize("n_tok,pos_0,window,kv_pos0,gate", [(300, 0, 0, 0, True), (250, 40, 33, 8, True),
+                                                             (200, 700, 0, 0, False)])
+def test_prefill_ext_head_dim_64(gpu, orc, n_tok, pos_0, window, kv_pos0, gate):
+    """The same entry point at head_dim 64 (32q/8kv): windows and the gate
+    for head_dim-64 layers (the LFM2 prompt path, lfm_hip_prefill_f16, has
+    neither and keeps its 64-column kernel)."""
+    rng = np.random.default_rng(n_tok + window + 64)
+    q, k16, v16, g, got = run(gpu, rng, 2, n_tok, pos_0, 32, 8, window=window, kv_pos0=kv_pos0, gate=gate, hd=64)
+    for s in range(2):
+        want = oracle(orc, q, k16, v16, g, s, pos_0, kv_pos0, window, 32, 8)
+        parity(got[s], want, what=f"prefill ext d64 window={window} s={s} n={n_tok} pos0={pos_0}")
