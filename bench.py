@@ -621,28 +621,37 @@ def decode_cases(rng):
     ]
 
 
-def run_prefill(hip, la, rng, steps):
+def prefill_counts(steps, warmup):
+    """Timed launches and warm-up launches of a prefill row.  One config-4
+    launch is ~0.3 ms; on MI355X the shader clock takes about 60 launches
+    (~20 ms) of this load to settle (the first 10 ran 20 % slower than the
+    60th), so a prefill row warms up for at least 60 launches."""
+    return max(10, steps // 2), max(60, warmup // 2)
+
+
+def run_prefill(hip, la, rng, steps, warmup):
     pf = PrefillWorkload(la, rng)
-    n = max(5, steps // 5)
-    pms = time_steps(hip, pf, n, 3)
+    n, w = prefill_counts(steps, warmup)
+    pms = time_steps(hip, pf, n, w)
     pkms = time_main_kernel(hip, la, pf, n)
     prefill = dict(workload="cfg4_prefill_b4_n4096_32q8kv_d64", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
                    kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4),
-                   flops=pf.flops, pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1))
+                   flops=pf.flops, pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1),
+                   launches=n, warmup_launches=w)
     log(f"prefill: {pms:.3f} ms/step, {prefill['TFLOPs']} TFLOP/s")
     return prefill
 
 
-def run_prefill_lfm3(hip, la, rng, steps, window):
+def run_prefill_lfm3(hip, la, rng, steps, warmup, window):
     pf = Lfm3PrefillWorkload(la, rng, window=window)
-    n = max(5, steps // 5)
-    pms = time_steps(hip, pf, n, 3)
+    n, w = prefill_counts(steps, warmup)
+    pms = time_steps(hip, pf, n, w)
     pkms = time_main_kernel(hip, la, pf, n)
     kind = f"swa{window}" if window else "full"
     row = dict(workload=f"lfm3_{kind}_prefill_b4_n4096_16q4kv_d128_gate", TFLOPs=round(pf.flops / (pms * 1e-3) / 1e12, 1),
                kernel_TFLOPs=round(pf.flops / (pkms * 1e-3) / 1e12, 1), ms_per_step=round(pms, 4), flops=pf.flops,
                pct_fp16_mfma_peak=round(100 * pf.flops / (pms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFS, 1),
-               kernel="k_prefill_ext<128>")
+               kernel="k_prefill_ext<128>", launches=n, warmup_launches=w)
     log(f"lfm3 {kind} prefill: {pms:.3f} ms/step, {row['TFLOPs']} TFLOP/s")
     del pf
     return row
@@ -696,15 +705,15 @@ def main():
                           "unit": "us", "n_gpus": 1, "higher_is_better": False, "engine_step": es}), flush=True)
         return
     if args.prefill128_only:
-        rows = [run_prefill_lfm3(hip, la, rng, args.steps, w) for w in (0, 256)]
+        rows = [run_prefill_lfm3(hip, la, rng, args.steps, args.warmup, w) for w in (0, 256)]
         print(json.dumps({"metric": "LFM3 prefill attn TFLOP/s, B4 x 4096, 16q/4kv d128", "value": rows[0]["TFLOPs"],
-                          "unit": "TFLOP/s", "n_gpus": 1, "steps": max(5, args.steps // 5),
+                          "unit": "TFLOP/s", "n_gpus": 1, "steps": prefill_counts(args.steps, args.warmup)[0],
                           "higher_is_better": True, "prefill_lfm3": rows}), flush=True)
         return
     if args.prefill_only:
-        prefill = run_prefill(hip, la, rng, args.steps)
+        prefill = run_prefill(hip, la, rng, args.steps, args.warmup)
         print(json.dumps({"metric": "prefill attn TFLOP/s, config 4", "value": prefill["TFLOPs"],
-                          "unit": "TFLOP/s", "n_gpus": 1, "steps": max(5, args.steps // 5),
+                          "unit": "TFLOP/s", "n_gpus": 1, "steps": prefill_counts(args.steps, args.warmup)[0],
                           "higher_is_better": True, "prefill": prefill}), flush=True)
         return
 
@@ -750,9 +759,9 @@ def main():
         secondary["engine_step_cfg1_host_in_out"] = es
         log(f"engine step (host in/out): {es['us_per_call']} us per call")
 
-    prefill = run_prefill(hip, la, rng, args.steps)
+    prefill = run_prefill(hip, la, rng, args.steps, args.warmup)
     for w in (0, 256):
-        row = run_prefill_lfm3(hip, la, rng, args.steps, w)
+        row = run_prefill_lfm3(hip, la, rng, args.steps, args.warmup, w)
         secondary[row["workload"]] = row
 
     if not args.quick:

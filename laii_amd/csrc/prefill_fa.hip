@@ -11,9 +11,9 @@
  * head (256 query columns, TQ = 256 / kv_mul), so each K/V block staged in
  * LDS serves every query head that reads it.
  *
- * Staging: 64-key K and V blocks (row-major, 128-B rows) go through 16
- * registers per thread into a ring of 3 LDS blocks: block b + 2 is fetched
- * while block b is computed and stored at the next block boundary.  The 16-B
+ * Staging: 64-key K and V blocks (row-major, 128-B rows) move from global
+ * memory straight into a ring of 3 LDS blocks (global_load_lds_dwordx4, no
+ * registers): block b + 2 is in flight while block b is computed.  The 16-B
  * chunks of row r are XOR-swizzled by 2*((r >> 2) & 3), which makes both the
  * K fragment reads (ds_read_b128) and the transposing V reads
  * (ds_read_b64_tr_b16) bank-conflict free.
@@ -98,6 +98,14 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
     return fmaxf(fmaxf(a, b), c);
 }
 
+/* 16 B per lane from global memory into LDS: lane l writes bytes
+ * [lds + 16 l, lds + 16 l + 16) of the wave's 1-KB piece at LDS address lds
+ * (held in M0).  The load counts in vmcnt like any other vector load; the
+ * caller waits for it explicitly before the barrier that publishes it. */
+__device__ __forceinline__ void fetch16_lds(const void *gaddr, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds) : "memory");
+}
+
 template <int HD>
 __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     static_assert(HD == 64, "prefill kernel is specialised for head_dim 64");
@@ -149,7 +157,13 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
         }
     }
     /* one fp16 rounding of q * scale * log2(e): the score accumulator holds
-     * q.k in log2 units, so the exponentials need no multiply */
+     * q.k in log2 units, so the exponentials need no multiply.  The
+     * conversion is pinned before the first block fetch: the wait for the Q
+     * loads would otherwise sit after the fetch and wait for it too. */
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int st = 0; st < HD / 32; ++st) asm volatile("" ::"v"(qf[nt][st]));
     const uint32_t lo_pos = P.pos_0 + t0;                               /* smallest query position */
     const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;     /* largest query position  */
     const uint32_t n_keys = hi_pos + 1u;
@@ -158,34 +172,41 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     /* steps [0, nfull) lie entirely at or below the lowest query row */
     const uint32_t nfull  = min((lo_pos + 1u) / SB, nsub);
 
-    /* ---- staging through registers: thread tid moves 16-B chunks tid and
-     * tid + 256 of each 8-KB K and V block; chunk p sits at byte 16*p of the
-     * block (row p/8, slot p%8) and holds the row's global chunk
-     * (p%8) ^ swz(row) */
-    uint32_t st_row[2], st_col[2];
+    /* ---- staging: thread tid moves 16-B chunks tid and tid + 256 of each
+     * 8-KB K and V block; chunk p sits at byte 16*p of the block (row p/8,
+     * slot p%8) and holds the row's global chunk (p%8) ^ swz(row).  Wave w's
+     * chunks form the 1-KB pieces w and w + 4 of the block. */
+    uint32_t st_row[2], st_col[2], st_off[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
         const uint32_t p = (uint32_t)tid + 256u * e, r = p >> 3;
         st_row[e] = r;
-        st_col[e] = 8u * ((p & 7u) ^ (2u * ((r >> 2) & 3u))); /* halfs */
+        st_col[e] = 8u * ((p & 7u) ^ (2u * ((r >> 2) & 3u)));         /* halfs */
+        st_off[e] = (r * (uint32_t)row + st_col[e]) * sizeof(uint16_t); /* bytes */
     }
-    u32x4_t stage[4];
-    auto load_regs = [&](uint32_t blk) {
+    const uint32_t wv       = __builtin_amdgcn_readfirstlane((uint32_t)wave);
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring; /* LDS address of the ring */
+    const size_t blk_bytes  = (size_t)KB * row * sizeof(uint16_t);
+    /* 4 fetches per wave and block (vmcnt counts them) */
+    auto fetch_block = [&](uint32_t blk) {
+        const uint32_t slot = ring_lds + (blk % NBUF) * (2 * BLKB);
+        const bool full     = (blk + 1u) * KB <= n_keys;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            uint32_t key = blk * KB + st_row[e];
-            key = key < n_keys ? key : n_keys - 1u; /* rows past the keys: masked */
-            const size_t off = (size_t)key * row + st_col[e];
-            stage[e]     = *reinterpret_cast<const u32x4_t *>(kc + off);
-            stage[2 + e] = *reinterpret_cast<const u32x4_t *>(vc + off);
-        }
-    };
-    auto store_regs = [&](uint32_t blk) {
-        uint8_t *dst = ring + (blk % NBUF) * (2 * BLKB) + 16 * tid;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            *reinterpret_cast<u32x4_t *>(dst + 4096 * e)        = stage[e];
-            *reinterpret_cast<u32x4_t *>(dst + BLKB + 4096 * e) = stage[2 + e];
+            const uint8_t *kp, *vp;
+            if (full) {
+                kp = reinterpret_cast<const uint8_t *>(kc) + blk * blk_bytes + st_off[e];
+                vp = reinterpret_cast<const uint8_t *>(vc) + blk * blk_bytes + st_off[e];
+            } else {
+                uint32_t key = blk * KB + st_row[e];
+                key = key < n_keys ? key : n_keys - 1u; /* rows past the keys: masked */
+                const size_t off = (size_t)key * row + st_col[e];
+                kp = reinterpret_cast<const uint8_t *>(kc + off);
+                vp = reinterpret_cast<const uint8_t *>(vc + off);
+            }
+            const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
+            fetch16_lds(kp, piece);
+            fetch16_lds(vp, piece + (uint32_t)BLKB);
         }
     };
 
@@ -309,20 +330,21 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
         for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
     };
 
-    /* entering LDS block b: block b (stored at the previous entry) becomes
-     * visible to every wave; the slot of block b + 1 is free (its previous
-     * block, b - 2, was last read before this barrier), so block b + 1 moves
-     * from the staging registers into it and block b + 2 is fetched */
+    /* entering LDS block b: this wave's fetches of block b have landed
+     * (those of block b + 1 may still be in flight), and the barrier makes
+     * every wave's part visible.  The slot of block b + 2 held block b - 1,
+     * which every wave finished before the barrier, so block b + 2 is
+     * fetched into it. */
     auto enter_block = [&](uint32_t b) {
+        if (b + 1u < nblk) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (b + 1u < nblk) store_regs(b + 1u);
-        if (b + 2u < nblk) load_regs(b + 2u);
+        if (b + 2u < nblk) fetch_block(b + 2u);
     };
 
     /* ---- steps: P(k) and PV(k), then S^T(k + 1) in the same registers -- */
-    load_regs(0u);
-    store_regs(0u);
-    if (nblk > 1u) load_regs(1u);
+    fetch_block(0u);
+    if (nblk > 1u) fetch_block(1u);
     enter_block(0u);
     float4_t scur[2][NT];
     if (nfull > 0u) scores(std::false_type{}, 0u, scur);
