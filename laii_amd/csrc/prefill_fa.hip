@@ -12,16 +12,17 @@
  * LDS serves every query head that reads it.
  *
  * Staging: 64-key K and V blocks (row-major, 128-B rows) move from global
- * memory straight into a ring of 3 LDS blocks (global_load_lds_dwordx4, no
- * registers): block b + 2 is in flight while block b is computed.  The 16-B
+ * memory straight into a ring of 4 LDS blocks (global_load_lds_dwordx4, no
+ * registers): block b + 2 is in flight while block b is computed and block
+ * b - 1 is still read by the P.V product that trails the scores by a step.  The 16-B
  * chunks of row r are XOR-swizzled by 2*((r >> 2) & 3), which makes both the
  * K fragment reads (ds_read_b128) and the transposing V reads
  * (ds_read_b64_tr_b16) bank-conflict free.
  *
- * Compute runs in 32-key steps.  Step k turns the scores S^T(k) into P, runs
- * PV(k), and then computes S^T(k+1) into the same registers (no copy between
- * pipeline stages); the two waves of each SIMD overlap one wave's
- * exponentials with the other's MFMAs:
+ * Compute runs in 32-key steps.  Step k computes S^T(k+1) into a second
+ * register set, turns the scores S^T(k) into P and runs PV(k): the MFMAs of
+ * S^T(k+1) overlap the exponentials of P(k) within the wave, and the two
+ * waves of each SIMD overlap each other's:
  *   S^T(k+1) = K . Q^T - m   16x16x32 f16 MFMA on Q * scale * log2(e),
  *                            rounded once from fp32 to fp16, so scores come
  *                            out in log2 units; the running max enters as
@@ -59,7 +60,7 @@ typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
 constexpr float kLog2e  = 1.4426950408889634f;
 constexpr int KB        = 64;          /* keys per LDS block                       */
 constexpr int SB        = 32;          /* keys per compute step                    */
-constexpr int NBUF      = 3;           /* LDS ring of K/V blocks                   */
+constexpr int NBUF      = 4;           /* LDS ring of K/V blocks                   */
 constexpr int ROWB      = 128;         /* bytes per K/V row of one head (d = 64)   */
 constexpr int BLKB      = KB * ROWB;   /* bytes per K (or V) block                 */
 constexpr float kLazy   = 8.0f;        /* headroom in log2 units (P <= 2^8)         */
@@ -330,11 +331,12 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
         for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
     };
 
-    /* entering LDS block b: this wave's fetches of block b have landed
-     * (those of block b + 1 may still be in flight), and the barrier makes
-     * every wave's part visible.  The slot of block b + 2 held block b - 1,
-     * which every wave finished before the barrier, so block b + 2 is
-     * fetched into it. */
+    /* entering LDS block b (at the start of step 2b - 1, before S^T(2b)):
+     * this wave's fetches of block b have landed (those of block b + 1 may
+     * still be in flight), and the barrier makes every wave's part visible.
+     * Block b - 1 is still in use (P.V of step 2b - 1); the slot of block
+     * b + 2 held block b - 2, which every wave finished before the barrier,
+     * so block b + 2 is fetched into it. */
     auto enter_block = [&](uint32_t b) {
         if (b + 1u < nblk) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
         else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -355,21 +357,40 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
         rescale(std::true_type{}, any_raise, scur, mx);
     }
 
-    /* S^T(k + 1) is computed after P(k) has consumed S^T(k): measured on
-     * MI355X against computing it first into a second register set (which
-     * then had to be copied back each step, 18 v_mov_b64), 726-747 vs
-     * 710-714 TFLOP/s at B4 x 4096 and 254 -> 222 VGPRs */
-    auto step = [&](auto mask_tag, uint32_t k) {
-        accumulate(k, scur);
+    /* Step k computes S^T(k + 1) into the other register set before P(k), so
+     * its MFMAs overlap the exponentials of P(k) within the wave; the loop
+     * runs two steps per iteration with the sets swapping roles (no register
+     * copies).  Measured on MI355X at B4 x 4096 against computing S^T(k + 1)
+     * after P(k) in the same registers: 127.7 vs 137.3 k cycles per
+     * workgroup, bit-identical (253 VGPRs, no spills). */
+    float4_t snxt[2][NT];
+    auto step = [&](auto mask_tag, uint32_t k, float4_t(&sc)[2][NT], float4_t(&sn)[2][NT])
+                    __attribute__((always_inline)) {
         if (((k + 1u) & 1u) == 0u) enter_block((k + 1u) >> 1);
-        scores(mask_tag, k + 1u, scur);
+        scores(mask_tag, k + 1u, sn);
+        accumulate(k, sc);
         float mx[NT];
-        const bool any_raise = step_max(std::false_type{}, scur, mx);
-        rescale(std::false_type{}, any_raise, scur, mx);
+        const bool any_raise = step_max(std::false_type{}, sn, mx);
+        rescale(std::false_type{}, any_raise, sn, mx);
     };
     uint32_t k = 0;
-    for (; k + 1u < nfull; ++k) step(std::false_type{}, k);
-    for (; k + 1u < nsub; ++k) step(std::true_type{}, k);
+    /* steps k .. k_end - 1; S^T(k) is in scur on entry and on exit */
+    auto run_steps = [&](auto mask_tag, uint32_t k_end) __attribute__((always_inline)) {
+        for (; k + 2u <= k_end; k += 2u) {
+            step(mask_tag, k, scur, snxt);
+            step(mask_tag, k + 1u, snxt, scur);
+        }
+        if (k < k_end) {
+            step(mask_tag, k, scur, snxt);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) scur[mt][nt] = snxt[mt][nt];
+            ++k;
+        }
+    };
+    run_steps(std::false_type{}, nfull > 0u ? nfull - 1u : 0u); /* S^T(k + 1) unmasked */
+    run_steps(std::true_type{}, nsub - 1u);
     accumulate(k, scur);
 
     /* ---- epilogue: O / l ------------------------------------------------- */
