@@ -22,11 +22,13 @@
  * 2 * ((r >> 2) & 3): the layout of the head_dim-64 prefill kernel
  * (prefill_fa.hip), whose K fragment reads (ds_read_b128) and transposing V
  * reads (ds_read_b64_tr_b16) it serves without bank conflicts.  Blocks move
- * global -> registers -> a ring of 3 LDS blocks: block b + 2 is fetched
- * while block b is computed, one barrier per block.
+ * from global memory straight into a ring of 4 LDS blocks
+ * (global_load_lds_dwordx4): block b + 2 is in flight while S^T(b) is
+ * computed and block b - 1 is still read by P.V; one barrier per block.
  *
- * Per 32-key block (software pipelined as in the head_dim-64 kernel: P(k)
- * and PV(k), then S^T(k + 1) into the same registers):
+ * Per 32-key block (software pipelined as in the head_dim-64 kernel: step b
+ * computes S^T(b + 1) into a second register set, then P(b) and PV(b), so
+ * the MFMAs of the scores overlap the exponentials within the wave):
  *   S^T = K . Q^T - m        16x16x32 f16 MFMA on q * scale * log2(e)
  *                            rounded once to fp16 (scores in log2 units);
  *                            the running max is the accumulator's initial
@@ -59,7 +61,7 @@ typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int KB       = 32;            /* keys per block (one compute step)       */
-constexpr int NBUF     = 3;             /* LDS ring of blocks                      */
+constexpr int NBUF     = 4;             /* LDS ring of blocks                      */
 constexpr int HALFB    = KB * 128;      /* bytes of one 64-dim half of a block     */
 constexpr int NT       = 2;             /* 16-column tiles per wave                */
 constexpr float kLazy  = 8.0f;          /* headroom in log2 units (P <= 2^8)        */
@@ -95,6 +97,14 @@ __device__ __forceinline__ half4_t lds_read_tr(const uint8_t *p) {
 }
 
 __device__ __forceinline__ float max3(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
+
+/* 16 B per lane from global memory into LDS: lane l writes bytes
+ * [lds + 16 l, lds + 16 l + 16) of the wave's 1-KB piece at LDS address lds
+ * (held in M0).  The load counts in vmcnt like any other vector load; the
+ * caller waits for it explicitly before the barrier that publishes it. */
+__device__ __forceinline__ void fetch16_lds(const void *gaddr, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds) : "memory");
+}
 
 /* HD 128 (LFM3 layers) or 64: blocks of NH = HD / 64 halves for K, then V */
 template <int HD>
@@ -146,6 +156,12 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
             qf[nt][st] = h;
         }
     }
+    /* the conversion is pinned before the first block fetch: the wait for
+     * the Q loads would otherwise sit after the fetch and wait for it too */
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int st = 0; st < NS; ++st) asm volatile("" ::"v"(qf[nt][st]));
     /* key rows [r_lo, r_hi) of the buffer, in 32-key blocks */
     const uint32_t lo_pos = P.pos_0 + t0;
     const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;
@@ -163,35 +179,32 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
     const uint32_t u1     = max(u0, min(b_hi, b_diag));
     auto block_masked = [&](uint32_t b) { return b < u0 || b >= u1; };
 
-    /* ---- staging: thread tid moves 16-B chunks tid + 256 e (e < NH) of the
-     * K block and of the V block; chunk p is row p / CPR, global chunk
-     * c = p % CPR of that row, stored in half c / 8 at slot
-     * ((c % 8) ^ swz(row)) */
-    uint32_t st_row[NH], st_dst[NH], st_col[NH];
+    /* ---- staging: the K part of a block (NH halves of 4 KB) is NH * 4
+     * pieces of 1 KB; wave w fetches pieces w + 4 e (e < NH) of it and of the
+     * V part.  Lane l's 16 B land at byte u = 1024 (w + 4 e) + 16 l: half
+     * u / HALFB, row r = (u % HALFB) / 128, slot j = (u % 128) / 16, holding
+     * the row's global chunk 8 * half + (j ^ swz(r)) */
+    uint32_t st_row[NH], st_col[NH];
 #pragma unroll
     for (int e = 0; e < NH; ++e) {
-        const uint32_t p = (uint32_t)tid + 256u * e, r = p / CPR, c = p % CPR;
+        const uint32_t u = 1024u * (uint32_t)(wave + 4 * e) + 16u * (uint32_t)lane;
+        const uint32_t r = (u % HALFB) / 128u, j = (u % 128u) / 16u;
         st_row[e] = r;
-        st_col[e] = 8u * c; /* halfs within the head's row */
-        st_dst[e] = (c >> 3) * HALFB + r * 128u + 16u * ((c & 7u) ^ (2u * ((r >> 2) & 3u)));
+        st_col[e] = 8u * (8u * (u / HALFB) + (j ^ (2u * ((r >> 2) & 3u)))); /* halfs within the head's row */
     }
-    u32x4_t stage[2 * NH];
-    auto load_regs = [&](uint32_t b) {
+    const uint32_t wv       = __builtin_amdgcn_readfirstlane((uint32_t)wave);
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring; /* LDS address of the ring */
+    /* 2 NH fetches per wave and block (vmcnt counts them) */
+    auto fetch_block = [&](uint32_t b) {
+        const uint32_t slot = ring_lds + (b % NBUF) * BLKB;
 #pragma unroll
         for (int e = 0; e < NH; ++e) {
             uint32_t r = b * KB + st_row[e];
             r = r < r_hi ? r : r_hi - 1u; /* rows past the keys: masked */
-            const size_t off = (size_t)r * row + st_col[e];
-            stage[e]      = *reinterpret_cast<const u32x4_t *>(kc + off);
-            stage[NH + e] = *reinterpret_cast<const u32x4_t *>(vc + off);
-        }
-    };
-    auto store_regs = [&](uint32_t b) {
-        uint8_t *dst = ring + (b % NBUF) * BLKB;
-#pragma unroll
-        for (int e = 0; e < NH; ++e) {
-            *reinterpret_cast<u32x4_t *>(dst + st_dst[e])                  = stage[e];
-            *reinterpret_cast<u32x4_t *>(dst + NH * HALFB + st_dst[e]) = stage[NH + e];
+            const size_t off     = (size_t)r * row + st_col[e];
+            const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
+            fetch16_lds(kc + off, piece);
+            fetch16_lds(vc + off, piece + (uint32_t)(NH * HALFB));
         }
     };
 
@@ -324,36 +337,61 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
         for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
     };
 
-    /* entering block b: block b (stored at the previous entry) becomes
-     * visible to every wave; the slot of block b + 1 is free (its previous
-     * block, b - 2, was last read before this barrier), so block b + 1 moves
-     * from the staging registers into it and block b + 2 is fetched */
+    /* entering block b (at the start of step b - 1, before S^T(b)): this
+     * wave's fetches of block b have landed (those of block b + 1 may still
+     * be in flight), and the barrier makes every wave's part visible.  Block
+     * b - 1 is still in use (P.V of step b - 1); the slot of block b + 2 held
+     * block b - 2, which every wave finished before the barrier, so block
+     * b + 2 is fetched into it. */
     auto enter_block = [&](uint32_t b) {
+        if (b + 1u < b_hi) {
+            if constexpr (NH == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
         __syncthreads();
-        if (b + 1u < b_hi) store_regs(b + 1u);
-        if (b + 2u < b_hi) load_regs(b + 2u);
+        if (b + 2u < b_hi) fetch_block(b + 2u);
     };
 
-    load_regs(b_lo);
-    store_regs(b_lo);
-    if (b_lo + 1u < b_hi) load_regs(b_lo + 1u);
+    fetch_block(b_lo);
+    if (b_lo + 1u < b_hi) fetch_block(b_lo + 1u);
     enter_block(b_lo);
     float4_t scur[2][NT];
     if (block_masked(b_lo)) scores(std::true_type{}, b_lo, scur);
     else scores(std::false_type{}, b_lo, scur);
     update_max(scur);
-    auto step = [&](auto mask_tag, uint32_t b) {
-        accumulate(b, scur);
+    /* step b: S^T(b + 1) into the other register set, then P(b) and PV(b);
+     * two steps per iteration with the sets swapping roles */
+    float4_t snxt[2][NT];
+    auto step = [&](auto mask_tag, uint32_t b, float4_t(&sc)[2][NT], float4_t(&sn)[2][NT])
+                    __attribute__((always_inline)) {
         enter_block(b + 1u);
-        scores(mask_tag, b + 1u, scur);
-        update_max(scur);
+        scores(mask_tag, b + 1u, sn);
+        accumulate(b, sc);
+        update_max(sn);
+    };
+    uint32_t b = b_lo;
+    /* steps b .. b_end - 1; S^T(b) is in scur on entry and on exit */
+    auto run_steps = [&](auto mask_tag, uint32_t b_end) __attribute__((always_inline)) {
+        for (; b + 2u <= b_end; b += 2u) {
+            step(mask_tag, b, scur, snxt);
+            step(mask_tag, b + 1u, snxt, scur);
+        }
+        if (b < b_end) {
+            step(mask_tag, b, scur, snxt);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) scur[mt][nt] = snxt[mt][nt];
+            ++b;
+        }
     };
     /* blocks [u0, u1) need no mask; masked ones sit below (window edge)
      * and above (diagonal) */
-    uint32_t b = b_lo;
-    for (; b + 1u < u0; ++b) step(std::true_type{}, b);
-    for (; b + 1u < u1; ++b) step(std::false_type{}, b);
-    for (; b + 1u < b_hi; ++b) step(std::true_type{}, b);
+    run_steps(std::true_type{}, u0 > 0u ? u0 - 1u : 0u);
+    run_steps(std::false_type{}, u1 > 0u ? u1 - 1u : 0u);
+    run_steps(std::true_type{}, b_hi - 1u);
     accumulate(b, scur);
 
     /* ---- epilogue: O * gate / l ------------------------------------------ */
