@@ -131,40 +131,6 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     const uint16_t *vc = P.v + (size_t)s * P.kv_seq_stride + (size_t)kvh * HD;
     const size_t row   = (size_t)P.n_head_kv * HD;
 
-    /* ---- columns of this lane: (head j, row t) per N-tile -------------- */
-    uint32_t col_pos[NT]; /* absolute position of the column's query row */
-    bool col_ok[NT];
-    half8_t qf[NT][HD / 32];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t c = (uint32_t)(wave * 64 + nt * 16 + l16);
-        const uint32_t j = c / P.tq, t = t0 + c % P.tq;
-        col_ok[nt]  = t < P.n_tok;
-        col_pos[nt] = P.pos_0 + t;
-        const float *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q +
-                                 kvh * P.kv_mul + j) * HD + 8 * g;
-#pragma unroll
-        for (int st = 0; st < HD / 32; ++st) {
-            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-            if (col_ok[nt]) {
-                a = *reinterpret_cast<const float4 *>(qp + 32 * st);
-                b = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
-            }
-            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            half8_t h;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = (_Float16)(x[e] * P.qmul);
-            qf[nt][st] = h;
-        }
-    }
-    /* one fp16 rounding of q * scale * log2(e): the score accumulator holds
-     * q.k in log2 units, so the exponentials need no multiply.  The
-     * conversion is pinned before the first block fetch: the wait for the Q
-     * loads would otherwise sit after the fetch and wait for it too. */
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int st = 0; st < HD / 32; ++st) asm volatile("" ::"v"(qf[nt][st]));
     const uint32_t lo_pos = P.pos_0 + t0;                               /* smallest query position */
     const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;     /* largest query position  */
     const uint32_t n_keys = hi_pos + 1u;
@@ -210,6 +176,51 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
             fetch16_lds(vp, piece + (uint32_t)BLKB);
         }
     };
+
+    /* the first two blocks are in flight before the Q loads: the wait for Q
+     * (which also covers these older fetches) then takes one memory round
+     * trip, not two */
+    fetch_block(0u);
+    if (nblk > 1u) fetch_block(1u);
+
+    /* ---- columns of this lane: (head j, row t) per N-tile -------------- */
+    uint32_t col_pos[NT]; /* absolute position of the column's query row */
+    bool col_ok[NT];
+    half8_t qf[NT][HD / 32];
+    /* all Q loads are issued before any is used (qp is a valid row for a
+     * padding column too; its values are zeroed after): with a use between
+     * them the compiler waited for each column tile's loads, one memory
+     * round trip per tile */
+    float4 qraw[NT][HD / 32][2];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t c = (uint32_t)(wave * 64 + nt * 16 + l16);
+        const uint32_t j = c / P.tq, t = t0 + c % P.tq;
+        col_ok[nt]  = t < P.n_tok;
+        col_pos[nt] = P.pos_0 + t;
+        const float *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q +
+                                 kvh * P.kv_mul + j) * HD + 8 * g;
+#pragma unroll
+        for (int st = 0; st < HD / 32; ++st) {
+            qraw[nt][st][0] = *reinterpret_cast<const float4 *>(qp + 32 * st);
+            qraw[nt][st][1] = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int st = 0; st < HD / 32; ++st) {
+            const float4 a = qraw[nt][st][0], b = qraw[nt][st][1];
+            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            half8_t h;
+            /* one fp16 rounding of q * scale * log2(e): the score
+             * accumulator holds q.k in log2 units, so the exponentials need
+             * no multiply */
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = col_ok[nt] ? (_Float16)(x[e] * P.qmul) : (_Float16)0.0f;
+            qf[nt][st] = h;
+        }
 
     /* fragment offsets in a block (bytes).  K: row 16*mt + l16, chunk 4*st + g.
      * V (transposing read): lane l16 of group g addresses row 4g + l16/4 of
@@ -345,8 +356,6 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     };
 
     /* ---- steps: P(k) and PV(k), then S^T(k + 1) in the same registers -- */
-    fetch_block(0u);
-    if (nblk > 1u) fetch_block(1u);
     enter_block(0u);
     float4_t scur[2][NT];
     if (nfull > 0u) scores(std::false_type{}, 0u, scur);
