@@ -105,6 +105,11 @@ __device__ __forceinline__ float max3(float a, float b, float c) { return fmaxf(
 __device__ __forceinline__ void fetch16_lds(const void *gaddr, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds) : "memory");
 }
+/* the same from a wave-uniform base (SGPRs) plus a 32-bit per-lane byte
+ * offset: no per-lane 64-bit address arithmetic */
+__device__ __forceinline__ void fetch16_lds(uint32_t voff, const void *sbase, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
 
 /* HD 128 (LFM3 layers) or 64: blocks of NH = HD / 64 halves for K, then V */
 template <int HD>
@@ -165,14 +170,26 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
     /* 2 NH fetches per wave and block (vmcnt counts them) */
     auto fetch_block = [&](uint32_t b) {
         const uint32_t slot = ring_lds + (b % NBUF) * BLKB;
+        if ((b + 1u) * KB <= r_hi) {
+            /* a whole block: uniform base, fixed per-lane offsets */
+            const size_t boff = (size_t)b * KB * row;
 #pragma unroll
-        for (int e = 0; e < NH; ++e) {
-            uint32_t r = b * KB + st_row[e];
-            r = r < r_hi ? r : r_hi - 1u; /* rows past the keys: masked */
-            const size_t off     = (size_t)r * row + st_col[e];
-            const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
-            fetch16_lds(kc + off, piece);
-            fetch16_lds(vc + off, piece + (uint32_t)(NH * HALFB));
+            for (int e = 0; e < NH; ++e) {
+                const uint32_t voff  = (st_row[e] * (uint32_t)row + st_col[e]) * (uint32_t)sizeof(uint16_t);
+                const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
+                fetch16_lds(voff, kc + boff, piece);
+                fetch16_lds(voff, vc + boff, piece + (uint32_t)(NH * HALFB));
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < NH; ++e) {
+                uint32_t r = b * KB + st_row[e];
+                r = r < r_hi ? r : r_hi - 1u; /* rows past the keys: masked */
+                const size_t off     = (size_t)r * row + st_col[e];
+                const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
+                fetch16_lds(kc + off, piece);
+                fetch16_lds(vc + off, piece + (uint32_t)(NH * HALFB));
+            }
         }
     };
 

@@ -106,6 +106,11 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
 __device__ __forceinline__ void fetch16_lds(const void *gaddr, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gaddr), "{m0}"(lds) : "memory");
 }
+/* the same from a wave-uniform base (SGPRs) plus a 32-bit per-lane byte
+ * offset: no per-lane 64-bit address arithmetic */
+__device__ __forceinline__ void fetch16_lds(uint32_t voff, const void *sbase, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
 
 template <int HD>
 __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
@@ -157,23 +162,26 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     /* 4 fetches per wave and block (vmcnt counts them) */
     auto fetch_block = [&](uint32_t blk) {
         const uint32_t slot = ring_lds + (blk % NBUF) * (2 * BLKB);
-        const bool full     = (blk + 1u) * KB <= n_keys;
+        if ((blk + 1u) * KB <= n_keys) {
+            /* a whole block: uniform base, fixed per-lane offsets */
+            const uint8_t *kb = reinterpret_cast<const uint8_t *>(kc) + blk * blk_bytes;
+            const uint8_t *vb = reinterpret_cast<const uint8_t *>(vc) + blk * blk_bytes;
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const uint8_t *kp, *vp;
-            if (full) {
-                kp = reinterpret_cast<const uint8_t *>(kc) + blk * blk_bytes + st_off[e];
-                vp = reinterpret_cast<const uint8_t *>(vc) + blk * blk_bytes + st_off[e];
-            } else {
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
+                fetch16_lds(st_off[e], kb, piece);
+                fetch16_lds(st_off[e], vb, piece + (uint32_t)BLKB);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
                 uint32_t key = blk * KB + st_row[e];
                 key = key < n_keys ? key : n_keys - 1u; /* rows past the keys: masked */
-                const size_t off = (size_t)key * row + st_col[e];
-                kp = reinterpret_cast<const uint8_t *>(kc + off);
-                vp = reinterpret_cast<const uint8_t *>(vc + off);
+                const size_t off     = (size_t)key * row + st_col[e];
+                const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
+                fetch16_lds(kc + off, piece);
+                fetch16_lds(vc + off, piece + (uint32_t)BLKB);
             }
-            const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
-            fetch16_lds(kp, piece);
-            fetch16_lds(vp, piece + (uint32_t)BLKB);
         }
     };
 
