@@ -14,9 +14,9 @@
  * Staging: 64-key K and V blocks (row-major, 128-B rows) move from global
  * memory straight into a ring of 4 LDS blocks (global_load_lds_dwordx4, no
  * registers): block b + 2 is in flight while block b is computed and block
- * b - 1 is still read by the P.V product that trails the scores by a step.  The 16-B
- * chunks of row r are XOR-swizzled by 2*((r >> 2) & 3), which makes both the
- * K fragment reads (ds_read_b128) and the transposing V reads
+ * b - 1 is still read by the P.V product that trails the scores by a step.
+ * The 16-B chunks of row r are XOR-swizzled by 2*((r >> 2) & 3), which makes
+ * both the K fragment reads (ds_read_b128) and the transposing V reads
  * (ds_read_b64_tr_b16) bank-conflict free.
  *
  * Compute runs in 32-key steps.  Step k computes S^T(k+1) into a second
