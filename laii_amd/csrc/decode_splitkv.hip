@@ -27,8 +27,9 @@
  *                                16+4g..19+4g of column l%16), so P needs no
  *                                shuffle; P is split hi + lo like Q.  V^T comes
  *                                from LDS: V rows are loaded 16 B per lane,
- *                                four keys per lane are packed per dim and
- *                                written as 8-byte [d][key] runs.
+ *                                stored row-major (XOR-swizzled 16-B chunks)
+ *                                and read back transposed by
+ *                                ds_read_b64_tr_b16.
  * Loads of sub-tile i+1 are issued before sub-tile i is consumed.
  */
 #include <hip/hip_runtime.h>
@@ -45,11 +46,22 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v_t __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+
+/* transposing LDS read: within each 16-lane group, lane l receives element
+ * l % 4 of the 8-byte chunks addressed by lanes l/4, l/4 + 4, l/4 + 8 and
+ * l/4 + 12 */
+__device__ __forceinline__ half4v_t lds_read_tr(const uint8_t *p) {
+    return __builtin_bit_cast(half4v_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4 *)p));
+}
 
 constexpr float kLog2e     = 1.4426950408889634f;
 constexpr float kNegBig    = -1e30f; /* running-max sentinel (finite)          */
 constexpr float kLazyMax   = 8.0f;   /* running max raised only past m + 8 (log2 units) */
-constexpr int kVtStride    = 36;     /* halfs per d-row of the LDS V^T tile    */
+/* halfs of a wave's LDS V tile: 32 keys x head_dim, row-major */
+template <int HD> constexpr int vt_halfs() { return 32 * HD; }
 
 struct SplitParams {
     const float *q;
@@ -114,7 +126,7 @@ __device__ __forceinline__ float4_t mfma(half8_t a, half8_t b, float4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-/* LDS ordering between the lanes of one wave: each wave owns its V^T tile,
+/* LDS ordering between the lanes of one wave: each wave owns its V tile,
  * so no workgroup barrier is needed; wait for this wave's LDS traffic and
  * keep the compiler from moving LDS accesses across this point. */
 __device__ __forceinline__ void wave_lds_sync() {
@@ -494,26 +506,29 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
     }
 
-    /* one 32-key sub-tile: V^T to LDS, S^T, online softmax, O^T update */
+    /* One 32-key sub-tile: V to LDS, S^T, online softmax, O^T update.
+     * V of a sub-tile goes to the wave's LDS area row-major, each 64-dim half
+     * of a row as 128 B with its 16-B chunks XOR-swizzled by
+     * 2 * ((row >> 2) & 3); the P.V operand V^T then comes from transposing
+     * reads (ds_read_b64_tr_b16), conflict-free, with no VALU transpose.
+     * Lane (l16, g) reads row 4g + l16/4 of a 16-key half at dims
+     * 16 mt + 4 (l16 % 4), in the key order of P's accumulator layout. */
+    uint8_t *vrow = reinterpret_cast<uint8_t *>(vt);
+    /* this lane stores rows 4q..4q+3 (q = lane / CH, plus QPP per pass) of
+     * 16-byte chunk c; the four rows share one swizzle, 128 B apart */
+    const uint32_t vsq = (uint32_t)(lane / CH), vsc = (uint32_t)(lane % CH);
+    const uint32_t vst = (vsc >> 3) * 4096u + vsq * 512u + 16u * ((vsc & 7u) ^ (2u * (vsq & 3u)));
+    /* QPP is a multiple of 4, so later passes keep the swizzle */
+    static_assert(QPP % 4 == 0, "V store swizzle assumes whole 4-quad groups per pass");
+    /* the transposing read of dims 16 mt..16 mt + 15: chunk pair mt ^ g */
+    const uint32_t vtr = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)g + 16u * (uint32_t)((l16 >> 1) & 1) +
+                         8u * (uint32_t)(l16 & 1);
     auto process = [&](uint32_t p0, const u32x4_t (&kcur)[2][NS], const u32x4_t (&vcur)[NVL]) {
         wave_lds_sync(); /* previous sub-tile's V^T reads are done */
 #pragma unroll
-        for (int ps = 0; ps < HD / 64; ++ps) {
-            const int quad = ps * QPP + lane / CH;
-            const int c    = lane % CH;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const uint32_t a0 = vcur[ps * 4 + 0][w], a1 = vcur[ps * 4 + 1][w];
-                const uint32_t a2 = vcur[ps * 4 + 2][w], a3 = vcur[ps * 4 + 3][w];
-                u32x2_t even, odd; /* dims 8c+2w and 8c+2w+1 of keys 4quad..4quad+3 */
-                even[0] = (a0 & 0xFFFFu) | (a1 << 16);
-                even[1] = (a2 & 0xFFFFu) | (a3 << 16);
-                odd[0]  = (a0 >> 16) | (a1 & 0xFFFF0000u);
-                odd[1]  = (a2 >> 16) | (a3 & 0xFFFF0000u);
-                *reinterpret_cast<u32x2_t *>(&vt[(8 * c + 2 * w) * kVtStride + 4 * quad])     = even;
-                *reinterpret_cast<u32x2_t *>(&vt[(8 * c + 2 * w + 1) * kVtStride + 4 * quad]) = odd;
-            }
-        }
+        for (int j = 0; j < NVL; ++j)
+            *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u + (uint32_t)(j & 3) * 128u) =
+                vcur[j];
 
         /* S^T = K . Q^T (log2 units) */
         float4_t sacc[2][NT];
@@ -591,12 +606,11 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         /* O^T += V^T . P^T */
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) {
-            const uint16_t *src = &vt[(16 * mt + l16) * kVtStride + 4 * g];
-            const u32x2_t x0    = *reinterpret_cast<const u32x2_t *>(src);
-            const u32x2_t x1    = *reinterpret_cast<const u32x2_t *>(src + 16);
-            u32x4_t a;
-            a[0] = x0[0]; a[1] = x0[1]; a[2] = x1[0]; a[3] = x1[1];
-            const half8_t av = as_half8(a);
+            const uint8_t *vh   = vrow + (mt >> 2) * 4096u;
+            const uint32_t o    = vtr ^ (32u * (uint32_t)(mt & 3));
+            const half4v_t lo   = lds_read_tr(vh + o);
+            const half4v_t hi   = lds_read_tr(vh + 16u * 128u + o);
+            const half8_t av    = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 oacc[mt][nt] = mfma(av, ph[nt], oacc[mt][nt]);
@@ -696,7 +710,7 @@ constexpr size_t fresh_bytes(uint32_t W, uint32_t n_rows) {
  * mark their partials empty. */
 template <int HD, int NT, int W, bool FUSE>
 __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
-    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][vt_halfs<HD>()];
     const int lane       = threadIdx.x & 63;
     const uint32_t wave  = threadIdx.x >> 6;
     const uint32_t split = blockIdx.x, kvh = blockIdx.y * W + wave, s = blockIdx.z;
@@ -723,7 +737,7 @@ __global__ __launch_bounds__(64 * W) void k_splitkv(const SplitParams P) {
 template <int HD, int NT, int WW, bool FUSE>
 __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
     constexpr uint32_t D4 = HD / 4;
-    __shared__ __attribute__((aligned(16))) uint16_t vt_all[WW][HD * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[WW][vt_halfs<HD>()];
     const int lane       = threadIdx.x & 63;
     const uint32_t split = threadIdx.x >> 6, kvh = blockIdx.x, s = blockIdx.y;
     const SeqKeys k      = seq_keys(P, s);
@@ -869,7 +883,7 @@ __device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int l
 
 template <int HD, int NT, int W, bool FUSE>
 __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
-    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][HD * kVtStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][vt_halfs<HD>()];
     const lfm_bal_cfg &c = P.plan;
     const int lane       = threadIdx.x & 63;
     const uint32_t wave  = threadIdx.x >> 6;
@@ -1299,10 +1313,10 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool 
     }
     note_plan(grid ? "grid" : "balanced");
     uint32_t w = choose_waves(p.n_head_kv, HD);
-    /* fused prologue: the staged new rows and the V^T tiles stay within
+    /* fused prologue: the staged new rows and the V tiles stay within
      * 64 KB of LDS per workgroup */
     if (FUSE)
-        while (w > 1u && (size_t)w * HD * kVtStride * sizeof(uint16_t) + fresh_bytes<HD, FUSE>(w, p.n_rows) > 65536u)
+        while (w > 1u && (size_t)w * vt_halfs<HD>() * sizeof(uint16_t) + fresh_bytes<HD, FUSE>(w, p.n_rows) > 65536u)
             w >>= 1;
     /* a grid of fewer workgroups than compute units (one short sequence)
      * spreads its KV heads over more, smaller workgroups: measured on MI355X
