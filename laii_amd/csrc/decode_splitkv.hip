@@ -524,7 +524,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     const uint32_t vtr = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)g + 16u * (uint32_t)((l16 >> 1) & 1) +
                          8u * (uint32_t)(l16 & 1);
     auto process = [&](uint32_t p0, const u32x4_t (&kcur)[2][NS], const u32x4_t (&vcur)[NVL]) {
-        wave_lds_sync(); /* previous sub-tile's V^T reads are done */
+        wave_lds_sync(); /* previous sub-tile's transposing V reads are done */
 #pragma unroll
         for (int j = 0; j < NVL; ++j)
             *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u + (uint32_t)(j & 3) * 128u) =
@@ -602,7 +602,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                 for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha_nt[nt];
         }
 
-        wave_lds_sync(); /* V^T of this sub-tile is in LDS */
+        wave_lds_sync(); /* V of this sub-tile is in LDS */
         /* O^T += V^T . P^T */
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) {
