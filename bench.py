@@ -441,7 +441,10 @@ def box_peaks(hip, la, steps=10):
     lib = la.load()
     n_bytes = 2 << 30
     src = la.DeviceArray.zeros(n_bytes // 4, np.uint32)
-    n_wg = 8192
+    # 2048 x 256 threads: one residency round (32 waves per CU); 8192
+    # workgroups (four rounds) read 7 % slower on MI355X (6.69 vs 7.20 TB/s
+    # over 1 GiB), 1024 slower still
+    n_wg = 2048
     sink = la.DeviceArray.zeros(n_wg, np.uint32)
     rd = _Probe(lambda: check(lib.lfm_hip_probe_read(src.ptr, n_bytes, sink.ptr, n_wg, None),
                                  "lfm_hip_probe_read"))
@@ -454,7 +457,7 @@ def box_peaks(hip, la, steps=10):
     flops = wgs * 4 * iters * 8 * 16384
     return dict(read_GBps=round(n_bytes / (read_ms * 1e-3) / 1e9, 1),
                 mfma_f16_TFLOPs=round(flops / (mfma_ms * 1e-3) / 1e12, 1),
-                read="2 GiB streaming read, 8192 x 256 threads, 16-B nontemporal loads",
+                read="2 GiB streaming read, 2048 x 256 threads, 16-B nontemporal loads",
                 mfma="4096 x 4 waves, 8 independent 16x16x32 f16 MFMA chains per wave")
 
 
