@@ -141,6 +141,13 @@ __device__ __forceinline__ float gate_value(const float *gate, size_t idx, int i
     const float g = gate[idx];
     return is_logit ? 1.0f / (1.0f + expf(-g)) : g;
 }
+/* The same in two halves: the load, issued where a kernel starts so that its
+ * memory round trip overlaps the kernel's work instead of delaying the
+ * output, and the sigmoid where the value is used. */
+__device__ __forceinline__ float gate_raw(const float *gate, size_t idx) { return gate ? gate[idx] : 1.0f; }
+__device__ __forceinline__ float gate_apply(float raw, const float *gate, int is_logit) {
+    return (gate && is_logit) ? 1.0f / (1.0f + expf(-raw)) : raw;
+}
 
 /* Sum of squares of one head held in MFMA fragment order (lane (l16, g)
  * holds dims 32*st + 8*g + j), added in the order of the reference's AVX2
@@ -745,6 +752,12 @@ __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
     uint32_t chunk       = P.chunk;
     if ((uint64_t)chunk * P.n_splits < total) chunk = (((total + P.n_splits - 1u) / P.n_splits) + 31u) & ~31u;
     const size_t base = (size_t)(s * P.n_head_kv + kvh) * P.n_splits * P.ncols;
+    /* the gate of this thread's first merge item, loaded before the splits */
+    float graw0 = 1.0f;
+    if (threadIdx.x < P.ncols * D4) {
+        const uint32_t n0 = threadIdx.x / D4, r0 = n0 / P.kv_mul;
+        graw0 = gate_raw(P.gate, ((size_t)s * P.n_rows + r0) * P.n_head_q + kvh * P.kv_mul + (n0 - r0 * P.kv_mul));
+    }
     if (split < P.n_splits) {
         const uint32_t kb = k.lo + split * chunk;
         const uint32_t ke = min(kb + chunk, k.last + 1u);
@@ -780,7 +793,7 @@ __global__ __launch_bounds__(64 * WW) void k_splitkv_wg(const SplitParams P) {
         const uint32_t r  = n / P.kv_mul;
         const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
         const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
-        const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+        const float gv    = gate_apply(it == threadIdx.x ? graw0 : gate_raw(P.gate, orow), P.gate, P.gate_is_logit);
         const float inv   = (L > 0.0f) ? gv / L : 0.0f;
         const uint32_t d  = 4 * d4;
         if (d < P.out_dims)
@@ -969,6 +982,10 @@ __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
     const uint32_t grp = kvh / P.wpg;
     const uint32_t rem = item - w * per;
     const uint32_t n = rem / D4, d4 = rem - n * D4;
+    const uint32_t r  = n / P.kv_mul;
+    const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
+    const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+    const float graw  = live && q == 0u ? gate_raw(P.gate, orow) : 1.0f; /* before the slot loads */
     uint32_t T, G, tiles, before;
     if (!P.pos0_dev) {
         tiles  = lfm_bal_seq_tiles(&c, P.pos0_host);
@@ -1030,10 +1047,7 @@ __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
         M   = Mn;
     }
     if (!live || g0 == g1 || q != 0u) return; /* g0 == g1: written directly */
-    const uint32_t r  = n / P.kv_mul;
-    const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
-    const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
-    const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+    const float gv    = gate_apply(graw, P.gate, P.gate_is_logit);
     const float inv   = (L > 0.0f) ? gv / L : 0.0f;
     const uint32_t d  = 4 * d4;
     if (d < P.out_dims)
@@ -1056,6 +1070,11 @@ __global__ __launch_bounds__(256) void k_merge(const SplitParams P, uint32_t n_i
     const uint32_t n    = rest % P.ncols;
     const uint32_t pair = live ? rest / P.ncols : 0u; /* s * n_head_kv + kvh */
     const size_t base   = (size_t)pair * P.n_splits * P.ncols + n;
+    const uint32_t s  = pair / P.n_head_kv, kvh = pair % P.n_head_kv;
+    const uint32_t r  = n / P.kv_mul;
+    const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
+    const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+    const float graw  = live && sg == 0u ? gate_raw(P.gate, orow) : 1.0f; /* before the split loads */
     float M = kNegBig, L = 0.0f;
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live) {
@@ -1091,11 +1110,7 @@ __global__ __launch_bounds__(256) void k_merge(const SplitParams P, uint32_t n_i
         M   = Mn;
     }
     if (!live || sg != 0u) return;
-    const uint32_t s  = pair / P.n_head_kv, kvh = pair % P.n_head_kv;
-    const uint32_t r  = n / P.kv_mul;
-    const uint32_t h  = kvh * P.kv_mul + (n - r * P.kv_mul);
-    const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
-    const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+    const float gv    = gate_apply(graw, P.gate, P.gate_is_logit);
     const float inv   = (L > 0.0f) ? gv / L : 0.0f;
     const uint32_t d  = 4 * d4;
     if (d < P.out_dims)

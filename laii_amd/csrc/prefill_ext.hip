@@ -208,11 +208,14 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
      * them the compiler waited for each column tile's loads, one memory
      * round trip per tile */
     float4 qraw[NT][NS][2];
+    float graw[NT]; /* the output gates, loaded now: the epilogue does not wait for them */
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const uint32_t c = (uint32_t)(wave * 32 + nt * 16 + l16);
         const uint32_t j = c / P.tq, t = t0 + c % P.tq;
         col_ok[nt]  = t < P.n_tok;
+        graw[nt]    = (P.gate && col_ok[nt]) ? P.gate[((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j]
+                                             : 1.0f;
         col_pos[nt] = P.pos_0 + t;
         col_lo[nt]  = (P.window && col_pos[nt] + 1u > P.window) ? col_pos[nt] + 1u - P.window : 0u;
         const float *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q + kvh * P.kv_mul + j) * HD + 8 * g;
@@ -429,7 +432,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
         const size_t orow   = ((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j;
         float gv            = 1.0f;
         if (P.gate) {
-            const float gl = P.gate[orow];
+            const float gl = graw[nt];
             gv             = P.gate_is_logit ? 1.0f / (1.0f + expf(-gl)) : gl;
         }
         const float inv = lt > 0.0f ? gv / lt : 0.0f;
