@@ -626,6 +626,100 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         }
     };
 
+    /* The last two sub-tiles of a segment in one step (one-tile kernels):
+     * both score sets first, one column max and one lazy-max decision for
+     * the 64 keys, then P.V of each sub-tile through the wave's V tile in
+     * turn.  Segments of two sub-tiles (config 1, the LFM3 window ring) are
+     * mostly this dependent chain, which runs once instead of twice. */
+    auto process2 = [&](uint32_t p0, const u32x4_t (&ka)[2][NS], const u32x4_t (&va)[NVL],
+                        const u32x4_t (&kb)[2][NS], const u32x4_t (&vb)[NVL]) {
+        wave_lds_sync(); /* previous sub-tile's transposing V reads are done */
+#pragma unroll
+        for (int j = 0; j < NVL; ++j)
+            *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u + (uint32_t)(j & 3) * 128u) =
+                va[j];
+        float4_t sacc[2][2]; /* [sub-tile][16-key half] */
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                float4_t acc = (float4_t)0.0f;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    const half8_t kf = as_half8(u ? kb[kt][st] : ka[kt][st]);
+                    acc = mfma(kf, qh[0][st], acc);
+                    acc = mfma(kf, ql[0][st], acc);
+                }
+                sacc[u][kt] = acc;
+            }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const uint32_t pu = p0 + 32u * (uint32_t)u;
+            if ((pu < free_lo) || (pu + 31u > free_hi)) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t key = pu + (uint32_t)(16 * kt + 4 * g + i);
+                        const bool ok      = key < ke && key >= col_lo[0] && key <= col_hi[0];
+                        if (!ok) sacc[u][kt][i] = -INFINITY;
+                    }
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                mx = fmaxf(mx, fmaxf(fmaxf(sacc[u][kt][0], sacc[u][kt][1]), fmaxf(sacc[u][kt][2], sacc[u][kt][3])));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool raise  = mx > mrun[0] + kLazyMax;
+        const float mnew  = raise ? mx : mrun[0];
+        const float alpha = raise ? __builtin_amdgcn_exp2f(mrun[0] - mnew) : 1.0f;
+        mrun[0]           = mnew;
+        half8_t ph[2], pl[2];
+        float psum = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float pv    = __builtin_amdgcn_exp2f(sacc[u][kt][i] - mnew);
+                    psum             += pv;
+                    const _Float16 hi = (_Float16)pv;
+                    ph[u][4 * kt + i] = hi;
+                    pl[u][4 * kt + i] = (_Float16)(pv - (float)hi);
+                }
+        lrun[0] = lrun[0] * alpha + psum;
+        if (__builtin_amdgcn_ballot_w64(raise) != 0ull) {
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) oacc[mt][0] *= alpha;
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (u == 1) {
+                wave_lds_sync(); /* the first sub-tile's transposing reads are done */
+#pragma unroll
+                for (int j = 0; j < NVL; ++j)
+                    *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u +
+                                                 (uint32_t)(j & 3) * 128u) = vb[j];
+            }
+            wave_lds_sync(); /* V of this sub-tile is in LDS */
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const uint8_t *vh = vrow + (mt >> 2) * 4096u;
+                const uint32_t o  = vtr ^ (32u * (uint32_t)(mt & 3));
+                const half4v_t lo = lds_read_tr(vh + o);
+                const half4v_t hi = lds_read_tr(vh + 16u * 128u + o);
+                const half8_t av  = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                oacc[mt][0]       = mfma(av, ph[u], oacc[mt][0]);
+                oacc[mt][0]       = mfma(av, pl[u], oacc[mt][0]);
+            }
+        }
+    };
+
     /* two register buffers; the loads of sub-tile i+1 are in flight while
      * sub-tile i is consumed.  The loop body issues its loads unconditionally
      * and the last one or two sub-tiles are peeled: with a conditional load
@@ -640,6 +734,14 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         }
         process(p0, kd, vd);
     };
+    auto consume2 = [&](uint32_t p0, u32x4_t (&ka)[2][NS], u32x4_t (&va)[NVL], u32x4_t (&kb)[2][NS],
+                        u32x4_t (&vb)[NVL]) {
+        if constexpr (FUSE) {
+            if (has_fresh && p0 + 31u >= pos0) patch_new_rows(p0, ka, va);
+            if (has_fresh && p0 + 63u >= pos0) patch_new_rows(p0 + 32u, kb, vb);
+        }
+        process2(p0, ka, va, kb, vb);
+    };
     uint32_t it = 0;
     for (; it + 2u < nsub; it += 2u) {
         const uint32_t p0 = kb + 32u * it;
@@ -652,8 +754,12 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         const uint32_t p0 = kb + 32u * it;
         if (it + 1u < nsub) {
             load_tile(p0 + 32u, kB, vB, true);
-            consume(p0, kA, vA);
-            consume(p0 + 32u, kB, vB);
+            if constexpr (NT == 1) {
+                consume2(p0, kA, vA, kB, vB);
+            } else {
+                consume(p0, kA, vA);
+                consume(p0 + 32u, kB, vB);
+            }
         } else {
             consume(p0, kA, vA);
         }
