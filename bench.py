@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, datasheet
 # HBM bytes per launch of the headline kernel from two rocprofv3 PMC passes
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, factors from a 2 GiB read/copy
 # kernel); profiles/k_splitkv_decode_b64_ctx8192_pmc.md
-HEADLINE_TRAFFIC_BYTES = 1083295437
+HEADLINE_TRAFFIC_BYTES = 1078550016
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA, datasheet
 
 

@@ -1309,9 +1309,13 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
     p.wpg              = W;
     c.n_groups         = (p.n_head_kv + W - 1u) / W;
     c.n_res            = resident_wgs<HD, NT, W, FUSE>(fresh_bytes<HD, FUSE>(W, p.n_rows));
-    /* 16 waves per CU over a batch of equal sequences: two residency rounds of
-     * 8-wave workgroups at head_dim 64 (measured best on MI355X) */
-    c.target_waves = 16u * cus;
+    /* 8 waves per CU over a batch of equal sequences: one residency round of
+     * 8-wave workgroups at head_dim 64.  Measured on MI355X against two
+     * rounds (16 waves per CU), GB/s per step: B64 x 8192 6351-6473 ->
+     * 6629-6765, B16 x 8192 4708-4885 -> 5106-5253, B64 x 2048 4755-5007 ->
+     * 5276-5420, LFM3 B32 x 32768 d128 6317-6333 -> 6458-6489; 12 waves per
+     * CU (a partial second round) was slower than either */
+    c.target_waves = 8u * cus;
     /* each workgroup's partials cost about one 32-key tile per 32 query
      * columns: keep >= 12 tiles per workgroup per 32 columns (measured on
      * MI355X for 8 rows x 4 heads), and >= 2 tiles */

@@ -56,7 +56,7 @@ LFM_IDX_FN uint32_t lfm_bal_plan_wgs(const lfm_bal_cfg *c, uint32_t T, int unifo
     uint64_t G;
     if (uniform) {
         /* every unit gets n equal workgroups, about target_waves waves over
-         * the batch (several residency rounds absorb slow workgroups) */
+         * the batch (one residency round at the launcher's target) */
         const uint32_t tiles = T / c->n_seq;
         uint64_t ct = ((uint64_t)tiles * c->n_seq * c->n_head_kv + c->target_waves - 1u) / c->target_waves;
         if (ct < c->min_tiles) ct = c->min_tiles;

@@ -28,7 +28,7 @@ def sim(tmp_path_factory):
                                C.c_uint32, C.c_int, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
                                C.c_char_p, C.c_size_t]
 
-    def check(pos0, n_rows, nkv, W, ncols, window=0, cap=0, n_res=512, target=4096, min_tiles=None,
+    def check(pos0, n_rows, nkv, W, ncols, window=0, cap=0, n_res=512, target=2048, min_tiles=None,
               keys=None, mutant=0):
         pos0 = np.ascontiguousarray(pos0, np.uint32)
         if min_tiles is None:  # the host's rule (decode_splitkv.hip launch_bal)
@@ -69,7 +69,7 @@ def _random_case(rng):
         pos0 = rng.integers(0, 9000, n_seq)
     pos0[0] = 0 if rng.random() < 0.5 else pos0[0]
     kw = dict(window=window, cap=cap, n_res=int(rng.choice([64, 256, 512, 1024, 2048])),
-              target=int(rng.choice([1024, 4096])))
+              target=int(rng.choice([1024, 2048, 4096])))
     r = rng.random()
     if r < 0.2:  # forced short shares (LFM_ATTN_CHUNK-like): 1-3 tiles per workgroup, no round cap
         kw.update(min_tiles=int(rng.integers(1, 4)), n_res=0x7FFFFFFF, target=0x7FFFFFFF)
