@@ -58,6 +58,28 @@ const char *lfm_attn_last_error(void);
 const char *lfm_attn_last_plan(void);
 const char *lfm_attn_version(void);
 
+/* Tuning and tests, no reference counterpart: overrides of the split-KV
+ * launch plan, process-wide.  plan NULL, "" or "auto" lets the library
+ * choose; "grid", "balanced" or "wg" forces that form; waves (1, 2, 4, 8),
+ * chunk (keys per workgroup) and min_tiles (32-key tiles per balanced
+ * workgroup) force those counts, 0 = automatic.  The environment variables
+ * LFM_ATTN_PLAN, LFM_ATTN_WAVES, LFM_ATTN_CHUNK and LFM_ATTN_MINTILES seed
+ * the overrides once, at the library's first attention launch or first
+ * call of this function; launches never read the environment.  Set it
+ * between launches, not while another thread launches. */
+int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles);
+/* Diagnostic, no reference counterpart, needs no device: the plan the
+ * split-KV attention takes for a batch (n_seq sequences x n_rows rows, head
+ * shape, sliding window, keys_hint as lfm_hip_gqa_f16_varlen; positions on
+ * the device or one host position; fused = the step entry's prologue) on a
+ * device of n_cus compute units under the current overrides: *plan = "wg",
+ * "grid", "balanced" or "generic" (no split-KV kernel for the shape);
+ * out3 = {waves per workgroup, grid key splits, grid chunk} (0 where the
+ * plan has none). */
+int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                          uint32_t window_len, uint32_t keys_hint, int positions_on_device, int fused, uint32_t n_cus,
+                          const char **plan, uint32_t out3[3]);
+
 /* ---- device plumbing (so C11 callers need no HIP headers) ------------------ */
 int lfm_attn_device_count(int *count);
 int lfm_attn_set_device(int device);
@@ -93,6 +115,15 @@ int lfm_attn_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq, uin
                            uint32_t rope_dim, float freq_base, const float *rope_freqs,
                            uint32_t n_rope_freqs);
 
+/* Replaces the float-angle table of the production LFM2 stacks, built by
+ * lfm2_state_init (tools/lfm2_forward.c:572-581) and lfm2_batch_state_init
+ * (tools/lfm2_prefill_batch.c:727-736): freq_i = powf(base, -(2i / head_dim))
+ * in float, entries cosf / sinf of the float product (float)p * freq_i
+ * (freq_base <= 0 means 10000).  The table of LFM_PROLOGUE_TABLE.
+ * cos_tab/sin_tab: HOST float[max_seq][head_dim/2]. */
+int lfm_attn_rope_table_lfm2(float *cos_tab, float *sin_tab, uint32_t max_seq, uint32_t head_dim,
+                             float freq_base);
+
 /* Gen-1 RoPE row (host): cos_row[i], sin_row[i] of (float)pos * (1 /
  * powf(theta, 2i / head_dim)), i < head_dim / 2, computed in float with
  * powf/cosf/sinf on every call as lfm_rope_neox does (src/lfm_forward.c:97-111;
@@ -101,15 +132,34 @@ int lfm_attn_rope_lut_lfm3(float *cos_lut, float *sin_lut, uint32_t max_seq, uin
 int lfm_attn_rope_row_gen1(float *cos_row, float *sin_row, uint32_t head_dim, uint32_t pos, float theta);
 
 /* ---- prologue: per-head QK-RMSNorm + NeoX RoPE (+ RNE fp16 KV store) -------- */
-/* Replaces lfm2_qk_norm_rope_simd (tools/lfm2_kernels_fast.c:403-497, :511-547)
- * and lfm3_qk_norm_rope_simd (tools/lfm3_engine.c:463-525, :599-666).
+/* Prologue forms.  The reference runs two LFM2 prologues that differ in their
+ * RoPE table (an input here: cos_lut/sin_lut) and in the order in which
+ * RMSNorm adds the squares; rows match the chosen one bit for bit.
+ *   LFM_PROLOGUE_FAST   lfm2_qk_norm_rope_avx2 (tools/lfm2_kernels_fast.c:403-497),
+ *                       lfm3_qk_norm_rope_128_avx2 (tools/lfm3_engine.c:463-525):
+ *                       the fast decode context and LFM3.  Tables:
+ *                       lfm_attn_rope_lut_lfm2 / lfm_attn_rope_lut_lfm3.
+ *   LFM_PROLOGUE_TABLE  lfm2_qk_norm_and_rope (tools/lfm2_forward.c:775-830) and
+ *                       lfm2_qk_norm_and_rope_table (tools/lfm2_prefill_batch.c:
+ *                       826-893): the lfm2_forward.c decode, speculative verify
+ *                       and prompt prefill.  lfm2_rmsnorm's order
+ *                       (tools/lfm2_forward.c:669-684): eight fma chains over
+ *                       dims 8k + j, added in double.  Table:
+ *                       lfm_attn_rope_table_lfm2.
+ * Any other value returns LFM_ATTN_E_INVALID. */
+#define LFM_PROLOGUE_FAST  0
+#define LFM_PROLOGUE_TABLE 1
+
+/* Replaces lfm2_qk_norm_rope_simd (tools/lfm2_kernels_fast.c:403-497, :511-547),
+ * lfm3_qk_norm_rope_simd (tools/lfm3_engine.c:463-525, :599-666) and, with
+ * LFM_PROLOGUE_TABLE, lfm2_qk_norm_and_rope_table / lfm2_qk_norm_and_rope.
  * vec: [n_heads][head_dim] float.  norm_w: [head_dim] or NULL (no norm).
  * cos_lut/sin_lut: DEVICE [>= pos+1][head_dim/2].  With dst_f16 != NULL the
  * rotated heads are stored there as RNE fp16 and vec is not modified;
  * otherwise vec is rotated in place.  head_dim even, <= 256. */
 int lfm_hip_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
                          const float *norm_w, float eps, const float *cos_lut,
-                         const float *sin_lut, uint32_t pos, lfm_attn_stream_t stream);
+                         const float *sin_lut, uint32_t pos, int prologue, lfm_attn_stream_t stream);
 
 /* Replaces lfm2_store_fp32_to_fp16_simd (tools/lfm2_kernels_fast.c:500-507,
  * :549-555) and lfm3_store_f32_to_f16 (tools/lfm3_engine.c:133-153): RNE. */
@@ -124,13 +174,13 @@ int lfm_hip_store_fp32_to_fp16(uint16_t *dst_f16, const float *src, uint32_t n,
  * lfm3_forward_batch_core (tools/lfm3_engine.c:2006-2016) over many sequences.
  * q: [n_seq][n_rows][n_head_q][hd]; k, v: [n_seq][n_rows][n_head_kv][hd];
  * k_seq/v_seq: DEVICE arrays of n_seq DEVICE cache pointers; pos_0: DEVICE
- * uint32_t[n_seq]. */
+ * uint32_t[n_seq]; prologue: LFM_PROLOGUE_FAST or LFM_PROLOGUE_TABLE. */
 int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *const *k_seq,
                          uint16_t *const *v_seq, const uint32_t *pos_0, uint32_t n_seq,
                          uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
                          const float *q_norm_w, const float *k_norm_w, float eps,
                          const float *cos_lut, const float *sin_lut, uint32_t window_len,
-                         uint32_t cap, lfm_attn_stream_t stream);
+                         uint32_t cap, int prologue, lfm_attn_stream_t stream);
 
 /* ---- projections beside the attention path ------------------------------- */
 /* Blocks are the reference's packed GGUF layouts (tools/lfm2_cpuid_quants.c:76-127):
@@ -280,7 +330,10 @@ int lfm_hip_gqa_f16_varlen(const float *q, const float *gate, int gate_is_logit,
  * q: raw queries [n_seq][n_rows][n_head_q][head_dim] (left unchanged);
  * k, v: raw new-token rows [n_seq][n_rows][n_head_kv][head_dim];
  * q_norm_w, k_norm_w: [head_dim] or NULL (no norm); cos_lut/sin_lut: the RoPE
- * table [> last position][head_dim / 2]; the rest as lfm_hip_gqa_f16_varlen.
+ * table [> last position][head_dim / 2]; prologue: LFM_PROLOGUE_FAST (the
+ * lfm2_kernels_fast.c and LFM3 stacks) or LFM_PROLOGUE_TABLE (lfm2_forward.c
+ * and lfm2_prefill_batch.c, with the table of lfm_attn_rope_table_lfm2); the
+ * rest as lfm_hip_gqa_f16_varlen.
  * With a sliding window, window_len + n_rows - 1 <= cap (each row's window
  * survives the later rows' ring writes).  Head dims 64 and 128 run one
  * attention launch (plus the split merge where the keys are split); other
@@ -290,7 +343,7 @@ int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const f
                          uint32_t n_seq, uint32_t n_rows, uint32_t keys_hint, uint32_t n_head_q,
                          uint32_t n_head_kv, uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
                          const float *q_norm_w, const float *k_norm_w, float eps, const float *cos_lut,
-                         const float *sin_lut, lfm_attn_stream_t stream);
+                         const float *sin_lut, int prologue, lfm_attn_stream_t stream);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
@@ -421,6 +474,13 @@ typedef struct {
     const float *rope_freqs;  /* LFM3 rope_freqs factors or NULL                   */
     uint32_t n_rope_freqs;
     int lfm3;                 /* 1: LFM3 tables (lfm3_rope_lut_init), 0: LFM2      */
+    int prologue;             /* LFM2 only: LFM_PROLOGUE_FAST (lfm2_kernels_fast.c,
+                                 table lfm2_rope_lut_init) or LFM_PROLOGUE_TABLE
+                                 (lfm2_forward.c / lfm2_prefill_batch.c, their
+                                 float-angle table); LFM3 takes FAST only.  Sink
+                                 eviction counter-rotates with the
+                                 lfm2_rope_lut_init table either way, as
+                                 src/lfm2_api.c:883-888 does                      */
 } lfm_attn_geom;
 
 int lfm_attn_ctx_create(lfm_attn_ctx **out, const lfm_attn_geom *geom);

@@ -17,12 +17,19 @@ _int = C.c_int
 _vp = C.c_void_p
 _sz = C.c_size_t
 
+# prologue forms (LFM_PROLOGUE_* of include/lfm_attn.h)
+PROLOGUE_FAST = 0   # lfm2_kernels_fast.c / LFM3: double-angle tables, AVX2 kernels' sum order
+PROLOGUE_TABLE = 1  # lfm2_forward.c / lfm2_prefill_batch.c: float-angle table, lfm2_rmsnorm order
+
 # name -> (restype, argtypes); every function declared in include/lfm_attn.h
 SIGNATURES = {
     "lfm_attn_status_string": (C.c_char_p, [_int]),
     "lfm_attn_last_error": (C.c_char_p, []),
     "lfm_attn_last_plan": (C.c_char_p, []),
     "lfm_attn_version": (C.c_char_p, []),
+    "lfm_attn_set_tuning": (_int, [C.c_char_p, _u32, _u32, _u32]),
+    "lfm_attn_plan_preview": (_int, [_u32, _u32, _u32, _u32, _u32, _u32, _u32, _int, _int, _u32,
+                                     C.POINTER(C.c_char_p), C.POINTER(_u32)]),
     "lfm_attn_device_count": (_int, [C.POINTER(_int)]),
     "lfm_attn_set_device": (_int, [_int]),
     "lfm_attn_dev_alloc": (_int, [C.POINTER(_vp), _sz]),
@@ -37,7 +44,8 @@ SIGNATURES = {
     "lfm_attn_slot_of": (_u32, [_u32, _u32, _u32]),
     "lfm_attn_rope_lut_lfm2": (_int, [_vp, _vp, _u32, _u32, _f32]),
     "lfm_attn_rope_lut_lfm3": (_int, [_vp, _vp, _u32, _u32, _u32, _f32, _vp, _u32]),
-    "lfm_hip_qk_norm_rope": (_int, [_vp, _vp, _u32, _u32, _vp, _f32, _vp, _vp, _u32, _vp]),
+    "lfm_attn_rope_table_lfm2": (_int, [_vp, _vp, _u32, _u32, _f32]),
+    "lfm_hip_qk_norm_rope": (_int, [_vp, _vp, _u32, _u32, _vp, _f32, _vp, _vp, _u32, _int, _vp]),
     "lfm_hip_store_fp32_to_fp16": (_int, [_vp, _vp, _u32, _vp]),
     "lfm_hip_quantize_q8_K": (_int, [_vp, _vp, _u32, _u32, _vp]),
     "lfm_hip_matmul_q4_K": (_int, [_vp, _vp, _u32, _u32, _vp, _u32, _vp]),
@@ -45,7 +53,7 @@ SIGNATURES = {
     "lfm_hip_gqa_qkv_fused": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                      _u32, _u32, _vp, _u32, _vp]),
     "lfm_hip_qkv_prologue": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32,
-                                    _vp, _vp, _f32, _vp, _vp, _u32, _u32, _vp]),
+                                    _vp, _vp, _f32, _vp, _vp, _u32, _u32, _int, _vp]),
     "lfm_hip_online_gqa_f16": (_int, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _f32, _vp]),
     "lfm_hip_gqa_heads": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
                                  _f32, _vp]),
@@ -61,7 +69,7 @@ SIGNATURES = {
     "lfm_hip_gen1_gqa_step": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32,
                                      _vp, _vp, _vp]),
     "lfm_hip_gqa_f16_step": (_int, [_vp, _vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
-                                    _u32, _u32, _u32, _u32, _f32, _vp, _vp, _f32, _vp, _vp, _vp]),
+                                    _u32, _u32, _u32, _u32, _f32, _vp, _vp, _f32, _vp, _vp, _int, _vp]),
     "lfm_hip_gqa_f16_varlen_noalloc": (_int, [_vp, _vp, _int, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
                                               _u32, _u32, _u32, _u32, _f32, _vp]),
     "lfm_hip_kv_cache_shift_sinks": (_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _u32,
@@ -79,7 +87,7 @@ class Geom(C.Structure):
                 ("max_seq", _u32), ("sliding_window", _u32), ("swa_cap", _u32),
                 ("layer_is_swa", C.POINTER(C.c_uint8)), ("eps", _f32), ("rope_base", _f32),
                 ("rope_base_swa", _f32), ("rope_dim", _u32), ("rope_freqs", C.POINTER(_f32)),
-                ("n_rope_freqs", _u32), ("lfm3", _int)]
+                ("n_rope_freqs", _u32), ("lfm3", _int), ("prologue", _int)]
 
 
 class CacheModelC(C.Structure):

@@ -8,6 +8,8 @@ Function names and argument meaning follow the reference task contexts:
   qk_norm_rope                   lfm2/lfm3_qk_norm_rope_* tools/lfm2_kernels_fast.c:403-547,
                                                           tools/lfm3_engine.c:463-666
   rope_lut_lfm2 / rope_lut_lfm3  lfm2_rope_lut_init / lfm3_rope_lut_init
+  rope_table_lfm2                the float-angle table of lfm2_state_init /
+                                 lfm2_batch_state_init (prologue=PROLOGUE_TABLE)
 Tensors are DeviceArray objects (device memory) or raw device addresses (int).
 Every call raises LfmAttnError on a non-zero status; nothing falls back to
 the CPU.
@@ -20,7 +22,7 @@ from typing import Optional, Sequence, Union
 
 import numpy as np
 
-from ._lib import CacheModelC, Geom, check, load
+from ._lib import PROLOGUE_FAST, PROLOGUE_TABLE, CacheModelC, Geom, check, load
 
 Ptr = Union["DeviceArray", int, None]
 
@@ -128,10 +130,18 @@ def rope_lut_lfm3(max_seq: int, head_dim: int, rope_dim: int, freq_base: float,
     return c, s
 
 
+def rope_table_lfm2(max_seq: int, head_dim: int, freq_base: float):
+    c = np.empty((max_seq, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    check(load().lfm_attn_rope_table_lfm2(c.ctypes.data, s.ctypes.data, max_seq, head_dim, freq_base),
+          "lfm_attn_rope_table_lfm2")
+    return c, s
+
+
 def qk_norm_rope(vec: Ptr, dst_f16: Ptr, n_heads: int, head_dim: int, norm_w: Ptr, eps: float,
-                 cos_lut: Ptr, sin_lut: Ptr, pos: int, stream=None) -> None:
+                 cos_lut: Ptr, sin_lut: Ptr, pos: int, stream=None, prologue: int = PROLOGUE_FAST) -> None:
     check(load().lfm_hip_qk_norm_rope(_p(vec), _p(dst_f16), n_heads, head_dim, _p(norm_w), eps,
-                                      _p(cos_lut), _p(sin_lut), pos, stream), "lfm_hip_qk_norm_rope")
+                                      _p(cos_lut), _p(sin_lut), pos, prologue, stream), "lfm_hip_qk_norm_rope")
 
 
 def store_fp32_to_fp16(dst_f16: Ptr, src: Ptr, n: int, stream=None) -> None:
@@ -191,11 +201,11 @@ def gqa_qkv_fused(outs: Sequence[Ptr], ws: Sequence[Ptr], types: Sequence[int],
 def qkv_prologue(q: Ptr, k: Ptr, v: Ptr, k_seq: Ptr, v_seq: Ptr, pos_0: Ptr, n_seq: int,
                  n_rows: int, n_head_q: int, n_head_kv: int, head_dim: int, q_norm_w: Ptr,
                  k_norm_w: Ptr, eps: float, cos_lut: Ptr, sin_lut: Ptr, window_len: int = 0,
-                 cap: int = 0, stream=None) -> None:
+                 cap: int = 0, stream=None, prologue: int = PROLOGUE_FAST) -> None:
     check(load().lfm_hip_qkv_prologue(_p(q), _p(k), _p(v), _p(k_seq), _p(v_seq), _p(pos_0), n_seq,
                                       n_rows, n_head_q, n_head_kv, head_dim, _p(q_norm_w),
                                       _p(k_norm_w), eps, _p(cos_lut), _p(sin_lut), window_len, cap,
-                                      stream), "lfm_hip_qkv_prologue")
+                                      prologue, stream), "lfm_hip_qkv_prologue")
 
 
 def online_gqa_f16(q: Ptr, k_cache_f16: Ptr, v_cache_f16: Ptr, xb_out: Ptr, n_head_q: int,
@@ -261,7 +271,7 @@ def gqa_f16_step(q: Ptr, k: Ptr, v: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: 
                  pos_0: Ptr, out: Ptr, n_seq: int, n_rows: int, keys_hint: int, n_head_q: int,
                  n_head_kv: int, head_dim: int, q_norm_w: Ptr, k_norm_w: Ptr, eps: float,
                  cos_lut: Ptr, sin_lut: Ptr, window_len: int = 0, cap: int = 0,
-                 scale: Optional[float] = None, stream=None) -> None:
+                 scale: Optional[float] = None, stream=None, prologue: int = PROLOGUE_FAST) -> None:
     """One attention step with the prologue fused: raw q/k/v rows in, the new
     rows stored in the caches, attention out (lfm_hip_gqa_f16_step)."""
     if scale is None:
@@ -269,7 +279,7 @@ def gqa_f16_step(q: Ptr, k: Ptr, v: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: 
     check(load().lfm_hip_gqa_f16_step(_p(q), _p(k), _p(v), _p(gate), int(bool(gate_is_logit)), _p(k_seq),
                                       _p(v_seq), _p(pos_0), _p(out), n_seq, n_rows, keys_hint, n_head_q,
                                       n_head_kv, head_dim, window_len, cap, scale, _p(q_norm_w),
-                                      _p(k_norm_w), eps, _p(cos_lut), _p(sin_lut), stream),
+                                      _p(k_norm_w), eps, _p(cos_lut), _p(sin_lut), prologue, stream),
           "lfm_hip_gqa_f16_step")
 
 
@@ -285,6 +295,40 @@ def gqa_f16_varlen_noalloc(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v
                                                 _p(v_seq), _p(pos_0), _p(out), n_seq, n_rows,
                                                 keys_hint, n_head_q, n_head_kv, head_dim, window_len,
                                                 cap, scale, stream), "lfm_hip_gqa_f16_varlen_noalloc")
+
+
+def set_tuning(plan: Optional[str] = None, waves: int = 0, chunk: int = 0, min_tiles: int = 0) -> None:
+    """Launch-plan overrides for tests and tuning (lfm_attn_set_tuning):
+    plan None / "grid" / "balanced" / "wg", counts 0 = automatic."""
+    check(load().lfm_attn_set_tuning(None if plan is None else plan.encode(), waves, chunk, min_tiles),
+          "lfm_attn_set_tuning")
+
+
+class tuning:
+    """Context manager: the overrides inside, automatic choice afterwards."""
+
+    def __init__(self, plan: Optional[str] = None, waves: int = 0, chunk: int = 0, min_tiles: int = 0):
+        self.args = (plan, waves, chunk, min_tiles)
+
+    def __enter__(self):
+        set_tuning(*self.args)
+        return self
+
+    def __exit__(self, *exc):
+        set_tuning()
+        return False
+
+
+def plan_preview(n_seq: int, n_rows: int, n_head_q: int, n_head_kv: int, head_dim: int, window_len: int = 0,
+                 keys_hint: int = 0, positions_on_device: bool = True, fused: bool = False, n_cus: int = 256):
+    """(plan, waves, grid splits, grid chunk) the split-KV attention takes for
+    a batch, computed on the host (lfm_attn_plan_preview)."""
+    name = C.c_char_p()
+    out = (C.c_uint32 * 3)()
+    check(load().lfm_attn_plan_preview(n_seq, n_rows, n_head_q, n_head_kv, head_dim, window_len, keys_hint,
+                                       int(positions_on_device), int(fused), n_cus, C.byref(name), out),
+          "lfm_attn_plan_preview")
+    return name.value.decode(), int(out[0]), int(out[1]), int(out[2])
 
 
 def last_plan() -> str:
@@ -391,7 +435,7 @@ class EngineContext:
 
     def __init__(self, n_layers, n_head_q, n_head_kv, head_dim, max_seq, eps=1e-5,
                  rope_base=1e6, lfm3=False, sliding_window=0, swa_cap=0, layer_is_swa=None,
-                 rope_base_swa=1e4, rope_dim=0, rope_freqs=None):
+                 rope_base_swa=1e4, rope_dim=0, rope_freqs=None, prologue=PROLOGUE_FAST):
         self._keep = []
         g = Geom()
         g.n_layers, g.n_head_q, g.n_head_kv, g.head_dim = n_layers, n_head_q, n_head_kv, head_dim
@@ -407,6 +451,7 @@ class EngineContext:
             g.rope_freqs = rf.ctypes.data_as(C.POINTER(C.c_float))
             g.n_rope_freqs = rf.size
         g.lfm3 = 1 if lfm3 else 0
+        g.prologue = int(prologue)
         self.n_head_q, self.n_head_kv, self.head_dim = n_head_q, n_head_kv, head_dim
         h = C.c_void_p()
         check(load().lfm_attn_ctx_create(C.byref(h), C.byref(g)), "lfm_attn_ctx_create")

@@ -34,6 +34,11 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
 #include "attn_index.h"
 #include "kernels.h"
 #include "splitkv_plan.h"
@@ -88,6 +93,7 @@ struct SplitParams {
      * RoPE tables (AttnBatch) */
     const float *k_new, *v_new, *q_norm_w, *k_norm_w, *cos_lut, *sin_lut;
     float eps;
+    int prologue; /* LFM_PROLOGUE_FAST / LFM_PROLOGUE_TABLE */
 };
 
 __device__ __forceinline__ half8_t as_half8(u32x4_t v) { return __builtin_bit_cast(half8_t, v); }
@@ -199,6 +205,32 @@ __device__ __forceinline__ float sumsq_ref_order(const float (&x)[HD / 32][8], i
     }
 }
 
+/* Mean of squares of one head in the order of lfm2_rmsnorm
+ * (tools/lfm2_forward.c:669-684), the norm of the production LFM2 prologue
+ * (LFM_PROLOGUE_TABLE): column j is a fused multiply-add chain over dims
+ * 8k + j, k = 0 .. HD/8 - 1 in order, and the eight columns are then added
+ * in order in double; the result is (float)(sum / HD).  Dim 8k + j sits in
+ * fragment k / 4 of lane group g = k % 4, so the chain passes from group to
+ * group: at each step every lane forms fma(x, x, acc) with its own x and the
+ * value of group k % 4 is broadcast to the four lanes of the column.
+ * Returned on every lane. */
+template <int HD>
+__device__ __forceinline__ float meansq_table_order(const float (&x)[HD / 32][8], int l16) {
+#pragma clang fp contract(off)
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < HD / 32; ++st)
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                acc[j] = __shfl(__builtin_fmaf(x[st][j], x[st][j], acc[j]), l16 + 16 * gg);
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += (double)acc[j];
+    return (float)(ss / (double)HD);
+}
+
 /* QK-RMSNorm + NeoX RoPE of one head held in MFMA fragment order: lane
  * (l16, g) holds dims 32*st + 8*g + j (st < HD/32, j < 8) of the head of
  * its column, and the four lanes g = 0..3 of an l16 hold the whole head.
@@ -218,11 +250,12 @@ __device__ __forceinline__ void load8(const float *p, float (&x)[8]) {
 
 template <int HD>
 __device__ __forceinline__ void norm_rope_frag(float (&x)[HD / 32][8], uint32_t pos, const float *norm_w, float eps,
-                                               const float *cos_lut, const float *sin_lut, int g) {
+                                               const float *cos_lut, const float *sin_lut, int g, int prologue) {
     constexpr int NS = HD / 32, HALF = HD / 2;
     if (norm_w) {
-        const float ss   = sumsq_ref_order<HD>(x, g);
-        const float irms = 1.0f / sqrtf(ss / (float)HD + eps);
+        const float mean = prologue == LFM_PROLOGUE_TABLE ? meansq_table_order<HD>(x, (int)(threadIdx.x & 15u))
+                                                          : sumsq_ref_order<HD>(x, g) / (float)HD;
+        const float irms = 1.0f / sqrtf(mean + eps);
 #pragma unroll
         for (int st = 0; st < NS; ++st) {
             float w[8];
@@ -405,12 +438,20 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         }
         /* fused prologue: the raw query is normalised and rotated here, by
          * every wave that reads it (all lanes take part in the sums) */
-        if constexpr (FUSE) norm_rope_frag<HD>(x, abs, P.q_norm_w, P.eps, P.cos_lut, P.sin_lut, g);
+        if constexpr (FUSE) norm_rope_frag<HD>(x, abs, P.q_norm_w, P.eps, P.cos_lut, P.sin_lut, g, P.prologue);
 #pragma unroll
         for (int st = 0; st < NS; ++st)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float xs    = x[st][j] * P.qscale;
+                /* xs is rounded to fp32 before the split: otherwise the
+                 * compiler may fuse the product into a mixed-precision fma
+                 * that rounds x*qscale - hi straight to fp16 in some
+                 * instantiations and not others, and the lo parts of the
+                 * fused and plain kernels then differ on double-rounding
+                 * ties (about one element in 8000).  With xs rounded, xs - hi
+                 * is exact and lo is its only rounding. */
+                float xs = x[st][j] * P.qscale;
+                asm volatile("" : "+v"(xs));
                 const _Float16 hi = (_Float16)xs;
                 qh[nt][st][j]     = hi;
                 ql[nt][st][j]     = (_Float16)(xs - (float)hi);
@@ -454,7 +495,8 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
 #pragma unroll
                         for (int j = 0; j < 8; ++j) x[st][j] = 0.0f;
                 }
-                norm_rope_frag<HD>(x, real ? pos0 + r : pos0, P.k_norm_w, P.eps, P.cos_lut, P.sin_lut, g);
+                norm_rope_frag<HD>(x, real ? pos0 + r : pos0, P.k_norm_w, P.eps, P.cos_lut, P.sin_lut, g,
+                                   P.prologue);
                 if (real) {
                     const size_t off = (size_t)lfm_slot_of(pos0 + r, P.window, P.cap) * row + 8 * g;
 #pragma unroll
@@ -1245,17 +1287,51 @@ hipError_t launch_hd_nt_w(const SplitParams &p, uint32_t n_seq, hipStream_t stre
     return hipGetLastError();
 }
 
-/* Compute units of the current device (queried once). */
+/* ---- host side: device facts, overrides, plan choice, launches ------------ */
+
+constexpr int kMaxDevices = 64;
+
+/* Compute units of the current device, queried once per device. */
+std::atomic<uint32_t> g_cus[kMaxDevices];
 uint32_t device_cus() {
-    static uint32_t cus = 0;
-    if (!cus) {
-        int dev = 0, n = 0;
-        cus = (hipGetDevice(&dev) == hipSuccess &&
-               hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-                  ? (uint32_t)n
-                  : 256u;
-    }
-    return cus;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256u;
+    uint32_t c = dev < kMaxDevices ? g_cus[dev].load(std::memory_order_relaxed) : 0u;
+    if (c) return c;
+    int n = 0;
+    c = (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0) ? (uint32_t)n
+                                                                                                      : 256u;
+    if (dev < kMaxDevices) g_cus[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
+
+/* Launch-plan overrides for tests and tuning (lfm_attn_set_tuning).  The
+ * environment (LFM_ATTN_PLAN, _WAVES, _CHUNK, _MINTILES) seeds them once, at
+ * the first launch or the first lfm_attn_set_tuning; launches read only
+ * these values. */
+std::atomic<uint32_t> g_plan{0}, g_waves{0}, g_chunk{0}, g_min_tiles{0};
+std::once_flag g_tuning_once;
+
+int plan_code(const char *name) {
+    if (!name || !name[0] || !strcmp(name, "auto")) return 0;
+    if (!strcmp(name, "grid")) return 'g';
+    if (!strcmp(name, "balanced")) return 'b';
+    if (!strcmp(name, "wg")) return 'w';
+    return -1;
+}
+
+uint32_t env_count(const char *name) {
+    const char *e = getenv(name);
+    const long v  = e ? strtol(e, nullptr, 10) : 0;
+    return v > 0 && v < 0x7fffffffL ? (uint32_t)v : 0u;
+}
+
+void seed_tuning() {
+    const int pc = plan_code(getenv("LFM_ATTN_PLAN"));
+    g_plan.store(pc > 0 ? (uint32_t)pc : 0u);
+    g_waves.store(env_count("LFM_ATTN_WAVES"));
+    g_chunk.store(env_count("LFM_ATTN_CHUNK"));
+    g_min_tiles.store(env_count("LFM_ATTN_MINTILES"));
 }
 
 /* Split partials: the caller's scratch (the allocation-free entry point) or
@@ -1271,39 +1347,49 @@ void *split_ws(size_t bytes, hipStream_t stream, const Scratch *sc, int *st) {
 
 /* Waves per workgroup: W adjacent KV heads over one key chunk.  Measured on
  * MI355X: all KV heads of a row together (W = n_head_kv, up to 8) for
- * head_dim 64; W = 2 for head_dim 128, whose waves are register-heavy.
- * LFM_ATTN_WAVES overrides (tuning). */
-uint32_t choose_waves(uint32_t n_head_kv, uint32_t head_dim) {
+ * head_dim 64; W = 2 for head_dim 128, whose waves are register-heavy. */
+uint32_t choose_waves(uint32_t n_head_kv, uint32_t head_dim, const Tuning &t) {
     uint32_t w = head_dim == 64u ? 8u : 2u;
-    const char *env = getenv("LFM_ATTN_WAVES");
-    if (env && atoi(env) > 0) w = (uint32_t)atoi(env);
+    if (t.waves) w = t.waves;
     while (w > 1u && w > n_head_kv) w >>= 1;
     return w >= 8u ? 8u : (w >= 4u ? 4u : (w >= 2u ? 2u : 1u));
 }
 
+/* Dynamic LDS of a fused-prologue workgroup of w waves (its staged new K/V
+ * rows) and the V tiles every workgroup holds: together within 64 KB. */
+size_t fresh_bytes_rt(uint32_t head_dim, bool fuse, uint32_t w, uint32_t n_rows) {
+    return fuse ? (size_t)w * 2u * n_rows * head_dim * sizeof(uint16_t) : 0u;
+}
+bool lds_fits(uint32_t head_dim, bool fuse, uint32_t w, uint32_t n_rows) {
+    return (size_t)w * 32u * head_dim * sizeof(uint16_t) + fresh_bytes_rt(head_dim, fuse, w, n_rows) <= 65536u;
+}
+
 /* Workgroups of k_splitkv_bal<HD, NT, W, FUSE> resident on the whole
  * device at once, with `dyn` bytes of dynamic LDS each (queried once per
- * instantiation and LDS size). */
+ * device, instantiation and LDS size). */
 template <int HD, int NT, int W, bool FUSE>
 uint32_t resident_wgs(size_t dyn) {
-    static uint32_t cached = 0;
-    static size_t cached_dyn = 0;
-    if (cached && cached_dyn == dyn) return cached;
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE>, 64 * W,
+    static std::atomic<uint64_t> cached[kMaxDevices]; /* (dyn + 1) << 32 | workgroups */
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256u;
+    const uint64_t tag = (uint64_t)(dyn + 1u) << 32;
+    if (dev < kMaxDevices) {
+        const uint64_t v = cached[dev].load(std::memory_order_relaxed);
+        if ((v & ~0xffffffffull) == tag) return (uint32_t)v;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE>, 64 * W,
                                                      dyn) != hipSuccess)
         return 256u;
-    cached     = (uint32_t)((cus > 0 ? cus : 1) * (per_cu > 0 ? per_cu : 1));
-    cached_dyn = dyn;
-    return cached;
+    const uint32_t n = device_cus() * (uint32_t)(per_cu > 0 ? per_cu : 1);
+    if (dev < kMaxDevices) cached[dev].store(tag | n, std::memory_order_relaxed);
+    return n;
 }
 
 /* Balanced plan: launch sized for the plan the device will pick, partial
  * slots and the tile prefix table in the workspace, then the merge. */
 template <int HD, int NT, int W, bool FUSE>
-int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scratch *sc) {
+int launch_bal(SplitParams p, uint32_t keys_hint, const Tuning &t, hipStream_t stream, const Scratch *sc) {
     const uint32_t cus = device_cus();
     lfm_bal_cfg &c     = p.plan;
     p.wpg              = W;
@@ -1332,19 +1418,15 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
     const uint64_t fill  = t_max * 3u / (2u * (uint64_t)(c.n_res ? c.n_res : 1u));
     if (fill < c.min_tiles) c.min_tiles = (uint32_t)fill;
     if (c.min_tiles < 2u) c.min_tiles = 2u;
-    if (const char *env = getenv("LFM_ATTN_MINTILES")) /* tuning */
-        if (atoi(env) > 0) c.min_tiles = (uint32_t)atoi(env);
-    if (const char *env = getenv("LFM_ATTN_CHUNK")) {
-        /* about c keys per workgroup (tests, tuning): enough workgroups for
-         * the longest sequences keys_hint allows; longer ones get more keys */
-        const int ck = atoi(env);
-        if (ck > 0) {
-            c.min_tiles    = (uint32_t)(ck + 31) / 32u;
-            c.n_res        = 0x7fffffffu;
-            c.target_waves = 0x7fffffffu;
-            keys           = p.pos0_dev ? keys_hint : p.pos0_host + p.n_rows;
-            if (keys == 0u) keys = p.window ? p.window + p.n_rows - 1u : 4096u;
-        }
+    if (t.min_tiles) c.min_tiles = t.min_tiles;
+    if (t.chunk) {
+        /* about `chunk` keys per workgroup: enough workgroups for the longest
+         * sequences keys_hint allows; longer ones get more keys */
+        c.min_tiles    = (t.chunk + 31u) / 32u;
+        c.n_res        = 0x7fffffffu;
+        c.target_waves = 0x7fffffffu;
+        keys           = p.pos0_dev ? keys_hint : p.pos0_host + p.n_rows;
+        if (keys == 0u) keys = p.window ? p.window + p.n_rows - 1u : 4096u;
     }
     c.n_wg                  = lfm_bal_launch_wgs(&c, keys);
     const uint64_t n_launch = c.n_wg;
@@ -1370,97 +1452,15 @@ int launch_bal(SplitParams p, uint32_t keys_hint, hipStream_t stream, const Scra
     return hip_status(hipGetLastError());
 }
 
-/* Plan choice.  A batch whose sequences may differ in length (positions on
- * the device, more than one sequence) takes the balanced plan: measured on
- * MI355X, 64 sequences of 512..8192 keys run 23 % faster than on the
- * fixed-chunk grid, which leaves XCDs idle.  A batch that cannot be ragged
- * (one sequence, or one shared host position) takes the grid, which skips the
- * plan's position scan and table (1-9 % faster on equal-length batches).  So
- * does a sliding-window batch: no row reads more than window keys, which
- * bounds how ragged it can be (config 5's ring, B32 x 256 keys: 10.7 vs
- * 11.9 us per call).  LFM_ATTN_PLAN=grid|balanced|wg overrides (tuning and
- * tests). */
-bool use_grid_plan(const AttnBatch &b) {
-    const char *env = getenv("LFM_ATTN_PLAN");
-    if (env && (env[0] == 'g' || env[0] == 'w')) return true; /* wg: a form of the grid */
-    if (env && env[0] == 'b') return false;
-    return !b.pos0_dev || b.n_seq == 1u || b.window != 0u;
-}
+/* Waves of the in-workgroup form: 8 (4 at head_dim 128 or 64 query columns,
+ * whose waves need more than the 256 registers an 8-wave workgroup leaves
+ * them). */
+uint32_t wg_waves(uint32_t head_dim, uint32_t nt) { return (head_dim == 64u && nt <= 2u) ? 8u : 4u; }
 
-/* One workgroup per (sequence, KV head), the key splits as its waves and the
- * merge inside it (k_splitkv_wg): taken by grid-plan batches of at most as
- * many pairs as compute units whose planned splits fit the workgroup's waves
- * (short contexts, sliding windows), where a second (merge) launch would
- * cost about as much as the attention itself.  Measured on MI355X (us per
- * call, grid + merge kernel -> this form): SWA window 256, d128 16q/4kv, B16
- * 11.2 -> 10.8, B32 12.3 -> 11.2, B64 15.2 -> 12.5; d64 32q/8kv, B32 11.3 ->
- * 8.5; with more planned splits than waves (window 512: 8 splits, 4 waves)
- * the grid stays faster (15.6 vs 17.4).  LFM_ATTN_PLAN=grid keeps such a
- * batch on the two-kernel grid, =wg forces this form. */
-bool use_wg_plan(const SplitParams &p, uint32_t n_seq, uint32_t ww) {
-    const char *env = getenv("LFM_ATTN_PLAN");
-    if (env && env[0] == 'w') return p.n_splits >= 2u;
-    if (env && env[0] == 'g') return false;
-    if (getenv("LFM_ATTN_WAVES") || getenv("LFM_ATTN_CHUNK")) return false;
-    /* only when the planned splits fit the workgroup's waves as they are:
-     * lengthening them measured slower than the second launch (B1 ctx 1024,
-     * 16 splits on 8 waves: 10.3 vs 8.5 us) */
-    return p.n_splits >= 2u && p.n_splits <= ww && (uint64_t)n_seq * p.n_head_kv <= device_cus();
-}
-
-template <int HD, int NT>
-constexpr uint32_t wg_waves() {
-    /* 8 waves (4 at head_dim 128 or 64 query columns, whose waves need more
-     * than the 256 registers an 8-wave workgroup leaves them) */
-    return (HD == 64 && NT <= 2) ? 8u : 4u;
-}
-
-template <int HD, int NT, bool FUSE>
-int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
-    constexpr int WW = (int)wg_waves<HD, NT>();
-    if (p.n_splits > (uint32_t)WW) p.n_splits = WW; /* forced: the kernel lengthens the chunks */
-    hipEvent_t ev0, ev1;
-    profile_events(&ev0, &ev1);
-    if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW, FUSE>), dim3(p.n_head_kv, n_seq), dim3(64 * WW),
-                       (fresh_bytes<HD, FUSE>(WW, p.n_rows)), stream, p);
-    const hipError_t e = hipGetLastError();
-    if (ev1) (void)hipEventRecord(ev1, stream);
-    return hip_status(e);
-}
-
-template <int HD, int NT, bool FUSE>
-int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool grid, hipStream_t stream,
-                 const Scratch *sc) {
-    if (grid && use_wg_plan(p, n_seq, wg_waves<HD, NT>())) {
-        note_plan("wg");
-        return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
-    }
-    note_plan(grid ? "grid" : "balanced");
-    uint32_t w = choose_waves(p.n_head_kv, HD);
-    /* fused prologue: the staged new rows and the V tiles stay within
-     * 64 KB of LDS per workgroup */
-    if (FUSE)
-        while (w > 1u && (size_t)w * vt_halfs<HD>() * sizeof(uint16_t) + fresh_bytes<HD, FUSE>(w, p.n_rows) > 65536u)
-            w >>= 1;
-    /* a grid of fewer workgroups than compute units (one short sequence)
-     * spreads its KV heads over more, smaller workgroups: measured on MI355X
-     * at B1, 8 KV heads, ctx 256-4096, 9.6-12.0 us -> 8.2-10.5 us per call
-     * (8-row verify at ctx 4096: 29.2 -> 22.0 us); larger grids unchanged */
-    if (grid && !getenv("LFM_ATTN_WAVES"))
-        while (w > 1u && (uint64_t)p.n_splits * ((p.n_head_kv + w - 1u) / w) * n_seq < device_cus()) w >>= 1;
-    if (!grid) {
-        if (w == 8u) return launch_bal<HD, NT, 8, FUSE>(p, keys_hint, stream, sc);
-        if (w == 4u) return launch_bal<HD, NT, 4, FUSE>(p, keys_hint, stream, sc);
-        if (w == 2u) return launch_bal<HD, NT, 2, FUSE>(p, keys_hint, stream, sc);
-        return launch_bal<HD, NT, 1, FUSE>(p, keys_hint, stream, sc);
-    }
-    hipError_t e;
-    if (w == 8u) e = launch_hd_nt_w<HD, NT, 8, FUSE>(p, n_seq, stream);
-    else if (w == 4u) e = launch_hd_nt_w<HD, NT, 4, FUSE>(p, n_seq, stream);
-    else if (w == 2u) e = launch_hd_nt_w<HD, NT, 2, FUSE>(p, n_seq, stream);
-    else e = launch_hd_nt_w<HD, NT, 1, FUSE>(p, n_seq, stream);
-    return hip_status(e);
+/* 16-column tiles of the kernel instantiation a batch runs on. */
+uint32_t tiles_of(uint32_t head_dim, uint32_t ncols) {
+    const uint32_t nt = (ncols + 15u) / 16u;
+    return head_dim == 64u ? (nt <= 2u ? nt : 4u) : (nt <= 1u ? 1u : 2u);
 }
 
 /* Key chunk per wave (multiple of 32) and the number of chunks the grid
@@ -1468,8 +1468,8 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, bool 
  * follows the number of waves; about 4096 waves over the batch measured best
  * on MI355X (two residency rounds).  Chunks stay >= 16 x the query columns so
  * the split partials remain a small fraction of the KV bytes.
- * keys_hint bounds the keys per row; LFM_ATTN_CHUNK overrides. */
-void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, uint32_t *chunk) {
+ * keys_hint bounds the keys per row; the chunk override replaces the choice. */
+void choose_split(const AttnBatch &b, uint32_t keys_hint, const Tuning &t, uint32_t *n_splits, uint32_t *chunk) {
     uint32_t keys = keys_hint;
     if (keys == 0u) keys = b.window ? b.window + b.n_rows - 1u : 4096u;
     if (b.window && keys > b.window + b.n_rows - 1u) keys = b.window + b.n_rows - 1u;
@@ -1482,8 +1482,7 @@ void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, ui
      * large: keep a split at least 12 keys per column (measured on MI355X
      * for 8 rows x 4 heads: 384-key chunks beat 256 and 512 by 16 %) */
     if (c < 12 * ncols) c = 12 * ncols;
-    const char *env = getenv("LFM_ATTN_CHUNK");
-    if (env && atoi(env) > 0) c = (uint64_t)atoi(env);
+    if (t.chunk) c = t.chunk;
     c = (c + 31) & ~(uint64_t)31;
     uint64_t n = (keys + c - 1) / c;
     if (n > 1024) { n = 1024; c = (((keys + n - 1) / n) + 31) & ~(uint64_t)31; }
@@ -1491,21 +1490,134 @@ void choose_split(const AttnBatch &b, uint32_t keys_hint, uint32_t *n_splits, ui
     *chunk    = (uint32_t)c;
 }
 
+/* Launches of the chosen plan, per kernel instantiation. */
+template <int HD, int NT, bool FUSE>
+int launch_wg(SplitParams p, uint32_t n_seq, hipStream_t stream) {
+    constexpr int WW = HD == 64 && NT <= 2 ? 8 : 4;
+    if (p.n_splits > (uint32_t)WW) p.n_splits = WW; /* forced: the kernel lengthens the chunks */
+    hipEvent_t ev0, ev1;
+    profile_events(&ev0, &ev1);
+    if (ev0) (void)hipEventRecord(ev0, stream);
+    hipLaunchKernelGGL((k_splitkv_wg<HD, NT, WW, FUSE>), dim3(p.n_head_kv, n_seq), dim3(64 * WW),
+                       (fresh_bytes<HD, FUSE>(WW, p.n_rows)), stream, p);
+    const hipError_t e = hipGetLastError();
+    if (ev1) (void)hipEventRecord(ev1, stream);
+    return hip_status(e);
+}
+
+template <int HD, int NT, bool FUSE>
+int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, const PlanChoice &pc, const Tuning &t,
+                 hipStream_t stream, const Scratch *sc) {
+    /* a grid form with split keys writes partial slots: never launch one
+     * without them */
+    if (pc.kind != 'b' && p.n_splits > 1u && (!p.part_o || !p.part_ml)) return LFM_ATTN_E_INVALID;
+    note_plan(pc.kind == 'w' ? "wg" : pc.kind == 'g' ? "grid" : "balanced");
+    if (pc.kind == 'w') return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
+    const uint32_t w = pc.waves;
+    if (pc.kind == 'b') {
+        if (w == 8u) return launch_bal<HD, NT, 8, FUSE>(p, keys_hint, t, stream, sc);
+        if (w == 4u) return launch_bal<HD, NT, 4, FUSE>(p, keys_hint, t, stream, sc);
+        if (w == 2u) return launch_bal<HD, NT, 2, FUSE>(p, keys_hint, t, stream, sc);
+        return launch_bal<HD, NT, 1, FUSE>(p, keys_hint, t, stream, sc);
+    }
+    hipError_t e;
+    if (w == 8u) e = launch_hd_nt_w<HD, NT, 8, FUSE>(p, n_seq, stream);
+    else if (w == 4u) e = launch_hd_nt_w<HD, NT, 4, FUSE>(p, n_seq, stream);
+    else if (w == 2u) e = launch_hd_nt_w<HD, NT, 2, FUSE>(p, n_seq, stream);
+    else e = launch_hd_nt_w<HD, NT, 1, FUSE>(p, n_seq, stream);
+    return hip_status(e);
+}
+
 /* Head dim and 16-column tiles of the batch -> kernel instantiation. */
 template <bool FUSE>
-int dispatch_nt(const SplitParams &p, const AttnBatch &b, uint32_t keys_hint, bool grid, hipStream_t stream,
-                const Scratch *sc) {
-    const uint32_t nt = (p.ncols + 15u) / 16u;
+int dispatch_nt(const SplitParams &p, const AttnBatch &b, uint32_t keys_hint, const PlanChoice &pc, const Tuning &t,
+                hipStream_t stream, const Scratch *sc) {
+    const uint32_t nt = tiles_of(b.head_dim, p.ncols);
     if (b.head_dim == 64u) {
-        if (nt == 1u) return launch_hd_nt<64, 1, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
-        if (nt == 2u) return launch_hd_nt<64, 2, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
-        return launch_hd_nt<64, 4, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
+        if (nt == 1u) return launch_hd_nt<64, 1, FUSE>(p, b.n_seq, keys_hint, pc, t, stream, sc);
+        if (nt == 2u) return launch_hd_nt<64, 2, FUSE>(p, b.n_seq, keys_hint, pc, t, stream, sc);
+        return launch_hd_nt<64, 4, FUSE>(p, b.n_seq, keys_hint, pc, t, stream, sc);
     }
-    if (nt == 1u) return launch_hd_nt<128, 1, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
-    return launch_hd_nt<128, 2, FUSE>(p, b.n_seq, keys_hint, grid, stream, sc);
+    if (nt == 1u) return launch_hd_nt<128, 1, FUSE>(p, b.n_seq, keys_hint, pc, t, stream, sc);
+    return launch_hd_nt<128, 2, FUSE>(p, b.n_seq, keys_hint, pc, t, stream, sc);
 }
 
 } // namespace
+
+/* Plan choice (host only, no device access):
+ *  - grid or balanced: a batch whose sequences may differ in length
+ *    (positions on the device, more than one sequence) takes the balanced
+ *    plan: measured on MI355X, 64 sequences of 512..8192 keys run 23 %
+ *    faster than on the fixed-chunk grid, which leaves XCDs idle.  A batch
+ *    that cannot be ragged (one sequence, or one shared host position) takes
+ *    the grid, which skips the plan's position scan and table (1-9 % faster
+ *    on equal-length batches).  So does a sliding-window batch: no row reads
+ *    more than window keys, which bounds how ragged it can be (config 5's
+ *    ring, B32 x 256 keys: 10.7 vs 11.9 us per call).
+ *  - the grid's in-workgroup form (k_splitkv_wg: one workgroup per (sequence,
+ *    KV head), the key splits as its waves, the merge inside it): for grid
+ *    batches of at most as many pairs as compute units whose planned splits
+ *    fit the workgroup's waves (short contexts, sliding windows), where a
+ *    second (merge) launch would cost about as much as the attention itself.
+ *    Measured on MI355X (us per call, grid + merge kernel -> this form): SWA
+ *    window 256, d128 16q/4kv, B16 11.2 -> 10.8, B32 12.3 -> 11.2, B64 15.2
+ *    -> 12.5; d64 32q/8kv, B32 11.3 -> 8.5; with more planned splits than
+ *    waves (window 512: 8 splits, 4 waves) the grid stays faster (15.6 vs
+ *    17.4), and lengthening the splits to fit measured slower than the
+ *    second launch (B1 ctx 1024, 16 splits on 8 waves: 10.3 vs 8.5 us).
+ *  - waves per workgroup (choose_waves), fewer where a fused prologue's
+ *    staged rows and the V tiles would pass 64 KB of LDS, and a grid of
+ *    fewer workgroups than compute units (one short sequence) spreads its KV
+ *    heads over more, smaller workgroups: measured on MI355X at B1, 8 KV
+ *    heads, ctx 256-4096, 9.6-12.0 us -> 8.2-10.5 us per call (8-row verify
+ *    at ctx 4096: 29.2 -> 22.0 us); larger grids unchanged.
+ * The overrides force a plan ('g', 'b', 'w'), waves or a chunk; a waves or
+ * chunk override keeps the grid off its in-workgroup form. */
+PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on_device, bool fuse, uint32_t cus,
+                       const Tuning &t) {
+    PlanChoice pc{};
+    const uint32_t ncols  = b.n_rows * (b.n_head_q / b.n_head_kv);
+    bool grid             = !positions_on_device || b.n_seq == 1u || b.window != 0u;
+    if (t.plan == 'g' || t.plan == 'w') grid = true;
+    if (t.plan == 'b') grid = false;
+    if (grid) {
+        choose_split(b, keys_hint, t, &pc.n_splits, &pc.chunk);
+        const uint32_t ww = wg_waves(b.head_dim, tiles_of(b.head_dim, ncols));
+        bool wg = false;
+        if (t.plan == 'w') wg = pc.n_splits >= 2u;
+        else if (t.plan != 'g' && !t.waves && !t.chunk)
+            wg = pc.n_splits >= 2u && pc.n_splits <= ww && (uint64_t)b.n_seq * b.n_head_kv <= cus;
+        if (wg && lds_fits(b.head_dim, fuse, ww, b.n_rows)) {
+            pc.kind  = 'w';
+            pc.waves = ww;
+            if (pc.n_splits > ww) pc.n_splits = ww;
+            return pc;
+        }
+    }
+    uint32_t w = choose_waves(b.n_head_kv, b.head_dim, t);
+    while (w > 1u && !lds_fits(b.head_dim, fuse, w, b.n_rows)) w >>= 1;
+    if (grid && !t.waves)
+        while (w > 1u && (uint64_t)pc.n_splits * ((b.n_head_kv + w - 1u) / w) * b.n_seq < cus) w >>= 1;
+    pc.kind  = grid ? 'g' : 'b';
+    pc.waves = w;
+    return pc;
+}
+
+Tuning current_tuning() {
+    std::call_once(g_tuning_once, seed_tuning);
+    return Tuning{(char)g_plan.load(), g_waves.load(), g_chunk.load(), g_min_tiles.load()};
+}
+
+int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles) {
+    const int pc = plan_code(plan);
+    if (pc < 0 || (waves && waves != 1u && waves != 2u && waves != 4u && waves != 8u)) return LFM_ATTN_E_INVALID;
+    std::call_once(g_tuning_once, seed_tuning);
+    g_plan.store((uint32_t)pc);
+    g_waves.store(waves);
+    g_chunk.store(chunk);
+    g_min_tiles.store(min_tiles);
+    return LFM_ATTN_OK;
+}
 
 bool splitkv_supports(const AttnBatch &b) {
     if (b.head_dim != 64u && b.head_dim != 128u) return false;
@@ -1550,11 +1662,15 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, c
     p.cos_lut       = b.cos_lut;
     p.sin_lut       = b.sin_lut;
     p.eps           = b.eps;
-    const bool grid = use_grid_plan(b);
-    if (!grid) return b.k_new ? dispatch_nt<true>(p, b, keys_hint, grid, stream, sc)
-                              : dispatch_nt<false>(p, b, keys_hint, grid, stream, sc);
-    choose_split(b, keys_hint, &p.n_splits, &p.chunk);
-    if (p.n_splits > 1u) {
+    p.prologue      = b.prologue;
+    const Tuning t       = current_tuning();
+    const PlanChoice pc  = choose_plan(b, keys_hint, b.pos0_dev != nullptr, b.k_new != nullptr, device_cus(), t);
+    p.n_splits = pc.n_splits;
+    p.chunk    = pc.chunk;
+    /* both grid forms keep per-split partials in the workspace (the
+     * in-workgroup form merges them after a barrier); the balanced plan
+     * sizes its own */
+    if (pc.kind != 'b' && p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
         const size_t bytes  = n_part * b.head_dim * sizeof(float) + n_part * sizeof(float2) + 256;
         int st              = LFM_ATTN_OK;
@@ -1563,8 +1679,8 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, c
         p.part_o  = reinterpret_cast<float *>(ws);
         p.part_ml = reinterpret_cast<float2 *>(ws + ((n_part * b.head_dim * sizeof(float) + 255) & ~(size_t)255));
     }
-    return b.k_new ? dispatch_nt<true>(p, b, keys_hint, grid, stream, sc)
-                   : dispatch_nt<false>(p, b, keys_hint, grid, stream, sc);
+    return b.k_new ? dispatch_nt<true>(p, b, keys_hint, pc, t, stream, sc)
+                   : dispatch_nt<false>(p, b, keys_hint, pc, t, stream, sc);
 }
 
 } // namespace lfm

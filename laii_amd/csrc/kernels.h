@@ -40,6 +40,7 @@ struct AttnBatch {
     const float *q_norm_w = nullptr, *k_norm_w = nullptr; /* [head_dim] or null (no norm) */
     const float *cos_lut = nullptr, *sin_lut = nullptr;   /* [position][head_dim / 2]     */
     float eps = 0.0f;
+    int prologue = 0; /* LFM_PROLOGUE_FAST / LFM_PROLOGUE_TABLE: RMSNorm sum order */
 };
 
 /* Device workspace owned by the shim (grown on demand). */
@@ -59,6 +60,26 @@ struct Scratch {
  * not fit), else to the library workspace. */
 int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, const Scratch *sc = nullptr);
 bool splitkv_supports(const AttnBatch &b);
+
+/* Launch-plan overrides (tests, tuning): plan 0 automatic, 'g' grid, 'b'
+ * balanced, 'w' in-workgroup merge; 0 = automatic for the counts. */
+struct Tuning {
+    char plan;
+    uint32_t waves, chunk, min_tiles;
+};
+int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles);
+Tuning current_tuning();
+
+/* The split-KV launch a batch takes on a device of `cus` compute units
+ * (host only; of b it reads the shape, window and rows): kind 'w' (one workgroup per sequence and KV head, in-workgroup
+ * merge), 'g' (fixed key chunks + merge kernel) or 'b' (tile shares + merge
+ * kernel); waves per workgroup; grid key splits and chunk. */
+struct PlanChoice {
+    char kind;
+    uint32_t waves, n_splits, chunk;
+};
+PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on_device, bool fuse, uint32_t cus,
+                       const Tuning &t);
 
 /* Generic one-wave-per-head kernel (any head_dim % 8 == 0, <= 256), fp16 or
  * fp32 caches; follows the reference's per-key recurrence. */
@@ -82,14 +103,14 @@ int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, con
 /* Prologue kernels. */
 int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
                         const float *norm_w, float eps, const float *cos_lut,
-                        const float *sin_lut, uint32_t pos, hipStream_t stream);
+                        const float *sin_lut, uint32_t pos, int prologue, hipStream_t stream);
 int launch_store_f16(uint16_t *dst, const float *src, uint32_t n, hipStream_t stream);
 int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *const *k_seq,
                         uint16_t *const *v_seq, const uint32_t *pos_0, uint32_t n_seq,
                         uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
                         const float *q_norm_w, const float *k_norm_w, float eps,
                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
-                        uint32_t cap, hipStream_t stream);
+                        uint32_t cap, int prologue, hipStream_t stream);
 
 /* Gen-1 prologue (FP32 caches): Q normalised and rotated in place, K to
  * k_cache row pos, V copied to v_cache row pos. */

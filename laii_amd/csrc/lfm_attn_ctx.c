@@ -31,6 +31,8 @@ struct lfm_attn_ctx {
     float **k_norm;
     uint16_t **tables;    /* device: [n_layers][2] {k_cache, v_cache} pointer pairs */
     float *cos_full, *sin_full, *cos_swa, *sin_swa; /* device LUTs [max_seq][hd/2] */
+    float *cos_shift, *sin_shift; /* LFM_PROLOGUE_TABLE: the lfm2_rope_lut_init table
+                                     for sink eviction (else the full-layer table) */
     unsigned char *stage_host;  /* pinned: q | k | v | gate | pos | out */
     unsigned char *stage_dev;
     size_t off_k, off_v, off_g, off_pos, off_out, stage_in_bytes, out_bytes;
@@ -64,6 +66,8 @@ void lfm_attn_ctx_destroy(lfm_attn_ctx *c) {
     (void)hipFree(c->sin_full);
     (void)hipFree(c->cos_swa);
     (void)hipFree(c->sin_swa);
+    if (c->cos_shift != c->cos_full) (void)hipFree(c->cos_shift);
+    if (c->sin_shift != c->sin_full) (void)hipFree(c->sin_shift);
     (void)hipFree(c->stage_dev);
     if (c->stage_host) (void)hipHostFree(c->stage_host);
     (void)hipFree(c->file_dev);
@@ -81,15 +85,19 @@ void lfm_attn_ctx_destroy(lfm_attn_ctx *c) {
 }
 
 /* Build a RoPE table on the host (bit-identical to the reference builders)
- * and upload it. */
-static int upload_lut(lfm_attn_ctx *c, int swa, float **cos_d, float **sin_d) {
+ * and upload it.  which: 0 the full-layer table of the geometry's prologue,
+ * 1 the SWA table, 2 the lfm2_rope_lut_init table (LFM2 sink eviction). */
+static int upload_lut(lfm_attn_ctx *c, int which, float **cos_d, float **sin_d) {
     const lfm_attn_geom *g = &c->g;
     const size_t n = (size_t)g->max_seq * (g->head_dim / 2u);
     float *hc = (float *)malloc(n * sizeof(float));
     float *hs = (float *)malloc(n * sizeof(float));
     int st = (hc && hs) ? LFM_ATTN_OK : LFM_ATTN_E_NOMEM;
+    const int swa = which == 1;
     if (st == LFM_ATTN_OK) {
-        if (!g->lfm3)
+        if (!g->lfm3 && which == 0 && g->prologue == LFM_PROLOGUE_TABLE)
+            st = lfm_attn_rope_table_lfm2(hc, hs, g->max_seq, g->head_dim, g->rope_base);
+        else if (!g->lfm3)
             st = lfm_attn_rope_lut_lfm2(hc, hs, g->max_seq, g->head_dim, g->rope_base);
         else if (swa) /* tools/lfm3_engine.c:1720-1723: full rotation, no rope_freqs */
             st = lfm_attn_rope_lut_lfm3(hc, hs, g->max_seq, g->head_dim, g->head_dim,
@@ -115,9 +123,14 @@ int lfm_attn_ctx_create(lfm_attn_ctx **out, const lfm_attn_geom *geom) {
         g->n_head_q % g->n_head_kv != 0u || g->head_dim == 0u || g->head_dim % 8u != 0u ||
         g->head_dim > 256u || g->max_seq == 0u || g->max_seq >= 0x7FFFFFFFu)
         return LFM_ATTN_E_INVALID;
+    if (g->prologue != LFM_PROLOGUE_FAST && (g->prologue != LFM_PROLOGUE_TABLE || g->lfm3)) return LFM_ATTN_E_INVALID;
     int any_swa = 0;
     for (uint32_t l = 0; g->layer_is_swa && l < g->n_layers; ++l) any_swa |= g->layer_is_swa[l] != 0;
-    if (any_swa && (g->sliding_window == 0u || g->swa_cap < g->sliding_window)) return LFM_ATTN_E_INVALID;
+    /* a step of LFM_CTX_MAX_ROWS rows writes that many ring slots while its
+     * first row's window is still read: the ring holds window + 7 slots or
+     * more (the engines use window + 8, tools/lfm3_engine.c:1673) */
+    if (any_swa && (g->sliding_window == 0u || (uint64_t)g->swa_cap < (uint64_t)g->sliding_window + LFM_CTX_MAX_ROWS - 1u))
+        return LFM_ATTN_E_INVALID;
 
     lfm_attn_ctx *c = (lfm_attn_ctx *)calloc(1, sizeof *c);
     if (!c) return LFM_ATTN_E_NOMEM;
@@ -158,6 +171,12 @@ int lfm_attn_ctx_create(lfm_attn_ctx **out, const lfm_attn_geom *geom) {
         c->g = full;
         st = upload_lut(c, 0, &c->cos_full, &c->sin_full);
         if (st == LFM_ATTN_OK && any_swa) st = upload_lut(c, 1, &c->cos_swa, &c->sin_swa);
+        if (st == LFM_ATTN_OK && g->prologue == LFM_PROLOGUE_TABLE) {
+            st = upload_lut(c, 2, &c->cos_shift, &c->sin_shift);
+        } else {
+            c->cos_shift = c->cos_full;
+            c->sin_shift = c->sin_full;
+        }
         c->g = saved;
     }
     /* staging: q | k | v | gate | pos, then out */
@@ -240,7 +259,7 @@ int lfm_attn_ctx_forward(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
                               gate_logits ? (const float *)(d + c->off_g) : NULL, 1, kt, vt, posd,
                               (float *)(d + c->off_out), 1u, B, keys, g->n_head_q, g->n_head_kv, g->head_dim,
                               window, cap, 1.0f / sqrtf((float)g->head_dim), c->q_norm[layer], c->k_norm[layer],
-                              g->eps, cosd, sind, c->stream);
+                              g->eps, cosd, sind, g->prologue, c->stream);
     if (st != LFM_ATTN_OK) return st;
     st = st_of(hipMemcpyAsync(h + c->off_out, d + c->off_out, qn * sizeof(float),
                               hipMemcpyDeviceToHost, c->stream));
@@ -374,7 +393,7 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
                                       (const uint32_t *)(d + off_p), 1u, n_rows, g->n_head_q, g->n_head_kv,
                                       g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
                                       c->cos_swa + (size_t)kv_pos0 * half, c->sin_swa + (size_t)kv_pos0 * half, 0u,
-                                      0u, c->stream);
+                                      0u, g->prologue, c->stream);
         if (st == LFM_ATTN_OK)
             st = lfm_hip_lfm3_prefill_f16(qd, lin_k, lin_v, gd, 1, od, 1u, n_rows, pos_0, kv_pos0, 0u, window,
                                           g->n_head_q, g->n_head_kv, g->head_dim, scale, c->stream);
@@ -385,7 +404,7 @@ int lfm_attn_ctx_prefill(lfm_attn_ctx *c, uint32_t layer, uint32_t pos_0, uint32
         st = lfm_hip_qkv_prologue(qd, (const float *)(d + off_k), (const float *)(d + off_v), c->tables + 2u * layer,
                                   c->tables + 2u * layer + 1u, (const uint32_t *)(d + off_p), 1u, n_rows,
                                   g->n_head_q, g->n_head_kv, g->head_dim, c->q_norm[layer], c->k_norm[layer], g->eps,
-                                  c->cos_full, c->sin_full, 0u, 0u, c->stream);
+                                  c->cos_full, c->sin_full, 0u, 0u, g->prologue, c->stream);
         if (st == LFM_ATTN_OK && mfma128)
             st = lfm_hip_lfm3_prefill_f16(qd, c->k_cache[layer], c->v_cache[layer], gd, 1, od, 1u, n_rows, pos_0, 0u,
                                           0u, 0u, g->n_head_q, g->n_head_kv, g->head_dim, scale, c->stream);
@@ -464,8 +483,8 @@ int lfm_attn_ctx_shift_sinks(lfm_attn_ctx *c, uint32_t *inout_pos, uint32_t n_si
     }
     int st;
     if (!g->lfm3) {
-        st = lfm_hip_kv_cache_shift_sinks(c->k_cache, c->v_cache, L, nkv, g->head_dim, c->cos_full,
-                                          c->sin_full, g->max_seq, inout_pos, n_sink, n_discard,
+        st = lfm_hip_kv_cache_shift_sinks(c->k_cache, c->v_cache, L, nkv, g->head_dim, c->cos_shift,
+                                          c->sin_shift, g->max_seq, inout_pos, n_sink, n_discard,
                                           c->stream);
     } else {
         const float *cs = c->cos_swa ? c->cos_swa : c->cos_full;

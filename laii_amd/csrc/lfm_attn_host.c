@@ -6,6 +6,10 @@
  * the reference's CPU kernels read:
  *   lfm2_rope_lut_init  tools/lfm2_kernels_fast.c:370-388
  *   lfm3_rope_lut_init  tools/lfm3_engine.c:403-450
+ * The production LFM2 stacks (lfm2_forward.c, lfm2_prefill_batch.c) keep a
+ * second table whose angles are float products, built at state init
+ * (tools/lfm2_forward.c:572-581, tools/lfm2_prefill_batch.c:727-736):
+ * lfm_attn_rope_table_lfm2 repeats those libm calls.
  * Layout [pos][head_dim/2], entry i rotating the pair (i, i + head_dim/2).
  * The Gen-1 engine has no table: lfm_rope_neox (src/lfm_forward.c:97-111)
  * recomputes one position's angles in float on every call, which
@@ -27,6 +31,22 @@ int lfm_attn_rope_lut_lfm2(float *cos_lut, float *sin_lut, uint32_t max_seq, uin
             const double angle = (double)p * freq;
             cos_lut[(size_t)p * half + i] = (float)cos(angle);
             sin_lut[(size_t)p * half + i] = (float)sin(angle);
+        }
+    }
+    return LFM_ATTN_OK;
+}
+
+int lfm_attn_rope_table_lfm2(float *cos_tab, float *sin_tab, uint32_t max_seq, uint32_t head_dim,
+                             float freq_base) {
+    if (!cos_tab || !sin_tab || head_dim == 0u || (head_dim & 1u)) return LFM_ATTN_E_INVALID;
+    const uint32_t half = head_dim / 2u;
+    const float base    = freq_base > 0.0f ? freq_base : 10000.0f;
+    for (uint32_t i = 0; i < half; ++i) {
+        const float freq = powf(base, -((float)(2u * i) / (float)head_dim));
+        for (uint32_t p = 0; p < max_seq; ++p) {
+            const float phi = (float)p * freq;
+            cos_tab[(size_t)p * half + i] = cosf(phi);
+            sin_tab[(size_t)p * half + i] = sinf(phi);
         }
     }
     return LFM_ATTN_OK;

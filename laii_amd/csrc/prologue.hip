@@ -9,7 +9,10 @@
  *                                      tools/lfm3_engine.c:2006-2016
  *
  * Per head: irms = 1/sqrtf(sum(x^2)/head_dim + eps), the sum added in the
- * AVX2 kernels' order at head_dim 64 and 128; x <- (x*irms)*w (skipped
+ * AVX2 kernels' order at head_dim 64 and 128 (LFM_PROLOGUE_FAST) or in
+ * lfm2_rmsnorm's order (LFM_PROLOGUE_TABLE, the prologue of
+ * tools/lfm2_forward.c:775-830 and tools/lfm2_prefill_batch.c:826-893,
+ * any head_dim); x <- (x*irms)*w (skipped
  * when w is NULL); pairs (i, i+head_dim/2) rotate by the LUT row of the
  * position: lo' = lo*c - hi*s, hi' = hi*c + lo*s (fused multiply-add, as the
  * AVX2 kernels do).  fp16 stores round to nearest even.  One wave64 per head;
@@ -77,10 +80,43 @@ __device__ __forceinline__ float sumsq_ref_order(const float *in, uint32_t hd) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, t)));
 }
 
-/* Normalise + rotate one head held as pairs; writes fp32 (vec_out) or fp16. */
+/* Mean of squares of the head at `in` in the order of lfm2_rmsnorm
+ * (tools/lfm2_forward.c:669-684), the norm of LFM_PROLOGUE_TABLE: lane j < 8
+ * is the fused multiply-add chain over dims 8k + j of every full group of
+ * eight, the eight chains are added in order in double, then the dims past
+ * the last full group one at a time (exact double products); the result is
+ * (float)(sum / hd).  Returned on every lane. */
+__device__ __forceinline__ float meansq_table_order(const float *in, uint32_t hd) {
+#pragma clang fp contract(off)
+    const uint32_t j    = threadIdx.x & 7u;
+    const uint32_t full = hd & ~7u;
+    float col = 0.0f;
+    for (uint32_t d = 0; d < full; d += 8u) col = __builtin_fmaf(in[d + j], in[d + j], col);
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss += (double)__shfl(col, c);
+    for (uint32_t d = full; d < hd; ++d) ss += (double)in[d] * (double)in[d];
+    return (float)(ss / (double)hd);
+}
+
+/* a*b - c*d and a*b + c*d with every product rounded on its own */
+__device__ __forceinline__ float diff_of_products(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+    return a * b - c * d;
+}
+__device__ __forceinline__ float sum_of_products(float a, float b, float c, float d) {
+#pragma clang fp contract(off)
+    return a * b + c * d;
+}
+
+/* Normalise + rotate one head held as pairs; writes fp32 (vec_out) or fp16.
+ * LFM_PROLOGUE_TABLE rotates pairs of full groups of eight with fused
+ * multiply-adds and the rest with separately rounded products, as the AVX2
+ * loop and scalar tail of lfm2_qk_norm_and_rope_table do
+ * (tools/lfm2_prefill_batch.c:842-879). */
 __device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, uint16_t *dst_f16,
                                                uint32_t hd, const float *norm_w, float eps,
-                                               const float *cos_row, const float *sin_row) {
+                                               const float *cos_row, const float *sin_row, int prologue) {
     const uint32_t half = hd / 2u;
     const uint32_t lane = threadIdx.x;
     float x0[2], x1[2];
@@ -93,8 +129,9 @@ __device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, 
         ss += x0[j] * x0[j] + x1[j] * x1[j];
     }
     if (norm_w) {
-        const float sum  = (hd == 64u || hd == 128u) ? sumsq_ref_order(in, hd) : wave_sum_uniform(ss);
-        const float irms = 1.0f / sqrtf(sum / (float)hd + eps);
+        const float mean = prologue == LFM_PROLOGUE_TABLE ? meansq_table_order(in, hd)
+                         : ((hd == 64u || hd == 128u) ? sumsq_ref_order(in, hd) : wave_sum_uniform(ss)) / (float)hd;
+        const float irms = 1.0f / sqrtf(mean + eps);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const uint32_t i = lane + 64u * j;
@@ -109,8 +146,9 @@ __device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, 
         const uint32_t i = lane + 64u * j;
         if (i >= half) continue;
         const float c = cos_row[i], s = sin_row[i];
-        const float r0 = __builtin_fmaf(x0[j], c, -(x1[j] * s));
-        const float r1 = __builtin_fmaf(x1[j], c, x0[j] * s);
+        const bool fused = prologue != LFM_PROLOGUE_TABLE || i < (half & ~7u);
+        const float r0 = fused ? __builtin_fmaf(x0[j], c, -(x1[j] * s)) : diff_of_products(x0[j], c, x1[j], s);
+        const float r1 = fused ? __builtin_fmaf(x1[j], c, x0[j] * s) : sum_of_products(x1[j], c, x0[j], s);
         if (dst_f16) {
             dst_f16[i]        = f16_rne(r0);
             dst_f16[i + half] = f16_rne(r1);
@@ -123,10 +161,10 @@ __device__ __forceinline__ void norm_rope_head(const float *in, float *vec_out, 
 
 __global__ __launch_bounds__(64) void k_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t hd,
                                                      const float *norm_w, float eps,
-                                                     const float *cos_row, const float *sin_row) {
+                                                     const float *cos_row, const float *sin_row, int prologue) {
     const size_t off = (size_t)blockIdx.x * hd;
     norm_rope_head(vec + off, vec + off, dst_f16 ? dst_f16 + off : nullptr, hd, norm_w, eps,
-                   cos_row, sin_row);
+                   cos_row, sin_row, prologue);
 }
 
 __global__ __launch_bounds__(256) void k_store_f16(uint16_t *dst, const float *src, uint32_t n) {
@@ -147,6 +185,7 @@ struct PrologueParams {
     const float *sin_lut;
     uint32_t n_rows, n_head_q, n_head_kv, head_dim, window, cap;
     float eps;
+    int prologue;
 };
 
 /* blockIdx.x < n_head_q: query head, rotated in place.  Otherwise KV head
@@ -160,7 +199,7 @@ __global__ __launch_bounds__(64) void k_qkv_prologue(const PrologueParams P) {
     const float *sin_row = P.sin_lut + (size_t)pos * half;
     if (b < P.n_head_q) {
         float *qh = P.q + (((size_t)s * P.n_rows + r) * P.n_head_q + b) * hd;
-        norm_rope_head(qh, qh, nullptr, hd, P.q_norm_w, P.eps, cos_row, sin_row);
+        norm_rope_head(qh, qh, nullptr, hd, P.q_norm_w, P.eps, cos_row, sin_row, P.prologue);
         return;
     }
     const uint32_t j    = b - P.n_head_q;
@@ -169,7 +208,7 @@ __global__ __launch_bounds__(64) void k_qkv_prologue(const PrologueParams P) {
     const size_t src    = (((size_t)s * P.n_rows + r) * P.n_head_kv + j) * hd;
     uint16_t *kd = P.k_seq[s] + (size_t)slot * kv_dim + (size_t)j * hd;
     uint16_t *vd = P.v_seq[s] + (size_t)slot * kv_dim + (size_t)j * hd;
-    norm_rope_head(P.k + src, nullptr, kd, hd, P.k_norm_w, P.eps, cos_row, sin_row);
+    norm_rope_head(P.k + src, nullptr, kd, hd, P.k_norm_w, P.eps, cos_row, sin_row, P.prologue);
     for (uint32_t i = threadIdx.x; i < hd; i += 64u) vd[i] = f16_rne(P.v[src + i]);
 }
 
@@ -255,10 +294,10 @@ int launch_gen1_prologue(float *q, const float *k, const float *v, float *k_cach
 
 int launch_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
                         const float *norm_w, float eps, const float *cos_lut,
-                        const float *sin_lut, uint32_t pos, hipStream_t stream) {
+                        const float *sin_lut, uint32_t pos, int prologue, hipStream_t stream) {
     const size_t row = (size_t)pos * (head_dim / 2u);
     hipLaunchKernelGGL(k_qk_norm_rope, dim3(n_heads), dim3(64), 0, stream, vec, dst_f16, head_dim,
-                       norm_w, eps, cos_lut + row, sin_lut + row);
+                       norm_w, eps, cos_lut + row, sin_lut + row, prologue);
     return hip_status(hipGetLastError());
 }
 
@@ -272,9 +311,9 @@ int launch_qkv_prologue(float *q, const float *k, const float *v, uint16_t *cons
                         uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
                         const float *q_norm_w, const float *k_norm_w, float eps,
                         const float *cos_lut, const float *sin_lut, uint32_t window_len,
-                        uint32_t cap, hipStream_t stream) {
+                        uint32_t cap, int prologue, hipStream_t stream) {
     PrologueParams P{q, k, v, k_seq, v_seq, pos_0, q_norm_w, k_norm_w, cos_lut, sin_lut,
-                     n_rows, n_head_q, n_head_kv, head_dim, window_len, cap, eps};
+                     n_rows, n_head_q, n_head_kv, head_dim, window_len, cap, eps, prologue};
     hipLaunchKernelGGL(k_qkv_prologue, dim3(n_head_q + n_head_kv, n_rows, n_seq), dim3(64), 0,
                        stream, P);
     return hip_status(hipGetLastError());

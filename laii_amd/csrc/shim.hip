@@ -102,6 +102,7 @@ using lfm::AttnBatch;
 
 static inline hipStream_t to_stream(lfm_attn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0u; }
+static inline bool prologue_form_ok(int f) { return f == LFM_PROLOGUE_FAST || f == LFM_PROLOGUE_TABLE; }
 
 static int dispatch_f16(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream,
                         const lfm::Scratch *sc = nullptr) {
@@ -132,6 +133,37 @@ const char *lfm_attn_last_error(void) { return lfm::g_last_error; }
 const char *lfm_attn_last_plan(void) { return lfm::g_last_plan; }
 
 const char *lfm_attn_version(void) { return "lfm_attn 0.1 gfx950"; }
+
+int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles) {
+    return lfm::set_tuning(plan, waves, chunk, min_tiles);
+}
+
+int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
+                          uint32_t window_len, uint32_t keys_hint, int positions_on_device, int fused, uint32_t n_cus,
+                          const char **plan, uint32_t out3[3]) {
+    if (!plan || !out3 || n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u ||
+        n_head_q % n_head_kv != 0u || n_cus == 0u)
+        return LFM_ATTN_E_INVALID;
+    AttnBatch b;
+    b.n_seq = n_seq;
+    b.n_rows = n_rows;
+    b.n_head_q = n_head_q;
+    b.n_head_kv = n_head_kv;
+    b.head_dim = head_dim;
+    b.window = window_len;
+    if (!lfm::splitkv_supports(b)) {
+        *plan = "generic";
+        out3[0] = out3[1] = out3[2] = 0u;
+        return LFM_ATTN_OK;
+    }
+    const lfm::PlanChoice pc =
+        lfm::choose_plan(b, keys_hint, positions_on_device != 0, fused != 0, n_cus, lfm::current_tuning());
+    *plan   = pc.kind == 'w' ? "wg" : pc.kind == 'g' ? "grid" : "balanced";
+    out3[0] = pc.waves;
+    out3[1] = pc.kind == 'b' ? 0u : pc.n_splits;
+    out3[2] = pc.kind == 'b' ? 0u : pc.chunk;
+    return LFM_ATTN_OK;
+}
 
 int lfm_attn_profile_events(void *before, void *after) {
     if ((before == nullptr) != (after == nullptr)) return LFM_ATTN_E_INVALID;
@@ -209,11 +241,12 @@ uint32_t lfm_attn_slot_of(uint32_t p, uint32_t window_len, uint32_t cap) {
 /* ---- prologue ----------------------------------------------------------------- */
 int lfm_hip_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint32_t head_dim,
                          const float *norm_w, float eps, const float *cos_lut,
-                         const float *sin_lut, uint32_t pos, lfm_attn_stream_t stream) {
+                         const float *sin_lut, uint32_t pos, int prologue, lfm_attn_stream_t stream) {
     if (!vec || !cos_lut || !sin_lut || n_heads == 0u) return LFM_ATTN_E_INVALID;
     if (head_dim == 0u || (head_dim & 1u) || head_dim > 256u) return LFM_ATTN_E_INVALID;
+    if (!prologue_form_ok(prologue)) return LFM_ATTN_E_INVALID;
     return lfm::launch_qk_norm_rope(vec, dst_f16, n_heads, head_dim, norm_w, eps, cos_lut, sin_lut,
-                                    pos, to_stream(stream));
+                                    pos, prologue, to_stream(stream));
 }
 
 int lfm_hip_store_fp32_to_fp16(uint16_t *dst_f16, const float *src, uint32_t n,
@@ -228,14 +261,15 @@ int lfm_hip_qkv_prologue(float *q, const float *k, const float *v, uint16_t *con
                          uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
                          const float *q_norm_w, const float *k_norm_w, float eps,
                          const float *cos_lut, const float *sin_lut, uint32_t window_len,
-                         uint32_t cap, lfm_attn_stream_t stream) {
+                         uint32_t cap, int prologue, lfm_attn_stream_t stream) {
     if (!q || !k || !v || !k_seq || !v_seq || !pos_0 || !cos_lut || !sin_lut) return LFM_ATTN_E_INVALID;
     if (n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u) return LFM_ATTN_E_INVALID;
     if (head_dim == 0u || (head_dim & 1u) || head_dim > 256u) return LFM_ATTN_E_INVALID;
     if (window_len > 0u && (cap == 0u || window_len > cap)) return LFM_ATTN_E_INVALID;
+    if (!prologue_form_ok(prologue)) return LFM_ATTN_E_INVALID;
     return lfm::launch_qkv_prologue(q, k, v, k_seq, v_seq, pos_0, n_seq, n_rows, n_head_q, n_head_kv,
                                     head_dim, q_norm_w, k_norm_w, eps, cos_lut, sin_lut, window_len,
-                                    cap, to_stream(stream));
+                                    cap, prologue, to_stream(stream));
 }
 
 /* ---- FNV-1a 64 of a device buffer ------------------------------------------- */
@@ -509,8 +543,9 @@ int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const f
                          uint32_t n_seq, uint32_t n_rows, uint32_t keys_hint, uint32_t n_head_q,
                          uint32_t n_head_kv, uint32_t head_dim, uint32_t window_len, uint32_t cap, float scale,
                          const float *q_norm_w, const float *k_norm_w, float eps, const float *cos_lut,
-                         const float *sin_lut, lfm_attn_stream_t stream) {
+                         const float *sin_lut, int prologue, lfm_attn_stream_t stream) {
     if (!q || !k || !v || !k_seq || !v_seq || !pos_0 || !out || !cos_lut || !sin_lut) return LFM_ATTN_E_INVALID;
+    if (!prologue_form_ok(prologue)) return LFM_ATTN_E_INVALID;
     if (n_seq == 0u || n_rows == 0u || n_head_q == 0u || n_head_kv == 0u || n_head_q % n_head_kv != 0u)
         return LFM_ATTN_E_INVALID;
     if (n_seq > 65535u || n_head_kv > 65535u) return LFM_ATTN_E_INVALID;
@@ -547,6 +582,7 @@ int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const f
         b.cos_lut = cos_lut;
         b.sin_lut = sin_lut;
         b.eps = eps;
+        b.prologue = prologue;
         return lfm::launch_splitkv(b, keys_hint, st);
     }
     /* shapes the split-KV kernel does not take: the prologue on a copy of q
@@ -558,7 +594,7 @@ int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const f
     int r = lfm::hip_status(hipMemcpyAsync(qw, q, q_bytes, hipMemcpyDeviceToDevice, st));
     if (r != LFM_ATTN_OK) return r;
     r = lfm::launch_qkv_prologue(qw, k, v, k_seq, v_seq, pos_0, n_seq, n_rows, n_head_q, n_head_kv, head_dim,
-                                 q_norm_w, k_norm_w, eps, cos_lut, sin_lut, window_len, cap, st);
+                                 q_norm_w, k_norm_w, eps, cos_lut, sin_lut, window_len, cap, prologue, st);
     if (r != LFM_ATTN_OK) return r;
     b.q = qw;
     return lfm::launch_generic(b, false, st);

@@ -89,6 +89,9 @@ class Oracle:
         L.orc_rope_lut_lfm2.argtypes = [_f32p, _f32p, _u32, _u32, _f32]
         L.orc_rope_lut_lfm3.argtypes = [_f32p, _f32p, _u32, _u32, _u32, _f32, C.c_void_p, _u32]
         L.orc_qk_norm_rope.argtypes = [_f32p, C.c_void_p, _u32, _u32, C.c_void_p, _f32, _f32p, _f32p]
+        L.orc_rope_table_lfm2.argtypes = [_f32p, _f32p, _u32, _u32, _f32]
+        L.orc_qk_norm_rope_table.argtypes = [_f32p, C.c_void_p, _u32, _u32, C.c_void_p, _f32, _f32p,
+                                             _f32p]
         L.orc_online_gqa_f16.argtypes = [_f32p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32, _f32]
         L.orc_gqa_heads.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, _f32p,
                                     _u32, _u32, _u32, _u32, _u32, _f32]
@@ -150,16 +153,24 @@ class Oracle:
                                    _opt(rf, C.c_void_p), 0 if rf is None else rf.size)
         return c, s
 
-    def qk_norm_rope(self, vec, n_heads, head_dim, norm_w, eps, cos_row, sin_row, store_f16=False):
-        """Returns the rotated fp32 heads, or the RNE fp16 store when store_f16."""
+    def qk_norm_rope(self, vec, n_heads, head_dim, norm_w, eps, cos_row, sin_row, store_f16=False,
+                     table=False):
+        """Returns the rotated fp32 heads, or the RNE fp16 store when store_f16.
+        table: the production LFM2 stacks' prologue (orc_qk_norm_rope_table)."""
         v = np.ascontiguousarray(vec, np.float32).copy().reshape(-1)
         nw = None if norm_w is None else np.ascontiguousarray(norm_w, np.float32)
         dst = np.zeros(n_heads * head_dim, np.uint16) if store_f16 else None
-        self.lib.orc_qk_norm_rope(v, _opt(dst, C.c_void_p), n_heads, head_dim,
-                                  _opt(nw, C.c_void_p), eps,
-                                  np.ascontiguousarray(cos_row, np.float32),
-                                  np.ascontiguousarray(sin_row, np.float32))
+        fn = self.lib.orc_qk_norm_rope_table if table else self.lib.orc_qk_norm_rope
+        fn(v, _opt(dst, C.c_void_p), n_heads, head_dim, _opt(nw, C.c_void_p), eps,
+           np.ascontiguousarray(cos_row, np.float32), np.ascontiguousarray(sin_row, np.float32))
         return dst if store_f16 else v
+
+    def rope_table_lfm2(self, max_seq, head_dim, base):
+        """Float-angle table of the production LFM2 stacks."""
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        self.lib.orc_rope_table_lfm2(c, s, max_seq, head_dim, base)
+        return c, s
 
     # -- attention ---------------------------------------------------------------
     def online_gqa_f16(self, q, k16, v16, n_head_q, kv_mul, kv_dim, pos, scale=0.125):
@@ -340,6 +351,9 @@ class Reference:
         L.ref_qk_norm_rope_lfm3.argtypes = [_f32p, C.c_void_p, _u32, _u32, C.c_void_p, _f32, _f32p,
                                             _f32p, _u32, _u32, C.c_int]
         L.ref_store_fp32_to_fp16.argtypes = [_u16p, _f32p, _u32]
+        L.ref_rope_table_lfm2.argtypes = [_f32p, _f32p, _u32, _u32, _u32, _f32, C.c_int]
+        L.ref_qk_norm_rope_table.argtypes = [_f32p, _u32, _u32, C.c_void_p, _f32, _f32p, _f32p, _u32,
+                                             C.c_int]
         L.ref_fp16_to_fp32.restype = _f32
         L.ref_fp16_to_fp32.argtypes = [C.c_uint16]
         L.ref_online_gqa_f16.argtypes = [_f32p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32, _u32]
@@ -418,6 +432,22 @@ class Reference:
         out = np.empty(x.size, np.uint16)
         self.lib.ref_store_fp32_to_fp16(out, x, x.size)
         return out
+
+    def rope_table_lfm2(self, max_seq, head_dim, base, which=0, n_head_q=4):
+        """which 0: lfm2_batch_state_init's table, 1: lfm2_state_init's."""
+        c = np.empty((max_seq, head_dim // 2), np.float32)
+        s = np.empty_like(c)
+        assert self.lib.ref_rope_table_lfm2(c, s, max_seq, n_head_q, head_dim, base, which) == 0
+        return c, s
+
+    def qk_norm_rope_table(self, vec, n_heads, head_dim, norm_w, eps, cos_tab, sin_tab, pos, which=0):
+        """which 0: lfm2_qk_norm_and_rope_table, 1: lfm2_qk_norm_and_rope (in place on a copy)."""
+        v = np.ascontiguousarray(vec, np.float32).copy().reshape(-1)
+        nw = None if norm_w is None else np.ascontiguousarray(norm_w, np.float32)
+        assert self.lib.ref_qk_norm_rope_table(v, n_heads, head_dim, _opt(nw, C.c_void_p), eps,
+                                               np.ascontiguousarray(cos_tab, np.float32),
+                                               np.ascontiguousarray(sin_tab, np.float32), pos, which) == 0
+        return v
 
     def online_gqa_f16(self, q, k16, v16, n_head_q, kv_mul, kv_dim, pos, n_threads=2):
         out = np.zeros(n_head_q * 64, np.float32)

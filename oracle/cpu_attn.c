@@ -11,6 +11,11 @@
  *                                     partial-RoPE identity pairs.
  *   orc_qk_norm_rope                 : reference AVX2/scalar kernels (oracle/_ref),
  *                                     numpy float64 closed form, norm invariant.
+ *   orc_rope_table_lfm2,             : the reference's own table builders
+ *   orc_qk_norm_rope_table             (lfm2_batch_state_init, lfm2_state_init) and
+ *                                     prologues (lfm2_qk_norm_and_rope_table,
+ *                                     lfm2_qk_norm_and_rope) compiled from source
+ *                                     (oracle/_ref), bit-exact; float64 closed form.
  *   orc_online_gqa_f16, orc_gqa_heads, orc_lfm3_online_gqa_f16,
  *   orc_causal_rows_f16             : numpy float64 softmax(QK^T)V brute force,
  *                                     reference workers (oracle/_ref), golden
@@ -204,6 +209,72 @@ void orc_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads,
         for (uint32_t i = 0; i < half; ++i) {
             const float x0 = tmp[i], x1 = tmp[i + half];
             const float c = cos_row[i], s = sin_row[i];
+            const float r0 = fused ? fmaf(x0, c, -(x1 * s)) : x0 * c - x1 * s;
+            const float r1 = fused ? fmaf(x1, c, x0 * s) : x1 * c + x0 * s;
+            if (dst_f16 != NULL) {
+                dst_f16[(size_t)h * head_dim + i]        = orc_f32_to_f16(r0);
+                dst_f16[(size_t)h * head_dim + i + half] = orc_f32_to_f16(r1);
+            } else {
+                vec[(size_t)h * head_dim + i]        = r0;
+                vec[(size_t)h * head_dim + i + half] = r1;
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* A4, the production LFM2 stacks (lfm2_forward.c, lfm2_prefill_batch.c):
+ * float-angle table of lfm2_state_init / lfm2_batch_state_init
+ * (tools/lfm2_forward.c:572-581, tools/lfm2_prefill_batch.c:727-736):
+ * freq_i = powf(base, -((float)(2i) / (float)head_dim)), angle = (float)p *
+ * freq_i in float, entries cosf / sinf of it; base <= 0 means 10000. */
+void orc_rope_table_lfm2(float *cos_tab, float *sin_tab, uint32_t max_seq,
+                         uint32_t head_dim, float freq_base) {
+    const uint32_t half = head_dim / 2u;
+    const float base = freq_base > 0.0f ? freq_base : 10000.0f;
+    for (uint32_t i = 0; i < half; ++i) {
+        const float freq = powf(base, -((float)(2u * i) / (float)head_dim));
+        for (uint32_t p = 0; p < max_seq; ++p) {
+            const float angle = (float)p * freq;
+            cos_tab[(size_t)p * half + i] = cosf(angle);
+            sin_tab[(size_t)p * half + i] = sinf(angle);
+        }
+    }
+}
+
+/* A4, the production LFM2 stacks: lfm2_qk_norm_and_rope_table
+ * (tools/lfm2_prefill_batch.c:826-893) and lfm2_qk_norm_and_rope
+ * (tools/lfm2_forward.c:775-830) of the AVX2 build.  Per head, lfm2_rmsnorm
+ * (tools/lfm2_forward.c:669-706): eight fp32 accumulators, column j a fused
+ * multiply-add chain over dims 8k + j of every full group of eight, the
+ * columns then added in order 0..7 in double, dims past the last full group
+ * added in double one at a time; irms = 1/sqrtf((float)(ss / dim) + eps);
+ * x <- (x * irms) * w.  Rotation of pairs (i, i + half): pairs in full groups
+ * of eight use fmsub / fmadd (lo' = fma(lo, c, -(hi*s)), hi' = fma(hi, c,
+ * lo*s)), the rest separately rounded products.  Stores as orc_qk_norm_rope. */
+void orc_qk_norm_rope_table(float *vec, uint16_t *dst_f16, uint32_t n_heads,
+                            uint32_t head_dim, const float *norm_w, float eps,
+                            const float *cos_row, const float *sin_row) {
+    const uint32_t half = head_dim / 2u;
+    const uint32_t full = head_dim & ~7u, full_half = half & ~7u;
+    float tmp[512];
+    for (uint32_t h = 0; h < n_heads; ++h) {
+        const float *hp = vec + (size_t)h * head_dim;
+        for (uint32_t i = 0; i < head_dim; ++i) tmp[i] = hp[i];
+        if (norm_w != NULL) {
+            float col[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (uint32_t d = 0; d < full; d += 8u)
+                for (uint32_t j = 0; j < 8u; ++j) col[j] = fmaf(tmp[d + j], tmp[d + j], col[j]);
+            double ss = 0.0;
+            for (uint32_t j = 0; j < 8u; ++j) ss += (double)col[j];
+            for (uint32_t d = full; d < head_dim; ++d) ss += (double)tmp[d] * (double)tmp[d];
+            const float irms = 1.0f / sqrtf((float)(ss / (double)head_dim) + eps);
+            for (uint32_t i = 0; i < head_dim; ++i) tmp[i] = (tmp[i] * irms) * norm_w[i];
+        }
+        for (uint32_t i = 0; i < half; ++i) {
+            const float x0 = tmp[i], x1 = tmp[i + half];
+            const float c = cos_row[i], s = sin_row[i];
+            const int fused = i < full_half;
             const float r0 = fused ? fmaf(x0, c, -(x1 * s)) : x0 * c - x1 * s;
             const float r1 = fused ? fmaf(x1, c, x0 * s) : x1 * c + x0 * s;
             if (dst_f16 != NULL) {

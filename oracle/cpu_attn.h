@@ -39,6 +39,13 @@ void orc_qk_norm_rope(float *vec, uint16_t *dst_f16, uint32_t n_heads,
                       uint32_t head_dim, const float *norm_w, float eps,
                       const float *cos_row, const float *sin_row);
 
+/* ---- A4, production LFM2 stacks: float-angle table + lfm2_rmsnorm order - */
+void orc_rope_table_lfm2(float *cos_tab, float *sin_tab, uint32_t max_seq,
+                         uint32_t head_dim, float freq_base);
+void orc_qk_norm_rope_table(float *vec, uint16_t *dst_f16, uint32_t n_heads,
+                            uint32_t head_dim, const float *norm_w, float eps,
+                            const float *cos_row, const float *sin_row);
+
 /* ---- A1: LFM2 d=64 single-pass online softmax GQA ---------------------- */
 void orc_online_gqa_f16(const float *q, const uint16_t *k_cache_f16,
                         const uint16_t *v_cache_f16, float *xb_out,

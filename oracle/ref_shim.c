@@ -136,6 +136,72 @@ int ref_qk_norm_rope_lfm3(float *vec, uint16_t *dst_f16, uint32_t n_heads, uint3
     return 0;
 }
 
+/* The float-angle RoPE table of the production LFM2 stacks.  which = 0:
+ * lfm2_batch_state_init (tools/lfm2_prefill_batch.c:727-736); which = 1:
+ * lfm2_state_init (tools/lfm2_forward.c:572-581).  Each state is initialised
+ * for a model description carrying only what the table and the state's
+ * buffers read (n_embd = n_head_q * head_dim, no layers), the table copied
+ * out and the state freed. */
+int ref_rope_table_lfm2(float *cos_out, float *sin_out, uint32_t max_seq, uint32_t n_head_q,
+                        uint32_t head_dim, float freq_base, int which) {
+    LFM2Model *m = (LFM2Model *)calloc(1, sizeof *m);
+    if (!m) return -1;
+    m->cfg.n_embd         = n_head_q * head_dim;
+    m->cfg.n_head_q       = n_head_q;
+    m->cfg.head_dim       = head_dim;
+    m->cfg.n_vocab        = 256u;
+    m->cfg.n_ff           = 256u;
+    m->cfg.rope_freq_base = freq_base;
+    const size_t bytes    = (size_t)max_seq * (head_dim / 2u) * sizeof(float);
+    int rc                = -1;
+    shim_state st;
+    shim_save(&st);
+    if (which == 0) {
+        LFM2BatchState *s = (LFM2BatchState *)calloc(1, sizeof *s);
+        if (s && lfm2_batch_state_init(s, m, max_seq, 1u) && s->max_seq_len == max_seq) {
+            memcpy(cos_out, s->rope_cos, bytes);
+            memcpy(sin_out, s->rope_sin, bytes);
+            rc = 0;
+        }
+        if (s) lfm2_batch_state_free(s);
+        free(s);
+    } else {
+        LFM2State *s = (LFM2State *)calloc(1, sizeof *s);
+        if (s && lfm2_state_init(s, m, max_seq) && s->max_seq_len == max_seq) {
+            memcpy(cos_out, s->rope_cos, bytes);
+            memcpy(sin_out, s->rope_sin, bytes);
+            rc = 0;
+        }
+        if (s) lfm2_state_free(s);
+        free(s);
+    }
+    shim_restore(&st);
+    free(m);
+    return rc;
+}
+
+/* The prologue of the production LFM2 stacks on one token, in place:
+ * which = 0: lfm2_qk_norm_and_rope_table (tools/lfm2_prefill_batch.c:826-893);
+ * which = 1: lfm2_qk_norm_and_rope (tools/lfm2_forward.c:775-830), reading
+ * the table through a state that holds only it.  Both run lfm2_rmsnorm
+ * (tools/lfm2_forward.c:669-706) per head, then the NeoX rotation. */
+int ref_qk_norm_rope_table(float *vec, uint32_t n_heads, uint32_t head_dim, const float *norm_w,
+                           float eps, const float *cos_tab, const float *sin_tab, uint32_t pos,
+                           int which) {
+    GGUFTensor nw = shim_f32_tensor(norm_w, head_dim);
+    if (which == 0) {
+        lfm2_qk_norm_and_rope_table(cos_tab, sin_tab, vec, n_heads, head_dim, norm_w ? &nw : NULL, eps, pos);
+    } else {
+        LFM2State *s = (LFM2State *)calloc(1, sizeof *s);
+        if (!s) return -1;
+        s->rope_cos = (float *)cos_tab;
+        s->rope_sin = (float *)sin_tab;
+        lfm2_qk_norm_and_rope(s, vec, n_heads, head_dim, norm_w ? &nw : NULL, eps, pos);
+        free(s);
+    }
+    return 0;
+}
+
 /* lfm2_store_fp32_to_fp16_simd (tools/lfm2_kernels_fast.c:500-507) */
 void ref_store_fp32_to_fp16(uint16_t *dst, const float *src, uint32_t n) {
     uint32_t i = 0;

@@ -9,6 +9,13 @@ MAX_ABS = 2e-3
 REL_L2 = 1e-3
 
 
+def plan_overrides(la, env):
+    """la.tuning(...) for a case named in the LFM_ATTN_* variable form
+    ({"LFM_ATTN_PLAN": "grid", "LFM_ATTN_CHUNK": "96"}); {} = automatic."""
+    return la.tuning(env.get("LFM_ATTN_PLAN"), int(env.get("LFM_ATTN_WAVES", 0)),
+                     int(env.get("LFM_ATTN_CHUNK", 0)), int(env.get("LFM_ATTN_MINTILES", 0)))
+
+
 def f16(x: np.ndarray) -> np.ndarray:
     """IEEE binary16 bits of x, round-to-nearest-even (numpy's cast is RNE)."""
     return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)

@@ -118,7 +118,10 @@ def test_rejections_before_launch():
     assert lib.lfm_hip_gen1_gqa_step(FAKE, FAKE, FAKE, None, None, FAKE, FAKE, FAKE, 1, 10, 6, 4, 16, 1e-5,
                                      FAKE, FAKE, None) == E_INVALID
     assert lib.lfm_hip_gqa_f16_step(FAKE, FAKE, FAKE, None, 1, FAKE, FAKE, FAKE, FAKE, 1, 8, 0, 16, 4, 128, 256,
-                                    260, 0.088, None, None, 1e-5, FAKE, FAKE, None) == E_INVALID
+                                    260, 0.088, None, None, 1e-5, FAKE, FAKE, 0, None) == E_INVALID
+    # prologue forms other than FAST (0) and TABLE (1)
+    assert lib.lfm_hip_gqa_f16_step(FAKE, FAKE, FAKE, None, 1, FAKE, FAKE, FAKE, FAKE, 1, 1, 0, 16, 4, 128, 0,
+                                    0, 0.088, None, None, 1e-5, FAKE, FAKE, 2, None) == E_INVALID
     # LFM3 prefill: K/V buffer starting after the first row's window start
     # (row 0 at 1000 with window 256 needs position 745), with no window a
     # buffer not starting at 0, head_dim 96, heads not grouped evenly
@@ -131,9 +134,12 @@ def test_rejections_before_launch():
     assert f(FAKE, FAKE, FAKE, None, 1, FAKE, 2, 64, 0, 0, 64 * 512 - 8, 0, 16, 4, 128, 0.088, None) == E_INVALID
     assert lib.lfm_hip_prefill_f16(FAKE, FAKE, FAKE, FAKE, 1, 8, 0, 0, 8, 2, 128, 0.1, None) == E_UNSUPPORTED
     # prologue
-    assert lib.lfm_hip_qk_norm_rope(FAKE, None, 4, 63, None, 1e-5, FAKE, FAKE, 0, None) == E_INVALID
+    assert lib.lfm_hip_qk_norm_rope(FAKE, None, 4, 63, None, 1e-5, FAKE, FAKE, 0, 0, None) == E_INVALID
+    assert lib.lfm_hip_qk_norm_rope(FAKE, None, 4, 64, None, 1e-5, FAKE, FAKE, 0, -1, None) == E_INVALID
     assert lib.lfm_hip_qkv_prologue(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 16, 4, 128, None, None,
-                                    1e-5, FAKE, FAKE, 300, 264, None) == E_INVALID
+                                    1e-5, FAKE, FAKE, 300, 264, 0, None) == E_INVALID
+    assert lib.lfm_hip_qkv_prologue(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 1, 16, 4, 128, None, None,
+                                    1e-5, FAKE, FAKE, 0, 0, 7, None) == E_INVALID
     out5 = (C.c_uint32 * 5)()
     assert lib.lfm_attn_seg_plan(5, 300, 264, out5) == E_INVALID
     # peak probes: null, unaligned or empty inputs
@@ -160,6 +166,14 @@ def test_context_rejects_bad_geometry():
     g.layer_is_swa = C.cast(swa, C.POINTER(C.c_uint8))
     g.sliding_window, g.swa_cap = 256, 200
     assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # window > ring
+    g.swa_cap = 262
+    assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # 8-row steps need window + 7
+    g.layer_is_swa = None
+    g.prologue = 1
+    g.lfm3 = 1
+    assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # LFM3 takes the FAST prologue only
+    g.lfm3, g.prologue = 0, 2
+    assert lib.lfm_attn_ctx_create(C.byref(h), C.byref(g)) == E_INVALID  # no such prologue form
     assert lib.lfm_attn_ctx_forward(None, 0, 0, 1, FAKE, FAKE, FAKE, None, FAKE) == E_INVALID
 
 

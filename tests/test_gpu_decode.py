@@ -1,11 +1,10 @@
 """GPU parity of the decode / verify / LFM3 attention kernels against the CPU
 oracle (the restatement of the reference workers), through the C-ABI."""
-import os
 
 import numpy as np
 import pytest
 
-from helpers import f16, f16_to_f32, parity, rand_kv, softmax_attention_f64
+from helpers import f16, f16_to_f32, parity, plan_overrides, rand_kv, softmax_attention_f64
 
 pytestmark = pytest.mark.gpu
 
@@ -225,13 +224,10 @@ def test_split_count_invariance(gpu, orc):
     number of splits merged) must not change results beyond fp32 rounding."""
     la = gpu
     outs = []
-    for chunk in ("1000000", "96", "32", "160", "64"):
-        os.environ["LFM_ATTN_CHUNK"] = chunk
-        try:
+    for chunk in (1000000, 96, 32, 160, 64):
+        with la.tuning(chunk=chunk):
             got, want = _varlen_case(la, orc, np.random.default_rng(5), 3, 2, 32, 8, 64,
                                      [3000, 100, 2047])
-        finally:
-            os.environ.pop("LFM_ATTN_CHUNK", None)
         parity(got, want, what=f"chunk={chunk}")
         outs.append(got)
     for o in outs[1:]:
@@ -261,7 +257,7 @@ def plan_tol(n_rows, nq, nkv):
 def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
     """The balanced split (every workgroup takes the same number of key
     tiles, cut at sequence and head-group boundaries) and the fixed-chunk grid
-    (LFM_ATTN_PLAN=grid) both match the oracle on ragged batches; also with
+    (plan override "grid") both match the oracle on ragged batches; also with
     96-key shares (many more segments than sequences)."""
     la = gpu
     rng = np.random.default_rng(n_seq * 31 + hd)
@@ -271,13 +267,9 @@ def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
     outs = []
     for env in ({"LFM_ATTN_PLAN": "balanced"}, {"LFM_ATTN_PLAN": "grid"},
                 {"LFM_ATTN_PLAN": "balanced", "LFM_ATTN_CHUNK": "96"}):
-        os.environ.update(env)
-        try:
+        with plan_overrides(la, env):
             got, want = _varlen_case(la, orc, np.random.default_rng(4), n_seq, n_rows, nq, nkv, hd,
                                      ctx)
-        finally:
-            for k in env:
-                os.environ.pop(k, None)
         parity(got, want, what=f"{env}")
         outs.append(got)
     for o in outs[1:]:
@@ -294,8 +286,8 @@ def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
 ])
 def test_workgroup_merge_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq, max_ctx, win, cap, gate, default):
     """Small batches take one workgroup per (sequence, KV head) whose waves
-    split the keys and merge in place (k_splitkv_wg, LFM_ATTN_PLAN=wg forces
-    it); it matches the oracle and the two-kernel grid, and with no override
+    split the keys and merge in place (k_splitkv_wg, the "wg" override
+    forces it); it matches the oracle and the two-kernel grid, and with no override
     the automatic rule picks the expected form (lfm_attn_last_plan)."""
     la = gpu
     rng = np.random.default_rng(max_ctx + n_seq + hd)
@@ -303,14 +295,10 @@ def test_workgroup_merge_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq, max_ctx, win
     ctx[0] = max_ctx - 1
     outs = []
     for env in ({}, {"LFM_ATTN_PLAN": "wg"}, {"LFM_ATTN_PLAN": "grid"}):
-        os.environ.update(env)
-        try:
+        with plan_overrides(la, env):
             got, want = _varlen_case(la, orc, np.random.default_rng(9), n_seq, n_rows, nq, nkv, hd, ctx, win=win,
                                      cap=cap, gate=gate, slots=cap or None)
             plan = la.last_plan()
-        finally:
-            for k in env:
-                os.environ.pop(k, None)
         parity(got, want, what=f"{env}")
         assert plan == (default if not env else env["LFM_ATTN_PLAN"]), f"{env}: plan {plan}"
         outs.append(got)

@@ -137,16 +137,18 @@ def test_kv_export_import_round_trip(gpu):
 
 def test_context_range_errors(gpu):
     la = gpu
-    ctx = la.EngineContext(1, 16, 4, 128, 64, lfm3=True, sliding_window=16, swa_cap=20,
+    with pytest.raises(la.LfmAttnError) as e:    # 16 + 8 - 1 > 20 ring slots: refused at creation
+        la.EngineContext(1, 16, 4, 128, 64, lfm3=True, sliding_window=16, swa_cap=20, layer_is_swa=[1])
+    assert e.value.status == -1
+    ctx = la.EngineContext(1, 16, 4, 128, 64, lfm3=True, sliding_window=16, swa_cap=23,
                            layer_is_swa=[1])
     z = np.zeros((8, 16, 128), np.float32)
     zk = np.zeros((8, 4, 128), np.float32)
     with pytest.raises(la.LfmAttnError) as e:
         ctx.forward(0, 60, z[:8], zk[:8], zk[:8])  # past max_seq
     assert e.value.status == -2
-    with pytest.raises(la.LfmAttnError) as e:
-        ctx.forward(0, 0, z[:8], zk[:8], zk[:8])   # 16 + 8 - 1 > 20 ring slots
-    assert e.value.status == -1
+    out = ctx.forward(0, 0, z[:8], zk[:8], zk[:8])  # 8 rows on a window + 7 ring
+    assert np.all(out == 0.0)
     ctx.close()
 
 

@@ -5,12 +5,11 @@ the attention out -- against the oracle's prologue (A4/A5) followed by its
 attention (A1/A3), as the reference runs them
 (tools/lfm2_kernels_fast.c:1046-1066, tools/lfm2_prefill_batch.c:1029-1092,
 tools/lfm3_engine.c:1885-1896, 2006-2022)."""
-import os
 
 import numpy as np
 import pytest
 
-from helpers import f16, parity, rand_kv
+from helpers import f16, parity, plan_overrides, rand_kv
 
 pytestmark = pytest.mark.gpu
 
@@ -50,15 +49,11 @@ def _step_case(la, orc, seed, n_seq, n_rows, nq, nkv, hd, pos0, win=0, cap=0, ga
     out = la.DeviceArray.zeros(q.shape, np.float32)
     keys = win + n_rows - 1 if win else rows
     env = env or {}
-    os.environ.update(env)
-    try:
+    with plan_overrides(la, env):
         la.gqa_f16_step(qd, dev(la, k), dev(la, v), None if g is None else dev(la, g), True, la.pointer_table(kd),
                         la.pointer_table(vd), dev(la, pos0), out, n_seq, n_rows, keys, nq, nkv, hd,
                         None if qw is None else dev(la, qw), None if kw is None else dev(la, kw), EPS,
                         dev(la, cos), dev(la, sin), win, cap)
-    finally:
-        for key in env:
-            os.environ.pop(key, None)
     got = out.numpy()
     assert np.array_equal(qd.numpy(), q), "the step must leave q unchanged"
     for s in range(n_seq):

@@ -182,6 +182,97 @@ def test_qk_norm_rope_order_pins_a_planted_mistake(orc, ref):
     assert diffs > 0
 
 
+# ---- A4, the production LFM2 stacks (lfm2_forward.c, lfm2_prefill_batch.c) ----------------------
+
+def test_rope_table_lfm2_closed_form(orc):
+    """The float-angle table: entry (p, i) is cosf / sinf of the float
+    product fl(p * freq_i), freq_i = powf(base, -(2i/d)); against float64
+    cos / sin of that same float angle (<= 1 ulp), with freq_i within 1 ulp
+    of the float64 power.  The double-angle table differs from it past
+    position ~1000 by up to ~1e-3 (the float angle's rounding), which is what
+    makes the two prologues distinguishable."""
+    for hd, base in ((64, 1e6), (64, 1e4), (128, 1e6)):
+        c, s = orc.rope_table_lfm2(32768, hd, base)
+        i = np.arange(hd // 2)
+        freq64 = np.power(float(np.float32(base)), -(2.0 * i) / hd)
+        freq = freq64.astype(np.float32)
+        # the float angle, rebuilt with the table's own frequency (recovered
+        # from row 1, whose angle is exactly freq)
+        f1 = np.arctan2(s[1].astype(np.float64), c[1].astype(np.float64))
+        assert np.all(np.abs(f1 - freq64) <= 4e-7 * freq64)
+        ang = (np.arange(32768, dtype=np.float32)[:, None] * freq[None, :]).astype(np.float32).astype(np.float64)
+        for got, want in ((c, np.cos(ang)), (s, np.sin(ang))):
+            ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+            assert np.all(np.abs(got - want) <= ulp * 1.01 + 1e-30)
+    cd, _ = orc.rope_lut_lfm2(32768, 64, 1e6)
+    cf, _ = orc.rope_table_lfm2(32768, 64, 1e6)
+    assert np.abs(cd[:1024] - cf[:1024]).max() < 1e-4 and np.abs(cd - cf).max() > 5e-4
+
+
+def test_rope_table_lfm2_matches_reference(orc, ref):
+    """Bit for bit against the tables the reference's own state initialisers
+    build (lfm2_batch_state_init and lfm2_state_init, compiled from source)."""
+    for hd, base in ((64, 1e6), (64, 1e4), (128, 1e6), (64, 0.0)):
+        mine = orc.rope_table_lfm2(32768 if hd == 64 else 4096, hd, base)
+        for which in (0, 1):
+            theirs = ref.rope_table_lfm2(32768 if hd == 64 else 4096, hd, base, which=which)
+            assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(mine, theirs))
+
+
+def test_rope_table_lfm2_host_builder(orc):
+    """lfm_attn_rope_table_lfm2 (the product's host C11 builder, no device
+    needed) equals the oracle's table bit for bit."""
+    import laii_amd as la
+    for hd, base in ((64, 1e6), (128, 1e4)):
+        mine = la.rope_table_lfm2(32768, hd, base)
+        want = orc.rope_table_lfm2(32768, hd, base)
+        assert all(np.array_equal(a.view(np.uint32), b.view(np.uint32)) for a, b in zip(mine, want))
+
+
+@pytest.mark.parametrize("hd", [64, 128, 48, 40, 16, 8])
+def test_qk_norm_rope_table_matches_reference(orc, ref, hd):
+    """orc_qk_norm_rope_table bit for bit against lfm2_qk_norm_and_rope_table
+    and lfm2_qk_norm_and_rope (compiled from source) at the positions the
+    production stacks reach (0 .. 32767), with and without norm weights, on
+    inputs spanning six orders of magnitude; head dims with a scalar tail in
+    the norm (40) and in the rotation (48, 40, 16, 8) included."""
+    rng = np.random.default_rng(40 + hd)
+    c, s = orc.rope_table_lfm2(32768, hd, 1e6)
+    for pos in (0, 1, 1023, 8191, 32767):
+        for norm in (True, False):
+            x = (rng.standard_normal(8 * hd) * rng.choice([1e-3, 1.0, 40.0], 8 * hd)).astype(np.float32)
+            w = (1 + 0.05 * rng.standard_normal(hd)).astype(np.float32) if norm else None
+            mine = orc.qk_norm_rope(x, 8, hd, w, 1e-5, c[pos], s[pos], table=True)
+            for which in (0, 1):
+                theirs = ref.qk_norm_rope_table(x, 8, hd, w, 1e-5, c, s, pos, which=which)
+                assert np.array_equal(mine.view(np.uint32), theirs.view(np.uint32)), (pos, norm, which)
+            k16 = orc.qk_norm_rope(x, 8, hd, w, 1e-5, c[pos], s[pos], store_f16=True, table=True)
+            assert np.array_equal(k16, ref.store_f16(mine))
+            # float64 closed form with the table's own cos / sin
+            want = _norm_rope_f64(x, 8, hd, w, 1e-5, c[pos], s[pos])
+            assert np.abs(mine - want).max() <= 5e-6 * max(1.0, np.abs(want).max())
+
+
+def test_qk_norm_rope_table_order_is_pinned(orc, ref):
+    """The two LFM2 prologues add the squares in different orders; on these
+    inputs the fast kernels' order (a plausible mix-up) is not bit-identical
+    to lfm2_rmsnorm's, so the bit-exact check above tells them apart -- and
+    so does one with the table swapped for the double-angle one."""
+    rng = np.random.default_rng(11)
+    c, s = orc.rope_table_lfm2(32768, 64, 1e6)
+    cd, sd = orc.rope_lut_lfm2(32768, 64, 1e6)
+    d_order = d_table = 0
+    for _ in range(20):
+        x = (rng.standard_normal(16 * 64) * 3).astype(np.float32)
+        w = (1 + 0.05 * rng.standard_normal(64)).astype(np.float32)
+        theirs = ref.qk_norm_rope_table(x, 16, 64, w, 1e-5, c, s, 32767)
+        other_order = orc.qk_norm_rope(x, 16, 64, w, 1e-5, c[32767], s[32767])
+        other_table = orc.qk_norm_rope(x, 16, 64, w, 1e-5, cd[32767], sd[32767], table=True)
+        d_order += int(np.count_nonzero(other_order.view(np.uint32) != theirs.view(np.uint32)))
+        d_table += int(np.count_nonzero(other_table.view(np.uint32) != theirs.view(np.uint32)))
+    assert d_order > 0 and d_table > 0
+
+
 # ---- A1/A2/A3/A7 attention ----------------------------------------------------------------------
 
 def _brute(q, kf, vf, nq, nkv, hd, t0, t1, scale, gate=None, head_map=None):

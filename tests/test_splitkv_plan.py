@@ -133,3 +133,59 @@ def test_plan_check_rejects_planted_mistakes(sim, mutant):
         rc, _, _, _ = sim(pos0, n_rows, nkv, W, ncols, mutant=mutant, **kw)
         caught += rc != 0
     assert caught > 20, caught
+
+
+# ---- plan choice of the launch path (host only: lfm_attn_plan_preview) -------------------------
+
+BASELINE_PLANS = [
+    # (name, preview kwargs, expected (plan, waves))
+    ("cfg1 decode B1 16q/8kv ctx 1024", dict(n_seq=1, n_rows=1, n_head_q=16, n_head_kv=8, head_dim=64,
+                                            keys_hint=1024, positions_on_device=False), ("grid", 1)),
+    ("cfg1 engine step (fused)", dict(n_seq=1, n_rows=1, n_head_q=16, n_head_kv=8, head_dim=64, keys_hint=1024,
+                                      fused=True), ("grid", 1)),
+    ("cfg2 B64 x 8192", dict(n_seq=64, n_rows=1, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=8192),
+     ("balanced", 8)),
+    ("cfg2 fused step", dict(n_seq=64, n_rows=1, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=8192,
+                             fused=True), ("balanced", 8)),
+    ("cfg3 verify B16 x 8 rows", dict(n_seq=16, n_rows=8, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=4104),
+     ("balanced", 8)),
+    ("cfg5 SWA ring", dict(n_seq=32, n_rows=1, n_head_q=16, n_head_kv=4, head_dim=128, window_len=256,
+                           keys_hint=256), ("wg", 4)),
+    ("cfg5 full B32 x 32768", dict(n_seq=32, n_rows=1, n_head_q=16, n_head_kv=4, head_dim=128, keys_hint=32768),
+     ("balanced", 2)),
+]
+
+
+@pytest.mark.parametrize("name,kw,want", BASELINE_PLANS, ids=[c[0] for c in BASELINE_PLANS])
+def test_plan_choice_baseline_shapes(name, kw, want):
+    """The launch form each BASELINE configuration takes on a 256-CU MI355X
+    (the forms the bench measures), computed on the host without a device."""
+    import laii_amd as la
+    plan, waves, splits, chunk = la.plan_preview(**kw)
+    assert (plan, waves) == want, (name, plan, waves)
+    if plan != "balanced":
+        keys = kw["keys_hint"]
+        assert splits >= 1 and chunk % 32 == 0 and splits * chunk >= min(keys, kw.get("window_len") or keys)
+
+
+def test_plan_overrides_and_lds_budget():
+    """Overrides force a form and counts, and clear back to the automatic
+    choice; a forced in-workgroup form whose fused LDS (V tiles + staged new
+    rows) would pass 64 KB falls back to the grid, with fewer waves."""
+    import laii_amd as la
+    cfg2 = dict(n_seq=64, n_rows=1, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=8192)
+    with la.tuning("grid", chunk=96):
+        assert la.plan_preview(**cfg2)[0] == "grid" and la.plan_preview(**cfg2)[3] == 96
+    with la.tuning("wg"):
+        assert la.plan_preview(**cfg2)[0] == "wg"
+        mha = dict(n_seq=1, n_rows=64, n_head_q=8, n_head_kv=8, head_dim=64, keys_hint=4096, fused=True)
+        plan, waves, _, _ = la.plan_preview(**mha)
+        assert plan == "grid" and waves <= 2, (plan, waves)
+    with la.tuning(waves=2):
+        assert la.plan_preview(**cfg2)[:2] == ("balanced", 2)
+    assert la.plan_preview(**cfg2)[:2] == ("balanced", 8)
+    with pytest.raises(la.LfmAttnError):
+        la.set_tuning("fastest")
+    with pytest.raises(la.LfmAttnError):
+        la.set_tuning(waves=3)
+    assert la.plan_preview(n_seq=1, n_rows=1, n_head_q=4, n_head_kv=2, head_dim=32)[0] == "generic"
