@@ -82,6 +82,9 @@ int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, ui
 
 /* ---- device plumbing (so C11 callers need no HIP headers) ------------------ */
 int lfm_attn_device_count(int *count);
+/* Makes `device` current for this thread and resolves the device address of
+ * its no-alloc scratch (lfm_hip_gqa_f16_varlen_noalloc), which loads the
+ * library's code object there if it is not yet loaded. */
 int lfm_attn_set_device(int device);
 int lfm_attn_dev_alloc(void **ptr, size_t bytes);
 int lfm_attn_dev_free(void *ptr);
@@ -355,7 +358,10 @@ int lfm_hip_gqa_f16_step(const float *q, const float *k, const float *v, const f
  * is launched.  Every call on a device shares that device's array: calls that
  * overlap on one device (any streams) race.  Nothing in the array needs to
  * start at zero: every partial the merge reads is written earlier by the
- * same call. */
+ * same call.  The array's device address is looked up once per device, by
+ * lfm_attn_set_device or else by the first call of this function there:
+ * call one of them on each device before capturing a graph that contains
+ * this call, since the lookup may load the library's code object. */
 #define LFM_ATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
 int lfm_hip_gqa_f16_varlen_noalloc(const float *q, const float *gate, int gate_is_logit,
                                    const uint16_t *const *k_seq, const uint16_t *const *v_seq,

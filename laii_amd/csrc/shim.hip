@@ -180,7 +180,14 @@ int lfm_attn_device_count(int *count) {
     return lfm::hip_status(e);
 }
 
-int lfm_attn_set_device(int device) { return lfm::hip_status(hipSetDevice(device)); }
+int lfm_attn_set_device(int device) {
+    const int st = lfm::hip_status(hipSetDevice(device));
+    if (st != LFM_ATTN_OK) return st;
+    /* resolve the no-alloc scratch of this device now, outside any graph
+     * capture a caller may start later */
+    lfm::Scratch sc;
+    return lfm::noalloc_scratch(&sc);
+}
 
 int lfm_attn_dev_alloc(void **ptr, size_t bytes) {
     if (!ptr) return LFM_ATTN_E_INVALID;

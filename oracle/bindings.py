@@ -351,6 +351,9 @@ class Reference:
         L.ref_qk_norm_rope_lfm3.argtypes = [_f32p, C.c_void_p, _u32, _u32, C.c_void_p, _f32, _f32p,
                                             _f32p, _u32, _u32, C.c_int]
         L.ref_store_fp32_to_fp16.argtypes = [_u16p, _f32p, _u32]
+        L.ref_time_attn.argtypes = [C.c_int, C.c_int, _f32p, C.c_void_p, C.c_void_p, C.c_void_p, _u32p, _f32p,
+                                    _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                    C.POINTER(C.c_double), C.POINTER(_u32)]
         L.ref_rope_table_lfm2.argtypes = [_f32p, _f32p, _u32, _u32, _u32, _f32, C.c_int]
         L.ref_qk_norm_rope_table.argtypes = [_f32p, _u32, _u32, C.c_void_p, _f32, _f32p, _f32p, _u32,
                                              C.c_int]
@@ -432,6 +435,29 @@ class Reference:
         out = np.empty(x.size, np.uint16)
         self.lib.ref_store_fp32_to_fp16(out, x, x.size)
         return out
+
+    KIND = {"lfm2_decode": 0, "lfm2_rows": 1, "lfm3_decode": 2}
+
+    def time_attn(self, kind, fair, q, k_list, v_list, pos0, n_head_q, n_head_kv, head_dim, n_rows=1,
+                  gate=None, window=0, cap=0, n_threads=1, warm=3, reps=10):
+        """The reference's CPU attention over a multi-sequence batch
+        (ref_time_attn): kind "lfm2_decode" / "lfm2_rows" / "lfm3_decode";
+        fair False = the engine's dispatch per sequence (per row), True = every
+        item on all threads.  Returns (per-pass seconds [reps], threads, out)."""
+        n_seq = len(k_list)
+        q = np.ascontiguousarray(q, np.float32).reshape(-1)
+        out = np.zeros(n_seq * n_rows * n_head_q * head_dim, np.float32)
+        g = None if gate is None else np.ascontiguousarray(gate, np.float32).reshape(-1)
+        kp = (C.c_void_p * n_seq)(*[k.ctypes.data for k in k_list])
+        vp = (C.c_void_p * n_seq)(*[v.ctypes.data for v in v_list])
+        max_seq = max(int(k.size) // (n_head_kv * head_dim) for k in k_list)
+        times = (C.c_double * reps)()
+        used = _u32(0)
+        rc = self.lib.ref_time_attn(self.KIND[kind], int(fair), q, _opt(g, C.c_void_p), kp, vp,
+                                    np.ascontiguousarray(pos0, np.uint32), out, n_seq, n_rows, n_head_q, n_head_kv,
+                                    head_dim, window, cap, max_seq, n_threads, warm, reps, times, C.byref(used))
+        assert rc == 0
+        return np.array(times[:], np.float64), int(used.value), out
 
     def rope_table_lfm2(self, max_seq, head_dim, base, which=0, n_head_q=4):
         """which 0: lfm2_batch_state_init's table, 1: lfm2_state_init's."""

@@ -370,6 +370,182 @@ double ref_time_decode_batch_fair(const float *q, const uint16_t *const *k_seq,
     return best;
 }
 
+/* ---- CPU baseline of every decode-type configuration --------------------
+ * kind 0  LFM2 decode, one query row per sequence: OnlineGQATaskCtx +
+ *         lfm2_online_gqa_f16_worker_simd over ceil(n_head_q / 4) head groups
+ *         (tools/lfm2_kernels_fast.c:1052-1066); head_dim 64.
+ * kind 1  LFM2 causal rows (speculative verify, prefill): per row,
+ *         GQAAttnTaskCtx + lfm2_gqa_heads_worker_task over the query heads
+ *         (tools/lfm2_prefill_batch.c:1074-1091); row r of sequence s at
+ *         pos0[s] + r; head_dim 64.
+ * kind 2  LFM3 decode, one row per sequence: lfm3_online_gqa_f16_dispatch
+ *         with B = 1 (tools/lfm3_engine.c:1155-1204), B * n_head_q / 2 items;
+ *         gate (sigmoid values, [n_seq][n_head_q]) or NULL.
+ * fair 0  reference-faithful: the engine's dispatch on one pool of n_threads
+ *         (the calling thread is worker 0), sequence after sequence (row
+ *         after row for kind 1), as a multi-sequence batch would run on it;
+ * fair 1  fair-batched: every (sequence, row, item) of the batch claimed
+ *         dynamically by n_threads threads (FTZ/DAZ as the pool sets them),
+ *         each handing the reference worker a one-item claim range.
+ * Runs `warm` untimed passes, then `reps` timed ones; times_out[r] receives
+ * pass r's seconds, *threads_out the threads used. */
+typedef struct {
+    int kind;
+    const float *q, *gate;
+    const uint16_t *const *k_seq;
+    const uint16_t *const *v_seq;
+    const uint32_t *pos0;
+    float *out;
+    uint32_t n_seq, n_rows, n_head_q, n_head_kv, head_dim, window, cap, max_seq;
+    uint32_t per_seq; /* items per sequence */
+    atomic_uint next;
+    /* fair mode: persistent threads, one start and one end barrier per pass */
+    pthread_barrier_t start, end;
+    uint32_t passes;
+} attn_job;
+
+static uint32_t attn_items_per_seq(const attn_job *j) {
+    if (j->kind == 0) return (j->n_head_q + 3u) / 4u;
+    if (j->kind == 1) return j->n_rows * j->n_head_q;
+    return j->head_dim == 128u ? (j->n_head_q + 1u) / 2u : j->n_head_q;
+}
+
+/* one == 0: the engine's dispatch of sequence s (of row `item` for kind 1)
+ * on the real pool `pool`; one != 0: item `item` of sequence s alone, through
+ * the one-item claim range `pool`.  att: the heads task's score scratch. */
+static void attn_run(const attn_job *j, LFM2ThreadPool *pool, uint32_t s, uint32_t item, int one, float *att) {
+    const uint32_t hd = j->head_dim, kv_dim = j->n_head_kv * hd;
+    if (j->kind == 0) {
+        OnlineGQATaskCtx ctx = {
+            .pool = pool, .q = j->q + (size_t)s * j->n_head_q * hd, .k_cache_f16 = j->k_seq[s],
+            .v_cache_f16 = j->v_seq[s], .xb_out = j->out + (size_t)s * j->n_head_q * hd, .xb_q8_out = NULL,
+            .n_head_q = j->n_head_q, .kv_mul = j->n_head_q / j->n_head_kv, .kv_dim = kv_dim, .pos = j->pos0[s],
+            .scale = 1.0f / sqrtf((float)hd)};
+        if (one) lfm2_online_gqa_f16_worker_simd(&ctx, 0u, 1u);
+        else lfm2_parallel_for(pool, (j->n_head_q + 3u) / 4u, 1, lfm2_online_gqa_f16_worker_simd, &ctx);
+    } else if (j->kind == 1) {
+        const uint32_t r  = one ? item / j->n_head_q : item;
+        const size_t row  = ((size_t)s * j->n_rows + r) * j->n_head_q * hd;
+        GQAAttnTaskCtx ctx = {
+            .pool = pool, .q = j->q + row, .k_cache = NULL, .v_cache = NULL, .k_cache_f16 = j->k_seq[s],
+            .v_cache_f16 = j->v_seq[s], .att = att, .xb = j->out + row, .n_head_q = j->n_head_q,
+            .kv_mul = j->n_head_q / j->n_head_kv, .head_dim = hd, .kv_dim = kv_dim, .max_seq_len = j->max_seq,
+            .pos = j->pos0[s] + r, .scale = 1.0f / sqrtf((float)hd)};
+        if (one) lfm2_gqa_heads_worker_task(&ctx, 0u, 1u);
+        else lfm2_parallel_for(pool, j->n_head_q, 1, lfm2_gqa_heads_worker_task, &ctx);
+    } else {
+        const float *g = j->gate ? j->gate + (size_t)s * j->n_head_q : NULL;
+        if (!one) {
+            lfm3_online_gqa_f16_dispatch(pool, j->q + (size_t)s * j->n_head_q * hd, g, j->k_seq[s], j->v_seq[s],
+                                         j->out + (size_t)s * j->n_head_q * hd, NULL, 1u, j->pos0[s], j->window,
+                                         j->cap, j->n_head_q, j->n_head_kv, hd);
+            return;
+        }
+        const uint32_t per = hd == 128u ? 2u : 1u;
+        LFM3OnlineGQACtx ctx = {
+            .pool = pool, .q_batch = j->q + (size_t)s * j->n_head_q * hd, .gate_sig = g,
+            .k_cache_f16 = j->k_seq[s], .v_cache_f16 = j->v_seq[s], .xb_out = j->out + (size_t)s * j->n_head_q * hd,
+            .xb_q8_out = NULL, .B = 1u, .pos_0 = j->pos0[s], .window_len = j->window, .swa_cap = j->cap,
+            .n_head_q = j->n_head_q, .kv_mul = j->n_head_q / j->n_head_kv, .kv_dim = kv_dim, .head_dim = hd,
+            .n_groups = (j->n_head_q + per - 1u) / per, .scale = 1.0f / sqrtf((float)hd)};
+#if LFM2_HAS_AVX2
+        if (hd == 128u && lfm3_use_avx2()) {
+            lfm3_online_gqa_128_f16_worker_avx2(&ctx, 0u, 1u);
+            return;
+        }
+#endif
+        lfm3_online_gqa_f16_worker_scalar(&ctx, 0u, 1u);
+    }
+}
+
+/* One fair pass: items claimed until the batch is done. */
+static void attn_fair_pass(attn_job *j, float *att) {
+    LFM2ThreadPool one;
+    memset(&one, 0, sizeof one);
+    one.chunk_size = 1u;
+    for (;;) {
+        const uint32_t it = atomic_fetch_add_explicit(&j->next, 1u, memory_order_relaxed);
+        if (it >= j->n_seq * j->per_seq) break;
+        const uint32_t s = it / j->per_seq, item = it % j->per_seq;
+        /* the worker claims exactly `sub` from a range that ends after it */
+        const uint32_t sub = j->kind == 1 ? item % j->n_head_q : item;
+        one.n_items = sub + 1u;
+        atomic_store_explicit(&one.next_item, sub, memory_order_relaxed);
+        attn_run(j, &one, s, item, 1, att);
+    }
+}
+
+/* A helper thread of the fair mode: every pass between the two barriers. */
+static void *attn_fair_thread(void *arg) {
+    attn_job *j = (attn_job *)arg;
+    _mm_setcsr(_mm_getcsr() | 0x8040u);
+    float *att = (float *)calloc((size_t)j->n_head_q * (j->max_seq ? j->max_seq : 1u), sizeof(float));
+    for (uint32_t r = 0; r < j->passes; ++r) {
+        pthread_barrier_wait(&j->start);
+        attn_fair_pass(j, att);
+        pthread_barrier_wait(&j->end);
+    }
+    free(att);
+    return NULL;
+}
+
+int ref_time_attn(int kind, int fair, const float *q, const float *gate, const uint16_t *const *k_seq,
+                  const uint16_t *const *v_seq, const uint32_t *pos0, float *out, uint32_t n_seq, uint32_t n_rows,
+                  uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, uint32_t window, uint32_t cap,
+                  uint32_t max_seq, uint32_t n_threads, uint32_t warm, uint32_t reps, double *times_out,
+                  uint32_t *threads_out) {
+    if (kind < 0 || kind > 2 || n_seq == 0u || n_head_kv == 0u || n_head_q % n_head_kv != 0u) return -1;
+    if (kind != 2 && head_dim != 64u) return -1;
+    if (n_threads < 1u) n_threads = 1u;
+    if (n_threads > 256u) n_threads = 256u;
+    static attn_job job; /* one timing at a time (the barriers live in it) */
+    memset(&job, 0, sizeof job);
+    job.kind = kind, job.q = q, job.gate = gate, job.k_seq = k_seq, job.v_seq = v_seq, job.pos0 = pos0;
+    job.out = out, job.n_seq = n_seq, job.n_rows = kind == 1 ? n_rows : 1u, job.n_head_q = n_head_q;
+    job.n_head_kv = n_head_kv, job.head_dim = head_dim, job.window = window, job.cap = cap;
+    job.max_seq = max_seq, job.passes = warm + reps;
+    job.per_seq = attn_items_per_seq(&job);
+    shim_state st;
+    shim_save(&st);
+    LFM2ThreadPool pool;
+    pthread_t th[256];
+    float *att = (float *)calloc((size_t)n_head_q * (max_seq ? max_seq : 1u), sizeof(float));
+    if (!fair) {
+        lfm2_threadpool_init(&pool, n_threads);
+        if (threads_out) *threads_out = pool.n_threads;
+    } else {
+        if (threads_out) *threads_out = n_threads;
+        _mm_setcsr(_mm_getcsr() | 0x8040u);
+        pthread_barrier_init(&job.start, NULL, n_threads);
+        pthread_barrier_init(&job.end, NULL, n_threads);
+        for (uint32_t t = 1; t < n_threads; ++t) pthread_create(&th[t], NULL, attn_fair_thread, &job);
+    }
+    for (uint32_t r = 0; r < warm + reps; ++r) {
+        atomic_store(&job.next, 0u);
+        const double t0 = shim_now();
+        if (!fair) {
+            for (uint32_t s = 0; s < n_seq; ++s)
+                for (uint32_t row = 0; row < job.n_rows; ++row) attn_run(&job, &pool, s, row, 0, att);
+        } else {
+            pthread_barrier_wait(&job.start);
+            attn_fair_pass(&job, att);
+            pthread_barrier_wait(&job.end);
+        }
+        const double dt = shim_now() - t0;
+        if (r >= warm) times_out[r - warm] = dt;
+    }
+    if (!fair) {
+        lfm2_threadpool_free(&pool);
+    } else {
+        for (uint32_t t = 1; t < n_threads; ++t) pthread_join(th[t], NULL);
+        pthread_barrier_destroy(&job.start);
+        pthread_barrier_destroy(&job.end);
+    }
+    free(att);
+    shim_restore(&st);
+    return 0;
+}
+
 /* ---- attention-sink eviction ------------------------------------------ */
 /* A model description carrying only what the shift functions read:
  * n_layers, head_dim (n_embd / n_head_q for LFM2), n_head_kv, sliding_window
