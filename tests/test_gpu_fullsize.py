@@ -11,9 +11,14 @@ oracle (the restatement of the reference workers), through the C-ABI.
         (rope_freqs 1 x 32, 1e30 x 32), sigmoid gate
         (tools/lfm3_engine.c:403-450, 851-946, 1588-1597)
 
+K/V caches are 0.5 * N(0,1) rounded to fp16 and queries N(0,1), as BASELINE
+draws them.
+
 Every sequence is also checked by properties that hold at any size: finite
 outputs, and each output dim inside [min, max] of that dim over the values
 the row attends (a softmax is a convex combination)."""
+import os
+
 import numpy as np
 import pytest
 
@@ -28,15 +33,21 @@ def dev(la, arr):
     return la.DeviceArray.from_numpy(np.ascontiguousarray(arr))
 
 
-def fast_kv(rng, n_slots, nkv, hd):
-    """Random fp16 cache rows, drawn as bits: random sign and mantissa,
-    exponent so that |x| is in [2^-6, 2) -- fast at gigabyte sizes."""
-    n = n_slots * nkv * hd
-    bits = rng.integers(0, 1 << 16, n, dtype=np.uint16)
-    sign = bits & np.uint16(0x8000)
-    mant = bits & np.uint16(0x03FF)
-    expo = (np.uint16(9) + (bits >> np.uint16(10)) % np.uint16(7)).astype(np.uint16) << np.uint16(10)
-    return (sign | expo | mant).reshape(n_slots, nkv, hd)
+def normal_kv(seed, slots, nkv, hd):
+    """fp16 cache rows of 0.5 * N(0,1), BASELINE's K/V distribution: one
+    seeded float32 draw per sequence (child streams of SeedSequence(seed)),
+    rounded to nearest even, drawn on threads (gigabytes at full size)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    def one(args):
+        child, n = args
+        x = np.random.default_rng(child).standard_normal((n, nkv, hd), dtype=np.float32)
+        x *= np.float32(0.5)
+        return x.astype(np.float16).view(np.uint16)
+
+    kids = np.random.SeedSequence(seed).spawn(len(slots))
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+        return list(ex.map(one, zip(kids, [int(n) for n in slots])))
 
 
 def check_convex(out, lo, hi, what):
@@ -55,8 +66,9 @@ class _Decode:
         self.ctx = np.asarray(ctx, np.int64)
         self.n_seq = len(ctx)
         self.pos = (self.ctx - 1).astype(np.uint32)
-        self.k = [fast_kv(rng, int(c), nkv, hd) for c in self.ctx]
-        self.v = [fast_kv(rng, int(c), nkv, hd) for c in self.ctx]
+        seed = int(rng.integers(1 << 31))
+        self.k = normal_kv(seed, self.ctx, nkv, hd)
+        self.v = normal_kv(seed + 1, self.ctx, nkv, hd)
         self.kd = [dev(la, k) for k in self.k]
         self.vd = [dev(la, v) for v in self.v]
         self.kt, self.vt = la.pointer_table(self.kd), la.pointer_table(self.vd)
@@ -154,8 +166,8 @@ def test_cfg3_fullsize_verify(gpu, orc):
     rng = np.random.default_rng(3)
     n_seq, n_rows, nq, nkv, hd = 16, 8, 32, 8, 64
     pos0 = np.full(n_seq, 4096, np.uint32)
-    k = [fast_kv(rng, 4104, nkv, hd) for _ in range(n_seq)]
-    v = [fast_kv(rng, 4104, nkv, hd) for _ in range(n_seq)]
+    k = normal_kv(31, [4104] * n_seq, nkv, hd)
+    v = normal_kv(32, [4104] * n_seq, nkv, hd)
     kd, vd = [dev(la, x) for x in k], [dev(la, x) for x in v]
     q = rng.standard_normal((n_seq, n_rows, nq, hd), dtype=np.float32)
     out = la.DeviceArray.zeros(q.shape, np.float32)
@@ -176,7 +188,7 @@ def test_cfg3_fullsize_verify(gpu, orc):
 def test_cfg5_fullsize_lfm3_full_layer(gpu, orc, mode):
     """Config 5, full-attention layer: 32 sequences x ctx 32768, 16q/4kv
     d128, partial-RoPE prologue (theta 1e6; pairs i < 32 rotate, the rest are
-    identity) and the sigmoid gate from logits.  8 sequences against the
+    identity) and the sigmoid gate from logits.  16 sequences against the
     oracle, all 32 by bounds."""
     la = gpu
     rng = np.random.default_rng(5)
@@ -185,4 +197,4 @@ def test_cfg5_fullsize_lfm3_full_layer(gpu, orc, mode):
     d = _Decode(la, rng, np.full(32, 32768), 16, 4, 128, cos, sin, orc.rope_lut_lfm3(32768, 128, 128, 1e6, rf),
                 gate=True)
     got = d.run(mode)
-    d.check(orc, got, {0, 5, 9, 14, 18, 23, 27, 31}, f"cfg5 full {mode}")
+    d.check(orc, got, set(range(0, 32, 2)) | {31}, f"cfg5 full {mode}")
