@@ -58,16 +58,20 @@ const char *lfm_attn_last_error(void);
 const char *lfm_attn_last_plan(void);
 const char *lfm_attn_version(void);
 
-/* Tuning and tests, no reference counterpart: overrides of the split-KV
- * launch plan, process-wide.  plan NULL, "" or "auto" lets the library
- * choose; "grid", "balanced" or "wg" forces that form; waves (1, 2, 4, 8),
- * chunk (keys per workgroup) and min_tiles (32-key tiles per balanced
- * workgroup) force those counts, 0 = automatic.  The environment variables
- * LFM_ATTN_PLAN, LFM_ATTN_WAVES, LFM_ATTN_CHUNK and LFM_ATTN_MINTILES seed
- * the overrides once, at the library's first attention launch or first
- * call of this function; launches never read the environment.  Set it
- * between launches, not while another thread launches. */
-int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles);
+/* Tuning and tests, no reference counterpart: overrides of the launch
+ * plans, process-wide.  Split-KV attention: plan NULL, "" or "auto" lets the
+ * library choose; "grid", "balanced" or "wg" forces that form; waves (1, 2,
+ * 4, 8), chunk (keys per workgroup) and min_tiles (32-key tiles per balanced
+ * workgroup) force those counts.  prefill_chain: consecutive query tiles
+ * per workgroup of a sliding-window lfm_hip_lfm3_prefill_f16.  0 =
+ * automatic for every count.  The environment variables LFM_ATTN_PLAN,
+ * LFM_ATTN_WAVES, LFM_ATTN_CHUNK, LFM_ATTN_MINTILES and
+ * LFM_ATTN_PREFILL_CHAIN seed the overrides once, at the library's first
+ * launch or first call of this function; launches never read the
+ * environment.  Set it between launches, not while another thread
+ * launches. */
+int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles,
+                        uint32_t prefill_chain);
 /* Diagnostic, no reference counterpart, needs no device: the plan the
  * split-KV attention takes for a batch (n_seq sequences x n_rows rows, head
  * shape, sliding window, keys_hint as lfm_hip_gqa_f16_varlen; positions on

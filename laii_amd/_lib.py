@@ -27,7 +27,7 @@ SIGNATURES = {
     "lfm_attn_last_error": (C.c_char_p, []),
     "lfm_attn_last_plan": (C.c_char_p, []),
     "lfm_attn_version": (C.c_char_p, []),
-    "lfm_attn_set_tuning": (_int, [C.c_char_p, _u32, _u32, _u32]),
+    "lfm_attn_set_tuning": (_int, [C.c_char_p, _u32, _u32, _u32, _u32]),
     "lfm_attn_plan_preview": (_int, [_u32, _u32, _u32, _u32, _u32, _u32, _u32, _int, _int, _u32,
                                      C.POINTER(C.c_char_p), C.POINTER(_u32)]),
     "lfm_attn_device_count": (_int, [C.POINTER(_int)]),

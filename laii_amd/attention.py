@@ -297,18 +297,20 @@ def gqa_f16_varlen_noalloc(q: Ptr, gate: Ptr, gate_is_logit: bool, k_seq: Ptr, v
                                                 cap, scale, stream), "lfm_hip_gqa_f16_varlen_noalloc")
 
 
-def set_tuning(plan: Optional[str] = None, waves: int = 0, chunk: int = 0, min_tiles: int = 0) -> None:
+def set_tuning(plan: Optional[str] = None, waves: int = 0, chunk: int = 0, min_tiles: int = 0,
+               prefill_chain: int = 0) -> None:
     """Launch-plan overrides for tests and tuning (lfm_attn_set_tuning):
     plan None / "grid" / "balanced" / "wg", counts 0 = automatic."""
-    check(load().lfm_attn_set_tuning(None if plan is None else plan.encode(), waves, chunk, min_tiles),
-          "lfm_attn_set_tuning")
+    check(load().lfm_attn_set_tuning(None if plan is None else plan.encode(), waves, chunk, min_tiles,
+                                     prefill_chain), "lfm_attn_set_tuning")
 
 
 class tuning:
     """Context manager: the overrides inside, automatic choice afterwards."""
 
-    def __init__(self, plan: Optional[str] = None, waves: int = 0, chunk: int = 0, min_tiles: int = 0):
-        self.args = (plan, waves, chunk, min_tiles)
+    def __init__(self, plan: Optional[str] = None, waves: int = 0, chunk: int = 0, min_tiles: int = 0,
+                 prefill_chain: int = 0):
+        self.args = (plan, waves, chunk, min_tiles, prefill_chain)
 
     def __enter__(self):
         set_tuning(*self.args)

@@ -1306,10 +1306,10 @@ uint32_t device_cus() {
 }
 
 /* Launch-plan overrides for tests and tuning (lfm_attn_set_tuning).  The
- * environment (LFM_ATTN_PLAN, _WAVES, _CHUNK, _MINTILES) seeds them once, at
+ * environment (LFM_ATTN_PLAN, _WAVES, _CHUNK, _MINTILES, _PREFILL_CHAIN) seeds them once, at
  * the first launch or the first lfm_attn_set_tuning; launches read only
  * these values. */
-std::atomic<uint32_t> g_plan{0}, g_waves{0}, g_chunk{0}, g_min_tiles{0};
+std::atomic<uint32_t> g_plan{0}, g_waves{0}, g_chunk{0}, g_min_tiles{0}, g_prefill_chain{0};
 std::once_flag g_tuning_once;
 
 int plan_code(const char *name) {
@@ -1332,6 +1332,7 @@ void seed_tuning() {
     g_waves.store(env_count("LFM_ATTN_WAVES"));
     g_chunk.store(env_count("LFM_ATTN_CHUNK"));
     g_min_tiles.store(env_count("LFM_ATTN_MINTILES"));
+    g_prefill_chain.store(env_count("LFM_ATTN_PREFILL_CHAIN"));
 }
 
 /* Split partials: the caller's scratch (the allocation-free entry point) or
@@ -1605,10 +1606,10 @@ PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on
 
 Tuning current_tuning() {
     std::call_once(g_tuning_once, seed_tuning);
-    return Tuning{(char)g_plan.load(), g_waves.load(), g_chunk.load(), g_min_tiles.load()};
+    return Tuning{(char)g_plan.load(), g_waves.load(), g_chunk.load(), g_min_tiles.load(), g_prefill_chain.load()};
 }
 
-int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles) {
+int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles, uint32_t prefill_chain) {
     const int pc = plan_code(plan);
     if (pc < 0 || (waves && waves != 1u && waves != 2u && waves != 4u && waves != 8u)) return LFM_ATTN_E_INVALID;
     std::call_once(g_tuning_once, seed_tuning);
@@ -1616,6 +1617,7 @@ int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_ti
     g_waves.store(waves);
     g_chunk.store(chunk);
     g_min_tiles.store(min_tiles);
+    g_prefill_chain.store(prefill_chain);
     return LFM_ATTN_OK;
 }
 

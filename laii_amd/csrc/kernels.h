@@ -66,8 +66,9 @@ bool splitkv_supports(const AttnBatch &b);
 struct Tuning {
     char plan;
     uint32_t waves, chunk, min_tiles;
+    uint32_t prefill_chain; /* query tiles per sliding-window prefill workgroup */
 };
-int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles);
+int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles, uint32_t prefill_chain);
 Tuning current_tuning();
 
 /* The split-KV launch a batch takes on a device of `cus` compute units

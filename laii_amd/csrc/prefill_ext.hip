@@ -74,6 +74,7 @@ struct PrefillExtParams {
     float *out;         /* [n_seq][n_tok][n_head_q][HD]                             */
     uint64_t kv_seq_stride;
     uint32_t n_seq, n_tok, pos_0, kv_pos0, window, n_head_q, n_head_kv, kv_mul, tq, n_qtiles;
+    uint32_t chain;     /* consecutive query tiles per workgroup                    */
     int gate_is_logit;
     float qmul;         /* softmax scale * log2(e), applied to Q before its fp16 rounding */
 };
@@ -111,46 +112,61 @@ __device__ __forceinline__ void fetch16_lds(uint32_t voff, const void *sbase, ui
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 
-/* HD 128 (LFM3 layers) or 64: blocks of NH = HD / 64 halves for K, then V */
+/* Key-block geometry of query tile qt (positions t0 .. t0 + tq - 1): key
+ * rows [r_lo, r_hi) of the buffer in 32-key blocks [b_lo, b_hi), of which
+ * [u0, u1) need no per-key test -- every key >= the highest row's window
+ * start and <= the lowest row. */
+struct TileGeom {
+    uint32_t t0, lo_pos, hi_pos, r_hi, b_lo, b_hi, u0, u1;
+};
+
+__device__ __forceinline__ TileGeom tile_geom(const PrefillExtParams &P, uint32_t qt) {
+    TileGeom t;
+    t.t0     = qt * P.tq;
+    t.lo_pos = P.pos_0 + t.t0;
+    t.hi_pos = P.pos_0 + min(t.t0 + P.tq, P.n_tok) - 1u;
+    t.r_hi   = t.hi_pos + 1u - P.kv_pos0;
+    uint32_t first_key = P.window && t.lo_pos + 1u > P.window ? t.lo_pos + 1u - P.window : 0u;
+    first_key          = max(first_key, P.kv_pos0);
+    t.b_lo             = (first_key - P.kv_pos0) / KB;
+    t.b_hi             = (t.r_hi + KB - 1u) / KB;
+    const uint32_t free_key_lo = P.window && t.hi_pos + 1u > P.window ? t.hi_pos + 1u - P.window : 0u;
+    const uint32_t b_free = free_key_lo > P.kv_pos0 ? (free_key_lo - P.kv_pos0 + KB - 1u) / KB : 0u;
+    const uint32_t b_diag = (t.lo_pos - P.kv_pos0 + 1u) / KB;
+    t.u0 = min(max(t.b_lo, b_free), t.b_hi);
+    t.u1 = max(t.u0, min(t.b_hi, b_diag));
+    return t;
+}
+
+/* HD 128 (LFM3 layers) or 64: blocks of NH = HD / 64 halves for K, then V.
+ * A workgroup takes a chain of P.chain consecutive query tiles of one
+ * (sequence, KV head) (one tile for full layers): the blocks of its tiles
+ * form one stream through the LDS ring, so the next tile's first blocks are
+ * in flight while the current tile finishes, and a sliding-window tile --
+ * about window / 32 blocks -- does not pay the workgroup's set-up and the
+ * ring's fill on its own. */
 template <int HD>
 __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const PrefillExtParams P) {
     constexpr int NH   = HD / 64;            /* 64-dim halves per row              */
     constexpr int BLKB = 2 * NH * HALFB;     /* K halves, then V halves            */
     constexpr int NS   = HD / 32;            /* k-steps of Q.K^T                   */
     constexpr int NM   = HD / 16;            /* 16-dim tiles of O^T                */
-    constexpr int CPR  = HD / 8;             /* 16-byte chunks per row             */
     __shared__ __attribute__((aligned(1024))) uint8_t ring[NBUF * BLKB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    /* 1-D grid, heaviest query tiles first; consecutive workgroups take
+    /* 1-D grid, heaviest chains first; consecutive workgroups take
      * consecutive (sequence, KV head) pairs */
-    const uint32_t pairs = P.n_head_kv * P.n_seq;
-    const uint32_t qt    = P.n_qtiles - 1u - blockIdx.x / pairs;
-    const uint32_t pair  = blockIdx.x % pairs;
+    const uint32_t pairs    = P.n_head_kv * P.n_seq;
+    const uint32_t n_chains = (P.n_qtiles + P.chain - 1u) / P.chain;
+    const uint32_t chain    = n_chains - 1u - blockIdx.x / pairs;
+    const uint32_t pair     = blockIdx.x % pairs;
     const uint32_t kvh = pair % P.n_head_kv, s = pair / P.n_head_kv;
-    const uint32_t t0  = qt * P.tq;
+    const uint32_t qt_first = chain * P.chain, qt_end = min(qt_first + P.chain, P.n_qtiles);
 
     const uint16_t *kc = P.k + (size_t)s * P.kv_seq_stride + (size_t)kvh * HD;
     const uint16_t *vc = P.v + (size_t)s * P.kv_seq_stride + (size_t)kvh * HD;
     const size_t row   = (size_t)P.n_head_kv * HD;
-
-    /* key rows [r_lo, r_hi) of the buffer, in 32-key blocks */
-    const uint32_t lo_pos = P.pos_0 + t0;
-    const uint32_t hi_pos = P.pos_0 + min(t0 + P.tq, P.n_tok) - 1u;
-    const uint32_t r_hi   = hi_pos + 1u - P.kv_pos0;
-    uint32_t first_key    = P.window && lo_pos + 1u > P.window ? lo_pos + 1u - P.window : 0u;
-    first_key             = max(first_key, P.kv_pos0);
-    const uint32_t b_lo   = (first_key - P.kv_pos0) / KB;    /* first block       */
-    const uint32_t b_hi   = (r_hi + KB - 1u) / KB;           /* past the last     */
-    /* blocks needing no per-key test: every key >= the highest row's window
-     * start and <= the lowest row, i.e. blocks [u0, u1) */
-    const uint32_t free_key_lo = P.window && hi_pos + 1u > P.window ? hi_pos + 1u - P.window : 0u;
-    const uint32_t b_free = free_key_lo > P.kv_pos0 ? (free_key_lo - P.kv_pos0 + KB - 1u) / KB : 0u;
-    const uint32_t b_diag = (lo_pos - P.kv_pos0 + 1u) / KB;
-    const uint32_t u0     = min(max(b_lo, b_free), b_hi);
-    const uint32_t u1     = max(u0, min(b_hi, b_diag));
-    auto block_masked = [&](uint32_t b) { return b < u0 || b >= u1; };
 
     /* ---- staging: the K part of a block (NH halves of 4 KB) is NH * 4
      * pieces of 1 KB; wave w fetches pieces w + 4 e (e < NH) of it and of the
@@ -167,10 +183,23 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
     }
     const uint32_t wv       = __builtin_amdgcn_readfirstlane((uint32_t)wave);
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring; /* LDS address of the ring */
+
+    /* ---- the block stream: block j (over the chain's tiles in order) sits
+     * in ring slot j % NBUF; the fetch cursor runs two blocks ahead of the
+     * block being entered */
+    uint32_t n_stream = 0;
+    for (uint32_t qt = qt_first; qt < qt_end; ++qt) {
+        const TileGeom t = tile_geom(P, qt);
+        n_stream += t.b_hi - t.b_lo;
+    }
+    uint32_t f_qt = qt_first, f_j = 0;
+    TileGeom fg   = tile_geom(P, f_qt);
+    uint32_t f_b  = fg.b_lo;
     /* 2 NH fetches per wave and block (vmcnt counts them) */
-    auto fetch_block = [&](uint32_t b) {
-        const uint32_t slot = ring_lds + (b % NBUF) * BLKB;
-        if ((b + 1u) * KB <= r_hi) {
+    auto fetch_next = [&]() {
+        const uint32_t slot = ring_lds + (f_j % NBUF) * BLKB;
+        const uint32_t b    = f_b;
+        if ((b + 1u) * KB <= fg.r_hi) {
             /* a whole block: uniform base, fixed per-lane offsets */
             const size_t boff = (size_t)b * KB * row;
 #pragma unroll
@@ -184,59 +213,25 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
 #pragma unroll
             for (int e = 0; e < NH; ++e) {
                 uint32_t r = b * KB + st_row[e];
-                r = r < r_hi ? r : r_hi - 1u; /* rows past the keys: masked */
+                r = r < fg.r_hi ? r : fg.r_hi - 1u; /* rows past the keys: masked */
                 const size_t off     = (size_t)r * row + st_col[e];
                 const uint32_t piece = slot + 1024u * (wv + 4u * (uint32_t)e);
                 fetch16_lds(kc + off, piece);
                 fetch16_lds(vc + off, piece + (uint32_t)(NH * HALFB));
             }
         }
+        ++f_j;
+        if (++f_b == fg.b_hi && ++f_qt < qt_end) {
+            fg  = tile_geom(P, f_qt);
+            f_b = fg.b_lo;
+        }
     };
 
-    /* the first two blocks are in flight before the Q loads: the wait for Q
-     * (which also covers these older fetches) then takes one memory round
-     * trip, not two */
-    fetch_block(b_lo);
-    if (b_lo + 1u < b_hi) fetch_block(b_lo + 1u);
-
-    /* ---- columns of this lane: (head j, row t) per N-tile -------------- */
-    uint32_t col_pos[NT], col_lo[NT];
-    bool col_ok[NT];
-    half8_t qf[NT][NS];
-    /* all Q loads are issued before any is used (qp is a valid row for a
-     * padding column too; its values are zeroed after): with a use between
-     * them the compiler waited for each column tile's loads, one memory
-     * round trip per tile */
-    float4 qraw[NT][NS][2];
-    float graw[NT]; /* the output gates, loaded now: the epilogue does not wait for them */
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const uint32_t c = (uint32_t)(wave * 32 + nt * 16 + l16);
-        const uint32_t j = c / P.tq, t = t0 + c % P.tq;
-        col_ok[nt]  = t < P.n_tok;
-        graw[nt]    = (P.gate && col_ok[nt]) ? P.gate[((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j]
-                                             : 1.0f;
-        col_pos[nt] = P.pos_0 + t;
-        col_lo[nt]  = (P.window && col_pos[nt] + 1u > P.window) ? col_pos[nt] + 1u - P.window : 0u;
-        const float *qp = P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q + kvh * P.kv_mul + j) * HD + 8 * g;
-#pragma unroll
-        for (int st = 0; st < NS; ++st) {
-            qraw[nt][st][0] = *reinterpret_cast<const float4 *>(qp + 32 * st);
-            qraw[nt][st][1] = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int st = 0; st < NS; ++st) {
-            const float4 a = qraw[nt][st][0], b = qraw[nt][st][1];
-            const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            half8_t h;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[e] = col_ok[nt] ? (_Float16)(x[e] * P.qmul) : (_Float16)0.0f;
-            qf[nt][st] = h;
-        }
+    /* the first two blocks are in flight before the first tile's Q loads:
+     * the wait for Q (which also covers these older fetches) then takes one
+     * memory round trip, not two */
+    fetch_next();
+    if (n_stream > 1u) fetch_next();
 
     /* fragment offsets within a 64-dim half (bytes).  K: row 16*mt + l16,
      * chunk 4*(st % 2) + g.  V (transposing read): lane l16 of group g
@@ -249,203 +244,268 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
     for (int mt = 0; mt < 4; ++mt)
         voff[mt] = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)(mt ^ g) + 16u * ((l16 >> 1) & 1) +
                    8u * (l16 & 1);
-
-    float4_t oacc[NM][NT];
-    float4_t negm[NT];
-    float4_t lacc[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        negm[nt] = (float4_t)0.0f;
-        lacc[nt] = (float4_t)0.0f;
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
-    }
     const half8_t ones8 = (half8_t)(_Float16)1.0f;
 
-    /* S^T of block b: two 16-key tiles x NT column tiles */
-    auto scores = [&](auto mask_tag, uint32_t b, float4_t (&sc)[2][NT]) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        const uint8_t *kb = ring + (b % NBUF) * BLKB;
+    uint32_t j0 = 0; /* stream index of the current tile's first block */
+    for (uint32_t qt = qt_first; qt < qt_end; ++qt) {
+        const TileGeom tg = tile_geom(P, qt);
+        const uint32_t t0 = tg.t0;
+        auto block_masked = [&](uint32_t b) { return b < tg.u0 || b >= tg.u1; };
+        auto block_lds    = [&](uint32_t b) { return ring + ((j0 + b - tg.b_lo) % NBUF) * BLKB; };
+
+        /* ---- columns of this lane: (head j, row t) per N-tile -------------- */
+        uint32_t col_pos[NT], col_lo[NT];
+        bool col_ok[NT];
+        half8_t qf[NT][NS];
+        /* all Q loads are issued before any is used (qp is a valid row for a
+         * padding column too; its values are zeroed after): with a use between
+         * them the compiler waited for each column tile's loads, one memory
+         * round trip per tile */
+        float4 qraw[NT][NS][2];
+        float graw[NT]; /* the output gates, loaded now: the epilogue does not wait for them */
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
-            half8_t kf[NS];
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t c = (uint32_t)(wave * 32 + nt * 16 + l16);
+            const uint32_t j = c / P.tq, t = t0 + c % P.tq;
+            col_ok[nt]  = t < P.n_tok;
+            graw[nt]    = (P.gate && col_ok[nt]) ? P.gate[((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j]
+                                                 : 1.0f;
+            col_pos[nt] = P.pos_0 + t;
+            col_lo[nt]  = (P.window && col_pos[nt] + 1u > P.window) ? col_pos[nt] + 1u - P.window : 0u;
+            const float *qp =
+                P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q + kvh * P.kv_mul + j) * HD + 8 * g;
 #pragma unroll
-            for (int h = 0; h < NH; ++h) {
-                kf[2 * h]     = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff0));
-                kf[2 * h + 1] = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff1));
-            }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                float4_t a = mfma(kf[0], qf[nt][0], negm[nt]);
-#pragma unroll
-                for (int st = 1; st < NS; ++st) a = mfma(kf[st], qf[nt][st], a);
-                sc[mt][nt] = a;
+            for (int st = 0; st < NS; ++st) {
+                qraw[nt][st][0] = *reinterpret_cast<const float4 *>(qp + 32 * st);
+                qraw[nt][st][1] = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
             }
         }
-        if constexpr (MASK) {
-            /* element (mt, i) is key key0 + 16 mt + i of the column */
-            const int key0 = (int)(P.kv_pos0 + b * KB) + 4 * g;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                const float4 a = qraw[nt][st][0], b = qraw[nt][st][1];
+                const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                half8_t h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = col_ok[nt] ? (_Float16)(x[e] * P.qmul) : (_Float16)0.0f;
+                qf[nt][st] = h;
+            }
+
+        float4_t oacc[NM][NT];
+        float4_t negm[NT];
+        float4_t lacc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            negm[nt] = (float4_t)0.0f;
+            lacc[nt] = (float4_t)0.0f;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
+        }
+
+        /* S^T of block b: two 16-key tiles x NT column tiles */
+        auto scores = [&](auto mask_tag, uint32_t b, float4_t (&sc)[2][NT]) {
+            constexpr bool MASK = decltype(mask_tag)::value;
+            const uint8_t *kb = block_lds(b);
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                half8_t kf[NS];
+#pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    kf[2 * h]     = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff0));
+                    kf[2 * h + 1] = as_half8(*reinterpret_cast<const u32x4_t *>(kb + h * HALFB + mt * 16 * 128 + koff1));
+                }
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    float4_t a = mfma(kf[0], qf[nt][0], negm[nt]);
+#pragma unroll
+                    for (int st = 1; st < NS; ++st) a = mfma(kf[st], qf[nt][st], a);
+                    sc[mt][nt] = a;
+                }
+            }
+            if constexpr (MASK) {
+                /* element (mt, i) is key key0 + 16 mt + i of the column */
+                const int key0 = (int)(P.kv_pos0 + b * KB) + 4 * g;
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    const int hi = (int)col_pos[nt] - key0, lo = (int)col_lo[nt] - key0;
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (16 * mt + i > hi || 16 * mt + i < lo) sc[mt][nt][i] = -INFINITY;
+                }
+            }
+        };
+
+        /* lazy max per column: m is set by the first block holding one of the
+         * column's keys (its exact maximum there) and raised later only when a
+         * block exceeds it by more than kLazy, rescaling O, l and the pending
+         * scores (a rare, wave-uniform branch).  With a window, a column's first
+         * keys may lie in a later block than the tile's first; until then its
+         * scores are all masked, p = 0 and O = l = 0, so setting m needs no
+         * rescale (and exp2(-m) could overflow). */
+        bool mset[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) mset[nt] = false;
+        auto update_max = [&](float4_t (&sc)[2][NT]) {
+            float mx[NT];
+            bool any_raise = false;
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                const int hi = (int)col_pos[nt] - key0, lo = (int)col_lo[nt] - key0;
+                float v = max3(max3(sc[0][nt][0], sc[0][nt][1], sc[0][nt][2]), sc[0][nt][3], sc[1][nt][0]);
+                v = max3(max3(v, sc[1][nt][1], sc[1][nt][2]), sc[1][nt][3], -INFINITY);
+                mx[nt] = v;
+                any_raise |= v > kLazy || (!mset[nt] && v > -INFINITY);
+            }
+            if (__builtin_amdgcn_ballot_w64(any_raise) != 0ull) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    float v = mx[nt]; /* column max over the 4 lanes holding it */
+                    v = fmaxf(v, __shfl_xor(v, 16));
+                    v = fmaxf(v, __shfl_xor(v, 32));
+                    const bool raise  = v > kLazy || (!mset[nt] && v > -INFINITY);
+                    const float inc   = raise ? v : 0.0f;
+                    const float alpha = mset[nt] ? __builtin_amdgcn_exp2f(-inc) : 1.0f;
+                    mset[nt] = mset[nt] || raise;
+                    negm[nt] -= inc;
+                    lacc[nt] *= alpha;
+                    sc[0][nt] -= inc;
+                    sc[1][nt] -= inc;
+#pragma unroll
+                    for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
+                }
+            }
+        };
+
+        auto accumulate = [&](uint32_t b, const float4_t (&sc)[2][NT]) {
+            u32x4_t pf[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const float4_t a = sc[0][nt], c = sc[1][nt];
+                const half2_t h0 = exp_pk(a[0], a[1]);
+                const half2_t h1 = exp_pk(a[2], a[3]);
+                const half2_t h2 = exp_pk(c[0], c[1]);
+                const half2_t h3 = exp_pk(c[2], c[3]);
+                u32x4_t w;
+                w[0] = __builtin_bit_cast(uint32_t, h0);
+                w[1] = __builtin_bit_cast(uint32_t, h1);
+                w[2] = __builtin_bit_cast(uint32_t, h2);
+                w[3] = __builtin_bit_cast(uint32_t, h3);
+                pf[nt] = w;
+            }
+            const uint8_t *vb = block_lds(b) + NH * HALFB;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const uint8_t *vh = vb + (mt >> 2) * HALFB;
+                const half4_t lo  = lds_read_tr(vh + voff[mt & 3]);
+                const half4_t hi  = lds_read_tr(vh + 16 * 128 + voff[mt & 3]);
+                const half8_t av  = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
+        };
+
+        /* entering block b (at the start of step b - 1, before S^T(b)): this
+         * wave's fetches of block b have landed (those of the next stream
+         * block may still be in flight), and the barrier makes every wave's
+         * part visible.  The previous stream block is still in use (P.V of the
+         * previous step); the ring slot two blocks ahead held the block two
+         * behind, which every wave finished before the barrier, so the stream
+         * block two ahead -- of this tile or the next -- is fetched into it. */
+        auto enter_block = [&](uint32_t b) {
+            const uint32_t j = j0 + b - tg.b_lo;
+            if (j + 1u < n_stream) {
+                if constexpr (NH == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+                else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            __syncthreads();
+            if (j + 2u < n_stream) fetch_next();
+        };
+
+        const uint32_t b_lo = tg.b_lo, b_hi = tg.b_hi, u0 = tg.u0, u1 = tg.u1;
+        enter_block(b_lo);
+        float4_t scur[2][NT];
+        if (block_masked(b_lo)) scores(std::true_type{}, b_lo, scur);
+        else scores(std::false_type{}, b_lo, scur);
+        update_max(scur);
+        /* step b: S^T(b + 1) into the other register set, then P(b) and PV(b);
+         * two steps per iteration with the sets swapping roles */
+        float4_t snxt[2][NT];
+        auto step = [&](auto mask_tag, uint32_t b, float4_t(&sc)[2][NT], float4_t(&sn)[2][NT])
+                        __attribute__((always_inline)) {
+            enter_block(b + 1u);
+            scores(mask_tag, b + 1u, sn);
+            accumulate(b, sc);
+            update_max(sn);
+        };
+        uint32_t b = b_lo;
+        /* steps b .. b_end - 1; S^T(b) is in scur on entry and on exit */
+        auto run_steps = [&](auto mask_tag, uint32_t b_end) __attribute__((always_inline)) {
+            for (; b + 2u <= b_end; b += 2u) {
+                step(mask_tag, b, scur, snxt);
+                step(mask_tag, b + 1u, snxt, scur);
+            }
+            if (b < b_end) {
+                step(mask_tag, b, scur, snxt);
 #pragma unroll
                 for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (16 * mt + i > hi || 16 * mt + i < lo) sc[mt][nt][i] = -INFINITY;
+                    for (int nt = 0; nt < NT; ++nt) scur[mt][nt] = snxt[mt][nt];
+                ++b;
             }
-        }
-    };
+        };
+        /* blocks [u0, u1) need no mask; masked ones sit below (window edge)
+         * and above (diagonal) */
+        run_steps(std::true_type{}, u0 > 0u ? u0 - 1u : 0u);
+        run_steps(std::false_type{}, u1 > 0u ? u1 - 1u : 0u);
+        run_steps(std::true_type{}, b_hi - 1u);
+        accumulate(b, scur);
 
-    /* lazy max per column: m is set by the first block holding one of the
-     * column's keys (its exact maximum there) and raised later only when a
-     * block exceeds it by more than kLazy, rescaling O, l and the pending
-     * scores (a rare, wave-uniform branch).  With a window, a column's first
-     * keys may lie in a later block than the workgroup's first; until then
-     * its scores are all masked, p = 0 and O = l = 0, so setting m needs no
-     * rescale (and exp2(-m) could overflow). */
-    bool mset[NT];
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) mset[nt] = false;
-    auto update_max = [&](float4_t (&sc)[2][NT]) {
-        float mx[NT];
-        bool any_raise = false;
+        /* ---- epilogue: O * gate / l ------------------------------------------ */
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            float v = max3(max3(sc[0][nt][0], sc[0][nt][1], sc[0][nt][2]), sc[0][nt][3], sc[1][nt][0]);
-            v = max3(max3(v, sc[1][nt][1], sc[1][nt][2]), sc[1][nt][3], -INFINITY);
-            mx[nt] = v;
-            any_raise |= v > kLazy || (!mset[nt] && v > -INFINITY);
-        }
-        if (__builtin_amdgcn_ballot_w64(any_raise) != 0ull) {
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                float v = mx[nt]; /* column max over the 4 lanes holding it */
-                v = fmaxf(v, __shfl_xor(v, 16));
-                v = fmaxf(v, __shfl_xor(v, 32));
-                const bool raise  = v > kLazy || (!mset[nt] && v > -INFINITY);
-                const float inc   = raise ? v : 0.0f;
-                const float alpha = mset[nt] ? __builtin_amdgcn_exp2f(-inc) : 1.0f;
-                mset[nt] = mset[nt] || raise;
-                negm[nt] -= inc;
-                lacc[nt] *= alpha;
-                sc[0][nt] -= inc;
-                sc[1][nt] -= inc;
-#pragma unroll
-                for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha;
+            const float lt = lacc[nt][0];
+            if (!col_ok[nt]) continue;
+            const uint32_t c    = (uint32_t)(wave * 32 + nt * 16 + l16);
+            const uint32_t j    = c / P.tq, t = t0 + c % P.tq;
+            const size_t orow   = ((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j;
+            float gv            = 1.0f;
+            if (P.gate) {
+                const float gl = graw[nt];
+                gv             = P.gate_is_logit ? 1.0f / (1.0f + expf(-gl)) : gl;
             }
+            const float inv = lt > 0.0f ? gv / lt : 0.0f;
+            float *op       = P.out + orow * HD;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt)
+                *reinterpret_cast<float4 *>(op + 16 * mt + 4 * g) =
+                    make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv, oacc[mt][nt][2] * inv,
+                                oacc[mt][nt][3] * inv);
         }
-    };
-
-    auto accumulate = [&](uint32_t b, const float4_t (&sc)[2][NT]) {
-        u32x4_t pf[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const float4_t a = sc[0][nt], c = sc[1][nt];
-            const half2_t h0 = exp_pk(a[0], a[1]);
-            const half2_t h1 = exp_pk(a[2], a[3]);
-            const half2_t h2 = exp_pk(c[0], c[1]);
-            const half2_t h3 = exp_pk(c[2], c[3]);
-            u32x4_t w;
-            w[0] = __builtin_bit_cast(uint32_t, h0);
-            w[1] = __builtin_bit_cast(uint32_t, h1);
-            w[2] = __builtin_bit_cast(uint32_t, h2);
-            w[3] = __builtin_bit_cast(uint32_t, h3);
-            pf[nt] = w;
-        }
-        const uint8_t *vb = ring + (b % NBUF) * BLKB + NH * HALFB;
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt) {
-            const uint8_t *vh = vb + (mt >> 2) * HALFB;
-            const half4_t lo  = lds_read_tr(vh + voff[mt & 3]);
-            const half4_t hi  = lds_read_tr(vh + 16 * 128 + voff[mt & 3]);
-            const half8_t av  = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) oacc[mt][nt] = mfma(av, as_half8(pf[nt]), oacc[mt][nt]);
-        }
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) lacc[nt] = mfma(ones8, as_half8(pf[nt]), lacc[nt]);
-    };
-
-    /* entering block b (at the start of step b - 1, before S^T(b)): this
-     * wave's fetches of block b have landed (those of block b + 1 may still
-     * be in flight), and the barrier makes every wave's part visible.  Block
-     * b - 1 is still in use (P.V of step b - 1); the slot of block b + 2 held
-     * block b - 2, which every wave finished before the barrier, so block
-     * b + 2 is fetched into it. */
-    auto enter_block = [&](uint32_t b) {
-        if (b + 1u < b_hi) {
-            if constexpr (NH == 2) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        __syncthreads();
-        if (b + 2u < b_hi) fetch_block(b + 2u);
-    };
-
-    enter_block(b_lo);
-    float4_t scur[2][NT];
-    if (block_masked(b_lo)) scores(std::true_type{}, b_lo, scur);
-    else scores(std::false_type{}, b_lo, scur);
-    update_max(scur);
-    /* step b: S^T(b + 1) into the other register set, then P(b) and PV(b);
-     * two steps per iteration with the sets swapping roles */
-    float4_t snxt[2][NT];
-    auto step = [&](auto mask_tag, uint32_t b, float4_t(&sc)[2][NT], float4_t(&sn)[2][NT])
-                    __attribute__((always_inline)) {
-        enter_block(b + 1u);
-        scores(mask_tag, b + 1u, sn);
-        accumulate(b, sc);
-        update_max(sn);
-    };
-    uint32_t b = b_lo;
-    /* steps b .. b_end - 1; S^T(b) is in scur on entry and on exit */
-    auto run_steps = [&](auto mask_tag, uint32_t b_end) __attribute__((always_inline)) {
-        for (; b + 2u <= b_end; b += 2u) {
-            step(mask_tag, b, scur, snxt);
-            step(mask_tag, b + 1u, snxt, scur);
-        }
-        if (b < b_end) {
-            step(mask_tag, b, scur, snxt);
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) scur[mt][nt] = snxt[mt][nt];
-            ++b;
-        }
-    };
-    /* blocks [u0, u1) need no mask; masked ones sit below (window edge)
-     * and above (diagonal) */
-    run_steps(std::true_type{}, u0 > 0u ? u0 - 1u : 0u);
-    run_steps(std::false_type{}, u1 > 0u ? u1 - 1u : 0u);
-    run_steps(std::true_type{}, b_hi - 1u);
-    accumulate(b, scur);
-
-    /* ---- epilogue: O * gate / l ------------------------------------------ */
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-        const float lt = lacc[nt][0];
-        if (!col_ok[nt]) continue;
-        const uint32_t c    = (uint32_t)(wave * 32 + nt * 16 + l16);
-        const uint32_t j    = c / P.tq, t = t0 + c % P.tq;
-        const size_t orow   = ((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j;
-        float gv            = 1.0f;
-        if (P.gate) {
-            const float gl = graw[nt];
-            gv             = P.gate_is_logit ? 1.0f / (1.0f + expf(-gl)) : gl;
-        }
-        const float inv = lt > 0.0f ? gv / lt : 0.0f;
-        float *op       = P.out + orow * HD;
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt)
-            *reinterpret_cast<float4 *>(op + 16 * mt + 4 * g) =
-                make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv, oacc[mt][nt][2] * inv,
-                            oacc[mt][nt][3] * inv);
+        j0 += b_hi - b_lo;
     }
 }
 
 } // namespace
+
+/* Query tiles per workgroup: one unless set by lfm_attn_set_tuning.  On
+ * MI355X the sliding-window workload (B 4 x 4096, 16q/4kv, window 256) took
+ * 81.9 us with one tile per workgroup, 84.5 us with chains of 2 and 89.6 us
+ * with chains of 4: chaining removes the workgroup launches and ring fills
+ * but not the exposed latency of each tile's fp32 Q loads, and it lowers
+ * the number of workgroups that hide it for one another.  Full layers
+ * (window 0 or above 32 tiles) always take one tile per workgroup. */
+static uint32_t prefill_chain(uint32_t window, uint32_t tq, uint32_t n_qtiles) {
+    if (!window || window > 32u * tq) return 1u;
+    const uint32_t forced = current_tuning().prefill_chain; /* tests, tuning */
+    return forced ? min(forced, n_qtiles) : 1u;
+}
 
 bool prefill_ext_supports(uint32_t head_dim, uint32_t kv_mul) {
     return (head_dim == 128u || head_dim == 64u) && kv_mul >= 1u && kv_mul <= 32u && (128u % kv_mul) == 0u;
@@ -474,13 +534,15 @@ int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, con
     P.tq            = 128u / P.kv_mul;
     P.n_qtiles      = (n_tok + P.tq - 1u) / P.tq;
     P.qmul          = scale * kLog2e;
+    P.chain         = prefill_chain(window, P.tq, P.n_qtiles);
+    const uint32_t n_wg = ((P.n_qtiles + P.chain - 1u) / P.chain) * n_head_kv * n_seq;
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
     if (head_dim == 128u)
-        hipLaunchKernelGGL(k_prefill_ext<128>, dim3(P.n_qtiles * n_head_kv * n_seq), dim3(256), 0, stream, P);
+        hipLaunchKernelGGL(k_prefill_ext<128>, dim3(n_wg), dim3(256), 0, stream, P);
     else
-        hipLaunchKernelGGL(k_prefill_ext<64>, dim3(P.n_qtiles * n_head_kv * n_seq), dim3(256), 0, stream, P);
+        hipLaunchKernelGGL(k_prefill_ext<64>, dim3(n_wg), dim3(256), 0, stream, P);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
     return hip_status(e);

@@ -134,8 +134,9 @@ const char *lfm_attn_last_plan(void) { return lfm::g_last_plan; }
 
 const char *lfm_attn_version(void) { return "lfm_attn 0.1 gfx950"; }
 
-int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles) {
-    return lfm::set_tuning(plan, waves, chunk, min_tiles);
+int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles,
+                        uint32_t prefill_chain) {
+    return lfm::set_tuning(plan, waves, chunk, min_tiles, prefill_chain);
 }
 
 int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,

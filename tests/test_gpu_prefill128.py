@@ -25,8 +25,10 @@ def sigmoid(g):
     return (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
 
 
-def run(la, rng, n_seq, n_tok, pos_0, nq, nkv, window=0, kv_pos0=0, gate=True, q=None, k16=None, v16=None, hd=HD):
-    """fp32 Q rows, fp16 K/V buffers whose row r is position kv_pos0 + r."""
+def run(la, rng, n_seq, n_tok, pos_0, nq, nkv, window=0, kv_pos0=0, gate=True, q=None, k16=None, v16=None, hd=HD,
+        gate_values=None):
+    """fp32 Q rows, fp16 K/V buffers whose row r is position kv_pos0 + r
+    (gate logits drawn unless gate_values are given)."""
     HD = hd
     rows = pos_0 + n_tok - kv_pos0
     if q is None:
@@ -35,7 +37,8 @@ def run(la, rng, n_seq, n_tok, pos_0, nq, nkv, window=0, kv_pos0=0, gate=True, q
         k16 = np.stack([rand_kv(rng, rows, nkv, HD) for _ in range(n_seq)])
     if v16 is None:
         v16 = np.stack([rand_kv(rng, rows, nkv, HD) for _ in range(n_seq)])
-    g = rng.standard_normal((n_seq, n_tok, nq)).astype(np.float32) if gate else None
+    g = gate_values if gate_values is not None else (
+        rng.standard_normal((n_seq, n_tok, nq)).astype(np.float32) if gate else None)
     out = la.DeviceArray.zeros((n_seq, n_tok, nq, HD), np.float32)
     la.lfm3_prefill_f16(dev(la, q), dev(la, k16), dev(la, v16), None if g is None else dev(la, g), True, out, n_seq,
                         n_tok, pos_0, kv_pos0, rows * nkv * HD, window, nq, nkv, HD)
@@ -167,3 +170,47 @@ def test_prefill_ext_head_dim_64(gpu, orc, n_tok, pos_0, window, kv_pos0, gate):
     for s in range(2):
         want = oracle(orc, q, k16, v16, g, s, pos_0, kv_pos0, window, 32, 8)
         parity(got[s], want, what=f"prefill ext d64 window={window} s={s} n={n_tok} pos0={pos_0}")
+
+
+@pytest.mark.parametrize("chain", [2, 3, 5])
+@pytest.mark.parametrize("n_tok,pos_0,window,kv_pos0,nq,nkv,hd", [
+    (700, 0, 256, 0, 16, 4, 128),     # LFM3 SWA heads: 22 query tiles, ragged last chain
+    (400, 1000, 256, 745, 16, 4, 128),  # prompt after a cached window (linear copy)
+    (250, 40, 33, 8, 16, 8, 128),     # odd window, kv_mul 2 (64-position tiles)
+    (300, 5, 100, 0, 32, 8, 64),      # head_dim 64
+    (100, 500, 1, 500, 16, 4, 128),   # window 1
+])
+def test_prefill128_window_chains(gpu, orc, chain, n_tok, pos_0, window, kv_pos0, nq, nkv, hd):
+    """Sliding-window prefill with `chain` consecutive query tiles per
+    workgroup (their key blocks streamed through one LDS ring, the next
+    tile's first blocks fetched while the current one finishes): outputs
+    bit-identical to one tile per workgroup (same blocks, same order, same
+    arithmetic per tile) and within tolerance of the oracle."""
+    la = gpu
+    rng = np.random.default_rng(n_tok + window + chain)
+    with la.tuning(prefill_chain=1):
+        q, k16, v16, g, one = run(la, rng, 2, n_tok, pos_0, nq, nkv, window=window, kv_pos0=kv_pos0, hd=hd)
+    with la.tuning(prefill_chain=chain):
+        _, _, _, _, got = run(la, rng, 2, n_tok, pos_0, nq, nkv, window=window, kv_pos0=kv_pos0, q=q, k16=k16,
+                              v16=v16, hd=hd, gate_values=g)
+    assert np.array_equal(got.view(np.uint32), one.view(np.uint32)), "chained tiles differ from single tiles"
+    for s in range(2):
+        want = oracle(orc, q, k16, v16, g, s, pos_0, kv_pos0, window, nq, nkv)
+        parity(got[s], want, what=f"prefill window={window} chain={chain} s={s} n={n_tok} d{hd}")
+
+
+def test_prefill128_swa256_bench_shape_sampled(gpu, orc):
+    """The bench's sliding-window workload (B 4 x 4096, 16q/4kv d128, window
+    256, gate) with the automatic chain length: rows at chain and tile
+    boundaries against the oracle, and bit-identical to one tile per
+    workgroup."""
+    la = gpu
+    rng = np.random.default_rng(4256)
+    q, k16, v16, g, got = run(la, rng, 4, 4096, 0, 16, 4, window=256)
+    with la.tuning(prefill_chain=1):
+        _, _, _, _, one = run(la, rng, 4, 4096, 0, 16, 4, window=256, q=q, k16=k16, v16=v16, gate_values=g)
+    assert np.array_equal(got.view(np.uint32), one.view(np.uint32))
+    rows = [0, 31, 32, 127, 128, 255, 256, 257, 1023, 1024, 2047, 2048, 4064, 4095]
+    for s in (0, 3):
+        want = oracle(orc, q, k16, v16, g, s, 0, 0, 256, 16, 4, rows=rows)
+        parity(got[s][rows], want, what=f"prefill128 swa256 B4x4096 s={s} sampled")
