@@ -438,7 +438,8 @@ def time_steps(hip, wl, steps, warmup):
 
 # Launches of one step, by plan: split keys need the merge kernel after the
 # attention kernel except in the in-workgroup form ("wg").
-STEP_KERNELS = {"balanced": "k_splitkv_bal + k_merge_bal", "grid": "k_splitkv + k_merge (one launch when the "
+STEP_KERNELS = {"balanced": "k_splitkv_bal + k_merge_bal",
+                "balanced-dma": "k_splitkv_bal (LDS-streamed segments) + k_merge_bal", "grid": "k_splitkv + k_merge (one launch when the "
                 "keys are not split)", "wg": "k_splitkv_wg (merge inside the workgroup)", "generic": "k_generic"}
 
 

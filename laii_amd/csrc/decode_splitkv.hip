@@ -843,6 +843,301 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     }
 }
 
+/* ---- LDS-streamed segments (head_dim 64, no fused prologue) -----------------
+ * run_segment keeps one 32-key sub-tile in flight per wave, in registers, so
+ * a wave's throughput is one sub-tile per memory round trip; with two 16-
+ * column tiles (speculative verify) its registers leave no room for a
+ * second.  Here both K and V of each sub-tile move from global memory
+ * straight into a ring of DMA_NBUF sub-tiles in the wave's own LDS area
+ * (global_load_lds_dwordx4: no registers held while a load is in flight),
+ * three sub-tiles ahead of the one being consumed, and the wave reads K
+ * fragments (ds_read_b128) and the transposed V operand (ds_read_b64_tr_b16)
+ * from there.  Each sub-tile is [32 keys][128 B] of K then of V, the 16-B
+ * chunks of row r XOR-swizzled by 2 * ((r >> 2) & 3) (the layout run_segment
+ * stores V in).  The loads are inline assembly, invisible to the compiler's
+ * wait counting, so the waits are explicit: every vector memory operation in
+ * the key loop is one of these (8 per sub-tile), and before sub-tile t is
+ * read the wave waits until only the sub-tiles issued after it (at most 3 x
+ * 8) remain outstanding.  Waves never read each other's areas, so no
+ * workgroup barrier runs. */
+constexpr int DMA_NBUF    = 4;                 /* ring slots per wave           */
+constexpr int DMA_TILE    = 2 * 32 * 64 * 2;   /* bytes per slot: K, then V     */
+constexpr int DMA_AHEAD   = 3;                 /* sub-tiles in flight ahead      */
+constexpr int DMA_PER_SUB = 8;                 /* 1-KB loads per sub-tile        */
+static_assert(DMA_AHEAD < DMA_NBUF, "the slot being fetched must not be the one being read");
+
+/* 16 B per lane into LDS: lane l writes [lds + 16 l, lds + 16 l + 16) (lds in
+ * M0), from a wave-uniform base plus a 32-bit per-lane byte offset, or from
+ * a per-lane address; STREAM: the non-temporal cache policy. */
+template <bool STREAM>
+__device__ __forceinline__ void dma16(uint32_t voff, gu8_ptr sbase, uint32_t lds) {
+    if constexpr (STREAM)
+        asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+    else
+        asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+template <bool STREAM>
+__device__ __forceinline__ void dma16(gu8_ptr addr, uint32_t lds) {
+    if constexpr (STREAM) asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(addr), "{m0}"(lds) : "memory");
+    else asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(addr), "{m0}"(lds) : "memory");
+}
+
+/* Wait until at most `younger` sub-tiles' loads (wave-uniform, <= 3) are
+ * outstanding. */
+__device__ __forceinline__ void dma_wait(uint32_t younger) {
+    static_assert(DMA_AHEAD == 3 && DMA_PER_SUB == 8, "wait counts below");
+    if (younger >= 3u) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+    else if (younger == 2u) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (younger == 1u) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+template <int NT>
+__device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *ring, uint32_t s, uint32_t pos0,
+                                                uint32_t kvh, uint32_t kb, uint32_t ke, bool direct, size_t part) {
+    constexpr int HD          = 64;
+    constexpr int NS          = 2; /* MFMA k-steps of Q.K^T */
+    constexpr int NM          = 4; /* 16-dim tiles of O^T   */
+    constexpr bool PSPLIT     = NT == 1;
+    constexpr bool STREAM     = NT == 1; /* as load16's policy in run_segment */
+    const int lane = threadIdx.x & 63;
+    const int l16  = lane & 15;
+    const int g    = lane >> 4;
+    kb   = __builtin_amdgcn_readfirstlane(kb);
+    ke   = __builtin_amdgcn_readfirstlane(ke);
+    pos0 = __builtin_amdgcn_readfirstlane(pos0);
+    kvh  = __builtin_amdgcn_readfirstlane(kvh);
+    s    = __builtin_amdgcn_readfirstlane(s);
+    const uint32_t last = pos0 + P.n_rows - 1u;
+
+    gu16_ptr kc = (gu16_ptr)(P.k_seq ? P.k_seq[s] : P.k_base + (size_t)s * P.seq_stride);
+    gu16_ptr vc = (gu16_ptr)(P.v_seq ? P.v_seq[s] : P.v_base + (size_t)s * P.seq_stride);
+    const size_t row = (size_t)P.n_head_kv * HD;
+    kc += (size_t)kvh * HD;
+    vc += (size_t)kvh * HD;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+
+    /* lane l's 16 B of 1-KB piece e of a K or V sub-tile: row r = 8 e + l / 8,
+     * LDS chunk slot l % 8, holding the row's chunk (l % 8) ^ swizzle(r) */
+    uint32_t drow[4], dchunk[4], doff[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        drow[e]   = 8u * (uint32_t)e + ((uint32_t)lane >> 3);
+        dchunk[e] = ((uint32_t)lane & 7u) ^ (2u * ((drow[e] >> 2) & 3u));
+        doff[e]   = (uint32_t)((drow[e] * row + 8u * dchunk[e]) * sizeof(uint16_t));
+    }
+    const uint32_t nsub = (ke - kb + 31u) / 32u;
+    auto fetch = [&](uint32_t t) {
+        const uint32_t p0   = kb + 32u * t;
+        const uint32_t dst  = ring_lds + (t % (uint32_t)DMA_NBUF) * (uint32_t)DMA_TILE;
+        const uint32_t base = P.window ? (p0 % P.cap) : p0;
+        if (p0 + 32u <= ke && (!P.window || base + 32u <= P.cap)) {
+            gu8_ptr k0 = uniform_ptr((gu8_ptr)(kc + (size_t)base * row));
+            gu8_ptr v0 = uniform_ptr((gu8_ptr)(vc + (size_t)base * row));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dma16<STREAM>(doff[e], k0, dst + 1024u * (uint32_t)e);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dma16<STREAM>(doff[e], v0, dst + 4096u + 1024u * (uint32_t)e);
+            return;
+        }
+        /* a segment's last sub-tile, or one that wraps the ring: rows past
+         * ke read the last key's row (masked), slots wrap */
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t off = drow[e];
+            if (p0 + off >= ke) off = ke - 1u - p0;
+            uint32_t slot = base + off;
+            if (P.window) { while (slot >= P.cap) slot -= P.cap; }
+            const size_t eo = (size_t)slot * row + 8u * dchunk[e];
+            dma16<STREAM>((gu8_ptr)(kc + eo), dst + 1024u * (uint32_t)e);
+            dma16<STREAM>((gu8_ptr)(vc + eo), dst + 4096u + 1024u * (uint32_t)e);
+        }
+    };
+    /* the first sub-tiles are in flight while the query fragments are built
+     * (a previous segment of this wave has finished reading the ring) */
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (uint32_t t = 0; t < (uint32_t)DMA_AHEAD; ++t)
+        if (t < nsub) fetch(t);
+
+    /* ---- per-column row bounds and Q fragments (as run_segment) ------------- */
+    uint32_t col_lo[NT], col_hi[NT];
+    half8_t qh[NT][NS], ql[NT][NS];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t n = (uint32_t)(l16 + 16 * nt);
+        col_lo[nt] = 0xFFFFFFFFu;
+        col_hi[nt] = 0u;
+        float x[NS][8];
+        if (n < P.ncols) {
+            const uint32_t r = n / P.kv_mul;
+            const uint32_t h = kvh * P.kv_mul + (n - r * P.kv_mul);
+            col_lo[nt]       = lfm_plan_row(pos0 + r, P.window, P.cap).t_start;
+            col_hi[nt]       = pos0 + r;
+            const float *qp  = P.q + (((size_t)s * P.n_rows + r) * P.n_head_q + h) * HD + 8 * g;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) load8(qp + 32 * st, x[st]);
+        } else {
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[st][j] = 0.0f;
+        }
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float xs = x[st][j] * P.qscale;
+                asm volatile("" : "+v"(xs)); /* rounded once, as in run_segment */
+                const _Float16 hi = (_Float16)xs;
+                qh[nt][st][j]     = hi;
+                ql[nt][st][j]     = (_Float16)(xs - (float)hi);
+            }
+    }
+    const uint32_t free_lo = lfm_plan_row(last, P.window, P.cap).t_start;
+    const uint32_t free_hi = min(pos0, ke - 1u);
+
+    float4_t oacc[NM][NT];
+    float mrun[NT], lrun[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        mrun[nt] = kNegBig;
+        lrun[nt] = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
+    }
+    /* K fragment of key 16 kt + l16, dims 32 st + 8 g: chunk 4 st + g */
+    const uint32_t kswz  = (uint32_t)g ^ (2u * (((uint32_t)l16 >> 2) & 3u));
+    const uint32_t koff0 = (uint32_t)l16 * 128u + 16u * kswz;
+    const uint32_t koff1 = (uint32_t)l16 * 128u + 16u * (kswz ^ 4u);
+    const uint32_t vtr   = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)g +
+                         16u * (uint32_t)((l16 >> 1) & 1) + 8u * (uint32_t)(l16 & 1);
+
+    /* (Software pipelining this loop -- the score MFMAs of sub-tile t + 1
+     * issued before the softmax and P.V of t -- measured no faster on
+     * MI355X for the 8-row verify, 37.8-38.3 vs 37.6-37.9 us per step.) */
+    for (uint32_t t = 0; t < nsub; ++t) {
+        if (t + (uint32_t)DMA_AHEAD < nsub) {
+            /* the slot being refilled held sub-tile t - 1, whose LDS reads
+             * this wave has finished */
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            fetch(t + (uint32_t)DMA_AHEAD);
+        }
+        dma_wait(min(nsub - 1u - t, (uint32_t)DMA_AHEAD));
+        const uint32_t p0  = kb + 32u * t;
+        const uint8_t *kt0 = ring + (t % (uint32_t)DMA_NBUF) * (uint32_t)DMA_TILE;
+        const uint8_t *vt0 = kt0 + 4096;
+
+        /* S^T = K . Q^T (log2 units) */
+        float4_t sacc[2][NT];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const half8_t k0 = as_half8(*reinterpret_cast<const u32x4_t *>(kt0 + kt * 2048 + koff0));
+            const half8_t k1 = as_half8(*reinterpret_cast<const u32x4_t *>(kt0 + kt * 2048 + koff1));
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                float4_t acc = (float4_t)0.0f;
+                acc          = mfma(k0, qh[nt][0], acc);
+                acc          = mfma(k0, ql[nt][0], acc);
+                acc          = mfma(k1, qh[nt][1], acc);
+                acc          = mfma(k1, ql[nt][1], acc);
+                sacc[kt][nt] = acc;
+            }
+        }
+        if ((p0 < free_lo) || (p0 + 31u > free_hi)) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t key = p0 + (uint32_t)(16 * kt + 4 * g + i);
+                        const bool ok      = key < ke && key >= col_lo[nt] && key <= col_hi[nt];
+                        if (!ok) sacc[kt][nt][i] = -INFINITY;
+                    }
+        }
+        /* online softmax, lazy running max (as run_segment) */
+        half8_t ph[NT], pl[NT];
+        float alpha_nt[NT];
+        bool rose = false;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            float mx = fmaxf(fmaxf(fmaxf(sacc[0][nt][0], sacc[0][nt][1]), fmaxf(sacc[0][nt][2], sacc[0][nt][3])),
+                             fmaxf(fmaxf(sacc[1][nt][0], sacc[1][nt][1]), fmaxf(sacc[1][nt][2], sacc[1][nt][3])));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const bool raise  = mx > mrun[nt] + kLazyMax;
+            const float mnew  = raise ? mx : mrun[nt];
+            const float alpha = raise ? __builtin_amdgcn_exp2f(mrun[nt] - mnew) : 1.0f;
+            rose             |= raise;
+            alpha_nt[nt]      = alpha;
+            mrun[nt]          = mnew;
+            float psum        = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float pv     = __builtin_amdgcn_exp2f(sacc[kt][nt][i] - mnew);
+                    psum              += pv;
+                    const _Float16 hi  = (_Float16)pv;
+                    ph[nt][4 * kt + i] = hi;
+                    if constexpr (PSPLIT) pl[nt][4 * kt + i] = (_Float16)(pv - (float)hi);
+                }
+            lrun[nt] = lrun[nt] * alpha + psum;
+        }
+        if (__builtin_amdgcn_ballot_w64(rose) != 0ull) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] *= alpha_nt[nt];
+        }
+        /* O^T += V^T . P^T */
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) {
+            const uint32_t o  = vtr ^ (32u * (uint32_t)mt);
+            const half4v_t lo = lds_read_tr(vt0 + o);
+            const half4v_t hi = lds_read_tr(vt0 + 16u * 128u + o);
+            const half8_t av  = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                oacc[mt][nt] = mfma(av, ph[nt], oacc[mt][nt]);
+                if constexpr (PSPLIT) oacc[mt][nt] = mfma(av, pl[nt], oacc[mt][nt]);
+            }
+        }
+    }
+
+    /* ---- epilogue (as run_segment) ------------------------------------------ */
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        float lt = lrun[nt] + __shfl_xor(lrun[nt], 16);
+        lt += __shfl_xor(lt, 32);
+        const uint32_t n = (uint32_t)(l16 + 16 * nt);
+        if (n >= P.ncols) continue;
+        const uint32_t r = n / P.kv_mul;
+        const uint32_t h = kvh * P.kv_mul + (n - r * P.kv_mul);
+        if (direct) {
+            const size_t orow = ((size_t)s * P.n_rows + r) * P.n_head_q + h;
+            const float gv    = gate_value(P.gate, orow, P.gate_is_logit);
+            const float inv   = (lt > 0.0f) ? gv / lt : 0.0f;
+            float *op         = P.out + orow * HD;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt) {
+                const uint32_t d = (uint32_t)(16 * mt + 4 * g);
+                if (d < P.out_dims)
+                    *reinterpret_cast<float4 *>(op + d) = make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv,
+                                                                      oacc[mt][nt][2] * inv, oacc[mt][nt][3] * inv);
+            }
+        } else {
+            float *po = P.part_o + (part + n) * HD;
+#pragma unroll
+            for (int mt = 0; mt < NM; ++mt)
+                *reinterpret_cast<float4 *>(po + 16 * mt + 4 * g) =
+                    make_float4(oacc[mt][nt][0], oacc[mt][nt][1], oacc[mt][nt][2], oacc[mt][nt][3]);
+            if (g == 0) P.part_ml[part + n] = make_float2(mrun[nt], lt);
+        }
+    }
+}
+
 /* Dynamic LDS of the fused kernels: per wave, the staged new rows
  * ([n_rows][HD] K, then V, fp16). */
 extern __shared__ __attribute__((aligned(16))) uint16_t fresh_lds[];
@@ -1042,9 +1337,13 @@ __device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int l
     }
 }
 
-template <int HD, int NT, int W, bool FUSE>
+/* DMA: the waves run LDS-streamed segments (run_segment_dma; head_dim 64,
+ * no fused prologue), each with its DMA_NBUF-slot ring. */
+template <int HD, int NT, int W, bool FUSE, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
-    __shared__ __attribute__((aligned(16))) uint16_t vt_all[W][vt_halfs<HD>()];
+    static_assert(!DMA || (HD == 64 && !FUSE), "LDS-streamed segments: head_dim 64, no fused prologue");
+    constexpr size_t LDS_BYTES = DMA ? (size_t)W * DMA_NBUF * DMA_TILE : (size_t)W * vt_halfs<HD>() * 2u;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_area[LDS_BYTES];
     const lfm_bal_cfg &c = P.plan;
     const int lane       = threadIdx.x & 63;
     const uint32_t wave  = threadIdx.x >> 6;
@@ -1104,8 +1403,13 @@ __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
         if (kvh < P.n_head_kv) {
             uint32_t kb, ke;
             lfm_bal_seg_keys(&c, pos0, a, b, &kb, &ke);
-            run_segment<HD, NT, FUSE>(P, vt_all[wave], fresh_area<HD, FUSE>(P, wave), seq, pos0, kvh, kb, ke, direct,
-                                      ((size_t)slot * P.n_head_kv + kvh) * P.ncols);
+            const size_t part = ((size_t)slot * P.n_head_kv + kvh) * P.ncols;
+            if constexpr (DMA)
+                run_segment_dma<NT>(P, lds_area + (size_t)wave * DMA_NBUF * DMA_TILE, seq, pos0, kvh, kb, ke, direct,
+                                    part);
+            else
+                run_segment<HD, NT, FUSE>(P, reinterpret_cast<uint16_t *>(lds_area) + (size_t)wave * vt_halfs<HD>(),
+                                          fresh_area<HD, FUSE>(P, wave), seq, pos0, kvh, kb, ke, direct, part);
         }
     }
 }
@@ -1151,12 +1455,14 @@ __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
     float M = kNegBig, L = 0.0f;
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     if (live && g0 != g1) {
-        for (uint32_t g = g0 + q; g <= g1; g += 2u * SG) {
-            /* two slots' loads in flight before either is combined */
-            float2 ml[2];
-            float4 o[2];
+        /* up to MS slots' loads per lane in flight before any is combined:
+         * units of up to 16 workgroups (SG x MS) take one round trip */
+        constexpr uint32_t MS = 4;
+        for (uint32_t g = g0 + q; g <= g1; g += MS * SG) {
+            float2 ml[MS];
+            float4 o[MS];
 #pragma unroll
-            for (uint32_t j = 0; j < 2u; ++j) {
+            for (uint32_t j = 0; j < MS; ++j) {
                 ml[j] = make_float2(kNegBig, 0.0f);
                 o[j]  = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (g + j * SG <= g1) {
@@ -1167,7 +1473,7 @@ __global__ __launch_bounds__(256) void k_merge_bal(const SplitParams P) {
                 }
             }
 #pragma unroll
-            for (uint32_t j = 0; j < 2u; ++j) {
+            for (uint32_t j = 0; j < MS; ++j) {
                 if (!(ml[j].y > 0.0f)) continue;
                 const float Mn = fmaxf(M, ml[j].x);
                 const float a  = __builtin_amdgcn_exp2f(M - Mn);
@@ -1317,6 +1623,7 @@ int plan_code(const char *name) {
     if (!strcmp(name, "grid")) return 'g';
     if (!strcmp(name, "balanced")) return 'b';
     if (!strcmp(name, "wg")) return 'w';
+    if (!strcmp(name, "balanced-dma")) return 'd';
     return -1;
 }
 
@@ -1368,7 +1675,7 @@ bool lds_fits(uint32_t head_dim, bool fuse, uint32_t w, uint32_t n_rows) {
 /* Workgroups of k_splitkv_bal<HD, NT, W, FUSE> resident on the whole
  * device at once, with `dyn` bytes of dynamic LDS each (queried once per
  * device, instantiation and LDS size). */
-template <int HD, int NT, int W, bool FUSE>
+template <int HD, int NT, int W, bool FUSE, bool DMA>
 uint32_t resident_wgs(size_t dyn) {
     static std::atomic<uint64_t> cached[kMaxDevices]; /* (dyn + 1) << 32 | workgroups */
     int dev = 0;
@@ -1379,7 +1686,7 @@ uint32_t resident_wgs(size_t dyn) {
         if ((v & ~0xffffffffull) == tag) return (uint32_t)v;
     }
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE>, 64 * W,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_splitkv_bal<HD, NT, W, FUSE, DMA>, 64 * W,
                                                      dyn) != hipSuccess)
         return 256u;
     const uint32_t n = device_cus() * (uint32_t)(per_cu > 0 ? per_cu : 1);
@@ -1389,13 +1696,13 @@ uint32_t resident_wgs(size_t dyn) {
 
 /* Balanced plan: launch sized for the plan the device will pick, partial
  * slots and the tile prefix table in the workspace, then the merge. */
-template <int HD, int NT, int W, bool FUSE>
+template <int HD, int NT, int W, bool FUSE, bool DMA = false>
 int launch_bal(SplitParams p, uint32_t keys_hint, const Tuning &t, hipStream_t stream, const Scratch *sc) {
     const uint32_t cus = device_cus();
     lfm_bal_cfg &c     = p.plan;
     p.wpg              = W;
     c.n_groups         = (p.n_head_kv + W - 1u) / W;
-    c.n_res            = resident_wgs<HD, NT, W, FUSE>(fresh_bytes<HD, FUSE>(W, p.n_rows));
+    c.n_res            = resident_wgs<HD, NT, W, FUSE, DMA>(fresh_bytes<HD, FUSE>(W, p.n_rows));
     /* 8 waves per CU over a batch of equal sequences: one residency round of
      * 8-wave workgroups at head_dim 64.  Measured on MI355X against two
      * rounds (16 waves per CU), GB/s per step: B64 x 8192 6351-6473 ->
@@ -1403,6 +1710,9 @@ int launch_bal(SplitParams p, uint32_t keys_hint, const Tuning &t, hipStream_t s
      * 5276-5420, LFM3 B32 x 32768 d128 6317-6333 -> 6458-6489; 12 waves per
      * CU (a partial second round) was slower than either */
     c.target_waves = 8u * cus;
+    /* LDS-streamed waves: one round of the resident workgroups (the ring
+     * makes one per CU resident) */
+    if constexpr (DMA) c.target_waves = c.n_res * (uint32_t)W;
     /* each workgroup's partials cost about one 32-key tile per 32 query
      * columns: keep >= 12 tiles per workgroup per 32 columns (measured on
      * MI355X for 8 rows x 4 heads), and >= 2 tiles */
@@ -1443,7 +1753,7 @@ int launch_bal(SplitParams p, uint32_t keys_hint, const Tuning &t, hipStream_t s
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);
-    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W, FUSE>), dim3((uint32_t)n_launch), dim3(64 * W),
+    hipLaunchKernelGGL((k_splitkv_bal<HD, NT, W, FUSE, DMA>), dim3((uint32_t)n_launch), dim3(64 * W),
                        (fresh_bytes<HD, FUSE>(W, p.n_rows)), stream, p);
     hipError_t e = hipGetLastError();
     if (ev1) (void)hipEventRecord(ev1, stream);
@@ -1511,9 +1821,13 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, const
                  hipStream_t stream, const Scratch *sc) {
     /* a grid form with split keys writes partial slots: never launch one
      * without them */
-    if (pc.kind != 'b' && p.n_splits > 1u && (!p.part_o || !p.part_ml)) return LFM_ATTN_E_INVALID;
-    note_plan(pc.kind == 'w' ? "wg" : pc.kind == 'g' ? "grid" : "balanced");
+    if (pc.kind != 'b' && pc.kind != 'd' && p.n_splits > 1u && (!p.part_o || !p.part_ml)) return LFM_ATTN_E_INVALID;
+    note_plan(plan_name(pc.kind));
     if (pc.kind == 'w') return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
+    if (pc.kind == 'd') {
+        if constexpr (HD == 64 && NT <= 2 && !FUSE) return launch_bal<HD, NT, 4, FUSE, true>(p, keys_hint, t, stream, sc);
+        else return LFM_ATTN_E_INVALID; /* choose_plan never picks it here */
+    }
     const uint32_t w = pc.waves;
     if (pc.kind == 'b') {
         if (w == 8u) return launch_bal<HD, NT, 8, FUSE>(p, keys_hint, t, stream, sc);
@@ -1574,13 +1888,19 @@ int dispatch_nt(const SplitParams &p, const AttnBatch &b, uint32_t keys_hint, co
  *    at ctx 4096: 29.2 -> 22.0 us); larger grids unchanged.
  * The overrides force a plan ('g', 'b', 'w'), waves or a chunk; a waves or
  * chunk override keeps the grid off its in-workgroup form. */
+/* Batches the LDS-streamed balanced form runs: head_dim 64, at most two
+ * 16-column tiles, no fused prologue. */
+static bool dma_eligible(const AttnBatch &b, bool fuse) {
+    return b.head_dim == 64u && !fuse && tiles_of(64u, b.n_rows * (b.n_head_q / b.n_head_kv)) <= 2u;
+}
+
 PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on_device, bool fuse, uint32_t cus,
                        const Tuning &t) {
     PlanChoice pc{};
     const uint32_t ncols  = b.n_rows * (b.n_head_q / b.n_head_kv);
     bool grid             = !positions_on_device || b.n_seq == 1u || b.window != 0u;
     if (t.plan == 'g' || t.plan == 'w') grid = true;
-    if (t.plan == 'b') grid = false;
+    if (t.plan == 'b' || t.plan == 'd') grid = false;
     if (grid) {
         choose_split(b, keys_hint, t, &pc.n_splits, &pc.chunk);
         const uint32_t ww = wg_waves(b.head_dim, tiles_of(b.head_dim, ncols));
@@ -1601,7 +1921,21 @@ PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on
         while (w > 1u && (uint64_t)pc.n_splits * ((b.n_head_kv + w - 1u) / w) * b.n_seq < cus) w >>= 1;
     pc.kind  = grid ? 'g' : 'b';
     pc.waves = w;
+    /* the LDS-streamed form: forced, or by default for two 16-column tiles
+     * (speculative verify), where it measured faster on MI355X -- B16 x 8
+     * rows x 4104 keys 39.9-40.1 -> 37.6-37.9 us per step -- while one-tile
+     * batches run faster on the register form (B64 x 8192: 158.4-159.7 vs
+     * 162.4-163.6 us; ragged B64: 98.3-98.7 vs 102.1-102.7 us) */
+    const bool dma_default = t.plan == 0 && !t.waves && tiles_of(b.head_dim, ncols) == 2u;
+    if (!grid && (t.plan == 'd' || dma_default) && dma_eligible(b, fuse)) {
+        pc.kind  = 'd';
+        pc.waves = 4u;
+    }
     return pc;
+}
+
+const char *plan_name(char kind) {
+    return kind == 'w' ? "wg" : kind == 'g' ? "grid" : kind == 'd' ? "balanced-dma" : "balanced";
 }
 
 Tuning current_tuning() {
@@ -1672,7 +2006,7 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, c
     /* both grid forms keep per-split partials in the workspace (the
      * in-workgroup form merges them after a barrier); the balanced plan
      * sizes its own */
-    if (pc.kind != 'b' && p.n_splits > 1u) {
+    if (pc.kind != 'b' && pc.kind != 'd' && p.n_splits > 1u) {
         const size_t n_part = (size_t)b.n_seq * b.n_head_kv * p.n_splits * p.ncols;
         const size_t bytes  = n_part * b.head_dim * sizeof(float) + n_part * sizeof(float2) + 256;
         int st              = LFM_ATTN_OK;

@@ -62,13 +62,16 @@ int launch_splitkv(const AttnBatch &b, uint32_t keys_hint, hipStream_t stream, c
 bool splitkv_supports(const AttnBatch &b);
 
 /* Launch-plan overrides (tests, tuning): plan 0 automatic, 'g' grid, 'b'
- * balanced, 'w' in-workgroup merge; 0 = automatic for the counts. */
+ * balanced, 'd' balanced with LDS-streamed segments, 'w' in-workgroup
+ * merge; 0 = automatic for the counts. */
 struct Tuning {
     char plan;
     uint32_t waves, chunk, min_tiles;
     uint32_t prefill_chain; /* query tiles per sliding-window prefill workgroup */
 };
 int set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32_t min_tiles, uint32_t prefill_chain);
+/* "grid", "balanced", "balanced-dma" or "wg" for a PlanChoice kind */
+const char *plan_name(char kind);
 Tuning current_tuning();
 
 /* The split-KV launch a batch takes on a device of `cus` compute units

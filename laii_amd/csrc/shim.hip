@@ -159,10 +159,10 @@ int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, ui
     }
     const lfm::PlanChoice pc =
         lfm::choose_plan(b, keys_hint, positions_on_device != 0, fused != 0, n_cus, lfm::current_tuning());
-    *plan   = pc.kind == 'w' ? "wg" : pc.kind == 'g' ? "grid" : "balanced";
+    *plan   = lfm::plan_name(pc.kind);
     out3[0] = pc.waves;
-    out3[1] = pc.kind == 'b' ? 0u : pc.n_splits;
-    out3[2] = pc.kind == 'b' ? 0u : pc.chunk;
+    out3[1] = pc.kind == 'b' || pc.kind == 'd' ? 0u : pc.n_splits;
+    out3[2] = pc.kind == 'b' || pc.kind == 'd' ? 0u : pc.chunk;
     return LFM_ATTN_OK;
 }
 

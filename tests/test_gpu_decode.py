@@ -278,7 +278,7 @@ def test_balanced_plan_matches_grid_plan(gpu, orc, hd, nq, nkv, n_rows, n_seq):
 
 @pytest.mark.parametrize("hd,nq,nkv,n_rows,n_seq,max_ctx,win,cap,gate,default", [
     (64, 16, 8, 1, 1, 300, 0, 0, False, "wg"),       # config-1 heads, short context: the default small-batch form
-    (64, 32, 8, 8, 2, 400, 0, 0, False, "balanced"),  # verify rows (32 query columns; two sequences: balanced)
+    (64, 32, 8, 8, 2, 400, 0, 0, False, "balanced-dma"),  # verify rows (32 query columns; two sequences: balanced, LDS-streamed)
     (64, 32, 4, 8, 1, 1000, 0, 0, False, "wg"),      # 64 query columns (four-wave workgroups, 2 splits)
     (128, 16, 4, 1, 3, 500, 0, 0, False, "balanced"),  # LFM3 head_dim 128 (ragged: balanced by default)
     (128, 16, 4, 1, 1, 900, 200, 208, True, "wg"),   # SWA ring (window 200, 208 slots) + gate: 4 splits

@@ -83,6 +83,8 @@ def _batch(la, rng, n_seq, n_rows, nq, nkv, hd, ctx, win=0, cap=0, gate=False):
 @pytest.mark.parametrize("name,shape", [
     ("grid, one sequence", dict(n_seq=1, n_rows=1, nq=16, nkv=8, hd=64, ctx=[1023])),
     ("balanced, ragged", dict(n_seq=8, n_rows=1, nq=32, nkv=8, hd=64, ctx=[5, 700, 4096, 33, 1500, 2047, 1, 900])),
+    ("balanced LDS-streamed, verify rows", dict(n_seq=6, n_rows=8, nq=32, nkv=8, hd=64,
+                                                ctx=[4096, 17, 2500, 900, 4096, 64])),
     ("in-workgroup merge, ring + gate", dict(n_seq=4, n_rows=1, nq=16, nkv=4, hd=128, ctx=[1000] * 4,
                                              win=256, cap=264, gate=True)),
 ])

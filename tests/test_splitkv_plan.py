@@ -148,7 +148,9 @@ BASELINE_PLANS = [
     ("cfg2 fused step", dict(n_seq=64, n_rows=1, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=8192,
                              fused=True), ("balanced", 8)),
     ("cfg3 verify B16 x 8 rows", dict(n_seq=16, n_rows=8, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=4104),
-     ("balanced", 8)),
+     ("balanced-dma", 4)),
+    ("cfg3 fused verify step", dict(n_seq=16, n_rows=8, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=4104,
+                                    fused=True), ("balanced", 8)),
     ("cfg5 SWA ring", dict(n_seq=32, n_rows=1, n_head_q=16, n_head_kv=4, head_dim=128, window_len=256,
                            keys_hint=256), ("wg", 4)),
     ("cfg5 full B32 x 32768", dict(n_seq=32, n_rows=1, n_head_q=16, n_head_kv=4, head_dim=128, keys_hint=32768),
@@ -163,7 +165,7 @@ def test_plan_choice_baseline_shapes(name, kw, want):
     import laii_amd as la
     plan, waves, splits, chunk = la.plan_preview(**kw)
     assert (plan, waves) == want, (name, plan, waves)
-    if plan != "balanced":
+    if not plan.startswith("balanced"):
         keys = kw["keys_hint"]
         assert splits >= 1 and chunk % 32 == 0 and splits * chunk >= min(keys, kw.get("window_len") or keys)
 
@@ -184,6 +186,18 @@ def test_plan_overrides_and_lds_budget():
     with la.tuning(waves=2):
         assert la.plan_preview(**cfg2)[:2] == ("balanced", 2)
     assert la.plan_preview(**cfg2)[:2] == ("balanced", 8)
+    # the LDS-streamed form: head_dim 64, at most 32 query columns, no fused
+    # prologue; forced or (two 16-column tiles) by default
+    verify = dict(n_seq=16, n_rows=8, n_head_q=32, n_head_kv=8, head_dim=64, keys_hint=4104)
+    with la.tuning("balanced-dma"):
+        assert la.plan_preview(**cfg2)[:2] == ("balanced-dma", 4)
+        assert la.plan_preview(**dict(cfg2, fused=True))[:2] == ("balanced", 8)
+        assert la.plan_preview(**dict(cfg2, head_dim=128, n_head_q=16, n_head_kv=4))[0] == "balanced"
+        assert la.plan_preview(**dict(verify, n_rows=16))[0] == "balanced"  # 64 columns
+    with la.tuning("balanced"):
+        assert la.plan_preview(**verify)[:2] == ("balanced", 8)
+    with la.tuning(waves=8):
+        assert la.plan_preview(**verify)[:2] == ("balanced", 8)
     with pytest.raises(la.LfmAttnError):
         la.set_tuning("fastest")
     with pytest.raises(la.LfmAttnError):
