@@ -760,6 +760,8 @@ def main():
                     help="only the config-4 prefill workload (for kernel profiling)")
     ap.add_argument("--prefill128-only", action="store_true",
                     help="only the LFM3 head_dim-128 prefill workloads (for kernel profiling)")
+    ap.add_argument("--window", type=int, default=None,
+                    help="with --prefill128-only: only the row of this window (0 = the full layer)")
     ap.add_argument("--only", default=None,
                     help="only the named decode / verify / LFM3 workload of the secondary rows "
                          "(for kernel profiling), e.g. cfg3_verify_b16_rows8_ctx4096")
@@ -793,7 +795,8 @@ def main():
                           "unit": "us", "n_gpus": 1, "higher_is_better": False, "engine_step": es}), flush=True)
         return
     if args.prefill128_only:
-        rows = [run_prefill_lfm3(hip, la, rng, args.steps, args.warmup, w) for w in (0, 256)]
+        windows = (0, 256) if args.window is None else (args.window,)
+        rows = [run_prefill_lfm3(hip, la, rng, args.steps, args.warmup, w) for w in windows]
         print(json.dumps({"metric": "LFM3 prefill attn TFLOP/s, B4 x 4096, 16q/4kv d128", "value": rows[0]["TFLOPs"],
                           "unit": "TFLOP/s", "n_gpus": 1, "steps": prefill_counts(args.steps, args.warmup)[0],
                           "higher_is_better": True, "prefill_lfm3": rows}), flush=True)
