@@ -246,6 +246,34 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
                    8u * (l16 & 1);
     const half8_t ones8 = (half8_t)(_Float16)1.0f;
 
+    /* Q (fp32) and the output gates of a tile: all loads are issued before
+     * any is used (qp is a valid row for a padding column too; its values
+     * are zeroed after): with a use between them the compiler waited for
+     * each column tile's loads, one memory round trip per tile.  In a chain
+     * the next tile's loads are issued before the current tile's last P.V
+     * (its Q fragments and one score set are dead by then), so they land
+     * while that step and the epilogue run. */
+    float4 qraw[NT][NS][2];
+    float gnext[NT];
+    auto load_q = [&](uint32_t qt_) {
+        const uint32_t t0_ = qt_ * P.tq;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t c = (uint32_t)(wave * 32 + nt * 16 + l16);
+            const uint32_t j = c / P.tq, t = t0_ + c % P.tq;
+            const bool ok    = t < P.n_tok;
+            gnext[nt] = (P.gate && ok) ? P.gate[((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j] : 1.0f;
+            const float *qp =
+                P.q + (((size_t)s * P.n_tok + (ok ? t : 0u)) * P.n_head_q + kvh * P.kv_mul + j) * HD + 8 * g;
+#pragma unroll
+            for (int st = 0; st < NS; ++st) {
+                qraw[nt][st][0] = *reinterpret_cast<const float4 *>(qp + 32 * st);
+                qraw[nt][st][1] = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
+            }
+        }
+    };
+    load_q(qt_first);
+
     uint32_t j0 = 0; /* stream index of the current tile's first block */
     for (uint32_t qt = qt_first; qt < qt_end; ++qt) {
         const TileGeom tg = tile_geom(P, qt);
@@ -257,28 +285,15 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
         uint32_t col_pos[NT], col_lo[NT];
         bool col_ok[NT];
         half8_t qf[NT][NS];
-        /* all Q loads are issued before any is used (qp is a valid row for a
-         * padding column too; its values are zeroed after): with a use between
-         * them the compiler waited for each column tile's loads, one memory
-         * round trip per tile */
-        float4 qraw[NT][NS][2];
-        float graw[NT]; /* the output gates, loaded now: the epilogue does not wait for them */
+        float graw[NT]; /* the output gates (loaded with Q): the epilogue does not wait for them */
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const uint32_t c = (uint32_t)(wave * 32 + nt * 16 + l16);
-            const uint32_t j = c / P.tq, t = t0 + c % P.tq;
+            const uint32_t t = t0 + c % P.tq;
             col_ok[nt]  = t < P.n_tok;
-            graw[nt]    = (P.gate && col_ok[nt]) ? P.gate[((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j]
-                                                 : 1.0f;
+            graw[nt]    = gnext[nt];
             col_pos[nt] = P.pos_0 + t;
             col_lo[nt]  = (P.window && col_pos[nt] + 1u > P.window) ? col_pos[nt] + 1u - P.window : 0u;
-            const float *qp =
-                P.q + (((size_t)s * P.n_tok + (col_ok[nt] ? t : 0u)) * P.n_head_q + kvh * P.kv_mul + j) * HD + 8 * g;
-#pragma unroll
-            for (int st = 0; st < NS; ++st) {
-                qraw[nt][st][0] = *reinterpret_cast<const float4 *>(qp + 32 * st);
-                qraw[nt][st][1] = *reinterpret_cast<const float4 *>(qp + 32 * st + 4);
-            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -465,8 +480,21 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
         run_steps(std::true_type{}, u0 > 0u ? u0 - 1u : 0u);
         run_steps(std::false_type{}, u1 > 0u ? u1 - 1u : 0u);
         run_steps(std::true_type{}, b_hi - 1u);
+        /* the next tile's Q loads before the last P.V; on the chain's last
+         * tile the Q registers are cleared instead, so that no path carries
+         * the loaded values through a whole tile (a conditional load alone
+         * kept them live, and the kernel spilled) */
+        if (qt + 1u < qt_end) {
+            load_q(qt + 1u);
+        } else {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                gnext[nt] = 0.0f;
+#pragma unroll
+                for (int st = 0; st < NS; ++st) qraw[nt][st][0] = qraw[nt][st][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
         accumulate(b, scur);
-
         /* ---- epilogue: O * gate / l ------------------------------------------ */
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
@@ -488,6 +516,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
                     make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv, oacc[mt][nt][2] * inv,
                                 oacc[mt][nt][3] * inv);
         }
+        if (qt + 1u >= qt_end) break;
         j0 += b_hi - b_lo;
     }
 }
@@ -496,11 +525,13 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
 
 /* Query tiles per workgroup: one unless set by lfm_attn_set_tuning.  On
  * MI355X the sliding-window workload (B 4 x 4096, 16q/4kv, window 256) took
- * 81.9 us with one tile per workgroup, 84.5 us with chains of 2 and 89.6 us
- * with chains of 4: chaining removes the workgroup launches and ring fills
- * but not the exposed latency of each tile's fp32 Q loads, and it lowers
- * the number of workgroups that hide it for one another.  Full layers
- * (window 0 or above 32 tiles) always take one tile per workgroup. */
+ * 82.2 us with one tile per workgroup, 87.0 us with chains of 2, 89.1 us
+ * with chains of 4 and 102 us with chains of 8, with the next tile's Q in
+ * flight during each tile's last step (before that prefetch: 84.5 and
+ * 89.6 us for 2 and 4): the single-tile workgroups already hide each
+ * other's set-up, and a static chain per workgroup loses the dynamic
+ * balance of 2048 short workgroups over the CUs.  Full layers (window 0 or
+ * above 32 tiles) always take one tile per workgroup. */
 static uint32_t prefill_chain(uint32_t window, uint32_t tq, uint32_t n_qtiles) {
     if (!window || window > 32u * tq) return 1u;
     const uint32_t forced = current_tuning().prefill_chain; /* tests, tuning */
