@@ -557,26 +557,34 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
 
     /* One 32-key sub-tile: V to LDS, S^T, online softmax, O^T update.
      * V of a sub-tile goes to the wave's LDS area row-major, each 64-dim half
-     * of a row as 128 B with its 16-B chunks XOR-swizzled by
-     * 2 * ((row >> 2) & 3); the P.V operand V^T then comes from transposing
-     * reads (ds_read_b64_tr_b16), conflict-free, with no VALU transpose.
+     * of a row as 128 B with its 16-B chunks XOR-swizzled by row & 7; the
+     * P.V operand V^T then comes from transposing reads (ds_read_b64_tr_b16),
+     * bank-conflict free, with no VALU transpose.
      * Lane (l16, g) reads row 4g + l16/4 of a 16-key half at dims
      * 16 mt + 4 (l16 % 4), in the key order of P's accumulator layout. */
     uint8_t *vrow = reinterpret_cast<uint8_t *>(vt);
-    /* this lane stores rows 4q..4q+3 (q = lane / CH, plus QPP per pass) of
-     * 16-byte chunk c; the four rows share one swizzle, 128 B apart */
+    /* this lane stores rows 4q + i, i < 4 (q = lane / CH, plus QPP per pass)
+     * of 16-byte chunk c: row 4q + i holds it at slot c ^ ((4q + i) & 7) =
+     * (c ^ 4 (q & 1)) ^ i, 128 B apart */
     const uint32_t vsq = (uint32_t)(lane / CH), vsc = (uint32_t)(lane % CH);
-    const uint32_t vst = (vsc >> 3) * 4096u + vsq * 512u + 16u * ((vsc & 7u) ^ (2u * (vsq & 3u)));
-    /* QPP is a multiple of 4, so later passes keep the swizzle */
+    const uint32_t vst = (vsc >> 3) * 4096u + vsq * 512u;
+    const uint32_t vsw = (vsc & 7u) ^ (4u * (vsq & 1u));
+    auto vst_off = [&](int j) {
+        const uint32_t i = (uint32_t)(j & 3);
+        return vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u + i * 128u + 16u * (vsw ^ i);
+    };
+    /* QPP is a multiple of 4 (rows 16 or 32 apart), so later passes keep the swizzle */
     static_assert(QPP % 4 == 0, "V store swizzle assumes whole 4-quad groups per pass");
-    /* the transposing read of dims 16 mt..16 mt + 15: chunk pair mt ^ g */
-    const uint32_t vtr = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)g + 16u * (uint32_t)((l16 >> 1) & 1) +
-                         8u * (uint32_t)(l16 & 1);
+    /* the transposing read of dims 16 mt'..16 mt' + 15 (mt' = mt % 4) of row
+     * vr: chunk 2 mt' + ((l16 >> 1) & 1) at slot (2 mt' + b) ^ (vr & 7) = 2 mt'
+     * ^ (b ^ (vr & 7)), so the read address is vtr ^ (32 mt') */
+    const uint32_t vr  = (uint32_t)(4 * g + (l16 >> 2));
+    const uint32_t vtr = vr * 128u + 16u * ((uint32_t)((l16 >> 1) & 1) ^ (vr & 7u)) + 8u * (uint32_t)(l16 & 1);
     auto process = [&](uint32_t p0, const u32x4_t (&kcur)[2][NS], const u32x4_t (&vcur)[NVL]) {
         wave_lds_sync(); /* previous sub-tile's transposing V reads are done */
 #pragma unroll
         for (int j = 0; j < NVL; ++j)
-            *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u + (uint32_t)(j & 3) * 128u) =
+            *reinterpret_cast<u32x4_t *>(vrow + vst_off(j)) =
                 vcur[j];
 
         /* S^T = K . Q^T (log2 units) */
@@ -678,7 +686,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
         wave_lds_sync(); /* previous sub-tile's transposing V reads are done */
 #pragma unroll
         for (int j = 0; j < NVL; ++j)
-            *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u + (uint32_t)(j & 3) * 128u) =
+            *reinterpret_cast<u32x4_t *>(vrow + vst_off(j)) =
                 va[j];
         float4_t sacc[2][2]; /* [sub-tile][16-key half] */
 #pragma unroll
@@ -745,8 +753,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
                 wave_lds_sync(); /* the first sub-tile's transposing reads are done */
 #pragma unroll
                 for (int j = 0; j < NVL; ++j)
-                    *reinterpret_cast<u32x4_t *>(vrow + vst + (uint32_t)(j >> 2) * (uint32_t)QPP * 512u +
-                                                 (uint32_t)(j & 3) * 128u) = vb[j];
+                    *reinterpret_cast<u32x4_t *>(vrow + vst_off(j)) = vb[j];
             }
             wave_lds_sync(); /* V of this sub-tile is in LDS */
 #pragma unroll
@@ -853,8 +860,8 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
  * three sub-tiles ahead of the one being consumed, and the wave reads K
  * fragments (ds_read_b128) and the transposed V operand (ds_read_b64_tr_b16)
  * from there.  Each sub-tile is [32 keys][128 B] of K then of V, the 16-B
- * chunks of row r XOR-swizzled by 2 * ((r >> 2) & 3) (the layout run_segment
- * stores V in).  The loads are inline assembly, invisible to the compiler's
+ * chunks of row r XOR-swizzled by r & 7 (the layout run_segment stores V
+ * in).  The loads are inline assembly, invisible to the compiler's
  * wait counting, so the waits are explicit: every vector memory operation in
  * the key loop is one of these (8 per sub-tile), and before sub-tile t is
  * read the wave waits until only the sub-tiles issued after it (at most 3 x
@@ -923,7 +930,7 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         drow[e]   = 8u * (uint32_t)e + ((uint32_t)lane >> 3);
-        dchunk[e] = ((uint32_t)lane & 7u) ^ (2u * ((drow[e] >> 2) & 3u));
+        dchunk[e] = ((uint32_t)lane & 7u) ^ (drow[e] & 7u);
         doff[e]   = (uint32_t)((drow[e] * row + 8u * dchunk[e]) * sizeof(uint16_t));
     }
     const uint32_t nsub = (ke - kb + 31u) / 32u;
@@ -1007,11 +1014,11 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
         for (int mt = 0; mt < NM; ++mt) oacc[mt][nt] = (float4_t)0.0f;
     }
     /* K fragment of key 16 kt + l16, dims 32 st + 8 g: chunk 4 st + g */
-    const uint32_t kswz  = (uint32_t)g ^ (2u * (((uint32_t)l16 >> 2) & 3u));
+    const uint32_t kswz  = (uint32_t)g ^ ((uint32_t)l16 & 7u);
     const uint32_t koff0 = (uint32_t)l16 * 128u + 16u * kswz;
     const uint32_t koff1 = (uint32_t)l16 * 128u + 16u * (kswz ^ 4u);
-    const uint32_t vtr   = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)g +
-                         16u * (uint32_t)((l16 >> 1) & 1) + 8u * (uint32_t)(l16 & 1);
+    const uint32_t vr    = (uint32_t)(4 * g + (l16 >> 2));
+    const uint32_t vtr   = vr * 128u + 16u * ((uint32_t)((l16 >> 1) & 1) ^ (vr & 7u)) + 8u * (uint32_t)(l16 & 1);
 
     /* (Software pipelining this loop -- the score MFMAs of sub-tile t + 1
      * issued before the softmax and P.V of t -- measured no faster on

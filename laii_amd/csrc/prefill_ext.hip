@@ -19,7 +19,7 @@
  *
  * Each 32-key block of K (and of V) is kept in LDS as two 64-dim halves of
  * [32 keys][128 B], with the 16-B chunks of row r XOR-swizzled by
- * 2 * ((r >> 2) & 3): the layout of the head_dim-64 prefill kernel
+ * r & 7: the layout of the head_dim-64 prefill kernel
  * (prefill_fa.hip), whose K fragment reads (ds_read_b128) and transposing V
  * reads (ds_read_b64_tr_b16) it serves without bank conflicts.  Blocks move
  * from global memory straight into a ring of 4 LDS blocks
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
         const uint32_t u = 1024u * (uint32_t)(wave + 4 * e) + 16u * (uint32_t)lane;
         const uint32_t r = (u % HALFB) / 128u, j = (u % 128u) / 16u;
         st_row[e] = r;
-        st_col[e] = 8u * (8u * (u / HALFB) + (j ^ (2u * ((r >> 2) & 3u)))); /* halfs within the head's row */
+        st_col[e] = 8u * (8u * (u / HALFB) + (j ^ (r & 7u))); /* halfs within the head's row */
     }
     const uint32_t wv       = __builtin_amdgcn_readfirstlane((uint32_t)wave);
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring; /* LDS address of the ring */
@@ -236,14 +236,14 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
     /* fragment offsets within a 64-dim half (bytes).  K: row 16*mt + l16,
      * chunk 4*(st % 2) + g.  V (transposing read): lane l16 of group g
      * addresses row 4g + l16/4 of a 16-key half, dims 16*mt + 4*(l16 % 4) */
-    const uint32_t kswz  = (uint32_t)(g ^ (2 * ((l16 >> 2) & 3)));
+    const uint32_t kswz  = (uint32_t)(g ^ (l16 & 7));
     const uint32_t koff0 = (uint32_t)l16 * 128u + 16u * kswz;
     const uint32_t koff1 = (uint32_t)l16 * 128u + 16u * (kswz ^ 4u);
+    const uint32_t vr    = (uint32_t)(4 * g + (l16 >> 2)); /* V row read (its + 16 twin has the same swizzle) */
     uint32_t voff[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
-        voff[mt] = (uint32_t)(4 * g + (l16 >> 2)) * 128u + 32u * (uint32_t)(mt ^ g) + 16u * ((l16 >> 1) & 1) +
-                   8u * (l16 & 1);
+        voff[mt] = vr * 128u + 16u * ((2u * (uint32_t)mt + (uint32_t)((l16 >> 1) & 1)) ^ (vr & 7u)) + 8u * (l16 & 1);
     const half8_t ones8 = (half8_t)(_Float16)1.0f;
 
     /* Q (fp32) and the output gates of a tile: all loads are issued before

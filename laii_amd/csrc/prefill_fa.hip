@@ -15,9 +15,11 @@
  * memory straight into a ring of 4 LDS blocks (global_load_lds_dwordx4, no
  * registers): block b + 2 is in flight while block b is computed and block
  * b - 1 is still read by the P.V product that trails the scores by a step.
- * The 16-B chunks of row r are XOR-swizzled by 2*((r >> 2) & 3), which makes
- * both the K fragment reads (ds_read_b128) and the transposing V reads
- * (ds_read_b64_tr_b16) bank-conflict free.
+ * The 16-B chunks of row r are XOR-swizzled by r & 7, which makes both the
+ * K fragment reads (ds_read_b128) and the transposing V reads
+ * (ds_read_b64_tr_b16) bank-conflict free on gfx950's LDS (measured with
+ * SQ_LDS_BANK_CONFLICT: zero; the earlier swizzle 2*((r >> 2) & 3), laid
+ * out for half as many banks, spent half of the LDS cycles in conflicts).
  *
  * Compute runs in 32-key steps.  Step k computes S^T(k+1) into a second
  * register set, turns the scores S^T(k) into P and runs PV(k): the MFMAs of
@@ -153,7 +155,7 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     for (int e = 0; e < 2; ++e) {
         const uint32_t p = (uint32_t)tid + 256u * e, r = p >> 3;
         st_row[e] = r;
-        st_col[e] = 8u * ((p & 7u) ^ (2u * ((r >> 2) & 3u)));         /* halfs */
+        st_col[e] = 8u * ((p & 7u) ^ (r & 7u));                        /* halfs */
         st_off[e] = (r * (uint32_t)row + st_col[e]) * sizeof(uint16_t); /* bytes */
     }
     const uint32_t wv       = __builtin_amdgcn_readfirstlane((uint32_t)wave);
@@ -233,14 +235,15 @@ __global__ __launch_bounds__(256, 2) void k_prefill(const PrefillParams P) {
     /* fragment offsets in a block (bytes).  K: row 16*mt + l16, chunk 4*st + g.
      * V (transposing read): lane l16 of group g addresses row 4g + l16/4 of
      * a 16-key half, dims 16*mt + 4*(l16 % 4) */
-    const uint32_t kswz  = (uint32_t)(g ^ (2 * ((l16 >> 2) & 3)));
+    const uint32_t kswz  = (uint32_t)(g ^ (l16 & 7));
     const uint32_t koff0 = (uint32_t)l16 * ROWB + 16u * kswz;
     const uint32_t koff1 = (uint32_t)l16 * ROWB + 16u * (kswz ^ 4u);
+    const uint32_t vr    = (uint32_t)(4 * g + (l16 >> 2)); /* V row read (its + 16 twin has the same swizzle) */
     uint32_t voff[NM];
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt)
-        voff[mt] = BLKB + (uint32_t)(4 * g + (l16 >> 2)) * ROWB + 32u * (uint32_t)(mt ^ g) +
-                   16u * ((l16 >> 1) & 1) + 8u * (l16 & 1);
+        voff[mt] = BLKB + vr * ROWB + 16u * ((2u * (uint32_t)mt + (uint32_t)((l16 >> 1) & 1)) ^ (vr & 7u)) +
+                   8u * (l16 & 1);
 
     float4_t oacc[NM][NT];
     float4_t negm[NT]; /* -m splat: initial value of the score accumulator */
