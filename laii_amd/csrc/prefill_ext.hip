@@ -496,27 +496,68 @@ __global__ __launch_bounds__(256, HD == 64 ? 3 : 2) void k_prefill_ext(const Pre
         }
         accumulate(b, scur);
         /* ---- epilogue: O * gate / l ------------------------------------------ */
+        float inv[NT];
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const float lt = lacc[nt][0];
-            if (!col_ok[nt]) continue;
-            const uint32_t c    = (uint32_t)(wave * 32 + nt * 16 + l16);
-            const uint32_t j    = c / P.tq, t = t0 + c % P.tq;
-            const size_t orow   = ((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j;
-            float gv            = 1.0f;
+            float gv       = 1.0f;
             if (P.gate) {
                 const float gl = graw[nt];
                 gv             = P.gate_is_logit ? 1.0f / (1.0f + expf(-gl)) : gl;
             }
-            const float inv = lt > 0.0f ? gv / lt : 0.0f;
-            float *op       = P.out + orow * HD;
+            inv[nt] = lt > 0.0f ? gv / lt : 0.0f;
+        }
+        if (HD == 128 && qt + 1u >= qt_end) {
+            /* (head_dim 128: the head_dim-64 instance, at three waves per SIMD,
+             * has no registers to spare for it.)
+             * The workgroup's last tile: the ring is free once every wave's
+             * last P.V has read it (no fetch is outstanding), so each wave
+             * stages its 32 output rows there row-major and stores whole
+             * rows: one store instruction covers 64 / CHK rows of HD fp32,
+             * where the fragment layout covers 16 rows x 64 B per
+             * instruction (half of each 128-B line).  Row r's 16-B chunk q
+             * sits at slot q ^ (r & 15): conflict-free for both the fragment
+             * writes and the row reads. */
+            constexpr int CHK = HD / 4; /* 16-B chunks per output row */
+            __syncthreads();
+            uint8_t *ob = ring + (size_t)wave * 32u * (uint32_t)(HD * 4);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const uint32_t r = (uint32_t)(nt * 16 + l16);
+#pragma unroll
+                for (int mt = 0; mt < NM; ++mt) {
+                    const uint32_t q = (uint32_t)(4 * mt + g);
+                    *reinterpret_cast<float4_t *>(ob + r * (uint32_t)(HD * 4) + 16u * (q ^ (r & 15u))) =
+                        oacc[mt][nt] * inv[nt];
+                }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); /* this wave's rows are in LDS */
+            constexpr int RPI = 64 / CHK;                       /* rows per store instruction */
+            const uint32_t lg = (uint32_t)__builtin_ctz(P.tq); /* tq = 128 / kv_mul: a power of two */
+#pragma unroll 2
+            for (int k = 0; k < 32 / RPI; ++k) {
+                const uint32_t r = (uint32_t)(k * RPI + lane / CHK), q = (uint32_t)(lane % CHK);
+                const uint32_t c = (uint32_t)(wave * 32) + r;
+                const uint32_t j = c >> lg, t = t0 + (c & (P.tq - 1u));
+                const float4_t v = *reinterpret_cast<const float4_t *>(ob + r * (uint32_t)(HD * 4) + 16u * (q ^ (r & 15u)));
+                if (t < P.n_tok)
+                    *reinterpret_cast<float4_t *>(P.out + (((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j) * HD +
+                                                  4u * q) = v;
+            }
+            break;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            if (!col_ok[nt]) continue;
+            const uint32_t c  = (uint32_t)(wave * 32 + nt * 16 + l16);
+            const uint32_t j  = c / P.tq, t = t0 + c % P.tq;
+            float *op = P.out + (((size_t)s * P.n_tok + t) * P.n_head_q + kvh * P.kv_mul + j) * HD;
 #pragma unroll
             for (int mt = 0; mt < NM; ++mt)
                 *reinterpret_cast<float4 *>(op + 16 * mt + 4 * g) =
-                    make_float4(oacc[mt][nt][0] * inv, oacc[mt][nt][1] * inv, oacc[mt][nt][2] * inv,
-                                oacc[mt][nt][3] * inv);
+                    make_float4(oacc[mt][nt][0] * inv[nt], oacc[mt][nt][1] * inv[nt], oacc[mt][nt][2] * inv[nt],
+                                oacc[mt][nt][3] * inv[nt]);
         }
-        if (qt + 1u >= qt_end) break;
         j0 += b_hi - b_lo;
     }
 }
