@@ -54,15 +54,18 @@ const char *lfm_attn_last_error(void);
 /* Diagnostic, no reference counterpart: the form of this thread's last
  * decode / step attention launch -- "wg" (one workgroup per sequence and KV
  * head, in-workgroup merge), "grid" (fixed key chunks + merge kernel),
- * "balanced" (tile shares + merge kernel) or "generic" ("" before any). */
+ * "balanced" (tile shares + merge kernel), "balanced-dma" (the same with
+ * LDS-streamed segments) or "generic" ("" before any). */
 const char *lfm_attn_last_plan(void);
 const char *lfm_attn_version(void);
 
 /* Tuning and tests, no reference counterpart: overrides of the launch
  * plans, process-wide.  Split-KV attention: plan NULL, "" or "auto" lets the
- * library choose; "grid", "balanced" or "wg" forces that form; waves (1, 2,
- * 4, 8), chunk (keys per workgroup) and min_tiles (32-key tiles per balanced
- * workgroup) force those counts.  prefill_chain: consecutive query tiles
+ * library choose; "grid", "balanced", "balanced-dma" (the balanced plan with
+ * K and V streamed into per-wave LDS rings; head_dim 64, up to 32 query
+ * columns, no fused prologue, else "balanced") or "wg" forces that form;
+ * waves (1, 2, 4, 8), chunk (keys per workgroup) and min_tiles (32-key tiles
+ * per balanced workgroup) force those counts.  prefill_chain: consecutive query tiles
  * per workgroup of a sliding-window lfm_hip_lfm3_prefill_f16.  0 =
  * automatic for every count.  The environment variables LFM_ATTN_PLAN,
  * LFM_ATTN_WAVES, LFM_ATTN_CHUNK, LFM_ATTN_MINTILES and
@@ -77,7 +80,8 @@ int lfm_attn_set_tuning(const char *plan, uint32_t waves, uint32_t chunk, uint32
  * shape, sliding window, keys_hint as lfm_hip_gqa_f16_varlen; positions on
  * the device or one host position; fused = the step entry's prologue) on a
  * device of n_cus compute units under the current overrides: *plan = "wg",
- * "grid", "balanced" or "generic" (no split-KV kernel for the shape);
+ * "grid", "balanced", "balanced-dma" or "generic" (no split-KV kernel for
+ * the shape);
  * out3 = {waves per workgroup, grid key splits, grid chunk} (0 where the
  * plan has none). */
 int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim,
