@@ -850,7 +850,7 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
     }
 }
 
-/* ---- LDS-streamed segments (head_dim 64, no fused prologue) -----------------
+/* ---- LDS-streamed segments (no fused prologue) ------------------------------
  * run_segment keeps one 32-key sub-tile in flight per wave, in registers, so
  * a wave's throughput is one sub-tile per memory round trip; with two 16-
  * column tiles (speculative verify) its registers leave no room for a
@@ -859,19 +859,23 @@ __device__ __forceinline__ void run_segment(const SplitParams &P, uint16_t *vt, 
  * (global_load_lds_dwordx4: no registers held while a load is in flight),
  * three sub-tiles ahead of the one being consumed, and the wave reads K
  * fragments (ds_read_b128) and the transposed V operand (ds_read_b64_tr_b16)
- * from there.  Each sub-tile is [32 keys][128 B] of K then of V, the 16-B
- * chunks of row r XOR-swizzled by r & 7 (the layout run_segment stores V
- * in).  The loads are inline assembly, invisible to the compiler's
- * wait counting, so the waits are explicit: every vector memory operation in
- * the key loop is one of these (8 per sub-tile), and before sub-tile t is
- * read the wave waits until only the sub-tiles issued after it (at most 3 x
- * 8) remain outstanding.  Waves never read each other's areas, so no
- * workgroup barrier runs. */
-constexpr int DMA_NBUF    = 4;                 /* ring slots per wave           */
-constexpr int DMA_TILE    = 2 * 32 * 64 * 2;   /* bytes per slot: K, then V     */
-constexpr int DMA_AHEAD   = 3;                 /* sub-tiles in flight ahead      */
-constexpr int DMA_PER_SUB = 8;                 /* 1-KB loads per sub-tile        */
+ * from there.  Each sub-tile is K then V, each HD / 64 halves of [32
+ * keys][128 B], the 16-B chunks of row r XOR-swizzled by r & 7 (the layout
+ * run_segment stores V in).  The loads are inline assembly, invisible to the
+ * compiler's wait counting, so the waits are explicit: every vector memory
+ * operation in the key loop is one of these (dma_per_sub per sub-tile), and
+ * before sub-tile t is read the wave waits until only the sub-tiles issued
+ * after it (at most 3) remain outstanding.  Waves never read each other's
+ * areas, so no workgroup barrier runs.  The default for two 16-column tiles
+ * at head_dim 64 (verify rows); the one-tile forms measured slower than
+ * run_segment (head_dim 64 B64 x 8192: 162.4-163.6 vs 158.4-159.7 us per
+ * step; head_dim 128 B32 x 32768: 336.3-339.2 vs 333.0-333.2 us). */
+constexpr int DMA_NBUF  = 4; /* ring slots per wave      */
+constexpr int DMA_AHEAD = 3; /* sub-tiles in flight ahead */
 static_assert(DMA_AHEAD < DMA_NBUF, "the slot being fetched must not be the one being read");
+/* bytes per slot (K, then V: 32 keys x HD halfs each) and 1-KB loads per sub-tile */
+template <int HD> constexpr int dma_tile() { return 2 * 32 * HD * 2; }
+template <int HD> constexpr int dma_per_sub() { return 8 * (HD / 64); }
 
 /* 16 B per lane into LDS: lane l writes [lds + 16 l, lds + 16 l + 16) (lds in
  * M0), from a wave-uniform base plus a 32-bit per-lane byte offset, or from
@@ -890,21 +894,31 @@ __device__ __forceinline__ void dma16(gu8_ptr addr, uint32_t lds) {
 }
 
 /* Wait until at most `younger` sub-tiles' loads (wave-uniform, <= 3) are
- * outstanding. */
+ * outstanding: dma_per_sub<HD>() loads each. */
+template <int HD>
 __device__ __forceinline__ void dma_wait(uint32_t younger) {
-    static_assert(DMA_AHEAD == 3 && DMA_PER_SUB == 8, "wait counts below");
-    if (younger >= 3u) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
-    else if (younger == 2u) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (younger == 1u) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    static_assert(DMA_AHEAD == 3, "wait counts below");
+    if constexpr (HD == 64) {
+        if (younger >= 3u) asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+        else if (younger == 2u) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else if (younger == 1u) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        static_assert(HD == 128, "head_dim 64 or 128");
+        if (younger >= 3u) asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+        else if (younger == 2u) asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
+        else if (younger == 1u) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
 }
 
-template <int NT>
+template <int HD, int NT>
 __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *ring, uint32_t s, uint32_t pos0,
                                                 uint32_t kvh, uint32_t kb, uint32_t ke, bool direct, size_t part) {
-    constexpr int HD          = 64;
-    constexpr int NS          = 2; /* MFMA k-steps of Q.K^T */
-    constexpr int NM          = 4; /* 16-dim tiles of O^T   */
+    constexpr int NH          = HD / 64; /* 64-dim halves of a row: 4-KB K and V parts each */
+    constexpr int NS          = HD / 32; /* MFMA k-steps of Q.K^T */
+    constexpr int NM          = HD / 16; /* 16-dim tiles of O^T   */
+    constexpr uint32_t TILE   = (uint32_t)dma_tile<HD>();
     constexpr bool PSPLIT     = NT == 1;
     constexpr bool STREAM     = NT == 1; /* as load16's policy in run_segment */
     const int lane = threadIdx.x & 63;
@@ -924,8 +938,9 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
     vc += (size_t)kvh * HD;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
 
-    /* lane l's 16 B of 1-KB piece e of a K or V sub-tile: row r = 8 e + l / 8,
-     * LDS chunk slot l % 8, holding the row's chunk (l % 8) ^ swizzle(r) */
+    /* lane l's 16 B of 1-KB piece e of 64-dim half h of a K or V sub-tile:
+     * row r = 8 e + l / 8, LDS chunk slot l % 8 of the half, holding the row's
+     * chunk 8 h + ((l % 8) ^ swizzle(r)) */
     uint32_t drow[4], dchunk[4], doff[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -936,15 +951,22 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
     const uint32_t nsub = (ke - kb + 31u) / 32u;
     auto fetch = [&](uint32_t t) {
         const uint32_t p0   = kb + 32u * t;
-        const uint32_t dst  = ring_lds + (t % (uint32_t)DMA_NBUF) * (uint32_t)DMA_TILE;
+        const uint32_t dst  = ring_lds + (t % (uint32_t)DMA_NBUF) * TILE;
         const uint32_t base = P.window ? (p0 % P.cap) : p0;
         if (p0 + 32u <= ke && (!P.window || base + 32u <= P.cap)) {
             gu8_ptr k0 = uniform_ptr((gu8_ptr)(kc + (size_t)base * row));
             gu8_ptr v0 = uniform_ptr((gu8_ptr)(vc + (size_t)base * row));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dma16<STREAM>(doff[e], k0, dst + 1024u * (uint32_t)e);
+            for (int h = 0; h < NH; ++h)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dma16<STREAM>(doff[e], v0, dst + 4096u + 1024u * (uint32_t)e);
+                for (int e = 0; e < 4; ++e)
+                    dma16<STREAM>(doff[e] + 128u * (uint32_t)h, k0, dst + 4096u * (uint32_t)h + 1024u * (uint32_t)e);
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    dma16<STREAM>(doff[e] + 128u * (uint32_t)h, v0,
+                                  dst + 4096u * (uint32_t)(NH + h) + 1024u * (uint32_t)e);
             return;
         }
         /* a segment's last sub-tile, or one that wraps the ring: rows past
@@ -955,9 +977,12 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
             if (p0 + off >= ke) off = ke - 1u - p0;
             uint32_t slot = base + off;
             if (P.window) { while (slot >= P.cap) slot -= P.cap; }
-            const size_t eo = (size_t)slot * row + 8u * dchunk[e];
-            dma16<STREAM>((gu8_ptr)(kc + eo), dst + 1024u * (uint32_t)e);
-            dma16<STREAM>((gu8_ptr)(vc + eo), dst + 4096u + 1024u * (uint32_t)e);
+#pragma unroll
+            for (int h = 0; h < NH; ++h) {
+                const size_t eo = (size_t)slot * row + 64u * (uint32_t)h + 8u * dchunk[e];
+                dma16<STREAM>((gu8_ptr)(kc + eo), dst + 4096u * (uint32_t)h + 1024u * (uint32_t)e);
+                dma16<STREAM>((gu8_ptr)(vc + eo), dst + 4096u * (uint32_t)(NH + h) + 1024u * (uint32_t)e);
+            }
         }
     };
     /* the first sub-tiles are in flight while the query fragments are built
@@ -1030,24 +1055,28 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             fetch(t + (uint32_t)DMA_AHEAD);
         }
-        dma_wait(min(nsub - 1u - t, (uint32_t)DMA_AHEAD));
+        dma_wait<HD>(min(nsub - 1u - t, (uint32_t)DMA_AHEAD));
         const uint32_t p0  = kb + 32u * t;
-        const uint8_t *kt0 = ring + (t % (uint32_t)DMA_NBUF) * (uint32_t)DMA_TILE;
-        const uint8_t *vt0 = kt0 + 4096;
+        const uint8_t *kt0 = ring + (t % (uint32_t)DMA_NBUF) * TILE;
+        const uint8_t *vt0 = kt0 + NH * 4096;
 
-        /* S^T = K . Q^T (log2 units) */
+        /* S^T = K . Q^T (log2 units); k-step st reads 64-dim half st / 2 */
         float4_t sacc[2][NT];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) {
-            const half8_t k0 = as_half8(*reinterpret_cast<const u32x4_t *>(kt0 + kt * 2048 + koff0));
-            const half8_t k1 = as_half8(*reinterpret_cast<const u32x4_t *>(kt0 + kt * 2048 + koff1));
+            half8_t kf[NS];
+#pragma unroll
+            for (int st = 0; st < NS; ++st)
+                kf[st] = as_half8(*reinterpret_cast<const u32x4_t *>(kt0 + (st >> 1) * 4096 + kt * 2048 +
+                                                                     ((st & 1) ? koff1 : koff0)));
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 float4_t acc = (float4_t)0.0f;
-                acc          = mfma(k0, qh[nt][0], acc);
-                acc          = mfma(k0, ql[nt][0], acc);
-                acc          = mfma(k1, qh[nt][1], acc);
-                acc          = mfma(k1, ql[nt][1], acc);
+#pragma unroll
+                for (int st = 0; st < NS; ++st) {
+                    acc = mfma(kf[st], qh[nt][st], acc);
+                    acc = mfma(kf[st], ql[nt][st], acc);
+                }
                 sacc[kt][nt] = acc;
             }
         }
@@ -1101,9 +1130,10 @@ __device__ __forceinline__ void run_segment_dma(const SplitParams &P, uint8_t *r
         /* O^T += V^T . P^T */
 #pragma unroll
         for (int mt = 0; mt < NM; ++mt) {
-            const uint32_t o  = vtr ^ (32u * (uint32_t)mt);
-            const half4v_t lo = lds_read_tr(vt0 + o);
-            const half4v_t hi = lds_read_tr(vt0 + 16u * 128u + o);
+            const uint8_t *vh = vt0 + (mt >> 2) * 4096; /* 64-dim half */
+            const uint32_t o  = vtr ^ (32u * (uint32_t)(mt & 3));
+            const half4v_t lo = lds_read_tr(vh + o);
+            const half4v_t hi = lds_read_tr(vh + 16u * 128u + o);
             const half8_t av  = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
@@ -1344,12 +1374,13 @@ __device__ __forceinline__ void find_seq(const SplitParams &P, uint64_t t, int l
     }
 }
 
-/* DMA: the waves run LDS-streamed segments (run_segment_dma; head_dim 64,
- * no fused prologue), each with its DMA_NBUF-slot ring. */
+/* DMA: the waves run LDS-streamed segments (run_segment_dma; no fused
+ * prologue), each with its DMA_NBUF-slot ring. */
 template <int HD, int NT, int W, bool FUSE, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
-    static_assert(!DMA || (HD == 64 && !FUSE), "LDS-streamed segments: head_dim 64, no fused prologue");
-    constexpr size_t LDS_BYTES = DMA ? (size_t)W * DMA_NBUF * DMA_TILE : (size_t)W * vt_halfs<HD>() * 2u;
+    static_assert(!DMA || !FUSE, "LDS-streamed segments: no fused prologue");
+    constexpr size_t LDS_BYTES = DMA ? (size_t)W * DMA_NBUF * dma_tile<HD>() : (size_t)W * vt_halfs<HD>() * 2u;
+    static_assert(LDS_BYTES <= 163840, "one workgroup's LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t lds_area[LDS_BYTES];
     const lfm_bal_cfg &c = P.plan;
     const int lane       = threadIdx.x & 63;
@@ -1412,7 +1443,7 @@ __global__ __launch_bounds__(64 * W) void k_splitkv_bal(const SplitParams P) {
             lfm_bal_seg_keys(&c, pos0, a, b, &kb, &ke);
             const size_t part = ((size_t)slot * P.n_head_kv + kvh) * P.ncols;
             if constexpr (DMA)
-                run_segment_dma<NT>(P, lds_area + (size_t)wave * DMA_NBUF * DMA_TILE, seq, pos0, kvh, kb, ke, direct,
+                run_segment_dma<HD, NT>(P, lds_area + (size_t)wave * DMA_NBUF * dma_tile<HD>(), seq, pos0, kvh, kb, ke, direct,
                                     part);
             else
                 run_segment<HD, NT, FUSE>(P, reinterpret_cast<uint16_t *>(lds_area) + (size_t)wave * vt_halfs<HD>(),
@@ -1833,6 +1864,8 @@ int launch_hd_nt(const SplitParams &p, uint32_t n_seq, uint32_t keys_hint, const
     if (pc.kind == 'w') return launch_wg<HD, NT, FUSE>(p, n_seq, stream);
     if (pc.kind == 'd') {
         if constexpr (HD == 64 && NT <= 2 && !FUSE) return launch_bal<HD, NT, 4, FUSE, true>(p, keys_hint, t, stream, sc);
+        else if constexpr (HD == 128 && NT == 1 && !FUSE)
+            return launch_bal<HD, NT, 2, FUSE, true>(p, keys_hint, t, stream, sc);
         else return LFM_ATTN_E_INVALID; /* choose_plan never picks it here */
     }
     const uint32_t w = pc.waves;
@@ -1895,10 +1928,12 @@ int dispatch_nt(const SplitParams &p, const AttnBatch &b, uint32_t keys_hint, co
  *    at ctx 4096: 29.2 -> 22.0 us); larger grids unchanged.
  * The overrides force a plan ('g', 'b', 'w'), waves or a chunk; a waves or
  * chunk override keeps the grid off its in-workgroup form. */
-/* Batches the LDS-streamed balanced form runs: head_dim 64, at most two
- * 16-column tiles, no fused prologue. */
+/* Batches the LDS-streamed balanced form runs: no fused prologue; head_dim
+ * 64 with at most two 16-column tiles (4-wave workgroups), or head_dim 128
+ * with one (2-wave workgroups: a wave's ring is 64 KB). */
 static bool dma_eligible(const AttnBatch &b, bool fuse) {
-    return b.head_dim == 64u && !fuse && tiles_of(64u, b.n_rows * (b.n_head_q / b.n_head_kv)) <= 2u;
+    const uint32_t nt = tiles_of(b.head_dim, b.n_rows * (b.n_head_q / b.n_head_kv));
+    return !fuse && ((b.head_dim == 64u && nt <= 2u) || (b.head_dim == 128u && nt == 1u));
 }
 
 PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on_device, bool fuse, uint32_t cus,
@@ -1936,7 +1971,7 @@ PlanChoice choose_plan(const AttnBatch &b, uint32_t keys_hint, bool positions_on
     const bool dma_default = t.plan == 0 && !t.waves && tiles_of(b.head_dim, ncols) == 2u;
     if (!grid && (t.plan == 'd' || dma_default) && dma_eligible(b, fuse)) {
         pc.kind  = 'd';
-        pc.waves = 4u;
+        pc.waves = b.head_dim == 128u ? 2u : 4u;
     }
     return pc;
 }

@@ -1,6 +1,7 @@
 """GPU parity of the LDS-streamed balanced plan ("balanced-dma": k_splitkv_bal
-with run_segment_dma, head_dim 64, up to 32 query columns, K and V moved into
-each wave's LDS ring three 32-key sub-tiles ahead) against the oracle's
+with run_segment_dma -- head_dim 64 with up to 32 query columns, head_dim 128
+with up to 16 -- K and V moved into each wave's LDS ring three 32-key
+sub-tiles ahead) against the oracle's
 lfm3_online_gqa_f16 (tools/lfm3_engine.c:851-946 semantics: rows at positions
 ctx .. ctx + n_rows - 1 attend [t_start, pos]) and against the register
 plan ("balanced") on the same batches."""
@@ -68,10 +69,37 @@ def test_dma_plan_window_ring(gpu, orc, win, cap, n_rows):
     parity(got, want, what=f"balanced-dma window={win} cap={cap} rows={n_rows}")
 
 
+@pytest.mark.parametrize("nq,nkv,n_rows,n_seq,max_ctx,win,cap,gate", [
+    (16, 4, 1, 9, 5000, 0, 0, True),     # LFM3 full-layer heads, ragged, gate
+    (16, 4, 4, 3, 1200, 0, 0, False),    # 4 rows x 4 heads = 16 columns
+    (16, 4, 1, 7, 2000, 256, 264, True),  # LFM3 SWA ring (window 256, 264 slots) + gate
+    (8, 8, 1, 5, 300, 0, 0, False),      # short sequences, MHA
+    (16, 2, 1, 4, 900, 0, 0, True),      # two KV heads: one 2-wave workgroup per (sequence, share)
+])
+def test_dma_plan_head_dim_128(gpu, orc, nq, nkv, n_rows, n_seq, max_ctx, win, cap, gate):
+    """Head_dim 128 (two 64-dim halves per row, 16 KB per sub-tile, 2-wave
+    workgroups): the forced plan against the oracle and the register plan."""
+    la = gpu
+    rng = np.random.default_rng(max_ctx + n_seq + nq + win)
+    ctx = [int(c) for c in rng.integers(0, max_ctx, size=n_seq)]
+    ctx[0] = 0 if not win else 3
+    ctx[-1] = max_ctx - 1
+    outs = {}
+    for plan in ("balanced-dma", "balanced"):
+        with la.tuning(plan):
+            got, want = _varlen_case(la, orc, np.random.default_rng(11), n_seq, n_rows, nq, nkv, 128, ctx, win=win,
+                                     cap=cap, gate=gate, slots=cap or None)
+            assert la.last_plan() == plan
+        parity(got, want, what=f"{plan} d128 {nq}q/{nkv}kv rows={n_rows} win={win}")
+        outs[plan] = got
+    assert np.abs(outs["balanced-dma"] - outs["balanced"]).max() < plan_tol(n_rows, nq, nkv)
+
+
 def test_dma_plan_not_taken_where_ineligible(gpu, orc):
-    """head_dim 128 batches keep the register plan under the override."""
+    """Head_dim 128 with two 16-column tiles keeps the register plan under
+    the override."""
     la = gpu
     with la.tuning("balanced-dma"):
-        got, want = _varlen_case(la, orc, np.random.default_rng(2), 3, 1, 16, 4, 128, [100, 900, 2000])
+        got, want = _varlen_case(la, orc, np.random.default_rng(2), 3, 8, 16, 4, 128, [100, 900, 2000])
         assert la.last_plan() == "balanced"
-    parity(got, want, what="d128 under the balanced-dma override")
+    parity(got, want, what="d128 8 rows under the balanced-dma override")

@@ -192,7 +192,8 @@ def test_plan_overrides_and_lds_budget():
     with la.tuning("balanced-dma"):
         assert la.plan_preview(**cfg2)[:2] == ("balanced-dma", 4)
         assert la.plan_preview(**dict(cfg2, fused=True))[:2] == ("balanced", 8)
-        assert la.plan_preview(**dict(cfg2, head_dim=128, n_head_q=16, n_head_kv=4))[0] == "balanced"
+        assert la.plan_preview(**dict(cfg2, head_dim=128, n_head_q=16, n_head_kv=4))[:2] == ("balanced-dma", 2)
+        assert la.plan_preview(**dict(cfg2, head_dim=128, n_head_q=16, n_head_kv=4, n_rows=8))[0] == "balanced"
         assert la.plan_preview(**dict(verify, n_rows=16))[0] == "balanced"  # 64 columns
     with la.tuning("balanced"):
         assert la.plan_preview(**verify)[:2] == ("balanced", 8)
