@@ -88,6 +88,16 @@ int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, ui
                           uint32_t window_len, uint32_t keys_hint, int positions_on_device, int fused, uint32_t n_cus,
                           const char **plan, uint32_t out3[3]);
 
+/* Diagnostic, no reference counterpart, needs no device: the launch shape
+ * lfm_hip_lfm3_prefill_f16 takes for a prompt (n_seq x n_tok rows from
+ * position pos_0, sliding window or 0, head shape) under the current
+ * overrides: out4 = {query positions per tile, tiles per workgroup, short
+ * tiles at the sequence start dispatched first (their window reaches before
+ * position 0), workgroups}.  LFM_ATTN_E_UNSUPPORTED for a head shape that
+ * entry point does not take. */
+int lfm_attn_prefill_plan_preview(uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t window_len,
+                                  uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, uint32_t out4[4]);
+
 /* ---- device plumbing (so C11 callers need no HIP headers) ------------------ */
 int lfm_attn_device_count(int *count);
 /* Makes `device` current for this thread and resolves the device address of

@@ -30,6 +30,7 @@ SIGNATURES = {
     "lfm_attn_set_tuning": (_int, [C.c_char_p, _u32, _u32, _u32, _u32]),
     "lfm_attn_plan_preview": (_int, [_u32, _u32, _u32, _u32, _u32, _u32, _u32, _int, _int, _u32,
                                      C.POINTER(C.c_char_p), C.POINTER(_u32)]),
+    "lfm_attn_prefill_plan_preview": (_int, [_u32, _u32, _u32, _u32, _u32, _u32, _u32, C.POINTER(_u32)]),
     "lfm_attn_device_count": (_int, [C.POINTER(_int)]),
     "lfm_attn_set_device": (_int, [_int]),
     "lfm_attn_dev_alloc": (_int, [C.POINTER(_vp), _sz]),

@@ -333,6 +333,17 @@ def plan_preview(n_seq: int, n_rows: int, n_head_q: int, n_head_kv: int, head_di
     return name.value.decode(), int(out[0]), int(out[1]), int(out[2])
 
 
+def prefill_plan_preview(n_seq: int, n_tok: int, n_head_q: int, n_head_kv: int, head_dim: int = 128,
+                         pos_0: int = 0, window_len: int = 0):
+    """(query positions per tile, tiles per workgroup, short tiles dispatched
+    first, workgroups) of lfm3_prefill_f16 for a prompt, computed on the host
+    (lfm_attn_prefill_plan_preview)."""
+    out = (C.c_uint32 * 4)()
+    check(load().lfm_attn_prefill_plan_preview(n_seq, n_tok, pos_0, window_len, n_head_q, n_head_kv, head_dim, out),
+          "lfm_attn_prefill_plan_preview")
+    return tuple(int(x) for x in out)
+
+
 def last_plan() -> str:
     """Form of this thread's last decode / step attention launch: "wg",
     "grid", "balanced" or "generic" (lfm_attn_last_plan)."""

@@ -98,6 +98,14 @@ int launch_prefill(const float *q, const uint16_t *k, const uint16_t *v, float *
 
 /* Causal MFMA prefill for head_dim 128 with an optional sliding window and
  * output gate; K/V row r of a sequence's buffer holds position kv_pos0 + r. */
+/* The launch shape of a head_dim-128/64 prefill (host only): query
+ * positions per tile, tiles per workgroup, the short tiles at the sequence
+ * start dispatched first, workgroups. */
+struct PrefillExtPlan {
+    uint32_t tq, chain, n_light, n_wg;
+};
+PrefillExtPlan prefill_ext_plan(uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t window, uint32_t n_head_q,
+                                uint32_t n_head_kv);
 bool prefill_ext_supports(uint32_t head_dim, uint32_t kv_mul);
 int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, const float *gate, int gate_is_logit,
                        float *out, uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t kv_pos0,

@@ -589,6 +589,20 @@ static uint32_t prefill_chain(uint32_t window, uint32_t tq, uint32_t n_qtiles) {
     return forced ? min(forced, n_qtiles) : 1u;
 }
 
+PrefillExtPlan prefill_ext_plan(uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t window, uint32_t n_head_q,
+                                uint32_t n_head_kv) {
+    PrefillExtPlan pl{};
+    pl.tq       = 128u / (n_head_q / n_head_kv);
+    const uint32_t n_qtiles = (n_tok + pl.tq - 1u) / pl.tq;
+    pl.chain    = prefill_chain(window, pl.tq, n_qtiles);
+    /* tiles whose window reaches before the sequence start (first row's
+     * position + 1 < window): the first ceil((window - pos_0 - 1) / tq) */
+    pl.n_light  = (pl.chain == 1u && window > pos_0 + 1u) ? min(n_qtiles, (window - pos_0 - 1u + pl.tq - 1u) / pl.tq)
+                                                          : 0u;
+    pl.n_wg     = ((n_qtiles + pl.chain - 1u) / pl.chain) * n_head_kv * n_seq;
+    return pl;
+}
+
 bool prefill_ext_supports(uint32_t head_dim, uint32_t kv_mul) {
     return (head_dim == 128u || head_dim == 64u) && kv_mul >= 1u && kv_mul <= 32u && (128u % kv_mul) == 0u;
 }
@@ -613,16 +627,13 @@ int launch_prefill_ext(const float *q, const uint16_t *k, const uint16_t *v, con
     P.n_head_q      = n_head_q;
     P.n_head_kv     = n_head_kv;
     P.kv_mul        = n_head_q / n_head_kv;
-    P.tq            = 128u / P.kv_mul;
+    const PrefillExtPlan pl = prefill_ext_plan(n_seq, n_tok, pos_0, window, n_head_q, n_head_kv);
+    P.tq            = pl.tq;
     P.n_qtiles      = (n_tok + P.tq - 1u) / P.tq;
     P.qmul          = scale * kLog2e;
-    P.chain         = prefill_chain(window, P.tq, P.n_qtiles);
-    /* tiles whose window reaches before the sequence start (first row's
-     * position + 1 < window): the first ceil((window - pos_0 - 1) / tq) */
-    P.n_light = (P.chain == 1u && window > pos_0 + 1u)
-                    ? min(P.n_qtiles, (window - pos_0 - 1u + P.tq - 1u) / P.tq)
-                    : 0u;
-    const uint32_t n_wg = ((P.n_qtiles + P.chain - 1u) / P.chain) * n_head_kv * n_seq;
+    P.chain         = pl.chain;
+    P.n_light       = pl.n_light;
+    const uint32_t n_wg = pl.n_wg;
     hipEvent_t ev0, ev1;
     profile_events(&ev0, &ev1);
     if (ev0) (void)hipEventRecord(ev0, stream);

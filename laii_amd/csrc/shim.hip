@@ -166,6 +166,19 @@ int lfm_attn_plan_preview(uint32_t n_seq, uint32_t n_rows, uint32_t n_head_q, ui
     return LFM_ATTN_OK;
 }
 
+int lfm_attn_prefill_plan_preview(uint32_t n_seq, uint32_t n_tok, uint32_t pos_0, uint32_t window_len,
+                                  uint32_t n_head_q, uint32_t n_head_kv, uint32_t head_dim, uint32_t out4[4]) {
+    if (!out4 || n_seq == 0u || n_tok == 0u || n_head_q == 0u || n_head_kv == 0u || n_head_q % n_head_kv != 0u)
+        return LFM_ATTN_E_INVALID;
+    if (!lfm::prefill_ext_supports(head_dim, n_head_q / n_head_kv)) return LFM_ATTN_E_UNSUPPORTED;
+    const lfm::PrefillExtPlan pl = lfm::prefill_ext_plan(n_seq, n_tok, pos_0, window_len, n_head_q, n_head_kv);
+    out4[0] = pl.tq;
+    out4[1] = pl.chain;
+    out4[2] = pl.n_light;
+    out4[3] = pl.n_wg;
+    return LFM_ATTN_OK;
+}
+
 int lfm_attn_profile_events(void *before, void *after) {
     if ((before == nullptr) != (after == nullptr)) return LFM_ATTN_E_INVALID;
     lfm::g_prof_before = reinterpret_cast<hipEvent_t>(before);
