@@ -479,7 +479,7 @@ def box_peaks(hip, la, steps=10):
                 mfma="4096 x 4 waves, 8 independent 16x16x32 f16 MFMA chains per wave")
 
 
-CPU_WARM, CPU_REPS = 3, 10  # BASELINE.md's method: median of >= 10 passes after 3 warm-ups
+CPU_WARM, CPU_REPS = 3, 10  # the benchmark method: median of >= 10 timed passes after 3 warm-ups
 
 
 def _cpu_legs(ref, kind, q, k_list, v_list, pos0, nq, nkv, hd, n_threads, algo, unit, **kw):

@@ -40,7 +40,7 @@ def test_linear_plan(orc):
         assert la.slot_of(abs_pos, 0, 0) == abs_pos
 
 
-def test_survey_special_cases():
+def test_ring_special_cases():
     """pos 1000, window 256: cap 256 -> slots 233..255 then 0..232;
     cap 264 -> slots 217..263 then 0..208."""
     assert la.seg_plan(1000, 256, 256) == (745, 256, 233, 23, 233)
